@@ -1,0 +1,201 @@
+/*
+ * llambda_hip.h -- C ABI of libllambda_hip.so, the MI355X (gfx950) backend
+ * for llambda's quantized decode hot path.
+ *
+ * The library mirrors the conventions of the reference's native bridge
+ * (native/llambda_npu.h:1-70, native/llambda_npu.cpp:1-539):
+ *   - every function is extern "C" and takes plain pointers and sizes;
+ *   - status ints: 0 = success, -1 = failure with llambda_hip_last_error()
+ *     describing it (thread-local; cleared on entry of every call that can
+ *     fail); C++ exceptions never cross the boundary;
+ *   - sessions are opaque, owned by the caller, destroyed with a null-safe
+ *     destroy; element-count getters return 0 for null;
+ *   - a run is synchronous on host pointers: input copied to the device, the
+ *     kernels, output copied back, stream synchronised, before returning
+ *     (llambda.lisp:294-295, 343-344 pin Lisp arrays only for the call).
+ * One session may not be run from two threads at once (the Lisp side holds
+ * a per-projection run-mutex, llambda.lisp:4726); different sessions may.
+ *
+ * GGML type tags are llambda's (llambda.lisp:24-31): F32 = 0, Q5_0 = 6,
+ * Q8_0 = 8, Q4_K = 12, Q6_K = 14.  Packed rows are GGUF super-block bytes,
+ * verbatim; row r of an N x K tensor starts at r * row_bytes(type, K)
+ * (llambda.lisp:2147-2155, 3909-3927).
+ */
+#ifndef LLAMBDA_HIP_H
+#define LLAMBDA_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct llambda_hip_session llambda_hip_session;
+typedef struct llambda_hip_moe_session llambda_hip_moe_session;
+
+/* ---- probe, versions, errors -------------------------------------- */
+
+/* 1 = a gfx950 device is usable, 0 = none, -1 = error (last_error set).
+ * Replaces llambda_gpu_probe / llambda_npu_probe (native/llambda_npu.h:25, 45). */
+int llambda_hip_probe(void);
+
+/* Replaces llambda_npu_bridge_version (native/llambda_npu.h:26). */
+const char* llambda_hip_bridge_version(void);
+
+/* HIP runtime and driver versions.  Replaces llambda_npu_runtime_version
+ * (native/llambda_npu.h:27). */
+const char* llambda_hip_runtime_version(void);
+
+/* Thread-local description of the last failure.  Replaces
+ * llambda_npu_last_error (native/llambda_npu.h:28). */
+const char* llambda_hip_last_error(void);
+
+/* Lower-case hex SHA-256 of data into output (output_size >= 65).  Replaces
+ * llambda_npu_sha256 (native/llambda_npu.h:29-33), used for projection cache
+ * keys (llambda.lisp:2894-2993). */
+int llambda_hip_sha256(const void* data, size_t data_size, char* output, size_t output_size);
+
+/* ---- 2-D projection sessions -------------------------------------- */
+
+/* Open a packed-projection file written by the backend's exporter:
+ *   bytes 0..7   magic "LLHIPPRJ"
+ *   8..11        u32 format version (1)
+ *   12..15       u32 GGML type tag
+ *   16..23       u64 rows (N)
+ *   24..31       u64 columns (K)
+ *   32..39       u64 payload bytes (= N * row_bytes(type, K))
+ *   40..         payload: the tensor's GGUF bytes, verbatim
+ * cache_dir and cache_key are accepted for signature compatibility and not
+ * used.  Replaces llambda_npu_session_create (native/llambda_npu.h:35-39),
+ * called by make-session-function (accelerator.lisp:42-45). */
+int llambda_hip_session_create(const char* model_path, const char* cache_dir,
+                               const char* cache_key, llambda_hip_session** result);
+
+/* Upload an N x K tensor straight from host bytes (e.g. the GGUF mapping at
+ * the tensor's data offset).  No counterpart in the reference's bridge; it is
+ * the zero-copy form of session_create for callers that hold the mapping. */
+int llambda_hip_session_create_packed(const void* data, size_t data_size, int ggml_type,
+                                      int64_t rows, int64_t columns,
+                                      llambda_hip_session** result);
+
+/* Null-safe.  Replaces llambda_npu_session_destroy (native/llambda_npu.h:40). */
+void llambda_hip_session_destroy(llambda_hip_session* session);
+
+/* K and N; 0 for null.  Replace llambda_npu_session_{input,output}_element_count
+ * (native/llambda_npu.h:41-44), checked at registration (llambda.lisp:2686-2703). */
+size_t llambda_hip_session_input_element_count(const llambda_hip_session* session);
+size_t llambda_hip_session_output_element_count(const llambda_hip_session* session);
+
+/* output[N] = W x for input[K], synchronous.  -1 on null or count mismatch.
+ * Replaces llambda_npu_session_run (native/llambda_npu.h:45-50); the same
+ * contract as %gguf-model-matrix-vector-multiply-into (llambda.lisp:4542-4658). */
+int llambda_hip_session_run(llambda_hip_session* session, const float* input,
+                            size_t input_element_count, float* output,
+                            size_t output_element_count);
+
+/* Multi-token form: input [batch][K], output [batch][N], synchronous.  No
+ * counterpart in the reference (its prefill is one token at a time,
+ * llambda.lisp:1319-1341); row t equals session_run on row t. */
+int llambda_hip_session_run_batch(llambda_hip_session* session, const float* input,
+                                  size_t input_element_count, float* output,
+                                  size_t output_element_count, size_t batch);
+
+/* Device-resident form: input/output are device pointers ([batch][K],
+ * [batch][N]); the kernels are enqueued on `stream` (a hipStream_t, or null
+ * for the session's own stream) and the call returns without waiting.
+ * For callers that keep activations in HBM (and for benchmarking). */
+int llambda_hip_session_run_device(llambda_hip_session* session, const float* input,
+                                   float* output, size_t batch, void* stream);
+
+/* output[N*K] = the dequantised weights, bit-identical to dequantize-q4-k-m
+ * / dequantize-q6-k / dequantize-q5-0 / dequantize-q8-0 (llambda.lisp:
+ * 6815-6978, 3965-4009).  Verification hook; synchronous. */
+int llambda_hip_session_dequantize(llambda_hip_session* session, float* output,
+                                   size_t output_element_count);
+
+/* ---- routed-MoE layer sessions ------------------------------------ */
+
+enum {
+  LLAMBDA_HIP_MOE_QWEN3NEXT = 0, /* qwen3next-moe-into, llambda.lisp:5321-5426 */
+  LLAMBDA_HIP_MOE_NEMOTRON_H = 1 /* nemotron-h-moe-ffn-into, llambda.lisp:5827-5949 */
+};
+
+/* One MoE layer's tensors (host memory, copied at creation).  Expert tensors
+ * are the flat GGUF 3-D slabs: rows [e*rows, (e+1)*rows) belong to expert e
+ * (llambda.lisp:4951-4971).  Tensor names per llambda.lisp:5321-5426 and
+ * 5827-5949 (blk.N.<name>): */
+typedef struct llambda_hip_moe_desc {
+  int variant;                /* LLAMBDA_HIP_MOE_* */
+  int64_t hidden;             /* H */
+  int64_t expert_count;       /* E (rows of ffn_gate_inp) */
+  int64_t top_k;              /* min(E, expert_used_count) */
+  int64_t expert_ffn;         /* F (rows per expert of ffn_up_exps) */
+  int64_t shared_ffn;         /* Fs (rows of ffn_up_shexp); 0 = no shared expert */
+  const float* router;        /* ffn_gate_inp, F32 [E][H] */
+  const float* shared_gate_inp; /* ffn_gate_inp_shexp, F32 [H] (qwen3next) */
+  const float* router_bias;   /* exp_probs_b.bias, F32 [E] (nemotron) */
+  float expert_weights_scale; /* nemotron_h_moe.expert_weights_scale (default 1) */
+  int expert_weights_norm;    /* nemotron_h_moe.expert_weights_norm */
+  int gate_type;              /* ffn_gate_exps [E*F][H] (qwen3next) */
+  const void* gate_exps;
+  int up_type;                /* ffn_up_exps [E*F][H] */
+  const void* up_exps;
+  int down_type;              /* ffn_down_exps [E*H][F] */
+  const void* down_exps;
+  int shared_gate_type;       /* ffn_gate_shexp [Fs][H] (qwen3next) */
+  const void* shared_gate;
+  int shared_up_type;         /* ffn_up_shexp [Fs][H] */
+  const void* shared_up;
+  int shared_down_type;       /* ffn_down_shexp [H][Fs] */
+  const void* shared_down;
+} llambda_hip_moe_desc;
+
+/* Upload one layer.  No counterpart in the reference's bridge (its routed
+ * experts bypass the accelerator store, llambda.lisp:4951-4971); this is the
+ * per-layer hook registered under blk.N.ffn_gate_inp.weight. */
+int llambda_hip_moe_session_create(const llambda_hip_moe_desc* desc,
+                                   llambda_hip_moe_session** result);
+
+void llambda_hip_moe_session_destroy(llambda_hip_moe_session* session);
+
+/* H; 0 for null. */
+size_t llambda_hip_moe_session_hidden_size(const llambda_hip_moe_session* session);
+
+/* output[batch][H] = the layer's FFN output (before the residual add) for
+ * input[batch][H], token by token as the reference computes it.  Synchronous.
+ * top_indices / top_weights (optional, [batch][k]) receive the selected
+ * experts in rank order and their final weights; router_logits (optional,
+ * [batch][E]) the router logits (after the bias for nemotron).  Returns -1
+ * with the reference's error text when it would have signalled one
+ * (non-positive weight sum, fewer than k finite logits). */
+int llambda_hip_moe_session_run(llambda_hip_moe_session* session, const float* input,
+                                size_t input_element_count, float* output,
+                                size_t output_element_count, size_t batch,
+                                int64_t* top_indices, float* top_weights,
+                                float* router_logits);
+
+/* Device-resident form; enqueues on `stream` (null = the session's stream)
+ * and returns without waiting.  Errors raised by the kernels are reported by
+ * the next llambda_hip_moe_session_sync. */
+int llambda_hip_moe_session_run_device(llambda_hip_moe_session* session, const float* input,
+                                       float* output, size_t batch, void* stream);
+
+/* Wait for `stream` (null = the session's stream) and report any error flag
+ * raised by the kernels since the last check. */
+int llambda_hip_moe_session_sync(llambda_hip_moe_session* session, void* stream);
+
+/* ---- routing primitive ---------------------------------------------- */
+
+/* For each of `batch` rows of n logits, the k selected by
+ * select-top-k-logits-into (llambda.lisp:5265-5292): descending, lower
+ * index first among equal values, NaN and values <= -FLT_MAX never chosen,
+ * unfilled slots (-1, -FLT_MAX).  Host pointers, synchronous, on the device. */
+int llambda_hip_select_top_k(const float* logits, size_t n, size_t k, size_t batch,
+                             int64_t* top_indices, float* top_logits);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif

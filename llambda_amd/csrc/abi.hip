@@ -1,0 +1,685 @@
+// abi.hip -- the extern "C" boundary of libllambda_hip.so (include/llambda_hip.h).
+//
+// Conventions follow the reference's native bridge (native/llambda_npu.cpp):
+// thread-local last error cleared on entry, status 0 / -1, exceptions caught
+// at the boundary, null-safe destroy, synchronous runs on host pointers.
+#include "../../include/llambda_hip.h"
+
+#include <fcntl.h>
+#include <sys/mman.h>
+#include <sys/stat.h>
+#include <unistd.h>
+
+#include <climits>
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <mutex>
+#include <stdexcept>
+#include <string>
+#include <vector>
+
+#include "gemv.h"
+#include "moe.h"
+#include "sha256.h"
+
+using namespace llhip;
+
+namespace {
+
+thread_local std::string g_last_error;
+
+struct Failure : std::runtime_error {
+  using std::runtime_error::runtime_error;
+};
+
+[[noreturn]] void failf(const char* fmt, ...) {
+  char buf[1024];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof buf, fmt, ap);
+  va_end(ap);
+  throw Failure(buf);
+}
+
+void hip_check(hipError_t e, const char* what) {
+  if (e != hipSuccess) failf("%s failed: %s (%d)", what, hipGetErrorString(e), (int)e);
+}
+#define HIPC(expr) hip_check((expr), #expr)
+
+template <typename F>
+int guarded(F&& f) {
+  g_last_error.clear();
+  try {
+    f();
+    return 0;
+  } catch (const std::exception& e) {
+    g_last_error = e.what();
+  } catch (...) {
+    g_last_error = "unknown C++ exception";
+  }
+  return -1;
+}
+
+bool supported_type(int t) {
+  return t == kF32 || t == kQ4_K || t == kQ6_K || t == kQ5_0 || t == kQ8_0;
+}
+
+const char* type_name(int t) {
+  switch (t) {
+    case kF32: return "F32";
+    case kQ4_K: return "Q4_K";
+    case kQ6_K: return "Q6_K";
+    case kQ5_0: return "Q5_0";
+    case kQ8_0: return "Q8_0";
+    default: return "?";
+  }
+}
+
+// ggml-tensor-byte-size (llambda.lisp:2147-2155) for one row of K columns,
+// plus the layout limits of the kernels (units of 32 weights).
+int64_t checked_row_bytes(int type, int64_t columns, const char* what) {
+  if (!supported_type(type)) failf("%s: unsupported GGML tensor type tag %d", what, type);
+  const int be = block_weights(type);
+  if (columns <= 0) failf("%s: column count %lld must be positive", what, (long long)columns);
+  if (columns % be)
+    failf("%s: Tensor element count %lld is not a multiple of block size %d for type %s.", what,
+          (long long)columns, be, type_name(type));
+  if (type == kF32 && columns % 4)
+    failf("%s: F32 rows need a column count divisible by 4, got %lld", what, (long long)columns);
+  if (columns > kMaxColumns)
+    failf("%s: column count %lld exceeds the supported %lld", what, (long long)columns,
+          (long long)kMaxColumns);
+  return columns / be * block_bytes(type);
+}
+
+// RAII device buffer.
+struct DevBuf {
+  void* ptr = nullptr;
+  size_t bytes = 0;
+  DevBuf() = default;
+  DevBuf(const DevBuf&) = delete;
+  DevBuf& operator=(const DevBuf&) = delete;
+  ~DevBuf() { reset(); }
+  void reset() {
+    if (ptr) (void)hipFree(ptr);
+    ptr = nullptr;
+    bytes = 0;
+  }
+  void alloc(size_t n, const char* what) {
+    reset();
+    if (n == 0) n = 16;
+    hipError_t e = hipMalloc(&ptr, n);
+    if (e != hipSuccess) {
+      ptr = nullptr;
+      failf("hipMalloc of %zu bytes for %s failed: %s", n, what, hipGetErrorString(e));
+    }
+    bytes = n;
+  }
+  template <typename T>
+  T* as() const { return static_cast<T*>(ptr); }
+};
+
+int current_device_checked() {
+  int count = 0;
+  hipError_t e = hipGetDeviceCount(&count);
+  if (e != hipSuccess || count <= 0) failf("no HIP device available");
+  int dev = 0;
+  HIPC(hipGetDevice(&dev));
+  return dev;
+}
+
+// Upload packed bytes with kWeightPad readable (zeroed) bytes after them and
+// reject Inf/NaN fp16 scale fields as fp16-to-single-float does
+// (llambda.lisp:727-728).
+void upload_weights(DevBuf& buf, const void* host, size_t bytes, int type, int64_t nblocks,
+                    hipStream_t stream, const char* what) {
+  buf.alloc(bytes + kWeightPad, what);
+  HIPC(hipMemcpyAsync(buf.ptr, host, bytes, hipMemcpyHostToDevice, stream));
+  std::vector<uint8_t> zeros(kWeightPad, 0);
+  HIPC(hipMemcpyAsync(buf.as<uint8_t>() + bytes, zeros.data(), kWeightPad, hipMemcpyHostToDevice,
+                      stream));
+  if (type == kF32) {
+    HIPC(hipStreamSynchronize(stream));
+    return;
+  }
+  DevBuf flag;
+  flag.alloc(sizeof(unsigned long long), "validation flag");
+  const unsigned long long none = ULLONG_MAX;
+  HIPC(hipMemcpyAsync(flag.ptr, &none, sizeof none, hipMemcpyHostToDevice, stream));
+  HIPC(validate_launch(type, buf.as<uint8_t>(), nblocks, flag.as<unsigned long long>(), stream));
+  unsigned long long first_bad = 0;
+  HIPC(hipMemcpyAsync(&first_bad, flag.ptr, sizeof first_bad, hipMemcpyDeviceToHost, stream));
+  HIPC(hipStreamSynchronize(stream));
+  if (first_bad != ULLONG_MAX)
+    failf("%s: Unsupported fp16 special value (Inf/NaN scale) in block %llu.", what, first_bad);
+}
+
+}  // namespace
+
+// ------------------------------------------------------------------ sessions
+
+struct llambda_hip_session {
+  std::mutex run_mutex;
+  int device = 0;
+  int type = 0;
+  int64_t rows = 0, columns = 0, row_bytes = 0;
+  hipStream_t stream = nullptr;
+  DevBuf weights;
+  DevBuf x, y;  // staging for the host-pointer runs
+  size_t staged_tokens = 0;
+  ~llambda_hip_session() {
+    if (stream) (void)hipStreamDestroy(stream);
+  }
+  void ensure_staging(size_t batch) {
+    if (batch <= staged_tokens) return;
+    x.alloc(batch * (size_t)columns * sizeof(float), "session input");
+    y.alloc(batch * (size_t)rows * sizeof(float), "session output");
+    staged_tokens = batch;
+  }
+  void launch(const float* dx, float* dy, size_t batch, hipStream_t s) {
+    GemvProblem p{};
+    p.type = type;
+    p.weights = weights.as<uint8_t>();
+    p.row_bytes = row_bytes;
+    p.rows = rows;
+    p.columns = columns;
+    p.x = dx;
+    p.x_stride = columns;
+    p.tokens = (int)batch;
+    p.y = dy;
+    p.y_stride = rows;
+    HIPC(gemv_launch(p, s));
+  }
+};
+
+static llambda_hip_session* make_session(const void* data, size_t size, int type, int64_t rows,
+                                         int64_t columns) {
+  const int64_t rb = checked_row_bytes(type, columns, "session");
+  if (rows <= 0 || rows > INT_MAX) failf("session: row count %lld out of range", (long long)rows);
+  if ((uint64_t)rows * (uint64_t)rb != size)
+    failf("session: %zu bytes do not hold %lld rows of %lld %s columns (%lld bytes)", size,
+          (long long)rows, (long long)columns, type_name(type), (long long)(rows * rb));
+  if (!data) failf("session: null tensor data");
+  auto* s = new llambda_hip_session();
+  try {
+    s->device = current_device_checked();
+    s->type = type;
+    s->rows = rows;
+    s->columns = columns;
+    s->row_bytes = rb;
+    HIPC(hipStreamCreateWithFlags(&s->stream, hipStreamNonBlocking));
+    const int64_t nblocks = rows * (columns / block_weights(type));
+    upload_weights(s->weights, data, size, type, nblocks, s->stream, "session");
+  } catch (...) {
+    delete s;
+    throw;
+  }
+  return s;
+}
+
+extern "C" {
+
+int llambda_hip_probe(void) {
+  g_last_error.clear();
+  int count = 0;
+  hipError_t e = hipGetDeviceCount(&count);
+  if (e == hipErrorNoDevice || (e == hipSuccess && count == 0)) return 0;
+  if (e != hipSuccess) {
+    g_last_error = std::string("hipGetDeviceCount failed: ") + hipGetErrorString(e);
+    return -1;
+  }
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return -1;
+  hipDeviceProp_t prop;
+  if (hipGetDeviceProperties(&prop, dev) != hipSuccess) return -1;
+  return std::strncmp(prop.gcnArchName, "gfx950", 6) == 0 ? 1 : 0;
+}
+
+const char* llambda_hip_bridge_version(void) { return "llambda-hip 0.1.0 (gfx950)"; }
+
+const char* llambda_hip_runtime_version(void) {
+  thread_local std::string text;
+  int rt = 0, drv = 0;
+  const bool ok_rt = hipRuntimeGetVersion(&rt) == hipSuccess;
+  const bool ok_drv = hipDriverGetVersion(&drv) == hipSuccess;
+  char buf[128];
+  snprintf(buf, sizeof buf, "HIP runtime %d, driver %d", ok_rt ? rt : -1, ok_drv ? drv : -1);
+  text = buf;
+  return text.c_str();
+}
+
+const char* llambda_hip_last_error(void) { return g_last_error.c_str(); }
+
+int llambda_hip_sha256(const void* data, size_t data_size, char* output, size_t output_size) {
+  return guarded([&] {
+    if (!output || output_size < 65) failf("sha256: output buffer must hold 65 bytes");
+    if (!data && data_size) failf("sha256: null data");
+    sha256_hex(data ? data : "", data_size, output);
+  });
+}
+
+int llambda_hip_session_create(const char* model_path, const char* cache_dir,
+                               const char* cache_key, llambda_hip_session** result) {
+  (void)cache_dir;
+  (void)cache_key;
+  return guarded([&] {
+    if (!result) failf("session_create: null result pointer");
+    *result = nullptr;
+    if (!model_path) failf("session_create: null model path");
+    const int fd = open(model_path, O_RDONLY);
+    if (fd < 0) failf("session_create: cannot open %s", model_path);
+    struct stat st;
+    if (fstat(fd, &st) != 0) {
+      close(fd);
+      failf("session_create: cannot stat %s", model_path);
+    }
+    const size_t size = (size_t)st.st_size;
+    if (size < 40) {
+      close(fd);
+      failf("session_create: %s is not a packed projection (too short)", model_path);
+    }
+    void* map = mmap(nullptr, size, PROT_READ, MAP_PRIVATE, fd, 0);
+    close(fd);
+    if (map == MAP_FAILED) failf("session_create: cannot map %s", model_path);
+    struct Unmap {
+      void* p;
+      size_t n;
+      ~Unmap() { munmap(p, n); }
+    } unmap{map, size};
+    const uint8_t* b = static_cast<const uint8_t*>(map);
+    if (std::memcmp(b, "LLHIPPRJ", 8) != 0)
+      failf("session_create: %s is not a packed projection (bad magic)", model_path);
+    uint32_t version, type;
+    uint64_t rows, columns, payload;
+    std::memcpy(&version, b + 8, 4);
+    std::memcpy(&type, b + 12, 4);
+    std::memcpy(&rows, b + 16, 8);
+    std::memcpy(&columns, b + 24, 8);
+    std::memcpy(&payload, b + 32, 8);
+    if (version != 1) failf("session_create: unsupported packed projection version %u", version);
+    if (payload != size - 40)
+      failf("session_create: %s payload size %llu does not match the file (%zu bytes)", model_path,
+            (unsigned long long)payload, size - 40);
+    *result = make_session(b + 40, (size_t)payload, (int)type, (int64_t)rows, (int64_t)columns);
+  });
+}
+
+int llambda_hip_session_create_packed(const void* data, size_t data_size, int ggml_type,
+                                      int64_t rows, int64_t columns,
+                                      llambda_hip_session** result) {
+  return guarded([&] {
+    if (!result) failf("session_create_packed: null result pointer");
+    *result = nullptr;
+    *result = make_session(data, data_size, ggml_type, rows, columns);
+  });
+}
+
+void llambda_hip_session_destroy(llambda_hip_session* session) { delete session; }
+
+size_t llambda_hip_session_input_element_count(const llambda_hip_session* session) {
+  return session ? (size_t)session->columns : 0;
+}
+
+size_t llambda_hip_session_output_element_count(const llambda_hip_session* session) {
+  return session ? (size_t)session->rows : 0;
+}
+
+int llambda_hip_session_run_batch(llambda_hip_session* s, const float* input, size_t n_in,
+                                  float* output, size_t n_out, size_t batch) {
+  return guarded([&] {
+    if (!s) failf("session_run: null session");
+    if (!input || !output) failf("session_run: null input or output");
+    if (batch == 0) failf("session_run: batch must be positive");
+    if (batch > (size_t)INT_MAX / 2) failf("session_run: batch too large");
+    if (n_in != batch * (size_t)s->columns)
+      failf("session_run: input element count %zu does not match %zu x %lld", n_in, batch,
+            (long long)s->columns);
+    if (n_out != batch * (size_t)s->rows)
+      failf("session_run: output element count %zu does not match %zu x %lld", n_out, batch,
+            (long long)s->rows);
+    std::lock_guard<std::mutex> lock(s->run_mutex);
+    HIPC(hipSetDevice(s->device));
+    s->ensure_staging(batch);
+    HIPC(hipMemcpyAsync(s->x.ptr, input, n_in * sizeof(float), hipMemcpyHostToDevice, s->stream));
+    s->launch(s->x.as<float>(), s->y.as<float>(), batch, s->stream);
+    HIPC(hipMemcpyAsync(output, s->y.ptr, n_out * sizeof(float), hipMemcpyDeviceToHost, s->stream));
+    HIPC(hipStreamSynchronize(s->stream));
+  });
+}
+
+int llambda_hip_session_run(llambda_hip_session* s, const float* input, size_t n_in,
+                            float* output, size_t n_out) {
+  return llambda_hip_session_run_batch(s, input, n_in, output, n_out, 1);
+}
+
+int llambda_hip_session_run_device(llambda_hip_session* s, const float* input, float* output,
+                                   size_t batch, void* stream) {
+  return guarded([&] {
+    if (!s) failf("session_run_device: null session");
+    if (!input || !output) failf("session_run_device: null input or output");
+    if (batch == 0 || batch > (size_t)INT_MAX / 2) failf("session_run_device: bad batch %zu", batch);
+    HIPC(hipSetDevice(s->device));
+    s->launch(input, output, batch, stream ? static_cast<hipStream_t>(stream) : s->stream);
+  });
+}
+
+int llambda_hip_session_dequantize(llambda_hip_session* s, float* output, size_t n_out) {
+  return guarded([&] {
+    if (!s) failf("session_dequantize: null session");
+    if (!output) failf("session_dequantize: null output");
+    if (n_out != (size_t)(s->rows * s->columns))
+      failf("session_dequantize: output element count %zu does not match %lld x %lld", n_out,
+            (long long)s->rows, (long long)s->columns);
+    std::lock_guard<std::mutex> lock(s->run_mutex);
+    HIPC(hipSetDevice(s->device));
+    DevBuf out;
+    out.alloc(n_out * sizeof(float), "dequantized weights");
+    if (s->type == kF32) {
+      HIPC(hipMemcpyAsync(out.ptr, s->weights.ptr, n_out * sizeof(float), hipMemcpyDeviceToDevice,
+                          s->stream));
+    } else {
+      HIPC(dequant_launch(s->type, s->weights.as<uint8_t>(), s->row_bytes, s->rows, s->columns,
+                          out.as<float>(), s->stream));
+    }
+    HIPC(hipMemcpyAsync(output, out.ptr, n_out * sizeof(float), hipMemcpyDeviceToHost, s->stream));
+    HIPC(hipStreamSynchronize(s->stream));
+  });
+}
+
+}  // extern "C"
+
+// ------------------------------------------------------------- MoE sessions
+
+struct llambda_hip_moe_session {
+  std::mutex run_mutex;
+  int device = 0;
+  hipStream_t stream = nullptr;
+  MoePlan plan{};
+  DevBuf router, bias, gate, up, down, sh_gate, sh_up, sh_down;
+  DevBuf logits, top_idx, top_w, shared_w, counts, perm, chunks, chunk_counts, act, down_out,
+      error;
+  DevBuf x, y;
+  int staged = 0;
+  ~llambda_hip_moe_session() {
+    if (stream) (void)hipStreamDestroy(stream);
+  }
+  // Size the scratch for `tokens` tokens (grows only).
+  void ensure_capacity(int tokens) {
+    if (tokens <= plan.capacity) return;
+    MoePlan& p = plan;
+    const size_t T = (size_t)tokens, K = (size_t)p.top_k, E = (size_t)p.experts;
+    const size_t pairs = T * (K + 1);
+    const size_t act_w = (size_t)std::max(p.ffn, p.shared_ffn);
+    logits.alloc(T * (E + 1) * sizeof(float), "router logits");
+    top_idx.alloc(T * K * sizeof(int), "top-k indices");
+    top_w.alloc(T * K * sizeof(float), "top-k weights");
+    shared_w.alloc(T * sizeof(float), "shared weights");
+    perm.alloc(pairs * sizeof(int), "permutation");
+    p.capacity = tokens;
+    chunks.alloc((size_t)moe_max_chunks(p, tokens, 1) * sizeof(MoeChunk), "chunk table");
+    act.alloc(pairs * act_w * sizeof(float), "activations");
+    down_out.alloc(pairs * (size_t)p.hidden * sizeof(float), "expert outputs");
+    p.logits = logits.as<float>();
+    p.top_idx = top_idx.as<int>();
+    p.top_w = top_w.as<float>();
+    p.shared_w = shared_w.as<float>();
+    p.perm = perm.as<int>();
+    p.chunks = chunks.as<MoeChunk>();
+    p.act = act.as<float>();
+    p.down_out = down_out.as<float>();
+  }
+  void ensure_staging(int tokens) {
+    if (tokens <= staged) return;
+    x.alloc((size_t)tokens * plan.hidden * sizeof(float), "MoE input");
+    y.alloc((size_t)tokens * plan.hidden * sizeof(float), "MoE output");
+    staged = tokens;
+  }
+  int take_error(hipStream_t s) {
+    int flag = 0;
+    HIPC(hipMemcpyAsync(&flag, plan.error, sizeof flag, hipMemcpyDeviceToHost, s));
+    HIPC(hipStreamSynchronize(s));
+    if (flag) {
+      const int zero = 0;
+      HIPC(hipMemcpyAsync(plan.error, &zero, sizeof zero, hipMemcpyHostToDevice, s));
+      HIPC(hipStreamSynchronize(s));
+    }
+    return flag;
+  }
+};
+
+static void raise_moe_error(int flag, int variant) {
+  const char* layer = variant == kQwen3Next ? "Qwen3Next" : "Nemotron-H MoE";
+  if (flag & 2) failf("%s layer router produced non-positive top-k weight sum.", layer);
+  if (flag & 1)
+    failf("%s layer router produced fewer than top-k selectable logits (Expert index -1 is out of range).",
+          layer);
+  failf("%s layer failed (error flags %d)", layer, flag);
+}
+
+extern "C" {
+
+int llambda_hip_moe_session_create(const llambda_hip_moe_desc* d,
+                                   llambda_hip_moe_session** result) {
+  return guarded([&] {
+    if (!result) failf("moe_session_create: null result pointer");
+    *result = nullptr;
+    if (!d) failf("moe_session_create: null description");
+    if (d->variant != LLAMBDA_HIP_MOE_QWEN3NEXT && d->variant != LLAMBDA_HIP_MOE_NEMOTRON_H)
+      failf("moe_session_create: unknown variant %d", d->variant);
+    const bool qwen = d->variant == LLAMBDA_HIP_MOE_QWEN3NEXT;
+    const int64_t H = d->hidden, E = d->expert_count, K = d->top_k, F = d->expert_ffn,
+                  Fs = d->shared_ffn;
+    if (H <= 0 || H % 32 || H > (1 << 16)) failf("moe_session_create: hidden %lld unsupported", (long long)H);
+    if (E <= 0 || E > kMoeMaxExperts)
+      failf("moe_session_create: expert count %lld outside 1..%d", (long long)E, kMoeMaxExperts);
+    if (K <= 0 || K > E || K > kMoeMaxTopK)
+      failf("moe_session_create: top_k %lld outside 1..min(E, %d)", (long long)K, kMoeMaxTopK);
+    if (F <= 0 || F % 32 || F > (1 << 16)) failf("moe_session_create: expert ffn %lld unsupported", (long long)F);
+    if (Fs < 0 || Fs % 32 || Fs > (1 << 16)) failf("moe_session_create: shared ffn %lld unsupported", (long long)Fs);
+    if (!d->router) failf("moe_session_create: missing router (ffn_gate_inp)");
+    if (!d->up_exps || !d->down_exps) failf("moe_session_create: missing expert tensors");
+    if (qwen && !d->gate_exps) failf("moe_session_create: missing ffn_gate_exps");
+    if (qwen && d->gate_type != d->up_type)
+      failf("moe_session_create: ffn_gate_exps and ffn_up_exps must share a type");
+    if (!qwen && !d->router_bias) failf("moe_session_create: missing exp_probs_b.bias");
+    if (Fs > 0) {
+      if (!d->shared_up || !d->shared_down) failf("moe_session_create: missing shared expert tensors");
+      if (qwen && (!d->shared_gate || !d->shared_gate_inp))
+        failf("moe_session_create: missing ffn_gate_shexp or ffn_gate_inp_shexp");
+      if (qwen && d->shared_gate_type != d->shared_up_type)
+        failf("moe_session_create: ffn_gate_shexp and ffn_up_shexp must share a type");
+    }
+    const int types[] = {d->up_type, d->down_type, Fs > 0 ? d->shared_up_type : kQ4_K,
+                         Fs > 0 ? d->shared_down_type : kQ4_K};
+    for (int t : types)
+      if (t == kF32 || !supported_type(t))
+        failf("moe_session_create: expert tensors must be Q4_K, Q6_K, Q5_0 or Q8_0 (got tag %d)", t);
+    const int64_t up_rb = checked_row_bytes(d->up_type, H, "ffn_up_exps");
+    const int64_t down_rb = checked_row_bytes(d->down_type, F, "ffn_down_exps");
+    // LDS limit of the grouped kernels: kMoeChunkTokens rows of activations
+    if ((size_t)kMoeChunkTokens * (std::max(H, std::max(F, Fs)) * 17 / 16) * 4 > 160 * 1024)
+      failf("moe_session_create: hidden/ffn too large for the LDS tiles");
+
+    auto* s = new llambda_hip_moe_session();
+    try {
+      s->device = current_device_checked();
+      HIPC(hipStreamCreateWithFlags(&s->stream, hipStreamNonBlocking));
+      MoePlan& p = s->plan;
+      p.variant = qwen ? kQwen3Next : kNemotronH;
+      p.hidden = (int)H;
+      p.experts = (int)E;
+      p.top_k = (int)K;
+      p.ffn = (int)F;
+      p.shared_ffn = (int)Fs;
+      p.weights_scale = qwen ? 1.0f : d->expert_weights_scale;
+      p.weights_norm = qwen ? 1 : (d->expert_weights_norm ? 1 : 0);
+      // router [E (+1 shared gate row)][H]
+      const size_t rbytes = (size_t)(E + 1) * H * sizeof(float);
+      s->router.alloc(rbytes, "router");
+      HIPC(hipMemcpyAsync(s->router.ptr, d->router, (size_t)E * H * sizeof(float),
+                          hipMemcpyHostToDevice, s->stream));
+      if (qwen && Fs > 0)
+        HIPC(hipMemcpyAsync(s->router.as<float>() + E * H, d->shared_gate_inp, (size_t)H * sizeof(float),
+                            hipMemcpyHostToDevice, s->stream));
+      p.router = s->router.as<float>();
+      if (!qwen) {
+        s->bias.alloc((size_t)E * sizeof(float), "router bias");
+        HIPC(hipMemcpyAsync(s->bias.ptr, d->router_bias, (size_t)E * sizeof(float),
+                            hipMemcpyHostToDevice, s->stream));
+        p.bias = s->bias.as<float>();
+      }
+      const int64_t up_blocks = E * F * (H / block_weights(d->up_type));
+      const int64_t down_blocks = E * H * (F / block_weights(d->down_type));
+      p.up_type = d->up_type;
+      p.down_type = d->down_type;
+      p.gate_type = qwen ? d->gate_type : d->up_type;
+      if (qwen) {
+        upload_weights(s->gate, d->gate_exps, (size_t)(E * F * up_rb), d->gate_type, up_blocks,
+                       s->stream, "ffn_gate_exps");
+        p.gate = s->gate.as<uint8_t>();
+      }
+      upload_weights(s->up, d->up_exps, (size_t)(E * F * up_rb), d->up_type, up_blocks, s->stream,
+                     "ffn_up_exps");
+      upload_weights(s->down, d->down_exps, (size_t)(E * H * down_rb), d->down_type, down_blocks,
+                     s->stream, "ffn_down_exps");
+      p.up = s->up.as<uint8_t>();
+      p.down = s->down.as<uint8_t>();
+      if (Fs > 0) {
+        const int64_t sh_up_rb = checked_row_bytes(d->shared_up_type, H, "ffn_up_shexp");
+        const int64_t sh_down_rb = checked_row_bytes(d->shared_down_type, Fs, "ffn_down_shexp");
+        p.sh_up_type = d->shared_up_type;
+        p.sh_down_type = d->shared_down_type;
+        p.sh_gate_type = qwen ? d->shared_gate_type : d->shared_up_type;
+        if (qwen) {
+          upload_weights(s->sh_gate, d->shared_gate, (size_t)(Fs * sh_up_rb), d->shared_gate_type,
+                         Fs * (H / block_weights(d->shared_gate_type)), s->stream, "ffn_gate_shexp");
+          p.sh_gate = s->sh_gate.as<uint8_t>();
+        }
+        upload_weights(s->sh_up, d->shared_up, (size_t)(Fs * sh_up_rb), d->shared_up_type,
+                       Fs * (H / block_weights(d->shared_up_type)), s->stream, "ffn_up_shexp");
+        upload_weights(s->sh_down, d->shared_down, (size_t)(H * sh_down_rb), d->shared_down_type,
+                       H * (Fs / block_weights(d->shared_down_type)), s->stream, "ffn_down_shexp");
+        p.sh_up = s->sh_up.as<uint8_t>();
+        p.sh_down = s->sh_down.as<uint8_t>();
+      }
+      s->counts.alloc((size_t)E * sizeof(int), "expert histogram");
+      s->chunk_counts.alloc(2 * sizeof(int), "chunk counts");
+      s->error.alloc(sizeof(int), "error flag");
+      p.counts = s->counts.as<int>();
+      p.chunk_counts = s->chunk_counts.as<int>();
+      p.error = s->error.as<int>();
+      p.capacity = 0;
+      s->ensure_capacity(1);
+      HIPC(moe_reset_launch(p, s->stream));
+      HIPC(hipStreamSynchronize(s->stream));
+    } catch (...) {
+      delete s;
+      throw;
+    }
+    *result = s;
+  });
+}
+
+void llambda_hip_moe_session_destroy(llambda_hip_moe_session* session) { delete session; }
+
+size_t llambda_hip_moe_session_hidden_size(const llambda_hip_moe_session* session) {
+  return session ? (size_t)session->plan.hidden : 0;
+}
+
+int llambda_hip_moe_session_run(llambda_hip_moe_session* s, const float* input, size_t n_in,
+                                float* output, size_t n_out, size_t batch, int64_t* top_indices,
+                                float* top_weights, float* router_logits) {
+  return guarded([&] {
+    if (!s) failf("moe_session_run: null session");
+    if (!input || !output) failf("moe_session_run: null input or output");
+    if (batch == 0 || batch > (1u << 20)) failf("moe_session_run: bad batch %zu", batch);
+    const size_t H = (size_t)s->plan.hidden;
+    if (n_in != batch * H || n_out != batch * H)
+      failf("moe_session_run: element counts %zu/%zu do not match %zu x %zu", n_in, n_out, batch, H);
+    std::lock_guard<std::mutex> lock(s->run_mutex);
+    HIPC(hipSetDevice(s->device));
+    const int T = (int)batch;
+    s->ensure_capacity(T);
+    s->ensure_staging(T);
+    HIPC(hipMemcpyAsync(s->x.ptr, input, n_in * sizeof(float), hipMemcpyHostToDevice, s->stream));
+    HIPC(moe_forward_launch(s->plan, s->x.as<float>(), s->y.as<float>(), T, s->stream));
+    HIPC(hipMemcpyAsync(output, s->y.ptr, n_out * sizeof(float), hipMemcpyDeviceToHost, s->stream));
+    const size_t K = (size_t)s->plan.top_k, E = (size_t)s->plan.experts;
+    std::vector<int> idx;
+    if (top_indices) {
+      idx.resize(batch * K);
+      HIPC(hipMemcpyAsync(idx.data(), s->plan.top_idx, idx.size() * sizeof(int),
+                          hipMemcpyDeviceToHost, s->stream));
+    }
+    if (top_weights)
+      HIPC(hipMemcpyAsync(top_weights, s->plan.top_w, batch * K * sizeof(float),
+                          hipMemcpyDeviceToHost, s->stream));
+    if (router_logits)
+      HIPC(hipMemcpy2DAsync(router_logits, E * sizeof(float), s->plan.logits, (E + 1) * sizeof(float),
+                            E * sizeof(float), batch, hipMemcpyDeviceToHost, s->stream));
+    const int flag = s->take_error(s->stream);
+    for (size_t i = 0; i < idx.size(); ++i) top_indices[i] = idx[i];
+    if (flag) raise_moe_error(flag, s->plan.variant);
+  });
+}
+
+int llambda_hip_moe_session_run_device(llambda_hip_moe_session* s, const float* input,
+                                       float* output, size_t batch, void* stream) {
+  return guarded([&] {
+    if (!s) failf("moe_session_run_device: null session");
+    if (!input || !output) failf("moe_session_run_device: null input or output");
+    if (batch == 0 || batch > (1u << 20)) failf("moe_session_run_device: bad batch %zu", batch);
+    std::lock_guard<std::mutex> lock(s->run_mutex);
+    HIPC(hipSetDevice(s->device));
+    const int T = (int)batch;
+    if (T > s->plan.capacity) {
+      // growing frees scratch that queued work may still use
+      HIPC(hipStreamSynchronize(stream ? static_cast<hipStream_t>(stream) : s->stream));
+      HIPC(hipStreamSynchronize(s->stream));
+      s->ensure_capacity(T);
+    }
+    HIPC(moe_forward_launch(s->plan, input, output, T,
+                            stream ? static_cast<hipStream_t>(stream) : s->stream));
+  });
+}
+
+int llambda_hip_moe_session_sync(llambda_hip_moe_session* s, void* stream) {
+  return guarded([&] {
+    if (!s) failf("moe_session_sync: null session");
+    std::lock_guard<std::mutex> lock(s->run_mutex);
+    HIPC(hipSetDevice(s->device));
+    const int flag = s->take_error(stream ? static_cast<hipStream_t>(stream) : s->stream);
+    if (flag) raise_moe_error(flag, s->plan.variant);
+  });
+}
+
+int llambda_hip_select_top_k(const float* logits, size_t n, size_t k, size_t batch,
+                             int64_t* top_indices, float* top_logits) {
+  return guarded([&] {
+    if (!logits || !top_indices || !top_logits) failf("select_top_k: null argument");
+    if (n == 0 || n > (size_t)kMoeMaxExperts) failf("select_top_k: n must be in 1..%d", kMoeMaxExperts);
+    if (k == 0 || k > (size_t)kMoeMaxTopK) failf("select_top_k: k must be in 1..%d", kMoeMaxTopK);
+    if (batch == 0 || batch > (1u << 20)) failf("select_top_k: bad batch %zu", batch);
+    current_device_checked();
+    hipStream_t stream;
+    HIPC(hipStreamCreateWithFlags(&stream, hipStreamNonBlocking));
+    struct StreamGuard {
+      hipStream_t s;
+      ~StreamGuard() { (void)hipStreamDestroy(s); }
+    } guard{stream};
+    DevBuf dl, di, dv;
+    dl.alloc(batch * n * sizeof(float), "logits");
+    di.alloc(batch * k * sizeof(int), "indices");
+    dv.alloc(batch * k * sizeof(float), "values");
+    HIPC(hipMemcpyAsync(dl.ptr, logits, batch * n * sizeof(float), hipMemcpyHostToDevice, stream));
+    HIPC(topk_launch(dl.as<float>(), (int)n, (int)k, (int)batch, di.as<int>(), dv.as<float>(), stream));
+    std::vector<int> idx(batch * k);
+    HIPC(hipMemcpyAsync(idx.data(), di.ptr, idx.size() * sizeof(int), hipMemcpyDeviceToHost, stream));
+    HIPC(hipMemcpyAsync(top_logits, dv.ptr, batch * k * sizeof(float), hipMemcpyDeviceToHost, stream));
+    HIPC(hipStreamSynchronize(stream));
+    for (size_t i = 0; i < idx.size(); ++i) top_indices[i] = idx[i];
+  });
+}
+
+}  // extern "C"

@@ -1,0 +1,89 @@
+// common.h -- shared device helpers for the gfx950 kernels of libllambda_hip.
+//
+// Block formats are GGML's, as llambda reads them (llambda.lisp:2126-2155,
+// 4338-4506):
+//   Q4_K  144 B / 256 weights: fp16 d, fp16 dmin, 12 B packed 6-bit
+//         scales/mins, 128 B nibbles.
+//   Q6_K  210 B / 256 weights: 128 B low nibbles (ql), 64 B 2-bit highs (qh),
+//         16 int8 scales, fp16 d.
+//   Q5_0  22 B / 32 weights:   fp16 d, u32 high bits, 16 B nibbles.
+//   Q8_0  34 B / 32 weights:   fp16 d, 32 int8.
+//   F32   4 B / weight.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace llhip {
+
+enum GgmlType : int {
+  kF32 = 0,
+  kQ5_0 = 6,
+  kQ8_0 = 8,
+  kQ4_K = 12,
+  kQ6_K = 14,
+};
+
+constexpr int kWave = 64;
+
+// Bytes and weights per block for each supported type.
+__host__ __device__ constexpr int block_bytes(int type) {
+  return type == kQ4_K ? 144 : type == kQ6_K ? 210 : type == kQ5_0 ? 22 : type == kQ8_0 ? 34 : 4;
+}
+__host__ __device__ constexpr int block_weights(int type) {
+  return (type == kQ4_K || type == kQ6_K) ? 256 : (type == kQ5_0 || type == kQ8_0) ? 32 : 1;
+}
+
+// Device allocations of packed weights carry this many readable bytes past
+// their end: the dword-granular loads of 2-byte-aligned blocks may touch up to
+// 3 bytes beyond the last block.
+constexpr size_t kWeightPad = 64;
+
+// A dword-aligned 16-byte vector: lets the compiler emit global_load_dwordx4
+// at 4-byte alignment (the hardware requires dword alignment only).
+typedef uint32_t u32x4a4 __attribute__((ext_vector_type(4), aligned(4)));
+
+__device__ __forceinline__ float half_bits_to_float(uint32_t bits16) {
+  return (float)__builtin_bit_cast(_Float16, (uint16_t)bits16);
+}
+
+// Five consecutive dwords starting at the dword containing byte address p,
+// returned as the 16 bytes at p (p must be 2-byte aligned; the fifth dword is
+// read even when p is dword aligned, hence kWeightPad).
+__device__ __forceinline__ uint4 load16_unaligned2(const uint8_t* p) {
+  // pointer arithmetic (not an integer round trip) keeps the global address
+  // space visible to the compiler, so these become global_load, not flat_load
+  const uint32_t shift = (uint32_t)(reinterpret_cast<uintptr_t>(p) & 3u);
+  const uint32_t* base = reinterpret_cast<const uint32_t*>(p - shift);
+  u32x4a4 v = *reinterpret_cast<const u32x4a4*>(base);
+  uint32_t e = base[4];
+  uint4 r;
+  r.x = __builtin_amdgcn_alignbyte(v.y, v.x, shift);
+  r.y = __builtin_amdgcn_alignbyte(v.z, v.y, shift);
+  r.z = __builtin_amdgcn_alignbyte(v.w, v.z, shift);
+  r.w = __builtin_amdgcn_alignbyte(e, v.w, shift);
+  return r;
+}
+
+__device__ __forceinline__ uint4 load16_aligned(const uint8_t* p) {
+  return *reinterpret_cast<const uint4*>(p);
+}
+
+__device__ __forceinline__ float ubyte(uint32_t v, int k) {
+  return (float)((v >> (8 * k)) & 0xFFu);
+}
+
+// Sum across `width` consecutive lanes (width a power of two <= 64).
+template <int WIDTH>
+__device__ __forceinline__ float segment_sum(float v) {
+#pragma unroll
+  for (int off = WIDTH / 2; off > 0; off >>= 1) v += __shfl_xor(v, off, kWave);
+  return v;
+}
+
+__device__ __forceinline__ float segment_sum_dyn(float v, int width) {
+  for (int off = width / 2; off > 0; off >>= 1) v += __shfl_xor(v, off, kWave);
+  return v;
+}
+
+}  // namespace llhip

@@ -1,0 +1,220 @@
+"""Routed-MoE layer sessions on the HIP backend.
+
+A ``MoeLayer`` holds the tensors one layer of qwen3next-moe-into
+(llambda.lisp:5321-5426) or nemotron-h-moe-ffn-into (llambda.lisp:5827-5949)
+reads; ``HipMoeSession`` uploads them once and runs the whole feed-forward
+(router, top-k, gating, experts, combine) on the device for a batch of
+tokens.  In the reference the routed experts bypass the accelerator store
+(llambda.lisp:4951-4971); this session is the per-layer hook registered under
+the layer's router tensor name, blk.N.ffn_gate_inp.weight.
+"""
+from __future__ import annotations
+
+import ctypes
+from dataclasses import dataclass
+from typing import Optional, Tuple
+
+import numpy as np
+
+from . import ggml, native, synthetic
+from .hip_backend import HipBackendError, _check
+
+QWEN3NEXT = 0
+NEMOTRON_H = 1
+
+Packed = Tuple[int, np.ndarray]  # (GGML type tag, bytes)
+
+
+@dataclass
+class MoeLayer:
+    variant: int
+    hidden: int
+    expert_count: int
+    top_k: int
+    expert_ffn: int
+    shared_ffn: int
+    router: np.ndarray                        # F32 [E][H]   ffn_gate_inp
+    up: Packed                                # [E*F][H]      ffn_up_exps
+    down: Packed                              # [E*H][F]      ffn_down_exps
+    gate: Optional[Packed] = None             # [E*F][H]      ffn_gate_exps (qwen3next)
+    shared_gate_inp: Optional[np.ndarray] = None  # F32 [H]  ffn_gate_inp_shexp (qwen3next)
+    router_bias: Optional[np.ndarray] = None  # F32 [E]       exp_probs_b.bias (nemotron)
+    expert_weights_scale: float = 1.0
+    expert_weights_norm: bool = False
+    shared_gate: Optional[Packed] = None      # [Fs][H]       ffn_gate_shexp (qwen3next)
+    shared_up: Optional[Packed] = None        # [Fs][H]       ffn_up_shexp
+    shared_down: Optional[Packed] = None      # [H][Fs]       ffn_down_shexp
+
+    def weight_bytes(self) -> int:
+        """Packed bytes of every tensor the layer can read."""
+        n = self.router.nbytes
+        for t in (self.gate, self.up, self.down, self.shared_gate, self.shared_up, self.shared_down):
+            if t is not None:
+                n += t[1].nbytes
+        for v in (self.shared_gate_inp, self.router_bias):
+            if v is not None:
+                n += v.nbytes
+        return n
+
+    def expert_bytes(self) -> int:
+        """Packed bytes of one routed expert (gate + up + down)."""
+        per = ggml.row_bytes(self.up[0], self.hidden) * self.expert_ffn
+        if self.gate is not None:
+            per += ggml.row_bytes(self.gate[0], self.hidden) * self.expert_ffn
+        per += ggml.row_bytes(self.down[0], self.expert_ffn) * self.hidden
+        return per
+
+    def shared_bytes(self) -> int:
+        if not self.shared_ffn:
+            return 0
+        n = ggml.row_bytes(self.shared_up[0], self.hidden) * self.shared_ffn
+        if self.shared_gate is not None:
+            n += ggml.row_bytes(self.shared_gate[0], self.hidden) * self.shared_ffn
+        n += ggml.row_bytes(self.shared_down[0], self.shared_ffn) * self.hidden
+        if self.shared_gate_inp is not None:
+            n += self.shared_gate_inp.nbytes
+        return n
+
+
+class HipMoeSession:
+    def __init__(self, layer: MoeLayer):
+        self.layer = layer
+        keep = []
+
+        def arr(a, dtype):
+            if a is None:
+                return None
+            a = np.ascontiguousarray(a, dtype=dtype)
+            keep.append(a)
+            return a.ctypes.data
+
+        d = native.MoeDesc()
+        d.variant = layer.variant
+        d.hidden = layer.hidden
+        d.expert_count = layer.expert_count
+        d.top_k = layer.top_k
+        d.expert_ffn = layer.expert_ffn
+        d.shared_ffn = layer.shared_ffn
+        d.router = arr(layer.router, np.float32)
+        d.shared_gate_inp = arr(layer.shared_gate_inp, np.float32)
+        d.router_bias = arr(layer.router_bias, np.float32)
+        d.expert_weights_scale = layer.expert_weights_scale
+        d.expert_weights_norm = int(bool(layer.expert_weights_norm))
+        for name, field in (("gate", "gate_exps"), ("up", "up_exps"), ("down", "down_exps"),
+                            ("shared_gate", "shared_gate"), ("shared_up", "shared_up"),
+                            ("shared_down", "shared_down")):
+            pair = getattr(layer, name)
+            if pair is not None:
+                setattr(d, name + "_type", pair[0])
+                setattr(d, field, arr(pair[1], np.uint8))
+        handle = ctypes.c_void_p()
+        _check(native.lib().llambda_hip_moe_session_create(ctypes.byref(d), ctypes.byref(handle)),
+               "HIP MoE session creation")
+        self.pointer = handle.value
+
+    def close(self) -> None:
+        if self.pointer:
+            native.lib().llambda_hip_moe_session_destroy(self.pointer)
+            self.pointer = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:  # noqa: BLE001 - interpreter shutdown
+            pass
+
+    def _live(self):
+        if not self.pointer:
+            raise HipBackendError("HIP MoE session is closed.")
+        return self.pointer
+
+    def run(self, x: np.ndarray, with_routing: bool = False):
+        """FFN output (before the residual) for x [tokens][H]; with_routing also
+        returns (top_indices, top_weights, router_logits)."""
+        L = self.layer
+        x = np.ascontiguousarray(x, dtype=np.float32).reshape(-1, L.hidden)
+        tokens = x.shape[0]
+        y = np.empty_like(x)
+        idx = w = logits = None
+        if with_routing:
+            idx = np.empty((tokens, L.top_k), dtype=np.int64)
+            w = np.empty((tokens, L.top_k), dtype=np.float32)
+            logits = np.empty((tokens, L.expert_count), dtype=np.float32)
+        _check(native.lib().llambda_hip_moe_session_run(
+            self._live(), x.ctypes.data, x.size, y.ctypes.data, y.size, tokens,
+            idx.ctypes.data if idx is not None else None,
+            w.ctypes.data if w is not None else None,
+            logits.ctypes.data if logits is not None else None), "HIP MoE run")
+        return (y, idx, w, logits) if with_routing else y
+
+    def run_device(self, x_ptr: int, y_ptr: int, tokens: int, stream: int = 0) -> None:
+        _check(native.lib().llambda_hip_moe_session_run_device(self._live(), x_ptr, y_ptr, tokens,
+                                                               stream or None),
+               "HIP MoE device run")
+
+    def sync(self, stream: int = 0) -> None:
+        _check(native.lib().llambda_hip_moe_session_sync(self._live(), stream or None),
+               "HIP MoE sync")
+
+
+def select_top_k(logits: np.ndarray, k: int):
+    """Device top-k of each row of logits [batch][n] (select-top-k-logits-into)."""
+    logits = np.ascontiguousarray(logits, dtype=np.float32)
+    if logits.ndim == 1:
+        logits = logits[None, :]
+    batch, n = logits.shape
+    idx = np.empty((batch, k), dtype=np.int64)
+    val = np.empty((batch, k), dtype=np.float32)
+    _check(native.lib().llambda_hip_select_top_k(logits.ctypes.data, n, k, batch, idx.ctypes.data,
+                                                 val.ctypes.data), "HIP top-k")
+    return idx, val
+
+
+# ------------------------------------------------------------ synthetic layers
+
+def synthetic_qwen3next(rng: np.random.Generator, *, hidden=2048, experts=512, top_k=10, ffn=512,
+                        shared_ffn=512, gate_type=ggml.Q4_K, down_type=ggml.Q6_K,
+                        router_std=0.02) -> MoeLayer:
+    """A Qwen3Next-shaped layer: gate/up Q4_K, down Q6_K, router F32 ~ N(0, 0.02)."""
+    gen = synthetic.packed
+    return MoeLayer(
+        variant=QWEN3NEXT, hidden=hidden, expert_count=experts, top_k=top_k, expert_ffn=ffn,
+        shared_ffn=shared_ffn,
+        router=rng.normal(0.0, router_std, size=(experts, hidden)).astype(np.float32),
+        gate=(gate_type, gen(gate_type, rng, experts * ffn, hidden)),
+        up=(gate_type, gen(gate_type, rng, experts * ffn, hidden)),
+        down=(down_type, gen(down_type, rng, experts * hidden, ffn)),
+        shared_gate_inp=(rng.normal(0.0, router_std, size=hidden).astype(np.float32)
+                         if shared_ffn else None),
+        shared_gate=(gate_type, gen(gate_type, rng, shared_ffn, hidden)) if shared_ffn else None,
+        shared_up=(gate_type, gen(gate_type, rng, shared_ffn, hidden)) if shared_ffn else None,
+        shared_down=(down_type, gen(down_type, rng, hidden, shared_ffn)) if shared_ffn else None,
+    )
+
+
+def zipf_bias(rng: np.random.Generator, experts: int, s: float = 1.1, c: float = 0.5) -> np.ndarray:
+    """Per-expert router bias b_e = c * log(p_e) for Zipf(s) probabilities over a
+    random permutation of expert ranks."""
+    ranks = rng.permutation(experts) + 1
+    p = ranks.astype(np.float64) ** (-s)
+    p /= p.sum()
+    return (c * np.log(p)).astype(np.float32)
+
+
+def synthetic_nemotron_h(rng: np.random.Generator, *, hidden=2688, experts=128, top_k=6, ffn=1856,
+                         shared_ffn=3712, expert_type=ggml.Q5_0, down_type=ggml.Q5_0,
+                         router_std=0.02, zipf_s=1.1, zipf_c=0.5, weights_scale=1.0,
+                         weights_norm=True) -> MoeLayer:
+    """A Nemotron-H-MoE-shaped layer: relu^2 experts, biased sigmoid routing."""
+    gen = synthetic.packed
+    return MoeLayer(
+        variant=NEMOTRON_H, hidden=hidden, expert_count=experts, top_k=top_k, expert_ffn=ffn,
+        shared_ffn=shared_ffn,
+        router=rng.normal(0.0, router_std, size=(experts, hidden)).astype(np.float32),
+        router_bias=zipf_bias(rng, experts, zipf_s, zipf_c),
+        expert_weights_scale=weights_scale, expert_weights_norm=weights_norm,
+        up=(expert_type, gen(expert_type, rng, experts * ffn, hidden)),
+        down=(down_type, gen(down_type, rng, experts * hidden, ffn)),
+        shared_up=(expert_type, gen(expert_type, rng, shared_ffn, hidden)) if shared_ffn else None,
+        shared_down=(down_type, gen(down_type, rng, hidden, shared_ffn)) if shared_ffn else None,
+    )

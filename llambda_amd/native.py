@@ -1,0 +1,109 @@
+"""ctypes bindings of libllambda_hip.so -- the foreign-function layer.
+
+This is the Python counterpart of the reference's CFFI declarations for its
+native bridge (llambda.lisp:82-127): one binding per exported function of
+include/llambda_hip.h.  Loading fails loudly when the library is missing;
+there is no fallback implementation.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import threading
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.environ.get("LLAMBDA_HIP_LIBRARY", os.path.join(HERE, "libllambda_hip.so"))
+
+_lock = threading.Lock()
+_lib = None
+
+c_int = ctypes.c_int
+c_size = ctypes.c_size_t
+c_i64 = ctypes.c_int64
+c_void_p = ctypes.c_void_p
+c_char_p = ctypes.c_char_p
+c_float_p = ctypes.POINTER(ctypes.c_float)
+
+
+class MoeDesc(ctypes.Structure):
+    """llambda_hip_moe_desc."""
+    _fields_ = [
+        ("variant", c_int),
+        ("hidden", c_i64),
+        ("expert_count", c_i64),
+        ("top_k", c_i64),
+        ("expert_ffn", c_i64),
+        ("shared_ffn", c_i64),
+        ("router", c_void_p),
+        ("shared_gate_inp", c_void_p),
+        ("router_bias", c_void_p),
+        ("expert_weights_scale", ctypes.c_float),
+        ("expert_weights_norm", c_int),
+        ("gate_type", c_int), ("gate_exps", c_void_p),
+        ("up_type", c_int), ("up_exps", c_void_p),
+        ("down_type", c_int), ("down_exps", c_void_p),
+        ("shared_gate_type", c_int), ("shared_gate", c_void_p),
+        ("shared_up_type", c_int), ("shared_up", c_void_p),
+        ("shared_down_type", c_int), ("shared_down", c_void_p),
+    ]
+
+
+# name -> (restype, argtypes); the complete export list of include/llambda_hip.h
+SIGNATURES = {
+    "llambda_hip_probe": (c_int, []),
+    "llambda_hip_bridge_version": (c_char_p, []),
+    "llambda_hip_runtime_version": (c_char_p, []),
+    "llambda_hip_last_error": (c_char_p, []),
+    "llambda_hip_sha256": (c_int, [c_void_p, c_size, c_char_p, c_size]),
+    "llambda_hip_session_create": (c_int, [c_char_p, c_char_p, c_char_p, ctypes.POINTER(c_void_p)]),
+    "llambda_hip_session_create_packed": (c_int, [c_void_p, c_size, c_int, c_i64, c_i64,
+                                                  ctypes.POINTER(c_void_p)]),
+    "llambda_hip_session_destroy": (None, [c_void_p]),
+    "llambda_hip_session_input_element_count": (c_size, [c_void_p]),
+    "llambda_hip_session_output_element_count": (c_size, [c_void_p]),
+    "llambda_hip_session_run": (c_int, [c_void_p, c_void_p, c_size, c_void_p, c_size]),
+    "llambda_hip_session_run_batch": (c_int, [c_void_p, c_void_p, c_size, c_void_p, c_size, c_size]),
+    "llambda_hip_session_run_device": (c_int, [c_void_p, c_void_p, c_void_p, c_size, c_void_p]),
+    "llambda_hip_session_dequantize": (c_int, [c_void_p, c_void_p, c_size]),
+    "llambda_hip_moe_session_create": (c_int, [ctypes.POINTER(MoeDesc), ctypes.POINTER(c_void_p)]),
+    "llambda_hip_moe_session_destroy": (None, [c_void_p]),
+    "llambda_hip_moe_session_hidden_size": (c_size, [c_void_p]),
+    "llambda_hip_moe_session_run": (c_int, [c_void_p, c_void_p, c_size, c_void_p, c_size, c_size,
+                                            c_void_p, c_void_p, c_void_p]),
+    "llambda_hip_moe_session_run_device": (c_int, [c_void_p, c_void_p, c_void_p, c_size, c_void_p]),
+    "llambda_hip_moe_session_sync": (c_int, [c_void_p, c_void_p]),
+    "llambda_hip_select_top_k": (c_int, [c_void_p, c_size, c_size, c_size, c_void_p, c_void_p]),
+}
+
+
+class NativeLibraryMissing(RuntimeError):
+    pass
+
+
+def library_path() -> str:
+    return LIB_PATH
+
+
+def lib():
+    """The loaded library (loaded once).  Raises NativeLibraryMissing when the
+    shared object has not been built."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    with _lock:
+        if _lib is None:
+            if not os.path.exists(LIB_PATH):
+                raise NativeLibraryMissing(
+                    f"{LIB_PATH} is missing; build it with `python -m llambda_amd.build`")
+            L = ctypes.CDLL(LIB_PATH)
+            for name, (restype, argtypes) in SIGNATURES.items():
+                fn = getattr(L, name)
+                fn.restype = restype
+                fn.argtypes = argtypes
+            _lib = L
+    return _lib
+
+
+def last_error() -> str:
+    msg = lib().llambda_hip_last_error()
+    return msg.decode(errors="replace") if msg else ""

@@ -1,0 +1,238 @@
+"""ctypes front end of the CPU oracle (oracle/llambda_oracle.c).
+
+TEST INFRASTRUCTURE ONLY.  Only tests/, ``__graft_entry__.smoke()`` and
+``bench.py``'s cpu_baseline leg may import this module, and only as the
+parity checker or the reported CPU baseline.  The product path
+(``llambda_amd``) never imports it.
+
+The C restatement follows the reference's CPU kernels (llambda.lisp); see the
+header of ``llambda_oracle.h`` for which check pins each function.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import subprocess
+from dataclasses import dataclass
+from typing import Optional
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "build", "liboracle.so")
+
+TYPE_F32 = 0
+TYPE_Q5_0 = 6
+TYPE_Q8_0 = 8
+TYPE_Q4_K = 12
+TYPE_Q6_K = 14
+
+_lib = None
+
+
+def build() -> str:
+    """Compile the oracle with its Makefile; returns the library path."""
+    subprocess.run(["make", "-s", "-C", HERE], check=True)
+    return LIB_PATH
+
+
+class OracleError(RuntimeError):
+    pass
+
+
+class MoeDesc(ctypes.Structure):
+    _fields_ = [
+        ("variant", ctypes.c_int),
+        ("hidden", ctypes.c_int64),
+        ("expert_count", ctypes.c_int64),
+        ("top_k", ctypes.c_int64),
+        ("expert_ffn", ctypes.c_int64),
+        ("shared_ffn", ctypes.c_int64),
+        ("router", ctypes.c_void_p),
+        ("shared_gate_inp", ctypes.c_void_p),
+        ("router_bias", ctypes.c_void_p),
+        ("expert_weights_scale", ctypes.c_float),
+        ("expert_weights_norm", ctypes.c_int),
+        ("gate_type", ctypes.c_int), ("gate_exps", ctypes.c_void_p),
+        ("up_type", ctypes.c_int), ("up_exps", ctypes.c_void_p),
+        ("down_type", ctypes.c_int), ("down_exps", ctypes.c_void_p),
+        ("shared_gate_type", ctypes.c_int), ("shared_gate", ctypes.c_void_p),
+        ("shared_up_type", ctypes.c_int), ("shared_up", ctypes.c_void_p),
+        ("shared_down_type", ctypes.c_int), ("shared_down", ctypes.c_void_p),
+    ]
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            build()
+        L = ctypes.CDLL(LIB_PATH)
+        L.oracle_last_error.restype = ctypes.c_char_p
+        L.oracle_row_bytes.restype = ctypes.c_int64
+        L.oracle_row_bytes.argtypes = [ctypes.c_int, ctypes.c_int64]
+        L.oracle_fp16_to_f32.argtypes = [ctypes.c_uint16, ctypes.POINTER(ctypes.c_float)]
+        L.oracle_get_scale_min_k4.argtypes = [ctypes.c_void_p, ctypes.c_int,
+                                              ctypes.POINTER(ctypes.c_int),
+                                              ctypes.POINTER(ctypes.c_int)]
+        L.oracle_dequantize.argtypes = [ctypes.c_int, ctypes.c_void_p, ctypes.c_int64,
+                                        ctypes.c_void_p]
+        L.oracle_dot_row.argtypes = [ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p,
+                                     ctypes.c_int64, ctypes.POINTER(ctypes.c_float)]
+        L.oracle_dot_product.restype = ctypes.c_float
+        L.oracle_dot_product.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int64]
+        L.oracle_gemv.argtypes = [ctypes.c_int, ctypes.c_void_p, ctypes.c_int64, ctypes.c_int64,
+                                  ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int]
+        L.oracle_select_top_k.argtypes = [ctypes.c_void_p, ctypes.c_int64, ctypes.c_int64,
+                                          ctypes.c_void_p, ctypes.c_void_p]
+        for name in ("oracle_sigmoid", "oracle_silu", "oracle_relu_squared"):
+            f = getattr(L, name)
+            f.restype = ctypes.c_float
+            f.argtypes = [ctypes.c_float]
+        L.oracle_moe_forward.argtypes = [ctypes.POINTER(MoeDesc), ctypes.c_void_p,
+                                         ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p,
+                                         ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int]
+        _lib = L
+    return _lib
+
+
+def _check(status: int) -> None:
+    if status != 0:
+        raise OracleError(lib().oracle_last_error().decode())
+
+
+def _ptr(a: Optional[np.ndarray]):
+    return None if a is None else a.ctypes.data
+
+
+def row_bytes(type_tag: int, columns: int) -> int:
+    n = lib().oracle_row_bytes(type_tag, columns)
+    if n < 0:
+        raise OracleError(lib().oracle_last_error().decode())
+    return n
+
+
+def fp16_to_f32(bits: int) -> float:
+    out = ctypes.c_float()
+    _check(lib().oracle_fp16_to_f32(bits, ctypes.byref(out)))
+    return out.value
+
+
+def get_scale_min_k4(scales: bytes, index: int):
+    buf = np.frombuffer(bytes(scales), dtype=np.uint8).copy()
+    sc, m = ctypes.c_int(), ctypes.c_int()
+    lib().oracle_get_scale_min_k4(buf.ctypes.data, index, ctypes.byref(sc), ctypes.byref(m))
+    return sc.value, m.value
+
+
+def dequantize(type_tag: int, data: np.ndarray, elements: int) -> np.ndarray:
+    data = np.ascontiguousarray(data, dtype=np.uint8)
+    out = np.empty(elements, dtype=np.float32)
+    _check(lib().oracle_dequantize(type_tag, data.ctypes.data, elements, out.ctypes.data))
+    return out
+
+
+def dot_row(type_tag: int, row: np.ndarray, x: np.ndarray) -> float:
+    row = np.ascontiguousarray(row, dtype=np.uint8)
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    out = ctypes.c_float()
+    _check(lib().oracle_dot_row(type_tag, row.ctypes.data, x.ctypes.data, x.size,
+                                ctypes.byref(out)))
+    return out.value
+
+
+def dot_product(left: np.ndarray, right: np.ndarray) -> np.float32:
+    left = np.ascontiguousarray(left, dtype=np.float32)
+    right = np.ascontiguousarray(right, dtype=np.float32)
+    return np.float32(lib().oracle_dot_product(left.ctypes.data, right.ctypes.data, left.size))
+
+
+def gemv(type_tag: int, matrix: np.ndarray, rows: int, columns: int, x: np.ndarray,
+         threads: int = 1) -> np.ndarray:
+    matrix = np.ascontiguousarray(matrix).view(np.uint8)
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    assert x.size == columns
+    assert matrix.size >= rows * row_bytes(type_tag, columns)
+    y = np.empty(rows, dtype=np.float32)
+    _check(lib().oracle_gemv(type_tag, matrix.ctypes.data, rows, columns, x.ctypes.data,
+                             y.ctypes.data, threads))
+    return y
+
+
+def select_top_k(logits: np.ndarray, k: int):
+    logits = np.ascontiguousarray(logits, dtype=np.float32)
+    idx = np.empty(k, dtype=np.int64)
+    val = np.empty(k, dtype=np.float32)
+    lib().oracle_select_top_k(logits.ctypes.data, logits.size, k, idx.ctypes.data,
+                              val.ctypes.data)
+    return idx, val
+
+
+def sigmoid(x: float) -> float:
+    return lib().oracle_sigmoid(x)
+
+
+def silu(x: float) -> float:
+    return lib().oracle_silu(x)
+
+
+def relu_squared(x: float) -> float:
+    return lib().oracle_relu_squared(x)
+
+
+@dataclass
+class MoeResult:
+    y: np.ndarray
+    top_indices: np.ndarray
+    top_weights: np.ndarray
+    router_logits: np.ndarray
+
+
+def moe_forward(layer, x: np.ndarray, threads: int = 1) -> MoeResult:
+    """Run one MoE layer token by token.
+
+    ``layer`` is any object with the attributes of ``llambda_amd.moe.MoeLayer``
+    (variant, hidden, expert_count, top_k, expert_ffn, shared_ffn, router,
+    shared_gate_inp, router_bias, expert_weights_scale, expert_weights_norm and
+    the (type, bytes) pairs gate/up/down/shared_gate/shared_up/shared_down).
+    """
+    x = np.ascontiguousarray(x, dtype=np.float32).reshape(-1, layer.hidden)
+    tokens = x.shape[0]
+    keep = []
+
+    def arr(a, dtype):
+        if a is None:
+            return None
+        a = np.ascontiguousarray(a, dtype=dtype)
+        keep.append(a)
+        return a.ctypes.data
+
+    d = MoeDesc()
+    d.variant = layer.variant
+    d.hidden = layer.hidden
+    d.expert_count = layer.expert_count
+    d.top_k = layer.top_k
+    d.expert_ffn = layer.expert_ffn
+    d.shared_ffn = layer.shared_ffn
+    d.router = arr(layer.router, np.float32)
+    d.shared_gate_inp = arr(layer.shared_gate_inp, np.float32)
+    d.router_bias = arr(layer.router_bias, np.float32)
+    d.expert_weights_scale = layer.expert_weights_scale
+    d.expert_weights_norm = int(layer.expert_weights_norm)
+    for name in ("gate", "up", "down", "shared_gate", "shared_up", "shared_down"):
+        pair = getattr(layer, name)
+        field = name if name.startswith("shared") else name + "_exps"
+        if pair is None:
+            setattr(d, name + "_type", 0)
+            setattr(d, field, None)
+        else:
+            setattr(d, name + "_type", pair[0])
+            setattr(d, field, arr(pair[1], np.uint8))
+    y = np.empty_like(x)
+    idx = np.empty((tokens, layer.top_k), dtype=np.int64)
+    w = np.empty((tokens, layer.top_k), dtype=np.float32)
+    logits = np.empty((tokens, layer.expert_count), dtype=np.float32)
+    _check(lib().oracle_moe_forward(ctypes.byref(d), x.ctypes.data, y.ctypes.data, tokens,
+                                    idx.ctypes.data, w.ctypes.data, logits.ctypes.data,
+                                    threads))
+    return MoeResult(y, idx, w, logits)

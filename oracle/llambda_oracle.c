@@ -1,0 +1,702 @@
+/*
+ * llambda_oracle.c -- CPU restatement of llambda's quantized decode hot path.
+ *
+ * TEST INFRASTRUCTURE ONLY: the parity checker and the CPU baseline.  The
+ * product (libllambda_hip.so) never links or calls this file.
+ *
+ * Build: oracle/Makefile, with -ffp-contract=off so that only the explicit
+ * fmaf() calls (the reference's f32.8-fmadd) fuse.
+ */
+#include "llambda_oracle.h"
+
+#include <float.h>
+#include <math.h>
+#include <pthread.h>
+#include <stdarg.h>
+#include <stdio.h>
+#include <stdlib.h>
+#include <string.h>
+
+#define QK_K 256           /* llambda.lisp:21 +qk-k+ */
+#define K_SCALE_SIZE 12    /* llambda.lisp:22 +k-scale-size+ */
+#define Q4_K_BYTES 144     /* 4 + 12 + 128, llambda.lisp:2142 */
+#define Q6_K_BYTES 210     /* 2 + 16 + 192, llambda.lisp:2144 */
+#define Q5_0_BYTES 22      /* llambda.lisp:2139 */
+#define Q8_0_BYTES 34      /* llambda.lisp:2140 */
+#define PARALLEL_MIN_ROWS 96 /* llambda.lisp:37 *gemv-min-parallel-rows* */
+
+static __thread char g_error[512];
+
+const char* oracle_last_error(void) { return g_error; }
+
+static int fail(const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_error, sizeof g_error, fmt, ap);
+  va_end(ap);
+  return -1;
+}
+
+/* ------------------------------------------------------------------ */
+/* Type table, llambda.lisp:2126-2155                                  */
+
+int64_t oracle_type_block_elements(int type) {
+  switch (type) {
+    case ORACLE_TYPE_F32: return 1;
+    case ORACLE_TYPE_Q5_0:
+    case ORACLE_TYPE_Q8_0: return 32;
+    case ORACLE_TYPE_Q4_K:
+    case ORACLE_TYPE_Q6_K: return QK_K;
+    default: return -1;
+  }
+}
+
+int64_t oracle_type_block_bytes(int type) {
+  switch (type) {
+    case ORACLE_TYPE_F32: return 4;
+    case ORACLE_TYPE_Q5_0: return Q5_0_BYTES;
+    case ORACLE_TYPE_Q8_0: return Q8_0_BYTES;
+    case ORACLE_TYPE_Q4_K: return Q4_K_BYTES;
+    case ORACLE_TYPE_Q6_K: return Q6_K_BYTES;
+    default: return -1;
+  }
+}
+
+/* ggml-tensor-byte-size: errors when the count is not a block multiple. */
+int64_t oracle_row_bytes(int type, int64_t columns) {
+  int64_t be = oracle_type_block_elements(type);
+  if (be <= 0) { fail("Unsupported GGML tensor type tag %d.", type); return -1; }
+  if (columns % be != 0) {
+    fail("Tensor element count %lld is not a multiple of block size %lld for type %d.",
+         (long long)columns, (long long)be, type);
+    return -1;
+  }
+  return columns / be * oracle_type_block_bytes(type);
+}
+
+/* ------------------------------------------------------------------ */
+/* Byte readers, llambda.lisp:676-760                                  */
+
+static inline uint16_t rd_u16(const uint8_t* p) { return (uint16_t)(p[0] | (p[1] << 8)); }
+static inline uint32_t rd_u32(const uint8_t* p) {
+  return (uint32_t)p[0] | ((uint32_t)p[1] << 8) | ((uint32_t)p[2] << 16) | ((uint32_t)p[3] << 24);
+}
+static inline int rd_s8(const uint8_t* p) { return (int)(int8_t)p[0]; }
+
+/* fp16-to-single-float, llambda.lisp:716-733.  The value is built in double
+ * (exact for every half) and rounded once to single; exponent 31 (Inf/NaN)
+ * is an error, as in the reference. */
+int oracle_fp16_to_f32(uint16_t bits, float* out) {
+  float sign = (bits & 0x8000) ? -1.0f : 1.0f;
+  int exponent = (bits >> 10) & 31;
+  int fraction = bits & 1023;
+  if (exponent == 0) {
+    if (fraction == 0) {
+      *out = sign * 0.0f;
+    } else {
+      *out = (float)((double)sign * ldexp(fraction / 1024.0, -14));
+    }
+    return 0;
+  }
+  if (exponent == 31) return fail("Unsupported fp16 special value: %x.", bits);
+  *out = (float)((double)sign * ldexp(1.0 + fraction / 1024.0, exponent - 15));
+  return 0;
+}
+
+static inline int read_fp16(const uint8_t* p, float* out) { return oracle_fp16_to_f32(rd_u16(p), out); }
+
+/* get-scale-min-k4, llambda.lisp:6794-6813; twin get-scale-min-k4-at,
+ * llambda.lisp:4316-4336. */
+void oracle_get_scale_min_k4(const uint8_t* s, int index, int* scale, int* min) {
+  int byte0 = s[index];
+  int byte4 = s[index + 4];
+  if (index < 4) {
+    *scale = byte0 & 63;
+    *min = byte4 & 63;
+  } else {
+    *scale = (byte4 & 0x0F) | (((s[index - 4] & 0xC0) >> 6) << 4);
+    *min = (byte4 >> 4) | (((s[index] & 0xC0) >> 6) << 4);
+  }
+}
+
+/* ------------------------------------------------------------------ */
+/* Scalar dequantisers                                                 */
+
+/* dequantize-q4-k-m, llambda.lisp:6815-6859 */
+static int dequant_q4_k(const uint8_t* src, int64_t n, float* dst) {
+  if (n % QK_K) return fail("Q4_K_M dequantization requires ELEMENT-COUNT to be a multiple of 256.");
+  for (int64_t b = 0; b < n / QK_K; ++b) {
+    const uint8_t* blk = src + b * Q4_K_BYTES;
+    float d, dmin;
+    if (read_fp16(blk, &d) || read_fp16(blk + 2, &dmin)) return -1;
+    const uint8_t* scales = blk + 4;
+    const uint8_t* qs = blk + 4 + K_SCALE_SIZE;
+    float* out = dst + b * QK_K;
+    int scale_index = 0;
+    for (int chunk = 0; chunk < QK_K / 64; ++chunk) {
+      int sc0, m0, sc1, m1;
+      oracle_get_scale_min_k4(scales, scale_index, &sc0, &m0);
+      oracle_get_scale_min_k4(scales, scale_index + 1, &sc1, &m1);
+      float delta0 = d * (float)sc0, offset0 = dmin * (float)m0;
+      float delta1 = d * (float)sc1, offset1 = dmin * (float)m1;
+      for (int lane = 0; lane < 32; ++lane) {
+        int packed = qs[chunk * 32 + lane];
+        out[chunk * 64 + lane] = delta0 * (float)(packed & 0x0F) - offset0;
+        out[chunk * 64 + 32 + lane] = delta1 * (float)(packed >> 4) - offset1;
+      }
+      scale_index += 2;
+    }
+  }
+  return 0;
+}
+
+/* dequantize-q6-k, llambda.lisp:6919-6978: (* d scale q) = fl(fl(d*scale)*q) */
+static int dequant_q6_k(const uint8_t* src, int64_t n, float* dst) {
+  if (n % QK_K) return fail("Q6_K dequantization requires ELEMENT-COUNT to be a multiple of 256.");
+  for (int64_t b = 0; b < n / QK_K; ++b) {
+    const uint8_t* blk = src + b * Q6_K_BYTES;
+    float d;
+    if (read_fp16(blk + Q6_K_BYTES - 2, &d)) return -1;
+    const uint8_t* ql = blk;
+    const uint8_t* qh = blk + QK_K / 2;
+    const uint8_t* sc = blk + QK_K / 2 + QK_K / 4;
+    float* out = dst + b * QK_K;
+    for (int chunk = 0; chunk < 2; ++chunk) {
+      const uint8_t* cql = ql + chunk * 64;
+      const uint8_t* cqh = qh + chunk * 32;
+      const uint8_t* csc = sc + chunk * 8;
+      for (int lane = 0; lane < 32; ++lane) {
+        int si = lane / 16;
+        int lo = cql[lane], hi = cql[32 + lane], top = cqh[lane];
+        int q1 = ((lo & 0x0F) | ((top & 3) << 4)) - 32;
+        int q2 = ((hi & 0x0F) | (((top >> 2) & 3) << 4)) - 32;
+        int q3 = ((lo >> 4) | (((top >> 4) & 3) << 4)) - 32;
+        int q4 = ((hi >> 4) | (((top >> 6) & 3) << 4)) - 32;
+        out[chunk * 128 + lane] = (d * (float)rd_s8(csc + si + 0)) * (float)q1;
+        out[chunk * 128 + 32 + lane] = (d * (float)rd_s8(csc + si + 2)) * (float)q2;
+        out[chunk * 128 + 64 + lane] = (d * (float)rd_s8(csc + si + 4)) * (float)q3;
+        out[chunk * 128 + 96 + lane] = (d * (float)rd_s8(csc + si + 6)) * (float)q4;
+      }
+    }
+  }
+  return 0;
+}
+
+/* dequantize-q5-0, llambda.lisp:3965-3990 */
+static int dequant_q5_0(const uint8_t* src, int64_t n, float* dst) {
+  if (n % 32) return fail("Q5_0 dequantization requires ELEMENT-COUNT to be a multiple of 32.");
+  for (int64_t b = 0; b < n / 32; ++b) {
+    const uint8_t* blk = src + b * Q5_0_BYTES;
+    float d;
+    if (read_fp16(blk, &d)) return -1;
+    uint32_t qh = rd_u32(blk + 2);
+    const uint8_t* qs = blk + 6;
+    for (int i = 0; i < 16; ++i) {
+      int packed = qs[i];
+      int xh0 = ((qh >> i) & 1) ? 0x10 : 0;
+      int xh1 = ((qh >> (i + 16)) & 1) ? 0x10 : 0;
+      int q0 = ((packed & 0x0F) | xh0) - 16;
+      int q1 = ((packed >> 4) | xh1) - 16;
+      dst[b * 32 + i] = d * (float)q0;
+      dst[b * 32 + 16 + i] = d * (float)q1;
+    }
+  }
+  return 0;
+}
+
+/* dequantize-q8-0, llambda.lisp:3992-4009 */
+static int dequant_q8_0(const uint8_t* src, int64_t n, float* dst) {
+  if (n % 32) return fail("Q8_0 dequantization requires ELEMENT-COUNT to be a multiple of 32.");
+  for (int64_t b = 0; b < n / 32; ++b) {
+    const uint8_t* blk = src + b * Q8_0_BYTES;
+    float d;
+    if (read_fp16(blk, &d)) return -1;
+    for (int i = 0; i < 32; ++i) dst[b * 32 + i] = d * (float)rd_s8(blk + 2 + i);
+  }
+  return 0;
+}
+
+int oracle_dequantize(int type, const uint8_t* src, int64_t n, float* dst) {
+  switch (type) {
+    case ORACLE_TYPE_F32: memcpy(dst, src, (size_t)n * 4); return 0;
+    case ORACLE_TYPE_Q4_K: return dequant_q4_k(src, n, dst);
+    case ORACLE_TYPE_Q6_K: return dequant_q6_k(src, n, dst);
+    case ORACLE_TYPE_Q5_0: return dequant_q5_0(src, n, dst);
+    case ORACLE_TYPE_Q8_0: return dequant_q8_0(src, n, dst);
+    default: return fail("Unsupported GGML tensor type tag %d.", type);
+  }
+}
+
+/* ------------------------------------------------------------------ */
+/* Fused row dots                                                      */
+
+/* f32.8-horizontal+: sb-simd's lane order is unpublished; lanes are summed
+ * 0..7 left to right here (parity unpinned for this order only). */
+static inline float horizontal_sum8(const float a[8]) {
+  float s = a[0];
+  for (int t = 1; t < 8; ++t) s = s + a[t];
+  return s;
+}
+
+/* dot-product-with-q4-k-m-tensor-data, llambda.lisp:4338-4382, with the
+ * group body of expand-q4-k-body, llambda.lisp:4145-4201. */
+static int dot_q4_k(const uint8_t* row, const float* x, int64_t n, float* out) {
+  if (n % QK_K) return fail("Q4_K_M dot product requires ELEMENT-COUNT to be a multiple of 256.");
+  float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+  for (int64_t b = 0; b < n / QK_K; ++b) {
+    const uint8_t* blk = row + b * Q4_K_BYTES;
+    float d, dmin;
+    if (read_fp16(blk, &d) || read_fp16(blk + 2, &dmin)) return -1;
+    const uint8_t* scales = blk + 4;
+    const uint8_t* qs = blk + 4 + K_SCALE_SIZE;
+    const float* vb = x + b * QK_K;
+    for (int j = 0; j < 4; ++j) { /* accumulate-body (2j 2j+1 32j 64j) */
+      int sc0, m0, sc1, m1;
+      oracle_get_scale_min_k4(scales, 2 * j, &sc0, &m0);
+      oracle_get_scale_min_k4(scales, 2 * j + 1, &sc1, &m1);
+      float delta0 = d * (float)sc0, offset0 = dmin * (float)m0;
+      float delta1 = d * (float)sc1, offset1 = dmin * (float)m1;
+      const uint8_t* q = qs + 32 * j;
+      const float* v = vb + 64 * j;
+      for (int g = 0; g < 4; ++g) {
+        for (int t = 0; t < 8; ++t) {
+          int packed = q[8 * g + t];
+          float wlo = (float)(packed & 0x0F) * delta0 - offset0;
+          float whi = (float)(packed >> 4) * delta1 - offset1;
+          acc[t] = fmaf(wlo, v[8 * g + t], acc[t]);
+          acc[t] = fmaf(whi, v[32 + 8 * g + t], acc[t]);
+        }
+      }
+    }
+  }
+  *out = horizontal_sum8(acc);
+  return 0;
+}
+
+/* dot-product-with-q6-k-tensor-data, llambda.lisp:4446-4506, with the group
+ * body of expand-q6-k-group, llambda.lisp:4203-4310. */
+static int dot_q6_k(const uint8_t* row, const float* x, int64_t n, float* out) {
+  if (n % QK_K) return fail("Q6_K dot product requires ELEMENT-COUNT to be a multiple of 256.");
+  float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+  for (int64_t b = 0; b < n / QK_K; ++b) {
+    const uint8_t* blk = row + b * Q6_K_BYTES;
+    float d;
+    if (read_fp16(blk + Q6_K_BYTES - 2, &d)) return -1;
+    const uint8_t* ql = blk;
+    const uint8_t* qh = blk + QK_K / 2;
+    const uint8_t* sc = blk + QK_K / 2 + QK_K / 4;
+    const float* vb = x + b * QK_K;
+    for (int h = 0; h < 2; ++h) {
+      const uint8_t* cql = ql + 64 * h;
+      const uint8_t* cqh = qh + 32 * h;
+      const uint8_t* csc = sc + 8 * h;
+      const float* cv = vb + 128 * h;
+      for (int pass = 0; pass < 2; ++pass) { /* start-lane 0 then 16 */
+        float delta[4];
+        for (int k = 0; k < 4; ++k) delta[k] = d * (float)rd_s8(csc + 2 * k + pass);
+        for (int g = 0; g < 2; ++g) {
+          for (int t = 0; t < 8; ++t) {
+            int L = 16 * pass + 8 * g + t;
+            int lo = cql[L], hi = cql[32 + L], top = cqh[L];
+            int q1 = ((lo & 0x0F) | ((top & 3) << 4)) - 32;
+            int q2 = ((hi & 0x0F) | (((top >> 2) & 3) << 4)) - 32;
+            int q3 = ((lo >> 4) | (((top >> 4) & 3) << 4)) - 32;
+            int q4 = ((hi >> 4) | (((top >> 6) & 3) << 4)) - 32;
+            float w1 = (float)q1 * delta[0];
+            float w2 = (float)q2 * delta[1];
+            float w3 = (float)q3 * delta[2];
+            float w4 = (float)q4 * delta[3];
+            acc[t] = fmaf(w1, cv[L], acc[t]);
+            acc[t] = fmaf(w2, cv[32 + L], acc[t]);
+            acc[t] = fmaf(w3, cv[64 + L], acc[t]);
+            acc[t] = fmaf(w4, cv[96 + L], acc[t]);
+          }
+        }
+      }
+    }
+  }
+  *out = horizontal_sum8(acc);
+  return 0;
+}
+
+/* dot-product-with-q5-0-tensor-data, llambda.lisp:4037-4066:
+ * sum += d * (q0*v0 + q1*v1), every operation rounded. */
+static int dot_q5_0(const uint8_t* row, const float* x, int64_t n, float* out) {
+  if (n % 32) return fail("Q5_0 dot product requires ELEMENT-COUNT to be a multiple of 32.");
+  float sum = 0.0f;
+  for (int64_t b = 0; b < n / 32; ++b) {
+    const uint8_t* blk = row + b * Q5_0_BYTES;
+    float d;
+    if (read_fp16(blk, &d)) return -1;
+    uint32_t qh = rd_u32(blk + 2);
+    const uint8_t* qs = blk + 6;
+    const float* v = x + b * 32;
+    for (int i = 0; i < 16; ++i) {
+      int packed = qs[i];
+      int xh0 = ((qh >> i) & 1) ? 0x10 : 0;
+      int xh1 = ((qh >> (i + 16)) & 1) ? 0x10 : 0;
+      int q0 = ((packed & 0x0F) | xh0) - 16;
+      int q1 = ((packed >> 4) | xh1) - 16;
+      float pair = (float)q0 * v[i] + (float)q1 * v[16 + i];
+      sum = sum + d * pair;
+    }
+  }
+  *out = sum;
+  return 0;
+}
+
+/* dot-product-with-q8-0-tensor-data, llambda.lisp:4068-4094:
+ * sum += (d * q) * v. */
+static int dot_q8_0(const uint8_t* row, const float* x, int64_t n, float* out) {
+  if (n % 32) return fail("Q8_0 dot product requires ELEMENT-COUNT to be a multiple of 32.");
+  float sum = 0.0f;
+  for (int64_t b = 0; b < n / 32; ++b) {
+    const uint8_t* blk = row + b * Q8_0_BYTES;
+    float d;
+    if (read_fp16(blk, &d)) return -1;
+    const float* v = x + b * 32;
+    for (int i = 0; i < 32; ++i) sum = sum + (d * (float)rd_s8(blk + 2 + i)) * v[i];
+  }
+  *out = sum;
+  return 0;
+}
+
+/* dot-product-with-f32-tensor-data, llambda.lisp:4096-4107 */
+static float dot_f32(const float* w, const float* x, int64_t n) {
+  float sum = 0.0f;
+  for (int64_t i = 0; i < n; ++i) sum = sum + x[i] * w[i];
+  return sum;
+}
+
+int oracle_dot_row(int type, const uint8_t* row, const float* x, int64_t n, float* out) {
+  switch (type) {
+    case ORACLE_TYPE_F32:
+      /* rows of an F32 tensor are 4-byte aligned in GGUF */
+      *out = dot_f32((const float*)(const void*)row, x, n);
+      return 0;
+    case ORACLE_TYPE_Q4_K: return dot_q4_k(row, x, n, out);
+    case ORACLE_TYPE_Q6_K: return dot_q6_k(row, x, n, out);
+    case ORACLE_TYPE_Q5_0: return dot_q5_0(row, x, n, out);
+    case ORACLE_TYPE_Q8_0: return dot_q8_0(row, x, n, out);
+    default: return fail("Unsupported GGML tensor type tag %d.", type);
+  }
+}
+
+/* dot-product, llambda.lisp:3491-3500 */
+float oracle_dot_product(const float* left, const float* right, int64_t n) {
+  float sum = 0.0f;
+  for (int64_t i = 0; i < n; ++i) sum = sum + left[i] * right[i];
+  return sum;
+}
+
+/* ------------------------------------------------------------------ */
+/* Persistent worker pool (the lparallel kernel of llambda.lisp:769-817) */
+
+typedef struct gemv_job {
+  int type;
+  const uint8_t* matrix;
+  int64_t row_bytes, columns, rows, parts;
+  const float* x;
+  float* y;
+  int status;              /* first failing part's status */
+  char error[512];
+  pthread_mutex_t error_lock;
+} gemv_job;
+
+typedef struct pool {
+  pthread_mutex_t lock;
+  pthread_cond_t start, done;
+  pthread_t* threads;
+  int size;                /* worker threads (the caller is one more part) */
+  unsigned long generation;
+  int pending;
+  int next_part;
+  gemv_job* job;
+} pool;
+
+static pool g_pool = {PTHREAD_MUTEX_INITIALIZER, PTHREAD_COND_INITIALIZER,
+                      PTHREAD_COND_INITIALIZER, NULL, 0, 0, 0, 0, NULL};
+static pthread_mutex_t g_pool_use = PTHREAD_MUTEX_INITIALIZER;
+
+/* lparallel:pdotimes over `parts` contiguous chunks of [0, rows). */
+static void run_part(gemv_job* job, int64_t part) {
+  int64_t base = job->rows / job->parts, extra = job->rows % job->parts;
+  int64_t start = part * base + (part < extra ? part : extra);
+  int64_t count = base + (part < extra ? 1 : 0);
+  for (int64_t r = start; r < start + count; ++r) {
+    float v;
+    if (oracle_dot_row(job->type, job->matrix + r * job->row_bytes, job->x, job->columns, &v)) {
+      pthread_mutex_lock(&job->error_lock);
+      if (job->status == 0) {
+        job->status = -1;
+        snprintf(job->error, sizeof job->error, "%s", g_error);
+      }
+      pthread_mutex_unlock(&job->error_lock);
+      return;
+    }
+    job->y[r] = v;
+  }
+}
+
+static void drain_parts(pool* p, gemv_job* job) {
+  for (;;) {
+    pthread_mutex_lock(&p->lock);
+    int part = p->next_part < job->parts ? p->next_part++ : -1;
+    pthread_mutex_unlock(&p->lock);
+    if (part < 0) return;
+    run_part(job, part);
+  }
+}
+
+static void* worker_main(void* arg) {
+  pool* p = (pool*)arg;
+  unsigned long seen = 0;
+  for (;;) {
+    pthread_mutex_lock(&p->lock);
+    while (p->generation == seen) pthread_cond_wait(&p->start, &p->lock);
+    seen = p->generation;
+    gemv_job* job = p->job;
+    pthread_mutex_unlock(&p->lock);
+    drain_parts(p, job);
+    pthread_mutex_lock(&p->lock);
+    if (--p->pending == 0) pthread_cond_signal(&p->done);
+    pthread_mutex_unlock(&p->lock);
+  }
+  return NULL;
+}
+
+/* ensure-gemv-kernel, llambda.lisp:774-792: grow the pool to threads-1
+ * workers (the caller works too). */
+static void ensure_pool(int threads) {
+  int want = threads - 1;
+  if (g_pool.size >= want) return;
+  g_pool.threads = (pthread_t*)realloc(g_pool.threads, sizeof(pthread_t) * (size_t)want);
+  for (int i = g_pool.size; i < want; ++i) {
+    pthread_create(&g_pool.threads[i], NULL, worker_main, &g_pool);
+    pthread_detach(g_pool.threads[i]);
+  }
+  g_pool.size = want;
+}
+
+int oracle_gemv(int type, const uint8_t* matrix, int64_t rows, int64_t columns,
+                const float* x, float* y, int threads) {
+  int64_t row_bytes = oracle_row_bytes(type, columns);
+  if (row_bytes < 0) return -1;
+  if (threads <= 0) threads = 1;
+  int parallel = (type == ORACLE_TYPE_Q4_K || type == ORACLE_TYPE_Q6_K) &&
+                 rows >= PARALLEL_MIN_ROWS && threads > 1;
+  gemv_job job;
+  memset(&job, 0, sizeof job);
+  job.type = type; job.matrix = matrix; job.row_bytes = row_bytes;
+  job.columns = columns; job.rows = rows; job.x = x; job.y = y;
+  pthread_mutex_init(&job.error_lock, NULL);
+  if (!parallel) {
+    job.parts = 1;
+    run_part(&job, 0);
+  } else {
+    job.parts = rows < threads ? rows : threads; /* parallel-gemv-part-count */
+    pthread_mutex_lock(&g_pool_use);
+    ensure_pool(threads);
+    pthread_mutex_lock(&g_pool.lock);
+    g_pool.job = &job;
+    g_pool.next_part = 0;
+    g_pool.pending = threads - 1;
+    g_pool.generation++;
+    pthread_cond_broadcast(&g_pool.start);
+    pthread_mutex_unlock(&g_pool.lock);
+    drain_parts(&g_pool, &job);
+    pthread_mutex_lock(&g_pool.lock);
+    while (g_pool.pending > 0) pthread_cond_wait(&g_pool.done, &g_pool.lock);
+    pthread_mutex_unlock(&g_pool.lock);
+    pthread_mutex_unlock(&g_pool_use);
+  }
+  pthread_mutex_destroy(&job.error_lock);
+  if (job.status) {
+    if (parallel) snprintf(g_error, sizeof g_error, "%s", job.error);
+    return -1;
+  }
+  return 0;
+}
+
+/* ------------------------------------------------------------------ */
+/* Routing and activations                                             */
+
+/* select-top-k-logits-into, llambda.lisp:5265-5292: sorted insertion with
+ * strict >, slots start at (-1, most-negative-single-float). */
+void oracle_select_top_k(const float* logits, int64_t n, int64_t k,
+                         int64_t* idx, float* val) {
+  for (int64_t i = 0; i < k; ++i) { idx[i] = -1; val[i] = -FLT_MAX; }
+  if (k <= 0) return;
+  for (int64_t li = 0; li < n; ++li) {
+    float v = logits[li];
+    if (v > val[k - 1]) {
+      int64_t ins = k - 1;
+      while (ins > 0 && v > val[ins - 1]) {
+        val[ins] = val[ins - 1];
+        idx[ins] = idx[ins - 1];
+        --ins;
+      }
+      val[ins] = v;
+      idx[ins] = li;
+    }
+  }
+}
+
+/* sigmoid, llambda.lisp:929-930: (exp (- x)) of a single-float is a single
+ * (computed in double and rounded); 1 + e and the quotient are double; the
+ * result is rounded to single.  SBCL traps the rounding overflow that
+ * exp(-x) > FLT_MAX would cause (x < -88.72); this restatement yields the
+ * IEEE limit (0) there instead. */
+float oracle_sigmoid(float x) {
+  float e = (float)exp((double)(-x));
+  return (float)(1.0 / (1.0 + (double)e));
+}
+
+/* silu, llambda.lisp:926-927 */
+float oracle_silu(float x) {
+  float e = (float)exp((double)(-x));
+  return (float)((double)x / (1.0 + (double)e));
+}
+
+/* relu-squared, llambda.lisp:938-940 */
+float oracle_relu_squared(float x) {
+  float r = x > 0.0f ? x : 0.0f;
+  return r * r;
+}
+
+/* ------------------------------------------------------------------ */
+/* Routed MoE layers                                                   */
+
+static int expert_gemv(int type, const uint8_t* slab, int64_t expert, int64_t rows,
+                       int64_t columns, const float* x, float* y, int threads) {
+  /* gguf-model-expert-matrix-vector-multiply-into, llambda.lisp:4951-4971:
+   * expert e's rows are [e*rows, (e+1)*rows) of the flat matrix. */
+  int64_t row_bytes = oracle_row_bytes(type, columns);
+  if (row_bytes < 0) return -1;
+  return oracle_gemv(type, slab + expert * rows * row_bytes, rows, columns, x, y, threads);
+}
+
+/* qwen3next-moe-into, llambda.lisp:5321-5426, for one token. */
+static int qwen3next_token(const oracle_moe_desc* m, const float* x, float* dest,
+                           int64_t* top_idx, float* top_w, float* logits, float* work,
+                           int threads) {
+  const int64_t H = m->hidden, E = m->expert_count, K = m->top_k, F = m->expert_ffn,
+                Fs = m->shared_ffn;
+  float* top_logits = work;                 /* [K] */
+  float* gate = top_logits + K;             /* [max(F, Fs)] */
+  int64_t FF = F > Fs ? F : Fs;
+  float* up = gate + FF;
+  float* down = up + FF;                    /* [H] */
+  for (int64_t i = 0; i < H; ++i) dest[i] = 0.0f;                       /* :5359 */
+  if (oracle_gemv(ORACLE_TYPE_F32, (const uint8_t*)m->router, E, H, x, logits, threads))
+    return -1;                                                          /* :5360-5363 */
+  oracle_select_top_k(logits, E, K, top_idx, top_logits);              /* :5364 */
+  float weight_sum = 0.0f;                                              /* :5365-5379 */
+  for (int64_t r = 0; r < K; ++r) {
+    float w = oracle_sigmoid(top_logits[r]);
+    top_w[r] = w;
+    weight_sum = weight_sum + w;
+  }
+  if (!(weight_sum > 0.0f))
+    return fail("Qwen3Next layer router produced non-positive top-k weight sum.");
+  for (int64_t r = 0; r < K; ++r) top_w[r] = top_w[r] / weight_sum;
+  for (int64_t r = 0; r < K; ++r) {                                     /* :5380-5409 */
+    int64_t e = top_idx[r];
+    if (e < 0 || e >= E) return fail("Expert index %lld is out of range.", (long long)e);
+    if (expert_gemv(m->gate_type, m->gate_exps, e, F, H, x, gate, threads)) return -1;
+    if (expert_gemv(m->up_type, m->up_exps, e, F, H, x, up, threads)) return -1;
+    for (int64_t i = 0; i < F; ++i) gate[i] = oracle_silu(gate[i]);
+    for (int64_t i = 0; i < F; ++i) gate[i] = gate[i] * up[i];
+    if (expert_gemv(m->down_type, m->down_exps, e, H, F, gate, down, threads)) return -1;
+    for (int64_t i = 0; i < H; ++i) dest[i] = dest[i] + top_w[r] * down[i];
+  }
+  if (Fs > 0) {                                                         /* :5410-5426 */
+    float shared_weight = oracle_sigmoid(oracle_dot_product(m->shared_gate_inp, x, H));
+    if (oracle_gemv(m->shared_gate_type, m->shared_gate, Fs, H, x, gate, threads)) return -1;
+    if (oracle_gemv(m->shared_up_type, m->shared_up, Fs, H, x, up, threads)) return -1;
+    for (int64_t i = 0; i < Fs; ++i) gate[i] = oracle_silu(gate[i]);
+    for (int64_t i = 0; i < Fs; ++i) gate[i] = gate[i] * up[i];
+    if (oracle_gemv(m->shared_down_type, m->shared_down, H, Fs, gate, down, threads)) return -1;
+    for (int64_t i = 0; i < H; ++i) dest[i] = dest[i] + shared_weight * down[i];
+  }
+  return 0;
+}
+
+/* nemotron-h-moe-ffn-into, llambda.lisp:5827-5949, for one token, without
+ * the optional latent projections (ffn_latent_down/up absent). */
+static int nemotron_token(const oracle_moe_desc* m, const float* x, float* dest,
+                          int64_t* top_idx, float* top_w, float* logits, float* work,
+                          int threads) {
+  const int64_t H = m->hidden, E = m->expert_count, K = m->top_k, F = m->expert_ffn,
+                Fs = m->shared_ffn;
+  float* top_logits = work;
+  int64_t FF = F > Fs ? F : Fs;
+  float* up = top_logits + K;               /* [FF] */
+  float* down = up + FF;                    /* [H] */
+  if (oracle_gemv(ORACLE_TYPE_F32, (const uint8_t*)m->router, E, H, x, logits, threads))
+    return -1;                                                          /* :5888-5891 */
+  for (int64_t e = 0; e < E; ++e) logits[e] = logits[e] + m->router_bias[e]; /* :5892 */
+  oracle_select_top_k(logits, E, K, top_idx, top_logits);              /* :5893 */
+  float weight_sum = 0.0f;                                              /* :5894-5913 */
+  for (int64_t r = 0; r < K; ++r) {
+    float w = oracle_sigmoid(top_logits[r]);
+    top_w[r] = w;
+    weight_sum = weight_sum + w;
+  }
+  if (m->expert_weights_norm) {
+    if (!(weight_sum > 0.0f))
+      return fail("Nemotron-H MoE layer router produced non-positive top-k weight sum.");
+    for (int64_t r = 0; r < K; ++r) top_w[r] = top_w[r] / weight_sum;
+  }
+  for (int64_t r = 0; r < K; ++r) top_w[r] = m->expert_weights_scale * top_w[r];
+  for (int64_t i = 0; i < H; ++i) dest[i] = 0.0f;                       /* :5914 */
+  for (int64_t r = 0; r < K; ++r) {                                     /* :5915-5932 */
+    int64_t e = top_idx[r];
+    if (e < 0 || e >= E) return fail("Expert index %lld is out of range.", (long long)e);
+    if (expert_gemv(m->up_type, m->up_exps, e, F, H, x, up, threads)) return -1;
+    for (int64_t i = 0; i < F; ++i) up[i] = oracle_relu_squared(up[i]);
+    if (expert_gemv(m->down_type, m->down_exps, e, H, F, up, down, threads)) return -1;
+    for (int64_t i = 0; i < H; ++i) dest[i] = dest[i] + top_w[r] * down[i];
+  }
+  if (Fs > 0) {                                                         /* :5939-5949 */
+    if (oracle_gemv(m->shared_up_type, m->shared_up, Fs, H, x, up, threads)) return -1;
+    for (int64_t i = 0; i < Fs; ++i) up[i] = oracle_relu_squared(up[i]);
+    if (oracle_gemv(m->shared_down_type, m->shared_down, H, Fs, up, down, threads)) return -1;
+    for (int64_t i = 0; i < H; ++i) dest[i] = dest[i] + down[i];
+  }
+  return 0;
+}
+
+int oracle_moe_forward(const oracle_moe_desc* m, const float* x, float* y, int64_t tokens,
+                       int64_t* top_indices, float* top_weights, float* router_logits,
+                       int threads) {
+  if (!m || !x || !y) return fail("null argument");
+  if (m->top_k <= 0 || m->top_k > m->expert_count) return fail("top_k out of range");
+  int64_t FF = m->expert_ffn > m->shared_ffn ? m->expert_ffn : m->shared_ffn;
+  size_t work_floats = (size_t)(m->top_k + 2 * FF + m->hidden + m->expert_count);
+  float* work = (float*)malloc(work_floats * sizeof(float));
+  int64_t* idx = (int64_t*)malloc((size_t)m->top_k * sizeof(int64_t));
+  float* w = (float*)malloc((size_t)m->top_k * sizeof(float));
+  float* logits = work + m->top_k + 2 * FF + m->hidden;
+  int status = 0;
+  for (int64_t t = 0; t < tokens && status == 0; ++t) {
+    const float* xt = x + t * m->hidden;
+    float* yt = y + t * m->hidden;
+    if (m->variant == 0)
+      status = qwen3next_token(m, xt, yt, idx, w, logits, work, threads);
+    else if (m->variant == 1)
+      status = nemotron_token(m, xt, yt, idx, w, logits, work, threads);
+    else
+      status = fail("unknown MoE variant %d", m->variant);
+    if (status == 0) {
+      if (top_indices) memcpy(top_indices + t * m->top_k, idx, (size_t)m->top_k * sizeof(int64_t));
+      if (top_weights) memcpy(top_weights + t * m->top_k, w, (size_t)m->top_k * sizeof(float));
+      if (router_logits)
+        memcpy(router_logits + t * m->expert_count, logits, (size_t)m->expert_count * sizeof(float));
+    }
+  }
+  free(work);
+  free(idx);
+  free(w);
+  return status;
+}

@@ -1,0 +1,125 @@
+/*
+ * llambda_oracle.h -- CPU restatement of llambda's quantized decode hot path.
+ *
+ * TEST INFRASTRUCTURE ONLY.  This library is the parity checker for the HIP
+ * path and the source of the reported CPU baseline.  Only tests/,
+ * __graft_entry__.smoke() and bench.py's cpu_baseline leg may load it, and
+ * only as the checker or the baseline, never as the thing measured or shipped.
+ *
+ * Every function restates one function of the reference (Common Lisp,
+ * llambda.lisp) and cites the file:line it follows.  Arithmetic order is the
+ * reference's: single-precision products and sums are rounded separately
+ * (the library is compiled with -ffp-contract=off) and only the reference's
+ * explicit f32.8-fmadd steps use fmaf().
+ *
+ * Parity pins (what checks each function beyond retyping it):
+ *   fp16 decode          all 65536 bit patterns vs numpy.float16 (tests)
+ *   get_scale_min_k4     independent bit-field decode of all 256 values of
+ *                        each scale byte position (tests)
+ *   dequantize Q4_K/Q6_K reference KATs tests.lisp:2386-2450, 2324-2367
+ *   fused Q4_K/Q6_K dot  reference KATs tests.lisp:2257-2322 plus float64
+ *                        dot of the dequantised row on random blocks
+ *   Q5_0/Q8_0            float64 closed forms of the block formulas
+ *   f32 dot              numpy float32 sequential accumulate (bit-exact)
+ *   select_top_k         stable descending sort with NaN excluded
+ *   sigmoid/silu/relu2   float64 closed forms
+ *   MoE layers           float64 restatement from dequantised weights
+ *                        (independent of the fused kernels)
+ *   horizontal+ of the 8-lane accumulator: sb-simd's internal order is not
+ *   published; this file sums lanes 0..7 left to right.  Parity unpinned for
+ *   that order; it moves results by a few ulp, far inside the 1e-4 bound.
+ */
+#ifndef LLAMBDA_ORACLE_H
+#define LLAMBDA_ORACLE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* GGML type tags, llambda.lisp:24-31. */
+enum {
+  ORACLE_TYPE_F32 = 0,
+  ORACLE_TYPE_Q5_0 = 6,
+  ORACLE_TYPE_Q8_0 = 8,
+  ORACLE_TYPE_Q4_K = 12,
+  ORACLE_TYPE_Q6_K = 14
+};
+
+const char* oracle_last_error(void);
+
+/* llambda.lisp:2126-2155 */
+int64_t oracle_type_block_elements(int type);
+int64_t oracle_type_block_bytes(int type);
+int64_t oracle_row_bytes(int type, int64_t columns); /* -1 on error */
+
+/* llambda.lisp:716-733 (fp16-to-single-float) */
+int oracle_fp16_to_f32(uint16_t bits, float* out);
+
+/* llambda.lisp:6794-6813 and 4316-4336 */
+void oracle_get_scale_min_k4(const uint8_t* scales, int index, int* scale, int* min);
+
+/* Scalar dequantisers: llambda.lisp:6815-6859, 6919-6978, 3965-4009 */
+int oracle_dequantize(int type, const uint8_t* src, int64_t elements, float* dst);
+
+/* Fused row dots: llambda.lisp:4338-4382 (Q4_K), 4446-4506 (Q6_K),
+ * 4037-4094 (Q5_0, Q8_0), 4096-4107 (F32). */
+int oracle_dot_row(int type, const uint8_t* row, const float* x, int64_t columns, float* out);
+
+/* llambda.lisp:3491-3500 (dot-product) */
+float oracle_dot_product(const float* left, const float* right, int64_t n);
+
+/* Row-parallel GEMV, llambda.lisp:4542-4658 with the worker runtime of
+ * 769-817: Q4_K/Q6_K use min(rows, threads) contiguous parts when
+ * rows >= 96; other types run serially.  threads <= 0 means 1. */
+int oracle_gemv(int type, const uint8_t* matrix, int64_t rows, int64_t columns,
+                const float* x, float* y, int threads);
+
+/* llambda.lisp:5265-5292 */
+void oracle_select_top_k(const float* logits, int64_t n, int64_t k,
+                         int64_t* top_indices, float* top_logits);
+
+/* llambda.lisp:926-940 */
+float oracle_sigmoid(float x);
+float oracle_silu(float x);
+float oracle_relu_squared(float x);
+
+/* One routed-MoE layer description.  Expert tensors are the flat GGUF
+ * [E * rows][columns] slabs (llambda.lisp:4951-4971). */
+typedef struct oracle_moe_desc {
+  int variant;                 /* 0 = qwen3next, 1 = nemotron_h_moe */
+  int64_t hidden;              /* H */
+  int64_t expert_count;        /* E */
+  int64_t top_k;               /* k, already min(E, used count) */
+  int64_t expert_ffn;          /* F */
+  int64_t shared_ffn;          /* Fs, 0 when there is no shared expert */
+  const float* router;         /* F32 [E][H] */
+  const float* shared_gate_inp;/* F32 [H], qwen3next only */
+  const float* router_bias;    /* F32 [E], nemotron only (exp_probs_b.bias) */
+  float expert_weights_scale;  /* nemotron only */
+  int expert_weights_norm;     /* nemotron only */
+  int gate_type;  const uint8_t* gate_exps;   /* qwen3next only: [E*F][H] */
+  int up_type;    const uint8_t* up_exps;     /* [E*F][H] */
+  int down_type;  const uint8_t* down_exps;   /* [E*H][F] */
+  int shared_gate_type; const uint8_t* shared_gate; /* [Fs][H], qwen3next */
+  int shared_up_type;   const uint8_t* shared_up;   /* [Fs][H] */
+  int shared_down_type; const uint8_t* shared_down; /* [H][Fs] */
+} oracle_moe_desc;
+
+/* llambda.lisp:5321-5426 (qwen3next-moe-into) and 5827-5949
+ * (nemotron-h-moe-ffn-into), run token by token as the reference's
+ * prefill does (llambda.lisp:1319-1341).  x, y: [tokens][H].  The optional
+ * outputs receive the selected experts and their final weights per token
+ * ([tokens][k]) and the router logits ([tokens][E], after the bias for
+ * nemotron). */
+int oracle_moe_forward(const oracle_moe_desc* desc, const float* x, float* y,
+                       int64_t tokens, int64_t* top_indices, float* top_weights,
+                       float* router_logits, int threads);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif

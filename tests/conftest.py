@@ -1,0 +1,22 @@
+import os
+import sys
+
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+if ROOT not in sys.path:
+    sys.path.insert(0, ROOT)
+
+
+def pytest_configure(config):
+    config.addinivalue_line("markers", "gpu: needs an MI355X (runs through the HIP C ABI)")
+
+
+@pytest.fixture(scope="session")
+def hip():
+    """The loaded HIP library; GPU tests fail loudly when it is missing."""
+    from llambda_amd import native
+    lib = native.lib()
+    status = lib.llambda_hip_probe()
+    assert status == 1, f"no usable gfx950 device (probe={status}): {native.last_error()}"
+    return lib

@@ -1,0 +1,85 @@
+"""Write reference_kats.json: the known-answer blocks and expected values of
+the reference's own tests for this path (tests.lisp), as data.
+
+  dequantize-q4-k-m        tests.lisp:2386-2416
+  dequantize-q6-k          tests.lisp:2418-2450
+  load-gguf-tensor-quantized tests.lisp:2324-2367
+  dot-product-with-q4-k-tensor-row tests.lisp:2257-2288
+  dot-product-with-q6-k-tensor-row tests.lisp:2290-2322
+  forward-primitives silu(2) tests.lisp:298-344
+
+The reference cannot run here (no Common Lisp implementation), so the blocks
+are rebuilt from the byte assignments those tests make and the expected
+values are the literals they assert.
+"""
+import json
+import os
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+
+
+def q4k_block():
+    b = bytearray(144)
+    b[0], b[1], b[2], b[3] = 0x00, 0x3C, 0x00, 0x3C      # d = dmin = 1.0
+    for i in range(4):
+        b[4 + i] = 2          # scales 0..3
+        b[8 + i] = 1          # mins 0..3
+        b[12 + i] = 0x12      # low nibble: scales 4..7 = 2, high nibble: mins 4..7 = 1
+    for i in range(128):
+        b[16 + i] = 0x76      # low nibble 6, high nibble 7
+    return bytes(b)
+
+
+def q6k_block():
+    b = bytearray(210)
+    for i in range(32):
+        b[i] = 0x31
+        b[32 + i] = 0x42
+        b[64 + i] = 0x31
+        b[96 + i] = 0x42
+    for i in range(64):
+        b[128 + i] = 0xAA
+    for i in range(16):
+        b[192 + i] = 2
+    b[208], b[209] = 0x00, 0x3C                            # d = 1.0
+    return bytes(b)
+
+
+def main():
+    kats = {
+        "source": "tests.lisp (llambda reference test suite)",
+        "q4_k_dequantize": {
+            "cite": "tests.lisp:2386-2416, 2324-2367",
+            "block_hex": q4k_block().hex(),
+            # (start, end, value) ranges the test asserts
+            "expect_ranges": [[0, 32, 11.0], [32, 64, 13.0], [192, 224, 11.0], [224, 256, 13.0]],
+            "expect_points": [[0, 11.0], [32, 13.0]],
+        },
+        "q6_k_dequantize": {
+            "cite": "tests.lisp:2418-2450, 2324-2367",
+            "block_hex": q6k_block().hex(),
+            "expect_ranges": [[0, 32, 2.0], [32, 64, 4.0], [64, 96, 6.0], [96, 128, 8.0],
+                              [128, 160, 2.0], [224, 256, 8.0]],
+            "expect_points": [[0, 2.0], [96, 8.0]],
+        },
+        "q4_k_dot": {
+            "cite": "tests.lisp:2257-2288",
+            "block_hex": q4k_block().hex(),
+            "activation": "((i mod 11) - 5) / 3",
+            "tolerance": 1e-4,
+        },
+        "q6_k_dot": {
+            "cite": "tests.lisp:2290-2322",
+            "block_hex": q6k_block().hex(),
+            "activation": "((i mod 13) - 6) / 4",
+            "tolerance": 1e-4,
+        },
+        "silu": {"cite": "tests.lisp:298-344", "x": 2.0, "expect": 1.7615942, "tolerance": 1e-5},
+    }
+    with open(os.path.join(HERE, "reference_kats.json"), "w") as fh:
+        json.dump(kats, fh, indent=1)
+        fh.write("\n")
+
+
+if __name__ == "__main__":
+    main()

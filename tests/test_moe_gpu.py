@@ -1,0 +1,217 @@
+"""GPU parity of the routed-MoE layer against the oracle, through the C ABI.
+
+Routing: the ordered top-k must equal the oracle's for every token whose
+top-(k+1) reference logits are separated by more than twice the router's
+fp32 error bound (K * 2^-24 * sum|w x|); the set must match wherever the
+k-th / (k+1)-th gap alone clears that bound.
+Outputs: per element, |y_gpu - y_oracle| <= 1e-4 * S_i where S_i is the
+absolute-value sum of the final contraction,
+  S_i = sum_r |w_r| sum_f |Wd_r[i,f] h_r[f]| + |s| sum_f |Wsd[i,f] hs[f]|,
+evaluated in float64 from the oracle's exact dequantised weights.
+"""
+import os
+
+import numpy as np
+import pytest
+
+import oracle
+from llambda_amd import ggml, synthetic
+from llambda_amd.hip_backend import HipBackendError
+from llambda_amd.moe import (NEMOTRON_H, QWEN3NEXT, HipMoeSession, select_top_k,
+                             synthetic_nemotron_h, synthetic_qwen3next)
+
+from helpers import REL
+
+pytestmark = pytest.mark.gpu
+
+THREADS = min(16, os.cpu_count() or 1)
+
+
+def _dq(pair, rows, columns, first_row=0):
+    t, data = pair
+    rb = ggml.row_bytes(t, columns)
+    chunk = data[first_row * rb:(first_row + rows) * rb]
+    return oracle.dequantize(t, chunk, rows * columns).reshape(rows, columns).astype(np.float64)
+
+
+def _silu(v):
+    return v / (1.0 + np.exp(-v))
+
+
+def output_bounds(layer, x, idx, w, shared_w):
+    """S_i per token (see module docstring), float64."""
+    H, F, Fs = layer.hidden, layer.expert_ffn, layer.shared_ffn
+    S = np.zeros((x.shape[0], H))
+    x64 = x.astype(np.float64)
+    by_expert = {}
+    for t in range(x.shape[0]):
+        for r in range(layer.top_k):
+            by_expert.setdefault(int(idx[t, r]), []).append((t, r))
+    for e, pairs in by_expert.items():
+        ts = np.array([p[0] for p in pairs])
+        ws = np.array([w[p] for p in pairs], dtype=np.float64)
+        up = _dq(layer.up, F, H, e * F) @ x64[ts].T
+        if layer.variant == QWEN3NEXT:
+            g = _dq(layer.gate, F, H, e * F) @ x64[ts].T
+            h = _silu(g) * up
+        else:
+            h = np.maximum(up, 0.0) ** 2
+        S[ts] += np.abs(ws)[:, None] * (np.abs(_dq(layer.down, H, F, e * H)) @ np.abs(h)).T
+    if Fs:
+        up = _dq(layer.shared_up, Fs, H) @ x64.T
+        if layer.variant == QWEN3NEXT:
+            h = _silu(_dq(layer.shared_gate, Fs, H) @ x64.T) * up
+        else:
+            h = np.maximum(up, 0.0) ** 2
+        S += np.abs(shared_w)[:, None] * (np.abs(_dq(layer.shared_down, H, Fs)) @ np.abs(h)).T
+    return S
+
+
+def router_bound(layer, x):
+    """K * 2^-24 * sum_i |w_i x_i| per token: a bound on the serial fp32 router
+    sum's deviation from the exact dot (plus the GPU's own, same order)."""
+    a = np.abs(layer.router.astype(np.float64)) @ np.abs(x.astype(np.float64)).T
+    return (layer.hidden * 2.0 ** -24) * a.max(axis=0)
+
+
+def check_layer(layer, x, label):
+    print(f"moe {label} tokens={x.shape[0]}", flush=True)
+    session = HipMoeSession(layer)
+    try:
+        y, idx, w, logits = session.run(x, with_routing=True)
+    finally:
+        session.close()
+    ref = oracle.moe_forward(layer, x, threads=THREADS)
+    k = layer.top_k
+    # routing
+    rb = router_bound(layer, x)
+    margins = []
+    for t in range(x.shape[0]):
+        row = ref.router_logits[t]
+        order = np.argsort(-row, kind="stable")[:k + 1]
+        top = row[order]
+        gap_k = top[k - 1] - top[k] if k < row.size else np.inf
+        if gap_k > 2 * rb[t]:
+            assert set(idx[t]) == set(ref.top_indices[t]), f"{label} token {t}: expert set differs"
+        if np.all(-np.diff(top) > 2 * rb[t]):
+            assert np.array_equal(idx[t], ref.top_indices[t]), f"{label} token {t}: order differs"
+        margins.append(gap_k / max(rb[t], 1e-30))
+    # outputs, against the oracle's routing
+    shared_w = np.ones(x.shape[0])
+    if layer.variant == QWEN3NEXT and layer.shared_ffn:
+        shared_w = np.array([oracle.sigmoid(float(oracle.dot_product(layer.shared_gate_inp, xt)))
+                             for xt in x], dtype=np.float64)
+    S = output_bounds(layer, x, ref.top_indices, ref.top_weights, shared_w)
+    same = np.array([np.array_equal(idx[t], ref.top_indices[t]) for t in range(x.shape[0])])
+    err = np.abs(y.astype(np.float64) - ref.y.astype(np.float64))
+    bad = (err > REL * S) & same[:, None]
+    assert not bad.any(), (f"{label}: {int(bad.sum())} outputs exceed 1e-4*S "
+                           f"(max ratio {np.max(err[same] / np.maximum(S[same], 1e-300)):.3e})")
+    assert same.mean() > 0.9, f"{label}: routing matched on only {same.mean():.2%} of tokens"
+    # weights of identically routed tokens agree to fp32 rounding
+    np.testing.assert_allclose(w[same], ref.top_weights[same], rtol=1e-6, atol=1e-7)
+    return y, idx
+
+
+@pytest.mark.parametrize("seed", [1, 2, 3])
+def test_qwen3next_decode(hip, seed):
+    rng = np.random.default_rng(seed)
+    layer = synthetic_qwen3next(rng)
+    x = synthetic.activations(rng, 1, layer.hidden)
+    check_layer(layer, x, f"qwen3next seed={seed}")
+
+
+def test_qwen3next_prefill_256(hip):
+    rng = np.random.default_rng(100)
+    layer = synthetic_qwen3next(rng)
+    x = synthetic.activations(rng, 256, layer.hidden)
+    y, idx = check_layer(layer, x, "qwen3next prefill")
+    # batch invariance: every token of the batch equals its own decode run
+    session = HipMoeSession(layer)
+    try:
+        for t in range(0, 256, 37):
+            y1 = session.run(x[t:t + 1])
+            np.testing.assert_array_equal(y1[0], y[t])
+    finally:
+        session.close()
+
+
+def test_nemotron_h_decode_and_batch(hip):
+    rng = np.random.default_rng(7)
+    layer = synthetic_nemotron_h(rng)
+    x = synthetic.activations(rng, 48, layer.hidden)
+    check_layer(layer, x, "nemotron")
+    y1, _ = check_layer(layer, x[:1], "nemotron decode")
+
+
+def test_nemotron_h_1024_batch_invariance(hip):
+    rng = np.random.default_rng(8)
+    layer = synthetic_nemotron_h(rng)
+    x = synthetic.activations(rng, 1024, layer.hidden)
+    session = HipMoeSession(layer)
+    try:
+        y, idx, w, logits = session.run(x, with_routing=True)
+        assert np.isfinite(y).all()
+        # expert load is skewed by the Zipf bias
+        counts = np.bincount(idx.reshape(-1), minlength=layer.expert_count)
+        assert counts.max() > 4 * counts.mean()
+        for t0 in (0, 511, 1000):
+            yc = session.run(x[t0:t0 + 24])
+            np.testing.assert_array_equal(yc, y[t0:t0 + 24])
+    finally:
+        session.close()
+
+
+def test_small_qwen_shapes(hip):
+    rng = np.random.default_rng(9)
+    layer = synthetic_qwen3next(rng, hidden=256, experts=20, top_k=3, ffn=64, shared_ffn=32,
+                                gate_type=ggml.Q8_0, down_type=ggml.Q5_0)
+    x = synthetic.activations(rng, 13, layer.hidden)
+    check_layer(layer, x, "qwen small")
+
+
+def test_nemotron_unnormalised_scaled(hip):
+    rng = np.random.default_rng(10)
+    layer = synthetic_nemotron_h(rng, hidden=512, experts=64, top_k=4, ffn=256, shared_ffn=0,
+                                 expert_type=ggml.Q4_K, down_type=ggml.Q6_K, weights_scale=2.5,
+                                 weights_norm=False)
+    x = synthetic.activations(rng, 9, layer.hidden)
+    check_layer(layer, x, "nemotron no-norm")
+
+
+def test_nan_input_reports_reference_error(hip):
+    rng = np.random.default_rng(11)
+    layer = synthetic_qwen3next(rng, hidden=256, experts=16, top_k=2, ffn=64, shared_ffn=64)
+    x = np.full((1, 256), np.nan, dtype=np.float32)
+    session = HipMoeSession(layer)
+    try:
+        with pytest.raises(HipBackendError, match="router"):
+            session.run(x)
+        # the session stays usable after the error
+        good = synthetic.activations(rng, 2, 256)
+        assert np.isfinite(session.run(good)).all()
+    finally:
+        session.close()
+
+
+def _ref_topk(row, k):
+    idx, val = oracle.select_top_k(row, k)
+    return idx, val
+
+
+@pytest.mark.parametrize("n,k", [(512, 10), (128, 6), (1, 1), (1000, 64), (65, 7)])
+def test_select_top_k_random(hip, n, k):
+    rng = np.random.default_rng(n * 100 + k)
+    logits = rng.normal(size=(33, n)).astype(np.float32)
+    # ties and specials
+    logits[1, :] = 0.0
+    logits[2, ::3] = np.nan
+    logits[3, : n // 2] = -np.inf
+    logits[4, :] = np.float32(-3.4028235e38)
+    logits[5, ::2] = -0.0
+    logits[6] = np.round(logits[6])
+    idx, val = select_top_k(logits, k)
+    for t in range(logits.shape[0]):
+        ri, rv = _ref_topk(logits[t], k)
+        assert np.array_equal(idx[t], ri), t
+        assert np.array_equal(val[t].view(np.uint32), rv.view(np.uint32)), t
