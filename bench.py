@@ -44,15 +44,18 @@ def _torch():
 
 
 class Timer:
-    """HIP events on the stream the kernels are launched on."""
+    """HIP events on the stream the kernels are launched on: a dedicated
+    (default-priority) stream, passed to the library by handle."""
 
     def __init__(self, torch):
         self.torch = torch
-        self.stream = torch.cuda.current_stream()
+        self.stream = torch.cuda.Stream()
         self.handle = self.stream.cuda_stream
+        assert self.handle, "a dedicated stream has a non-null handle"
 
     def time(self, fn, steps: int, warmup: int) -> float:
         torch = self.torch
+        torch.cuda.synchronize()
         for _ in range(warmup):
             fn()
         torch.cuda.synchronize()
@@ -164,7 +167,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--only", choices=["head", "q4k", "moe", "none"], default=None,
+    ap.add_argument("--only", choices=["head", "q4k", "moe", "copy", "none"], default=None,
                     help="run one workload group only (profiling)")
     ap.add_argument("--cpu-seconds", type=float, default=8.0,
                     help="bound on each CPU-baseline sample (0 disables)")
@@ -250,6 +253,19 @@ def main():
                  "GB/s": round(nbytes / (ms * 1e-3) / 1e9, 1)}
         workloads.append(entry)
         log(f"nemotron B=1024: {ms:.3f} ms, {entry['tokens_per_s']} tok/s")
+
+    if args.only == "copy":
+        # a plain device copy of known size: the HBM reference and the
+        # calibration of the FETCH_SIZE / WRITE_SIZE counters
+        n = 1 << 28  # floats (1 GiB)
+        a = torch.empty(n, device="cuda", dtype=torch.float32).fill_(1.0)
+        b = torch.empty_like(a)
+        with torch.cuda.stream(timer.stream):
+            ms = timer.time(lambda: b.copy_(a), max(5, steps // 20), 2)
+        gbs = 2 * 4 * n / (ms * 1e-3) / 1e9
+        workloads.append({"workload": "device copy 1 GiB -> 1 GiB (torch)", "ms_per_step": round(ms, 4),
+                          "GB/s (read+write)": round(gbs, 1)})
+        log(f"copy 1 GiB: {ms:.3f} ms, {gbs:.0f} GB/s read+write")
 
     if line is None:
         line = {"metric": METRIC, "value": None, "unit": "GB/s", "n_gpus": 1, "steps": steps,

@@ -73,6 +73,41 @@ __device__ __forceinline__ float ubyte(uint32_t v, int k) {
   return (float)((v >> (8 * k)) & 0xFFu);
 }
 
+// Hides a value's provenance from the optimiser.  Used on nibble masks such
+// as (v >> 4) & 0x0F0F0F0F so that their bytes convert with
+// v_cvt_f32_ubyte0..3 (one instruction per weight) instead of being folded
+// into a v_bfe_u32 per weight.
+__device__ __forceinline__ uint32_t opaque(uint32_t v) {
+  asm("" : "+v"(v));
+  return v;
+}
+
+// DPP lane permutations within rows of 16 lanes (gfx9 encodings).
+template <int CTRL>
+__device__ __forceinline__ float dpp(float v) {
+  return __builtin_bit_cast(
+      float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
+}
+constexpr int kDppXor1 = 0xB1;         // quad_perm [1,0,3,2]
+constexpr int kDppXor2 = 0x4E;         // quad_perm [2,3,0,1]
+constexpr int kDppHalfMirror = 0x141;  // lane i <- 7-i within 8
+constexpr int kDppMirror = 0x140;      // lane i <- 15-i within 16
+
+// Sum over aligned groups of 2^log2w lanes; every lane of a group receives
+// its group's sum.
+__device__ __forceinline__ float group_sum(float v, int log2w) {
+  if (log2w >= 1) v += dpp<kDppXor1>(v);
+  if (log2w >= 2) v += dpp<kDppXor2>(v);
+  if (log2w >= 3) v += dpp<kDppHalfMirror>(v);
+  if (log2w >= 4) v += dpp<kDppMirror>(v);
+  if (log2w >= 5) {
+    // xor 16 within groups of 32 lanes (ds_swizzle bit mode: and 0x1F, xor 0x10)
+    v += __builtin_bit_cast(float, __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, v), 0x401F));
+  }
+  if (log2w >= 6) v += __shfl_xor(v, 32, 64);
+  return v;
+}
+
 // Sum across `width` consecutive lanes (width a power of two <= 64).
 template <int WIDTH>
 __device__ __forceinline__ float segment_sum(float v) {

@@ -12,6 +12,7 @@
 // lanes are summed with cross-lane shuffles.  R rows per slot are loaded
 // before the first multiply so each lane keeps 2R 16-byte loads in flight.
 #include "gemv.h"
+#include "positions.h"
 
 #include <algorithm>
 
@@ -59,6 +60,96 @@ gemv_kernel(const uint8_t* __restrict__ w, int64_t row_bytes, int rows, int K,
         const float v = segment_sum_dyn(acc[r][t], lpr);
         if (l == 0 && row < rows && t < ntok) y[t * y_stride + row] = v;
       }
+    }
+  }
+}
+
+// ------------------------------------------------------------------------
+// Batch-1 row-streaming GEMV: every lane owns one 64-weight position of K
+// (positions.h) with its activations in registers, and streams rows.
+//   positions P = K/64 <= 64: a wavefront covers a row with L = pow2ceil(P)
+//     lanes, 64/L rows side by side; four independent wavefronts per block.
+//   P > 64: K is split over `kwaves` wavefronts of one block (<= 64
+//     positions each); their row sums meet in LDS.
+// R rows are loaded per lane before the first multiply.
+constexpr int kRowsMaxWaves = 8;
+
+template <int TYPE, int R>
+__global__ void __launch_bounds__(512)
+gemv_rows_kernel(const uint8_t* __restrict__ w, int64_t row_bytes, int rows, int positions,
+                 const float* __restrict__ x, float* __restrict__ y, int lanes_log2, int kwaves) {
+  using P = Pos<TYPE>;
+  __shared__ float partial[kRowsMaxWaves][R];
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int L = 1 << lanes_log2;
+  const int slot = lane >> lanes_log2;
+  const int l = lane & (L - 1);
+  const int slots = kWave >> lanes_log2;
+  int pos, rows_per_iter, base, stride;
+  if (kwaves == 1) {
+    pos = l;
+    rows_per_iter = slots * R;
+    const int waves_per_block = blockDim.x >> 6;
+    base = (blockIdx.x * waves_per_block + wave) * rows_per_iter;
+    stride = gridDim.x * waves_per_block * rows_per_iter;
+  } else {
+    const int per_wave = (positions + kwaves - 1) / kwaves;
+    pos = wave * per_wave + l;
+    if (l >= per_wave) pos = positions;  // idle lane
+    rows_per_iter = R;
+    base = blockIdx.x * R;
+    stride = gridDim.x * R;
+  }
+  const bool active = pos < positions;
+  float xr[64];
+  float g[P::kGroups];
+  if (active) {
+#pragma unroll
+    for (int e = 0; e < 64; e += 4) {
+      const float4 v = *reinterpret_cast<const float4*>(x + P::x_index(pos, e));
+      xr[e] = v.x; xr[e + 1] = v.y; xr[e + 2] = v.z; xr[e + 3] = v.w;
+    }
+  } else {
+#pragma unroll
+    for (int e = 0; e < 64; ++e) xr[e] = 0.f;
+  }
+  P::group_sums(xr, g);
+
+  for (; base < rows; base += stride) {
+    typename P::Raw raw[R];
+    bool ok[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const int row = base + (kwaves == 1 ? r * slots + slot : r);
+      ok[r] = active && row < rows;
+      if (ok[r]) raw[r] = P::load(w + (int64_t)row * row_bytes, pos);
+    }
+    float acc[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) acc[r] = ok[r] ? P::dot(raw[r], pos, xr, g) : 0.f;
+#pragma unroll
+    for (int r = 0; r < R; ++r) acc[r] = group_sum(acc[r], lanes_log2);
+    if (kwaves == 1) {
+      if (l == 0) {
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+          const int row = base + r * slots + slot;
+          if (row < rows) y[row] = acc[r];
+        }
+      }
+    } else {
+      if (lane == 0) {
+#pragma unroll
+        for (int r = 0; r < R; ++r) partial[wave][r] = acc[r];
+      }
+      __syncthreads();
+      if (threadIdx.x < R && base + (int)threadIdx.x < rows) {
+        float v = 0.f;
+        for (int q = 0; q < kwaves; ++q) v += partial[q][threadIdx.x];
+        y[base + threadIdx.x] = v;
+      }
+      __syncthreads();
     }
   }
 }
@@ -266,7 +357,46 @@ static hipError_t launch_nt(const GemvProblem& p, hipStream_t stream) {
   }
 }
 
+template <int TYPE, int R>
+static hipError_t launch_rows(const GemvProblem& p, hipStream_t stream) {
+  const int positions = (int)(p.columns / 64);
+  int lanes_log2 = 0, kwaves = 1;
+  if (positions <= 64) {
+    while ((1 << lanes_log2) < positions) ++lanes_log2;
+  } else {
+    lanes_log2 = 6;
+    kwaves = (positions + 63) / 64;
+  }
+  const int block = kwaves == 1 ? 256 : 64 * kwaves;
+  const auto kernel = gemv_rows_kernel<TYPE, R>;
+  int per_cu = 0;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, reinterpret_cast<const void*>(kernel),
+                                                   block, 0) != hipSuccess || per_cu < 1)
+    per_cu = 1;
+  const int rows_per_block = kwaves == 1 ? (block / 64) * (kWave >> lanes_log2) * R : R;
+  const int needed = (int)((p.rows + rows_per_block - 1) / rows_per_block);
+  const int grid = std::max(1, std::min(needed, device_cu_count() * per_cu));
+  hipLaunchKernelGGL(kernel, dim3(grid), dim3(block), 0, stream, p.weights, p.row_bytes,
+                     (int)p.rows, positions, p.x, p.y, lanes_log2, kwaves);
+  return hipGetLastError();
+}
+
+// The row-streaming kernel serves one token when K is a multiple of 64.
+static bool rows_path(const GemvProblem& p) {
+  return p.tokens == 1 && p.type != kF32 && p.columns % 64 == 0 &&
+         p.columns / 64 <= 64 * kRowsMaxWaves;
+}
+
 hipError_t gemv_launch(const GemvProblem& p, hipStream_t stream) {
+  if (rows_path(p)) {
+    switch (p.type) {
+      case kQ4_K: return launch_rows<kQ4_K, 4>(p, stream);
+      case kQ6_K: return launch_rows<kQ6_K, 4>(p, stream);
+      case kQ5_0: return launch_rows<kQ5_0, 2>(p, stream);
+      case kQ8_0: return launch_rows<kQ8_0, 2>(p, stream);
+      default: break;
+    }
+  }
   // Tokens are processed up to NT at a time (each chunk re-reads the
   // weights); NT is capped so the staged activations fit in LDS.
   const size_t per_token = p.type == kF32 ? (size_t)p.columns * sizeof(float)

@@ -83,8 +83,8 @@ struct Unit<kQ4_K> {
     const uint32_t qw[4] = {r.q.x, r.q.y, r.q.z, r.q.w};
 #pragma unroll
     for (int w = 0; w < 4; ++w) {
-      uint32_t lo = qw[w] & 0x0F0F0F0Fu;
-      uint32_t hi = (qw[w] >> 4) & 0x0F0F0F0Fu;
+      uint32_t lo = opaque(qw[w] & 0x0F0F0F0Fu);
+      uint32_t hi = opaque((qw[w] >> 4) & 0x0F0F0F0Fu);
 #pragma unroll
       for (int k = 0; k < 4; ++k) {
         wl[4 * w + k] = ubyte(lo, k);

@@ -408,14 +408,15 @@ typedef struct pool {
   pthread_cond_t start, done;
   pthread_t* threads;
   int size;                /* worker threads (the caller is one more part) */
+  int ready;               /* workers that have registered their generation */
   unsigned long generation;
-  int pending;
+  int pending;             /* workers still inside the current job */
   int next_part;
   gemv_job* job;
 } pool;
 
 static pool g_pool = {PTHREAD_MUTEX_INITIALIZER, PTHREAD_COND_INITIALIZER,
-                      PTHREAD_COND_INITIALIZER, NULL, 0, 0, 0, 0, NULL};
+                      PTHREAD_COND_INITIALIZER, NULL, 0, 0, 0, 0, 0, NULL};
 static pthread_mutex_t g_pool_use = PTHREAD_MUTEX_INITIALIZER;
 
 /* lparallel:pdotimes over `parts` contiguous chunks of [0, rows). */
@@ -450,7 +451,13 @@ static void drain_parts(pool* p, gemv_job* job) {
 
 static void* worker_main(void* arg) {
   pool* p = (pool*)arg;
-  unsigned long seen = 0;
+  /* a new worker joins at the current generation, so it never runs a job
+   * dispatched before it existed */
+  pthread_mutex_lock(&p->lock);
+  unsigned long seen = p->generation;
+  p->ready++;
+  pthread_cond_broadcast(&p->done);
+  pthread_mutex_unlock(&p->lock);
   for (;;) {
     pthread_mutex_lock(&p->lock);
     while (p->generation == seen) pthread_cond_wait(&p->start, &p->lock);
@@ -476,6 +483,9 @@ static void ensure_pool(int threads) {
     pthread_detach(g_pool.threads[i]);
   }
   g_pool.size = want;
+  pthread_mutex_lock(&g_pool.lock);
+  while (g_pool.ready < g_pool.size) pthread_cond_wait(&g_pool.done, &g_pool.lock);
+  pthread_mutex_unlock(&g_pool.lock);
 }
 
 int oracle_gemv(int type, const uint8_t* matrix, int64_t rows, int64_t columns,
@@ -500,7 +510,7 @@ int oracle_gemv(int type, const uint8_t* matrix, int64_t rows, int64_t columns,
     pthread_mutex_lock(&g_pool.lock);
     g_pool.job = &job;
     g_pool.next_part = 0;
-    g_pool.pending = threads - 1;
+    g_pool.pending = g_pool.size; /* every worker acknowledges every job */
     g_pool.generation++;
     pthread_cond_broadcast(&g_pool.start);
     pthread_mutex_unlock(&g_pool.lock);

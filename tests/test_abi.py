@@ -1,0 +1,98 @@
+"""The C ABI library loads and exports every symbol include/llambda_hip.h
+declares; host-only entry points behave without a GPU (no compute calls)."""
+import ctypes
+import hashlib
+import os
+import re
+
+import numpy as np
+import pytest
+
+from llambda_amd import native
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "llambda_hip.h")
+
+
+def declared_functions():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(llambda_hip_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_header_lists_the_bound_functions():
+    assert declared_functions() == sorted(native.SIGNATURES)
+
+
+def test_library_exports_every_declared_symbol():
+    lib = ctypes.CDLL(native.library_path())
+    missing = [n for n in declared_functions() if not hasattr(lib, n)]
+    assert not missing, missing
+
+
+def test_versions_and_probe():
+    L = native.lib()
+    assert L.llambda_hip_bridge_version().startswith(b"llambda-hip")
+    assert b"HIP runtime" in L.llambda_hip_runtime_version()
+    assert L.llambda_hip_probe() in (0, 1)
+
+
+@pytest.mark.parametrize("n", [0, 1, 55, 56, 63, 64, 65, 1000, 4096 + 17])
+def test_sha256_matches_hashlib(n):
+    data = bytes((i * 7 + 3) & 255 for i in range(n))
+    buf = np.frombuffer(data, dtype=np.uint8) if n else np.zeros(1, dtype=np.uint8)
+    out = ctypes.create_string_buffer(65)
+    assert native.lib().llambda_hip_sha256(buf.ctypes.data, n, out, 65) == 0
+    assert out.value.decode() == hashlib.sha256(data).hexdigest()
+
+
+def test_sha256_rejects_short_output():
+    out = ctypes.create_string_buffer(64)
+    assert native.lib().llambda_hip_sha256(None, 0, out, 64) == -1
+    assert "65" in native.last_error()
+
+
+def test_null_arguments_fail_with_last_error():
+    L = native.lib()
+    assert L.llambda_hip_session_run(None, None, 0, None, 0) == -1
+    assert "null session" in native.last_error()
+    assert L.llambda_hip_session_input_element_count(None) == 0
+    assert L.llambda_hip_session_output_element_count(None) == 0
+    assert L.llambda_hip_moe_session_hidden_size(None) == 0
+    L.llambda_hip_session_destroy(None)
+    L.llambda_hip_moe_session_destroy(None)
+    assert L.llambda_hip_session_create(None, None, None, None) == -1
+    assert "null result" in native.last_error()
+    # the error is cleared by the next successful call
+    out = ctypes.create_string_buffer(65)
+    assert L.llambda_hip_sha256(None, 0, out, 65) == 0
+    assert native.last_error() == ""
+
+
+def test_session_create_rejects_bad_files(tmp_path):
+    L = native.lib()
+    handle = ctypes.c_void_p()
+    p = tmp_path / "junk.bin"
+    p.write_bytes(b"not a projection at all, definitely longer than forty bytes")
+    assert L.llambda_hip_session_create(str(p).encode(), None, None, ctypes.byref(handle)) == -1
+    assert "bad magic" in native.last_error()
+    assert handle.value is None
+    assert L.llambda_hip_session_create(str(tmp_path / "absent").encode(), None, None,
+                                        ctypes.byref(handle)) == -1
+    assert "cannot open" in native.last_error()
+
+
+def test_packed_create_validates_geometry():
+    L = native.lib()
+    handle = ctypes.c_void_p()
+    buf = np.zeros(144 * 3, dtype=np.uint8)
+    # 2688 columns is not a Q4_K block multiple (ggml-tensor-byte-size)
+    assert L.llambda_hip_session_create_packed(buf.ctypes.data, buf.size, 12, 1, 2688,
+                                               ctypes.byref(handle)) == -1
+    assert "not a multiple of block size 256" in native.last_error()
+    assert L.llambda_hip_session_create_packed(buf.ctypes.data, buf.size, 12, 2, 256,
+                                               ctypes.byref(handle)) == -1
+    assert "do not hold" in native.last_error()
+    assert L.llambda_hip_session_create_packed(buf.ctypes.data, buf.size, 99, 3, 256,
+                                               ctypes.byref(handle)) == -1
+    assert "unsupported GGML tensor type" in native.last_error()

@@ -108,8 +108,12 @@ def check_layer(layer, x, label):
     assert not bad.any(), (f"{label}: {int(bad.sum())} outputs exceed 1e-4*S "
                            f"(max ratio {np.max(err[same] / np.maximum(S[same], 1e-300)):.3e})")
     assert same.mean() > 0.9, f"{label}: routing matched on only {same.mean():.2%} of tokens"
-    # weights of identically routed tokens agree to fp32 rounding
-    np.testing.assert_allclose(w[same], ref.top_weights[same], rtol=1e-6, atol=1e-7)
+    # gating weights of identically routed tokens agree up to the router
+    # logits' rounding (|d sigmoid / dl| <= 1/4 and the renormalisation keeps
+    # the scale): |dw| <= 1e-6 |w| + router bound
+    dw = np.abs(w.astype(np.float64) - ref.top_weights)
+    ok = dw <= 1e-6 * np.abs(ref.top_weights) + rb[:, None]
+    assert np.all(ok[same]), f"{label}: gating weights differ beyond the router bound"
     return y, idx
 
 
@@ -181,7 +185,8 @@ def test_nemotron_unnormalised_scaled(hip):
 
 def test_nan_input_reports_reference_error(hip):
     rng = np.random.default_rng(11)
-    layer = synthetic_qwen3next(rng, hidden=256, experts=16, top_k=2, ffn=64, shared_ffn=64)
+    layer = synthetic_qwen3next(rng, hidden=256, experts=16, top_k=2, ffn=64, shared_ffn=64,
+                                down_type=ggml.Q8_0)
     x = np.full((1, 256), np.nan, dtype=np.float32)
     session = HipMoeSession(layer)
     try:
