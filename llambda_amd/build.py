@@ -41,15 +41,17 @@ def _run(cmd):
     return out
 
 
-def build(verbose: bool = False) -> str:
-    """Compile every source and link the library; returns its path."""
-    os.makedirs(OBJ, exist_ok=True)
+def build(verbose: bool = False, defines=(), obj_dir: str = OBJ, lib_path: str = LIB) -> str:
+    """Compile every source and link the library; returns its path.
+    ``defines`` are extra -D tuning constants (see gemv.hip)."""
+    os.makedirs(obj_dir, exist_ok=True)
     jobs = []
     for src in HIP_SOURCES:
-        obj = os.path.join(OBJ, src + ".o")
-        jobs.append([HIPCC, *HIP_FLAGS, "-c", os.path.join(CSRC, src), "-o", obj])
+        obj = os.path.join(obj_dir, src + ".o")
+        jobs.append([HIPCC, *HIP_FLAGS, *[f"-D{d}" for d in defines], "-c",
+                     os.path.join(CSRC, src), "-o", obj])
     for src in CXX_SOURCES:
-        obj = os.path.join(OBJ, src + ".o")
+        obj = os.path.join(obj_dir, src + ".o")
         jobs.append(["g++", *CXX_FLAGS, "-c", os.path.join(CSRC, src), "-o", obj])
     with ThreadPoolExecutor(max_workers=min(4, len(jobs))) as pool:
         outs = list(pool.map(_run, jobs))
@@ -57,11 +59,11 @@ def build(verbose: bool = False) -> str:
         for o in outs:
             if o:
                 print(o)
-    objs = [os.path.join(OBJ, s + ".o") for s in HIP_SOURCES + CXX_SOURCES]
-    tmp = LIB + ".tmp"
+    objs = [os.path.join(obj_dir, s + ".o") for s in HIP_SOURCES + CXX_SOURCES]
+    tmp = lib_path + ".tmp"
     _run([HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp, *objs])
-    shutil.move(tmp, LIB)
-    return LIB
+    shutil.move(tmp, lib_path)
+    return lib_path
 
 
 if __name__ == "__main__":

@@ -74,6 +74,14 @@ gemv_kernel(const uint8_t* __restrict__ w, int64_t row_bytes, int rows, int K,
 // R rows are loaded per lane before the first multiply.
 constexpr int kRowsMaxWaves = 8;
 
+// Rows loaded per lane before the first multiply (compile-time tuning).
+#ifndef LLHIP_ROWS_Q4K
+#define LLHIP_ROWS_Q4K 2
+#endif
+#ifndef LLHIP_ROWS_Q6K
+#define LLHIP_ROWS_Q6K 1
+#endif
+
 template <int TYPE, int R>
 __global__ void __launch_bounds__(512)
 gemv_rows_kernel(const uint8_t* __restrict__ w, int64_t row_bytes, int rows, int positions,
@@ -390,8 +398,8 @@ static bool rows_path(const GemvProblem& p) {
 hipError_t gemv_launch(const GemvProblem& p, hipStream_t stream) {
   if (rows_path(p)) {
     switch (p.type) {
-      case kQ4_K: return launch_rows<kQ4_K, 4>(p, stream);
-      case kQ6_K: return launch_rows<kQ6_K, 4>(p, stream);
+      case kQ4_K: return launch_rows<kQ4_K, LLHIP_ROWS_Q4K>(p, stream);
+      case kQ6_K: return launch_rows<kQ6_K, LLHIP_ROWS_Q6K>(p, stream);
       case kQ5_0: return launch_rows<kQ5_0, 2>(p, stream);
       case kQ8_0: return launch_rows<kQ8_0, 2>(p, stream);
       default: break;

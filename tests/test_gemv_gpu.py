@@ -107,7 +107,9 @@ def test_fp16_special_rejected(hip, type_tag):
         make_hip_session_packed(w, type_tag, rows, columns)
 
 
-def test_batch_matches_single(hip):
+def test_batch_matches_oracle(hip):
+    """Every row of a multi-token run meets the bound against the oracle
+    (batch runs use the token-tiled kernel, single runs the row-streaming one)."""
     rows, columns = 515, 2048
     rng = np.random.default_rng(3)
     for type_tag in (ggml.Q4_K, ggml.Q6_K, ggml.Q8_0):
@@ -119,9 +121,9 @@ def test_batch_matches_single(hip):
                 yb = np.empty((batch, rows), dtype=np.float32)
                 s.run_batch_into(yb, x, batch)
                 for t in range(batch):
-                    y1 = np.empty(rows, dtype=np.float32)
-                    s.run_into(y1, x[t])
-                    assert np.array_equal(yb[t], y1), (type_tag, batch, t)
+                    y_ref = oracle.gemv(type_tag, w, rows, columns, x[t])
+                    bound = abs_dot_bound(type_tag, w, rows, columns, x[t])
+                    assert_within_bound(yb[t], y_ref, bound, f"batch {batch} token {t}")
         finally:
             s.close()
 
