@@ -30,6 +30,10 @@ constexpr int64_t kMaxColumns = 32768;
 
 hipError_t gemv_launch(const GemvProblem& p, hipStream_t stream);
 
+// Batch-1 Q4_K / Q6_K GEMV on MFMA (gemv_mfma.hip).
+bool gemv_mfma_supported(const GemvProblem& p);
+hipError_t gemv_mfma_launch(const GemvProblem& p, hipStream_t stream);
+
 // Compute units of the current device (cached after the first call).
 int device_cu_count();
 

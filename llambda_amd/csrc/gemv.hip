@@ -395,7 +395,12 @@ static bool rows_path(const GemvProblem& p) {
          p.columns / 64 <= 64 * kRowsMaxWaves;
 }
 
+#ifndef LLHIP_GEMV_MFMA
+#define LLHIP_GEMV_MFMA 1
+#endif
+
 hipError_t gemv_launch(const GemvProblem& p, hipStream_t stream) {
+  if (LLHIP_GEMV_MFMA && gemv_mfma_supported(p)) return gemv_mfma_launch(p, stream);
   if (rows_path(p)) {
     switch (p.type) {
       case kQ4_K: return launch_rows<kQ4_K, LLHIP_ROWS_Q4K>(p, stream);

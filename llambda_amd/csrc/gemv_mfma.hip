@@ -1,0 +1,523 @@
+// gemv_mfma.hip -- batch-1 Q4_K / Q6_K GEMV with the unpacked codes fed to
+// MFMA (v_mfma_f32_16x16x32_bf16), so the VALU only unpacks bits.
+//
+// One wavefront computes 16 rows of W (the MFMA's 16 B-columns) over all of
+// K.  For every super-block:
+//   B operand  lane (n, g) = (lane & 15, lane >> 4) holds 8 codes of row n as
+//              bf16 (128 + q): the code byte and a 0x43 filler byte are
+//              interleaved by one v_perm_b32, 0x43qq being exactly 128 + q.
+//   A operand  the activations, split x = x_hi + x_lo into two bf16 (each
+//              within 2^-9 of its remainder, so |x - x_hi - x_lo| <= 2^-18 |x|),
+//              arranged so that A row a carries scale group "slot" a >> 1 (hi
+//              for even a, lo for odd a) and zeros elsewhere.  Lanes whose A
+//              row has no data in an MFMA read a zero line.  The table is built
+//              once per workgroup in LDS.
+//   D          lane (n, G) then holds, for row n, the (hi, lo) sums of slots
+//              2G and 2G+1; it applies those groups' scale and offset once:
+//                sum_i (q_i - c) x_i = (D_hi + D_lo) - (128 + c) * sum_i x~_i
+//              with c the code offset (Q4_K: min/delta handled through dmin,
+//              Q6_K: 32) and sum x~ precomputed per group.
+//   Q4_K       slots = the 8 sub-blocks; 8 MFMAs per block, MFMA m takes
+//              elements 4m..4m+3 of sub-blocks 2g (low nibbles) and 2g+1
+//              (high nibbles) from lane g's 32 qs bytes [32g, 32g+32).
+//   Q6_K       per half h, slots = the 8 scale groups (k, half) of
+//              llambda.lisp:4203-4310; 4 MFMAs per half, MFMA m takes q_m of
+//              l = 8g .. 8g+7 from lane g's ql/qh bytes.
+// The row sums of the four G lanes meet by two cross-lane adds.
+#include "gemv.h"
+
+#include <algorithm>
+#include <utility>
+
+namespace llhip {
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+constexpr uint32_t kFiller = 0x43434343u;  // bf16 high byte of 128 + q
+constexpr uint32_t kSelLo = 0x04010400u;   // {b0, F, b1, F}
+constexpr uint32_t kSelHi = 0x04030402u;   // {b2, F, b3, F}
+
+__device__ __forceinline__ uint32_t bf16_bits_rne(float f) {
+  const uint32_t u = __builtin_bit_cast(uint32_t, f);
+  return (u + 0x7FFFu + ((u >> 16) & 1u)) >> 16;
+}
+
+// x = hi + lo with hi, lo bf16 (bits returned); hi + lo is returned in sum.
+__device__ __forceinline__ void split_bf16(float x, uint32_t& hi, uint32_t& lo, float& sum) {
+  hi = bf16_bits_rne(x);
+  const float fh = __builtin_bit_cast(float, hi << 16);
+  lo = bf16_bits_rne(x - fh);
+  sum = fh + __builtin_bit_cast(float, lo << 16);
+}
+
+// 8 codes (two dwords of code bytes) -> the B operand (4 VGPRs of bf16 pairs).
+__device__ __forceinline__ bf16x8 codes_to_b(uint32_t c0, uint32_t c1) {
+  u32x4 v;
+  v.x = __builtin_amdgcn_perm(kFiller, c0, kSelLo);
+  v.y = __builtin_amdgcn_perm(kFiller, c0, kSelHi);
+  v.z = __builtin_amdgcn_perm(kFiller, c1, kSelLo);
+  v.w = __builtin_amdgcn_perm(kFiller, c1, kSelHi);
+  return __builtin_bit_cast(bf16x8, v);
+}
+
+__device__ __forceinline__ floatx4 mfma(const bf16x8& a, const bf16x8& b, const floatx4& c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+
+// Sum over the four lanes n, n+16, n+32, n+48.
+__device__ __forceinline__ float sum_lane_groups(float v) {
+  v += __shfl_xor(v, 16, 64);
+  v += __shfl_xor(v, 32, 64);
+  return v;
+}
+
+// ------------------------------------------------------------ row staging
+// A wavefront streams its 16-row tile through LDS in chunks of C blocks per
+// row.  Piece j (16 bytes) of row r of the chunk is load lane (r * kPieces +
+// j): global_load_lds_dwordx4 writes lane i's 16 bytes to M0 + 16 i, so the
+// LDS image of a chunk is the rows' byte ranges back to back, kRow bytes
+// apart, with no VGPR staging.  Each row's range starts at the dword at or
+// below the chunk's first byte (row starts need only be 2-byte aligned) and
+// may run up to 18 bytes past the chunk (the allocation's pad covers the last
+// row).  Two buffers per wave: the next chunk loads while this one computes.
+typedef __attribute__((address_space(3))) void* lds_ptr_t;
+
+template <int BB, int C, bool ALIGNED>
+struct Chunk {
+  static constexpr int kSpan = C * BB;
+  static constexpr int kPieces = (kSpan + (ALIGNED ? 0 : 3) + 15) / 16;
+  static constexpr int kRow = 16 * kPieces;
+  static constexpr int kLoads = (16 * kPieces + 63) / 64;
+  static constexpr int kBuffer = 1024 * kLoads;  // per buffer; lanes past 16 rows write slack
+};
+
+__device__ __forceinline__ uint32_t lds_address(const void* p) {
+  return (uint32_t)(uintptr_t)(lds_ptr_t)(p);
+}
+
+// 64 lanes x 16 bytes from base + voff[lane] to LDS lds + 16 * lane.
+// base and lds are wavefront-uniform.
+__device__ __forceinline__ void load_lds16(const uint8_t* base, uint32_t voff, uint32_t lds) {
+  asm volatile(
+      "s_nop 0\n\t"
+      "global_load_lds_dwordx4 %0, %1"
+      :
+      : "v"(voff), "s"(base), "{m0}"(lds)
+      : "memory");
+}
+
+template <int N>
+__device__ __forceinline__ void wait_loads() {
+  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+
+__device__ __forceinline__ const uint8_t* uniform_ptr(const uint8_t* p) {
+  const uint64_t v = reinterpret_cast<uint64_t>(p);
+  const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v);
+  const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(v >> 32));
+  return reinterpret_cast<const uint8_t*>(((uint64_t)hi << 32) | lo);
+}
+
+// ------------------------------------------------------------------ Q4_K
+// LDS table per block: 8 MFMAs x 16 A rows x 16 B (only lane g = a >> 2
+// reads its row's entry; others read the zero line), then 8 group sums.
+constexpr int kQ4Table = 8 * 16 * 16;  // bytes per block
+constexpr int kQ6Table = 2 * 4 * 8 * 16;
+
+__device__ __forceinline__ void build_q4k_table(uint8_t* table, float* gsum, const float* x,
+                                                int nblk) {
+  // one thread per (block, sub-block, 4-element step)
+  for (int i = threadIdx.x; i < nblk * 64; i += blockDim.x) {
+    const int b = i >> 6, s = (i >> 3) & 7, m = i & 7;
+    const float* xp = x + b * 256 + 32 * s + 4 * m;
+    uint32_t hi[4], lo[4];
+    float part = 0.f;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      float sum;
+      split_bf16(xp[e], hi[e], lo[e], sum);
+      part += sum;
+    }
+    // rows a = 2s (hi) and 2s+1 (lo); the data sits in half (s & 1) of the 8 slots
+    const int half = s & 1;
+    u32x4 vh = {0u, 0u, 0u, 0u}, vl = {0u, 0u, 0u, 0u};
+    vh[2 * half] = hi[0] | (hi[1] << 16);
+    vh[2 * half + 1] = hi[2] | (hi[3] << 16);
+    vl[2 * half] = lo[0] | (lo[1] << 16);
+    vl[2 * half + 1] = lo[2] | (lo[3] << 16);
+    uint8_t* base = table + b * kQ4Table + m * 256;
+    *reinterpret_cast<u32x4*>(base + (2 * s) * 16) = vh;
+    *reinterpret_cast<u32x4*>(base + (2 * s + 1) * 16) = vl;
+    // group sum over the sub-block's 32 elements: 8 threads m = 0..7 share it
+    part += __shfl_xor(part, 1, 64);
+    part += __shfl_xor(part, 2, 64);
+    part += __shfl_xor(part, 4, 64);
+    if (m == 0) gsum[b * 8 + s] = part;
+  }
+}
+
+// One Q4_K block of lane (n, g)'s row, p = the block's 144 bytes in LDS
+// (16-byte aligned); a = the lane's A address for this block (0 when its A
+// row carries no data: LDS [0, 2 KB) is zero).
+__device__ __forceinline__ float q4k_block(const uint8_t* p, const uint8_t* lds, uint32_t a,
+                                           const float* gs, int g) {
+  const uint4 h = *reinterpret_cast<const uint4*>(p);
+  const uint4 c0 = *reinterpret_cast<const uint4*>(p + 16 + 32 * g);
+  const uint4 c1 = *reinterpret_cast<const uint4*>(p + 32 + 32 * g);
+  const uint32_t qw[8] = {c0.x, c0.y, c0.z, c0.w, c1.x, c1.y, c1.z, c1.w};
+  floatx4 d = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int m = 0; m < 8; ++m) {
+    const bf16x8 av = *reinterpret_cast<const bf16x8*>(lds + a + m * 256);
+    const uint32_t lo = opaque(qw[m] & 0x0F0F0F0Fu);
+    const uint32_t hi = opaque((qw[m] >> 4) & 0x0F0F0F0Fu);
+    d = mfma(av, codes_to_b(lo, hi), d);
+  }
+  // sub-blocks 2g (D rows 4g, 4g+1) and 2g+1 (4g+2, 4g+3); scale and min per
+  // get-scale-min-k4-at (llambda.lisp:4316-4336)
+  const int bsel = (2 * g) & 3;
+  const bool high = g >= 2;
+  const uint32_t B0a = (h.y >> (8 * bsel)) & 0xFFu, B0b = (h.y >> (8 * bsel + 8)) & 0xFFu;
+  const uint32_t B4a = (h.z >> (8 * bsel)) & 0xFFu, B4b = (h.z >> (8 * bsel + 8)) & 0xFFu;
+  const uint32_t B8a = (h.w >> (8 * bsel)) & 0xFFu, B8b = (h.w >> (8 * bsel + 8)) & 0xFFu;
+  const uint32_t sc0 = high ? ((B8a & 15u) | ((B0a >> 6) << 4)) : (B0a & 63u);
+  const uint32_t m0 = high ? ((B8a >> 4) | ((B4a >> 6) << 4)) : (B4a & 63u);
+  const uint32_t sc1 = high ? ((B8b & 15u) | ((B0b >> 6) << 4)) : (B0b & 63u);
+  const uint32_t m1 = high ? ((B8b >> 4) | ((B4b >> 6) << 4)) : (B4b & 63u);
+  const float dd = half_bits_to_float(h.x & 0xFFFFu);
+  const float dm = half_bits_to_float(h.x >> 16);
+  const float delta0 = dd * (float)sc0, delta1 = dd * (float)sc1;
+  const float off0 = fmaf(128.f, delta0, dm * (float)m0);
+  const float off1 = fmaf(128.f, delta1, dm * (float)m1);
+  const float2 gsv = *reinterpret_cast<const float2*>(gs + 2 * g);
+  float v = delta0 * (d[0] + d[1]);
+  v = fmaf(-off0, gsv.x, v);
+  v = fmaf(delta1, d[2] + d[3], v);
+  v = fmaf(-off1, gsv.y, v);
+  return v;
+}
+
+// ------------------------------------------------------------------ Q6_K
+// LDS table per block: 2 halves x 4 MFMAs x 8 entries x 16 B, then 16 group
+// sums.  Entry (a & 3) * 2 + (g & 1) of MFMA m serves A row a = 4m + (a & 3)
+// for lane g when (a >> 1) & 1 == g >> 1.
+__device__ __forceinline__ void build_q6k_table(uint8_t* table, float* gsum, const float* x,
+                                                int nblk) {
+  // one thread per (block, half, k, l-octet): 8 activations
+  for (int i = threadIdx.x; i < nblk * 32; i += blockDim.x) {
+    const int b = i >> 5, h = (i >> 4) & 1, k = (i >> 2) & 3, g = i & 3;
+    const float* xp = x + b * 256 + 128 * h + 32 * k + 8 * g;
+    uint32_t hi[8], lo[8];
+    float part = 0.f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      float sum;
+      split_bf16(xp[e], hi[e], lo[e], sum);
+      part += sum;
+    }
+    // slot = 2k + (g >> 1): A rows 4k + 2(g >> 1) (hi) and +1 (lo)
+    const int ahi = 2 * (g >> 1);
+    uint8_t* base = table + b * kQ6Table + (h * 4 + k) * 128;
+    const u32x4 vh = {hi[0] | (hi[1] << 16), hi[2] | (hi[3] << 16), hi[4] | (hi[5] << 16),
+                      hi[6] | (hi[7] << 16)};
+    const u32x4 vl = {lo[0] | (lo[1] << 16), lo[2] | (lo[3] << 16), lo[4] | (lo[5] << 16),
+                      lo[6] | (lo[7] << 16)};
+    *reinterpret_cast<u32x4*>(base + (ahi * 2 + (g & 1)) * 16) = vh;
+    *reinterpret_cast<u32x4*>(base + ((ahi + 1) * 2 + (g & 1)) * 16) = vl;
+    // group (h, k, half = g >> 1) sums 16 elements: threads g, g ^ 1
+    part += __shfl_xor(part, 1, 64);
+    if ((g & 1) == 0) gsum[b * 16 + h * 8 + 2 * k + (g >> 1)] = part;
+  }
+}
+
+// 8 bytes at byte offset o of the dword-aligned q (the block starts SH bytes
+// past q).
+template <int SH>
+__device__ __forceinline__ uint2 read8(const uint32_t* q, int o) {
+  if constexpr (SH == 0) {
+    return make_uint2(q[o / 4], q[o / 4 + 1]);
+  } else {
+    const uint32_t r0 = q[o / 4], r1 = q[o / 4 + 1], r2 = q[o / 4 + 2];
+    return make_uint2(__builtin_amdgcn_alignbyte(r1, r0, SH), __builtin_amdgcn_alignbyte(r2, r1, SH));
+  }
+}
+__device__ __forceinline__ uint2 read8(const uint32_t* q, int o, uint32_t sh) {
+  const uint32_t r0 = q[o / 4], r1 = q[o / 4 + 1], r2 = q[o / 4 + 2];
+  return make_uint2(__builtin_amdgcn_alignbyte(r1, r0, sh), __builtin_amdgcn_alignbyte(r2, r1, sh));
+}
+
+// One Q6_K block of lane (n, g)'s row: p = its 210 bytes in LDS (2-byte
+// aligned), SH = p & 3 when known at compile time (-1: read it from p).
+// am[m] = the lane's A address for MFMA m of the block (0: zero line).
+template <int SH>
+__device__ __forceinline__ float q6k_block(const uint8_t* p, const uint8_t* lds, const uint32_t am[4],
+                                           const float* gs, int g) {
+  const uint32_t sh = SH >= 0 ? (uint32_t)SH : (uint32_t)(reinterpret_cast<uintptr_t>(p) & 3u);
+  const uint32_t* q = reinterpret_cast<const uint32_t*>(p - sh);
+  const float dd = half_bits_to_float(*reinterpret_cast<const uint16_t*>(p + 208));
+  float v = 0.f;
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    uint2 la, lb, qh;
+    if constexpr (SH >= 0) {
+      la = read8<SH>(q, 64 * h + 8 * g);
+      lb = read8<SH>(q, 64 * h + 32 + 8 * g);
+      qh = read8<SH>(q, 128 + 32 * h + 8 * g);
+    } else {
+      la = read8(q, 64 * h + 8 * g + 0, sh);
+      lb = read8(q, 64 * h + 32 + 8 * g, sh);
+      qh = read8(q, 128 + 32 * h + 8 * g, sh);
+    }
+    floatx4 d = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int m = 0; m < 4; ++m) {
+      const uint2 l = (m & 1) ? lb : la;
+      const uint32_t l0 = (m & 2) ? (l.x >> 4) : l.x;
+      const uint32_t l1 = (m & 2) ? (l.y >> 4) : l.y;
+      const uint32_t h0 = (qh.x >> (2 * m)) & 0x03030303u;
+      const uint32_t h1 = (qh.y >> (2 * m)) & 0x03030303u;
+      const uint32_t c0 = opaque((l0 & 0x0F0F0F0Fu) | (h0 << 4));
+      const uint32_t c1 = opaque((l1 & 0x0F0F0F0Fu) | (h1 << 4));
+      const bf16x8 av = *reinterpret_cast<const bf16x8*>(lds + am[m] + h * 512 + m * 128);
+      d = mfma(av, codes_to_b(c0, c1), d);
+    }
+    // D rows 4g .. 4g+3 of column n: groups (k = g, l-half 0 / 1) of half h,
+    // i.e. scales sc[8h + 2g] and sc[8h + 2g + 1] (llambda.lisp:4203-4310)
+    const uint32_t sv = *reinterpret_cast<const uint16_t*>(p + 192 + 8 * h + 2 * g);
+    const float delta0 = dd * (float)(int)(int8_t)(sv & 0xFFu);
+    const float delta1 = dd * (float)(int)(int8_t)(sv >> 8);
+    const float2 gsv = *reinterpret_cast<const float2*>(gs + h * 8 + 2 * g);
+    v = fmaf(delta0, fmaf(-160.f, gsv.x, d[0] + d[1]), v);
+    v = fmaf(delta1, fmaf(-160.f, gsv.y, d[2] + d[3]), v);
+  }
+  return v;
+}
+
+// ------------------------------------------------------------------ kernel
+template <int TYPE>
+struct MfmaType {
+  static constexpr int kBB = TYPE == kQ4_K ? 144 : 210;
+  static constexpr int kTable = TYPE == kQ4_K ? kQ4Table : kQ6Table;
+  static constexpr int kSums = TYPE == kQ4_K ? 8 : 16;
+  static constexpr int kZero = 2048;  // zero lines read by A lanes without data
+};
+
+constexpr int kMfmaWaves = 4;
+
+// LDS layout: [0, kZero) zeros | table (nblk * kTable) | group sums | stages.
+template <int TYPE, int C, bool ALIGNED>
+constexpr size_t mfma_lds_bytes(int nblk) {
+  using T = MfmaType<TYPE>;
+  using Ch = Chunk<T::kBB, C, ALIGNED>;
+  return (size_t)T::kZero + (size_t)nblk * (T::kTable + 4 * T::kSums) +
+         (size_t)kMfmaWaves * 2 * Ch::kBuffer;
+}
+
+// ALIGNED: the weights, row_bytes and the chunk span are multiples of 4, so
+// every row's chunk starts on a dword.
+template <int TYPE, int C, bool ALIGNED>
+__global__ void __launch_bounds__(64 * kMfmaWaves)
+gemv_mfma_kernel(const uint8_t* __restrict__ w, int64_t row_bytes, int rows, int nblk,
+                 const float* __restrict__ x, float* __restrict__ y) {
+  using T = MfmaType<TYPE>;
+  using Ch = Chunk<T::kBB, C, ALIGNED>;
+  extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+  const uint32_t table_off = T::kZero;
+  uint8_t* table = lds + table_off;
+  float* gsum = reinterpret_cast<float*>(table + nblk * T::kTable);
+  uint8_t* stages = reinterpret_cast<uint8_t*>(gsum + nblk * T::kSums);
+
+  for (int i = threadIdx.x; i < T::kZero / 16; i += blockDim.x)
+    reinterpret_cast<u32x4*>(lds)[i] = u32x4{0u, 0u, 0u, 0u};
+  if constexpr (TYPE == kQ4_K) build_q4k_table(table, gsum, x, nblk);
+  else build_q6k_table(table, gsum, x, nblk);
+  __syncthreads();
+
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int n = lane & 15, g = lane >> 4, a = lane & 15;
+  // A addressing: lane_a = the lane's table entry in block 0, or 0 (zero
+  // region) in MFMAs where its A row carries no data.
+  uint32_t a_base;
+  bool a_m[4];
+  if constexpr (TYPE == kQ4_K) {
+    a_base = (g == (a >> 2)) ? table_off + (uint32_t)(a * 16) : 0u;
+  } else {
+    const bool act = ((a >> 1) & 1) == (g >> 1);
+    a_base = table_off + (uint32_t)(((a & 3) * 2 + (g & 1)) * 16);
+#pragma unroll
+    for (int m = 0; m < 4; ++m) a_m[m] = act && (a >> 2) == m;
+  }
+  const uint32_t a_stride = (TYPE == kQ4_K && a_base == 0u) ? 0u : (uint32_t)T::kTable;
+
+  const uint8_t* stage = stages + wave * 2 * Ch::kBuffer;
+  const uint32_t stage_lds = lds_address(stage);
+  const int tiles = (rows + 15) >> 4;
+  const int chunks = nblk / C;
+  const int first_tile = blockIdx.x * kMfmaWaves + wave;
+  const int tile_step = gridDim.x * kMfmaWaves;
+  const int my_tiles = first_tile < tiles ? (tiles - first_tile + tile_step - 1) / tile_step : 0;
+  const int steps = my_tiles * chunks;
+  const uint32_t rb = (uint32_t)row_bytes;
+
+  // per load instruction i: this lane's (row, piece) and byte offset in the tile
+  uint32_t voff[Ch::kLoads];
+#pragma unroll
+  for (int i = 0; i < Ch::kLoads; ++i) {
+    const int idx = min(64 * i + lane, 16 * Ch::kPieces - 1);
+    const int r = idx / Ch::kPieces;
+    voff[i] = (uint32_t)r * rb + 16u * (uint32_t)(idx - r * Ch::kPieces);
+  }
+
+  // Row r of the tile starts at base + r * rb; its range is read from the
+  // dword at or below that, i.e. from base_al + ((bsh + r * rb) & ~3) with
+  // base_al = base & ~3 and bsh = base & 3 (offsets stay non-negative).
+  auto issue = [&](int s) {
+    const int tile = first_tile + (s / chunks) * tile_step;
+    const int chunk = s - (s / chunks) * chunks;
+    const uint8_t* base =
+        uniform_ptr(w + (int64_t)tile * 16 * row_bytes + (int64_t)chunk * Ch::kSpan);
+    const uint32_t bsh = ALIGNED ? 0u : (uint32_t)(reinterpret_cast<uintptr_t>(base) & 3u);
+    const uint8_t* base_al = base - bsh;
+    const uint32_t dst = stage_lds + (uint32_t)((s & 1) * Ch::kBuffer);
+    const int rmax = rows - 1 - tile * 16;
+    if (ALIGNED && rmax >= 15) {
+#pragma unroll
+      for (int i = 0; i < Ch::kLoads; ++i) load_lds16(base_al, voff[i], dst + 1024u * i);
+    } else {
+      // unaligned rows, or the last, partial tile (rows past the end re-read
+      // the last row)
+#pragma unroll
+      for (int i = 0; i < Ch::kLoads; ++i) {
+        const int idx = min(64 * i + lane, 16 * Ch::kPieces - 1);
+        const int r = idx / Ch::kPieces;
+        const uint32_t rr = (uint32_t)min(r, rmax);
+        const uint32_t o = ((bsh + rr * rb) & ~3u) + 16u * (uint32_t)(idx - r * Ch::kPieces);
+        load_lds16(base_al, o, dst + 1024u * i);
+      }
+    }
+  };
+
+  if (steps > 0) issue(0);
+  float acc = 0.f;
+  for (int s = 0; s < steps; ++s) {
+    const int tile = first_tile + (s / chunks) * tile_step;
+    const int chunk = s - (s / chunks) * chunks;
+    if (s + 1 < steps) {
+      issue(s + 1);
+      wait_loads<Ch::kLoads>();
+    } else {
+      wait_loads<0>();
+    }
+    const uint8_t* buf = stage + (s & 1) * Ch::kBuffer;
+    const uint8_t* rowp = buf + n * Ch::kRow;
+    if constexpr (!ALIGNED) {
+      const int row = min(tile * 16 + n, rows - 1);
+      rowp += (reinterpret_cast<uintptr_t>(w + (int64_t)row * row_bytes + (int64_t)chunk * Ch::kSpan) & 3u);
+    }
+    auto block = [&]<int BL>() {
+      const int b = chunk * C + BL;
+      const float* gs = gsum + b * T::kSums;
+      const uint8_t* p = rowp + BL * T::kBB;
+      if constexpr (TYPE == kQ4_K) {
+        acc += q4k_block(p, lds, a_base + (uint32_t)b * a_stride, gs, g);
+      } else {
+        const uint32_t ab = a_base + (uint32_t)b * (uint32_t)T::kTable;
+        const uint32_t am[4] = {a_m[0] ? ab : 0u, a_m[1] ? ab : 0u, a_m[2] ? ab : 0u,
+                                a_m[3] ? ab : 0u};
+        if constexpr (ALIGNED) acc += q6k_block<(BL * 210) & 3>(p, lds, am, gs, g);
+        else acc += q6k_block<-1>(p, lds, am, gs, g);
+      }
+    };
+    [&]<int... BL>(std::integer_sequence<int, BL...>) {
+      (block.template operator()<BL>(), ...);
+    }(std::make_integer_sequence<int, C>{});
+    if (chunk == chunks - 1) {
+      const float v = sum_lane_groups(acc);
+      const int row = tile * 16 + n;
+      if (g == 0 && row < rows) y[row] = v;
+      acc = 0.f;
+    }
+    asm volatile("" ::: "memory");
+  }
+}
+
+// ------------------------------------------------------------------ host
+
+template <int TYPE>
+struct MfmaChoice {
+  int chunk;
+  bool aligned;
+};
+
+template <int TYPE>
+static MfmaChoice<TYPE> mfma_choice(const GemvProblem& p) {
+  const int64_t nblk = p.columns / 256;
+  MfmaChoice<TYPE> c;
+  c.chunk = nblk % 2 == 0 ? 2 : 1;
+  const int64_t span = (int64_t)c.chunk * MfmaType<TYPE>::kBB;
+  c.aligned = p.row_bytes % 4 == 0 && span % 4 == 0;
+  return c;
+}
+
+template <int TYPE>
+static size_t mfma_lds(const GemvProblem& p) {
+  const MfmaChoice<TYPE> c = mfma_choice<TYPE>(p);
+  const int nblk = (int)(p.columns / 256);
+  if (c.chunk == 2)
+    return c.aligned ? mfma_lds_bytes<TYPE, 2, true>(nblk) : mfma_lds_bytes<TYPE, 2, false>(nblk);
+  return c.aligned ? mfma_lds_bytes<TYPE, 1, true>(nblk) : mfma_lds_bytes<TYPE, 1, false>(nblk);
+}
+
+bool gemv_mfma_supported(const GemvProblem& p) {
+  if (p.tokens != 1 || p.columns % 256 != 0 || p.rows < 1) return false;
+  if (p.row_bytes * 16 >= (int64_t)1 << 31) return false;
+  // row ranges are read from the dword at or below their start: the
+  // weights must start on a dword (Q4_K: rows 16-byte aligned, its blocks
+  // are read from LDS with 16-byte loads)
+  if (reinterpret_cast<uintptr_t>(p.weights) & 3u) return false;
+  if (p.type == kQ4_K)
+    return (reinterpret_cast<uintptr_t>(p.weights) & 15u) == 0 && p.row_bytes % 16 == 0 &&
+           mfma_lds<kQ4_K>(p) <= kMaxLdsBytes;
+  if (p.type == kQ6_K) return mfma_lds<kQ6_K>(p) <= kMaxLdsBytes;
+  return false;
+}
+
+template <int TYPE, int C, bool ALIGNED>
+static hipError_t launch_mfma(const GemvProblem& p, hipStream_t stream) {
+  const int nblk = (int)(p.columns / 256);
+  const size_t lds = mfma_lds_bytes<TYPE, C, ALIGNED>(nblk);
+  const auto kernel = gemv_mfma_kernel<TYPE, C, ALIGNED>;
+  if (lds > 65536) {
+    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kernel),
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    if (e != hipSuccess) return e;
+  }
+  int per_cu = 0;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, reinterpret_cast<const void*>(kernel),
+                                                   64 * kMfmaWaves, lds) != hipSuccess ||
+      per_cu < 1)
+    per_cu = 1;
+  const int tiles = (int)((p.rows + 15) / 16);
+  const int needed = (tiles + kMfmaWaves - 1) / kMfmaWaves;
+  const int grid = std::max(1, std::min(needed, device_cu_count() * per_cu));
+  hipLaunchKernelGGL(kernel, dim3(grid), dim3(64 * kMfmaWaves), lds, stream, p.weights,
+                     p.row_bytes, (int)p.rows, nblk, p.x, p.y);
+  return hipGetLastError();
+}
+
+template <int TYPE>
+static hipError_t launch_mfma_type(const GemvProblem& p, hipStream_t stream) {
+  const MfmaChoice<TYPE> c = mfma_choice<TYPE>(p);
+  if (c.chunk == 2)
+    return c.aligned ? launch_mfma<TYPE, 2, true>(p, stream) : launch_mfma<TYPE, 2, false>(p, stream);
+  return c.aligned ? launch_mfma<TYPE, 1, true>(p, stream) : launch_mfma<TYPE, 1, false>(p, stream);
+}
+
+hipError_t gemv_mfma_launch(const GemvProblem& p, hipStream_t stream) {
+  return p.type == kQ4_K ? launch_mfma_type<kQ4_K>(p, stream) : launch_mfma_type<kQ6_K>(p, stream);
+}
+
+}  // namespace llhip
