@@ -398,7 +398,7 @@ struct llambda_hip_moe_session {
   MoePlan plan{};
   DevBuf router, bias, gate, up, down, sh_gate, sh_up, sh_down;
   DevBuf logits, top_idx, top_w, shared_w, counts, perm, chunks, chunk_counts, act, down_out,
-      error;
+      error, xq, xsum, aq, asum;
   DevBuf x, y;
   int staged = 0;
   ~llambda_hip_moe_session() {
@@ -420,6 +420,15 @@ struct llambda_hip_moe_session {
     chunks.alloc((size_t)moe_max_chunks(p, tokens, 1) * sizeof(MoeChunk), "chunk table");
     act.alloc(pairs * act_w * sizeof(float), "activations");
     down_out.alloc(pairs * (size_t)p.hidden * sizeof(float), "expert outputs");
+    const size_t H = (size_t)p.hidden;
+    xq.alloc(T * 2 * H * sizeof(uint16_t), "split input");
+    xsum.alloc(T * (H / 16 + H / 32) * sizeof(float), "input group sums");
+    aq.alloc(pairs * 2 * act_w * sizeof(uint16_t), "split activations");
+    asum.alloc(pairs * (act_w / 16 + act_w / 32) * sizeof(float), "activation group sums");
+    p.xq = xq.as<uint16_t>();
+    p.xsum = xsum.as<float>();
+    p.aq = aq.as<uint16_t>();
+    p.asum = asum.as<float>();
     p.logits = logits.as<float>();
     p.top_idx = top_idx.as<int>();
     p.top_w = top_w.as<float>();

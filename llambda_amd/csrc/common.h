@@ -36,8 +36,9 @@ __host__ __device__ constexpr int block_weights(int type) {
 
 // Device allocations of packed weights carry this many readable bytes past
 // their end: the dword-granular loads of 2-byte-aligned blocks may touch up to
-// 3 bytes beyond the last block.
-constexpr size_t kWeightPad = 64;
+// 3 bytes beyond the last block, and the grouped expert kernels stage whole
+// 256-element chunks (up to 288 bytes) of a row's last, partial chunk.
+constexpr size_t kWeightPad = 512;
 
 // A dword-aligned 16-byte vector: lets the compiler emit global_load_dwordx4
 // at 4-byte alignment (the hardware requires dword alignment only).

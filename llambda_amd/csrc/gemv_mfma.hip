@@ -25,46 +25,12 @@
 //              l = 8g .. 8g+7 from lane g's ql/qh bytes.
 // The row sums of the four G lanes meet by two cross-lane adds.
 #include "gemv.h"
+#include "mfma.h"
 
 #include <algorithm>
 #include <utility>
 
 namespace llhip {
-
-typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
-typedef float floatx4 __attribute__((ext_vector_type(4)));
-typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
-
-constexpr uint32_t kFiller = 0x43434343u;  // bf16 high byte of 128 + q
-constexpr uint32_t kSelLo = 0x04010400u;   // {b0, F, b1, F}
-constexpr uint32_t kSelHi = 0x04030402u;   // {b2, F, b3, F}
-
-__device__ __forceinline__ uint32_t bf16_bits_rne(float f) {
-  const uint32_t u = __builtin_bit_cast(uint32_t, f);
-  return (u + 0x7FFFu + ((u >> 16) & 1u)) >> 16;
-}
-
-// x = hi + lo with hi, lo bf16 (bits returned); hi + lo is returned in sum.
-__device__ __forceinline__ void split_bf16(float x, uint32_t& hi, uint32_t& lo, float& sum) {
-  hi = bf16_bits_rne(x);
-  const float fh = __builtin_bit_cast(float, hi << 16);
-  lo = bf16_bits_rne(x - fh);
-  sum = fh + __builtin_bit_cast(float, lo << 16);
-}
-
-// 8 codes (two dwords of code bytes) -> the B operand (4 VGPRs of bf16 pairs).
-__device__ __forceinline__ bf16x8 codes_to_b(uint32_t c0, uint32_t c1) {
-  u32x4 v;
-  v.x = __builtin_amdgcn_perm(kFiller, c0, kSelLo);
-  v.y = __builtin_amdgcn_perm(kFiller, c0, kSelHi);
-  v.z = __builtin_amdgcn_perm(kFiller, c1, kSelLo);
-  v.w = __builtin_amdgcn_perm(kFiller, c1, kSelHi);
-  return __builtin_bit_cast(bf16x8, v);
-}
-
-__device__ __forceinline__ floatx4 mfma(const bf16x8& a, const bf16x8& b, const floatx4& c) {
-  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
-}
 
 // Sum over the four lanes n, n+16, n+32, n+48.
 __device__ __forceinline__ float sum_lane_groups(float v) {
@@ -82,8 +48,6 @@ __device__ __forceinline__ float sum_lane_groups(float v) {
 // below the chunk's first byte (row starts need only be 2-byte aligned) and
 // may run up to 18 bytes past the chunk (the allocation's pad covers the last
 // row).  Two buffers per wave: the next chunk loads while this one computes.
-typedef __attribute__((address_space(3))) void* lds_ptr_t;
-
 template <int BB, int C, bool ALIGNED>
 struct Chunk {
   static constexpr int kSpan = C * BB;
@@ -92,33 +56,6 @@ struct Chunk {
   static constexpr int kLoads = (16 * kPieces + 63) / 64;
   static constexpr int kBuffer = 1024 * kLoads;  // per buffer; lanes past 16 rows write slack
 };
-
-__device__ __forceinline__ uint32_t lds_address(const void* p) {
-  return (uint32_t)(uintptr_t)(lds_ptr_t)(p);
-}
-
-// 64 lanes x 16 bytes from base + voff[lane] to LDS lds + 16 * lane.
-// base and lds are wavefront-uniform.
-__device__ __forceinline__ void load_lds16(const uint8_t* base, uint32_t voff, uint32_t lds) {
-  asm volatile(
-      "s_nop 0\n\t"
-      "global_load_lds_dwordx4 %0, %1"
-      :
-      : "v"(voff), "s"(base), "{m0}"(lds)
-      : "memory");
-}
-
-template <int N>
-__device__ __forceinline__ void wait_loads() {
-  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
-}
-
-__device__ __forceinline__ const uint8_t* uniform_ptr(const uint8_t* p) {
-  const uint64_t v = reinterpret_cast<uint64_t>(p);
-  const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v);
-  const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(v >> 32));
-  return reinterpret_cast<const uint8_t*>(((uint64_t)hi << 32) | lo);
-}
 
 // ------------------------------------------------------------------ Q4_K
 // LDS table per block: 8 MFMAs x 16 A rows x 16 B (only lane g = a >> 2
@@ -173,7 +110,7 @@ __device__ __forceinline__ float q4k_block(const uint8_t* p, const uint8_t* lds,
     const bf16x8 av = *reinterpret_cast<const bf16x8*>(lds + a + m * 256);
     const uint32_t lo = opaque(qw[m] & 0x0F0F0F0Fu);
     const uint32_t hi = opaque((qw[m] >> 4) & 0x0F0F0F0Fu);
-    d = mfma(av, codes_to_b(lo, hi), d);
+    d = mfma32(av, codes_to_b(lo, hi), d);
   }
   // sub-blocks 2g (D rows 4g, 4g+1) and 2g+1 (4g+2, 4g+3); scale and min per
   // get-scale-min-k4-at (llambda.lisp:4316-4336)
@@ -281,7 +218,7 @@ __device__ __forceinline__ float q6k_block(const uint8_t* p, const uint8_t* lds,
       const uint32_t c0 = opaque((l0 & 0x0F0F0F0Fu) | (h0 << 4));
       const uint32_t c1 = opaque((l1 & 0x0F0F0F0Fu) | (h1 << 4));
       const bf16x8 av = *reinterpret_cast<const bf16x8*>(lds + am[m] + h * 512 + m * 128);
-      d = mfma(av, codes_to_b(c0, c1), d);
+      d = mfma32(av, codes_to_b(c0, c1), d);
     }
     // D rows 4g .. 4g+3 of column n: groups (k = g, l-half 0 / 1) of half h,
     // i.e. scales sc[8h + 2g] and sc[8h + 2g + 1] (llambda.lisp:4203-4310)

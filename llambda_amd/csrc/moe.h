@@ -57,10 +57,61 @@ struct MoePlan {
   int* perm;           // [capacity * (top_k + 1)]
   MoeChunk* chunks;    // [max_chunks(capacity)]
   int* chunk_counts;   // [2]: routed chunks, shared chunks
-  float* act;          // [capacity * (top_k + 1)][max(ffn, shared_ffn)]
+  float* act;          // [capacity * (top_k + 1)][max(ffn, shared_ffn)]  (batch 1)
+  // split rows (moe_mfma.hip) of the multi-token path
+  uint16_t* xq;        // [capacity][2 hidden]           x as bf16 hi/lo
+  float* xsum;         // [capacity][hidden/16 + hidden/32]
+  uint16_t* aq;        // [capacity * (top_k + 1)][2 act_width]  activations
+  float* asum;         // [capacity * (top_k + 1)][act_width/16 + act_width/32]
   float* down_out;     // [capacity * (top_k + 1)][hidden]
   int* error;          // [1] nonzero after a run that hit a reference error
 };
+
+// Grouped expert product over a chunk table (moe_mfma.hip).
+enum MoeEpilogue : int {
+  kEpiSwiglu = 0,  // gate and up rows -> split silu(g) * u
+  kEpiRelu2 = 1,   // up rows -> split relu(u)^2
+  kEpiDown = 2,    // down rows -> fp32 output per pair
+};
+
+struct MoeGemmArgs {
+  // work: chunk table entries of `group` (routed 0, shared 1)
+  const MoeChunk* chunks;
+  const int* chunk_counts;
+  int group;
+  const int* perm;
+  int pairs;       // tokens * top_k: pair ids >= pairs are shared-expert pairs
+  int top_k;
+  int a_by_token;  // A row = the pair's token (1) or the pair itself (0)
+  // A: split rows
+  const uint16_t* aq;
+  int64_t aq_stride;  // u16 per row
+  const float* as;
+  int64_t as_stride;  // floats per row
+  int as32_off;       // offset of the 32-group sums in a row of as
+  int K;
+  // B: expert slabs of packed rows
+  const uint8_t* w0;  // gate (swiglu) or up / down
+  const uint8_t* w1;  // up (swiglu)
+  int64_t row_bytes;
+  int64_t expert_stride;
+  int N;
+  // output: split activations (swiglu, relu2) or fp32 rows (down)
+  uint16_t* oq;
+  int64_t oq_stride;
+  float* os;
+  int64_t os_stride;
+  int os32_off;
+  float* out;
+  int64_t out_stride;
+};
+
+hipError_t split_rows_launch(const float* x, int rows, int K, uint16_t* q, int64_t q_stride,
+                             float* s, int64_t s_stride, hipStream_t stream);
+hipError_t router_mfma_launch(const float* x, int T, const float* R, int Er, int H, float* logits,
+                              int ld, hipStream_t stream);
+hipError_t moe_gemm_launch(int type, int epi, const MoeGemmArgs& a, int mt, int max_chunks,
+                           hipStream_t stream);
 
 // Upper bound of the chunk table for `tokens` tokens with chunk size nt.
 int64_t moe_max_chunks(const MoePlan& p, int64_t tokens, int nt);

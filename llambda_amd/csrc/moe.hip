@@ -1,28 +1,12 @@
 // moe.hip -- routed-MoE feed-forward kernels for gfx950 (see moe.h).
 #include "moe.h"
+#include "activations.h"
 
 #include <algorithm>
 #include <cfloat>
 #include <climits>
 
 namespace llhip {
-
-// sigmoid / silu as llambda.lisp:926-930 evaluates them: exp of the single
-// argument is formed in double and rounded to single, 1 + e and the quotient
-// are double, the result is rounded to single.
-__device__ __forceinline__ float sigmoid_ref(float v) {
-  const float e = (float)exp(-(double)v);
-  return (float)(1.0 / (1.0 + (double)e));
-}
-__device__ __forceinline__ float silu_ref(float v) {
-  const float e = (float)exp(-(double)v);
-  return (float)((double)v / (1.0 + (double)e));
-}
-// relu-squared, llambda.lisp:938-940
-__device__ __forceinline__ float relu2_ref(float v) {
-  const float r = v > 0.f ? v : 0.f;
-  return __fmul_rn(r, r);
-}
 
 // ------------------------------------------------------------------ top-k
 // select-top-k-logits-into (llambda.lisp:5265-5292) keeps, in descending
@@ -532,10 +516,128 @@ static hipError_t launch_groups(const MoePlan& p, const float* x, int tokens, hi
   return e;
 }
 
+// Token-tile count (16 tokens each) of the grouped MFMA chunks: enough to
+// cover the average (token, rank) pairs per expert, at most 4.
+static int moe_mfma_tiles(const MoePlan& p, int tokens) {
+  const int64_t avg = ((int64_t)tokens * p.top_k + p.experts - 1) / p.experts;
+  return avg <= 16 ? 1 : avg <= 40 ? 2 : 4;
+}
+
+// The multi-token forward on MFMA (moe_mfma.hip): split x, router GEMM,
+// top-k, scan, grouped gate/up and down products, combine.
+static hipError_t moe_forward_mfma(const MoePlan& p, const float* x, float* y, int tokens,
+                                   hipStream_t s) {
+  const int has_shared = p.shared_ffn > 0;
+  const int H = p.hidden, E = p.experts, K = p.top_k;
+  const int act_w = std::max(p.ffn, p.shared_ffn);
+  const int64_t xs_stride = H / 16 + H / 32, as_stride = act_w / 16 + act_w / 32;
+  hipError_t e = split_rows_launch(x, tokens, H, p.xq, 2 * (int64_t)H, p.xsum, xs_stride, s);
+  if (e != hipSuccess) return e;
+  const int er = E + ((p.variant == kQwen3Next && has_shared) ? 1 : 0);
+  e = router_mfma_launch(x, tokens, p.router, er, H, p.logits, E + 1, s);
+  if (e != hipSuccess) return e;
+  const dim3 tgrid((tokens + 3) / 4);
+  switch (jpl_for(E)) {
+    case 1: e = launch(topk_gate_kernel<1>, tgrid, dim3(256), 0, s, p, tokens); break;
+    case 2: e = launch(topk_gate_kernel<2>, tgrid, dim3(256), 0, s, p, tokens); break;
+    case 4: e = launch(topk_gate_kernel<4>, tgrid, dim3(256), 0, s, p, tokens); break;
+    case 8: e = launch(topk_gate_kernel<8>, tgrid, dim3(256), 0, s, p, tokens); break;
+    case 16: e = launch(topk_gate_kernel<16>, tgrid, dim3(256), 0, s, p, tokens); break;
+    default: return hipErrorInvalidValue;
+  }
+  if (e != hipSuccess) return e;
+  const int mt = moe_mfma_tiles(p, tokens), nt = 16 * mt;
+  e = launch(moe_scan_kernel, dim3(1), dim3(kScanThreads), 0, s, p, tokens, nt, has_shared);
+  if (e != hipSuccess) return e;
+  const int64_t pairs = (int64_t)tokens * K;
+  const int routed_chunks = (int)(pairs / nt + std::min<int64_t>(E, pairs));
+  const int shared_chunks = (tokens + nt - 1) / nt;
+
+  MoeGemmArgs up{};
+  up.chunks = p.chunks;
+  up.chunk_counts = p.chunk_counts;
+  up.perm = p.perm;
+  up.pairs = (int)pairs;
+  up.top_k = K;
+  up.a_by_token = 1;
+  up.aq = p.xq;
+  up.aq_stride = 2 * (int64_t)H;
+  up.as = p.xsum;
+  up.as_stride = xs_stride;
+  up.as32_off = H / 16;
+  up.K = H;
+  up.oq = p.aq;
+  up.oq_stride = 2 * (int64_t)act_w;
+  up.os = p.asum;
+  up.os_stride = as_stride;
+  up.os32_off = act_w / 16;
+  const int epi = p.variant == kQwen3Next ? kEpiSwiglu : kEpiRelu2;
+
+  MoeGemmArgs a = up;
+  a.group = 0;
+  a.w0 = p.variant == kQwen3Next ? p.gate : p.up;
+  a.w1 = p.up;
+  a.row_bytes = row_bytes_of(p.up_type, H);
+  a.expert_stride = a.row_bytes * p.ffn;
+  a.N = p.ffn;
+  e = moe_gemm_launch(p.up_type, epi, a, mt, routed_chunks, s);
+  if (e != hipSuccess) return e;
+  if (has_shared) {
+    a = up;
+    a.group = 1;
+    a.w0 = p.variant == kQwen3Next ? p.sh_gate : p.sh_up;
+    a.w1 = p.sh_up;
+    a.row_bytes = row_bytes_of(p.sh_up_type, H);
+    a.expert_stride = 0;
+    a.N = p.shared_ffn;
+    e = moe_gemm_launch(p.sh_up_type, epi, a, mt, shared_chunks, s);
+    if (e != hipSuccess) return e;
+  }
+
+  MoeGemmArgs down{};
+  down.chunks = p.chunks;
+  down.chunk_counts = p.chunk_counts;
+  down.perm = p.perm;
+  down.pairs = (int)pairs;
+  down.top_k = K;
+  down.a_by_token = 0;
+  down.aq = p.aq;
+  down.aq_stride = 2 * (int64_t)act_w;
+  down.as = p.asum;
+  down.as_stride = as_stride;
+  down.as32_off = act_w / 16;
+  down.N = H;
+  down.out = p.down_out;
+  down.out_stride = H;
+  a = down;
+  a.group = 0;
+  a.K = p.ffn;
+  a.w0 = p.down;
+  a.row_bytes = row_bytes_of(p.down_type, p.ffn);
+  a.expert_stride = a.row_bytes * H;
+  e = moe_gemm_launch(p.down_type, kEpiDown, a, mt, routed_chunks, s);
+  if (e != hipSuccess) return e;
+  if (has_shared) {
+    a = down;
+    a.group = 1;
+    a.K = p.shared_ffn;
+    a.w0 = p.sh_down;
+    a.row_bytes = row_bytes_of(p.sh_down_type, p.shared_ffn);
+    a.expert_stride = 0;
+    e = moe_gemm_launch(p.sh_down_type, kEpiDown, a, mt, shared_chunks, s);
+    if (e != hipSuccess) return e;
+  }
+  return launch(moe_combine_kernel, dim3((H + 255) / 256, tokens), dim3(256), 0, s, p, y, tokens,
+                has_shared);
+}
+
 hipError_t moe_forward_launch(const MoePlan& p, const float* x, float* y, int tokens,
                               hipStream_t s) {
   if (tokens <= 0) return hipSuccess;
   if (tokens > p.capacity) return hipErrorInvalidValue;
+  // the MFMA path reads x with 16-byte loads
+  if (p.xq && (reinterpret_cast<uintptr_t>(x) & 15u) == 0)
+    return moe_forward_mfma(p, x, y, tokens, s);
   const int has_shared = p.shared_ffn > 0;
   // 1 router (+ the shared-gate row for qwen3next)
   GemvProblem r{};
