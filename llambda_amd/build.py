@@ -24,6 +24,9 @@ ARCH = "gfx950"
 HIP_FLAGS = [
     f"--offload-arch={ARCH}", "-O3", "-std=c++20", "-fPIC", "-Wall",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    # MFMA results in ordinary VGPRs: the kernels scale and add them with
+    # VALU instructions, which cannot read the accumulation registers
+    "-mllvm", "-amdgpu-mfma-vgpr-form=1",
 ]
 CXX_FLAGS = ["-O2", "-std=c++17", "-fPIC", "-Wall"]
 

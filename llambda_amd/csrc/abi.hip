@@ -421,10 +421,12 @@ struct llambda_hip_moe_session {
     act.alloc(pairs * act_w * sizeof(float), "activations");
     down_out.alloc(pairs * (size_t)p.hidden * sizeof(float), "expert outputs");
     const size_t H = (size_t)p.hidden;
-    xq.alloc(T * 2 * H * sizeof(uint16_t), "split input");
-    xsum.alloc(T * (H / 16 + H / 32) * sizeof(float), "input group sums");
-    aq.alloc(pairs * 2 * act_w * sizeof(uint16_t), "split activations");
-    asum.alloc(pairs * (act_w / 16 + act_w / 32) * sizeof(float), "activation group sums");
+    // the decode pipeline stages whole 256-element chunks (1 KB of split
+    // row) of a row's last, partial chunk: 1 KB of readable slack
+    xq.alloc(T * 2 * H * sizeof(uint16_t) + 1024, "split input");
+    xsum.alloc(T * (H / 16) * sizeof(float), "input group sums");
+    aq.alloc(pairs * 2 * act_w * sizeof(uint16_t) + 1024, "split activations");
+    asum.alloc(pairs * (act_w / 16) * sizeof(float), "activation group sums");
     p.xq = xq.as<uint16_t>();
     p.xsum = xsum.as<float>();
     p.aq = aq.as<uint16_t>();

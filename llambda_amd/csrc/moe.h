@@ -60,9 +60,9 @@ struct MoePlan {
   float* act;          // [capacity * (top_k + 1)][max(ffn, shared_ffn)]  (batch 1)
   // split rows (moe_mfma.hip) of the multi-token path
   uint16_t* xq;        // [capacity][2 hidden]           x as bf16 hi/lo
-  float* xsum;         // [capacity][hidden/16 + hidden/32]
+  float* xsum;         // [capacity][hidden/16]          16-group sums
   uint16_t* aq;        // [capacity * (top_k + 1)][2 act_width]  activations
-  float* asum;         // [capacity * (top_k + 1)][act_width/16 + act_width/32]
+  float* asum;         // [capacity * (top_k + 1)][act_width/16]
   float* down_out;     // [capacity * (top_k + 1)][hidden]
   int* error;          // [1] nonzero after a run that hit a reference error
 };
@@ -87,8 +87,7 @@ struct MoeGemmArgs {
   const uint16_t* aq;
   int64_t aq_stride;  // u16 per row
   const float* as;
-  int64_t as_stride;  // floats per row
-  int as32_off;       // offset of the 32-group sums in a row of as
+  int64_t as_stride;  // floats per row (16-group sums)
   int K;
   // B: expert slabs of packed rows
   const uint8_t* w0;  // gate (swiglu) or up / down
@@ -101,15 +100,16 @@ struct MoeGemmArgs {
   int64_t oq_stride;
   float* os;
   int64_t os_stride;
-  int os32_off;
   float* out;
   int64_t out_stride;
+  int depth;  // LDS stages per wave (set by the launcher)
 };
 
 hipError_t split_rows_launch(const float* x, int rows, int K, uint16_t* q, int64_t q_stride,
                              float* s, int64_t s_stride, hipStream_t stream);
 hipError_t router_mfma_launch(const float* x, int T, const float* R, int Er, int H, float* logits,
                               int ld, hipStream_t stream);
+// mt: token tiles per chunk (1, 2, 4), or 0 for a batch of one token.
 hipError_t moe_gemm_launch(int type, int epi, const MoeGemmArgs& a, int mt, int max_chunks,
                            hipStream_t stream);
 

@@ -519,6 +519,7 @@ static hipError_t launch_groups(const MoePlan& p, const float* x, int tokens, hi
 // Token-tile count (16 tokens each) of the grouped MFMA chunks: enough to
 // cover the average (token, rank) pairs per expert, at most 4.
 static int moe_mfma_tiles(const MoePlan& p, int tokens) {
+  if (tokens == 1) return 0;  // the decode pipeline: one token per chunk
   const int64_t avg = ((int64_t)tokens * p.top_k + p.experts - 1) / p.experts;
   return avg <= 16 ? 1 : avg <= 40 ? 2 : 4;
 }
@@ -530,7 +531,7 @@ static hipError_t moe_forward_mfma(const MoePlan& p, const float* x, float* y, i
   const int has_shared = p.shared_ffn > 0;
   const int H = p.hidden, E = p.experts, K = p.top_k;
   const int act_w = std::max(p.ffn, p.shared_ffn);
-  const int64_t xs_stride = H / 16 + H / 32, as_stride = act_w / 16 + act_w / 32;
+  const int64_t xs_stride = H / 16, as_stride = act_w / 16;
   hipError_t e = split_rows_launch(x, tokens, H, p.xq, 2 * (int64_t)H, p.xsum, xs_stride, s);
   if (e != hipSuccess) return e;
   const int er = E + ((p.variant == kQwen3Next && has_shared) ? 1 : 0);
@@ -546,7 +547,7 @@ static hipError_t moe_forward_mfma(const MoePlan& p, const float* x, float* y, i
     default: return hipErrorInvalidValue;
   }
   if (e != hipSuccess) return e;
-  const int mt = moe_mfma_tiles(p, tokens), nt = 16 * mt;
+  const int mt = moe_mfma_tiles(p, tokens), nt = 16 * std::max(mt, 1);
   e = launch(moe_scan_kernel, dim3(1), dim3(kScanThreads), 0, s, p, tokens, nt, has_shared);
   if (e != hipSuccess) return e;
   const int64_t pairs = (int64_t)tokens * K;
@@ -564,13 +565,11 @@ static hipError_t moe_forward_mfma(const MoePlan& p, const float* x, float* y, i
   up.aq_stride = 2 * (int64_t)H;
   up.as = p.xsum;
   up.as_stride = xs_stride;
-  up.as32_off = H / 16;
   up.K = H;
   up.oq = p.aq;
   up.oq_stride = 2 * (int64_t)act_w;
   up.os = p.asum;
   up.os_stride = as_stride;
-  up.os32_off = act_w / 16;
   const int epi = p.variant == kQwen3Next ? kEpiSwiglu : kEpiRelu2;
 
   MoeGemmArgs a = up;
@@ -605,7 +604,6 @@ static hipError_t moe_forward_mfma(const MoePlan& p, const float* x, float* y, i
   down.aq_stride = 2 * (int64_t)act_w;
   down.as = p.asum;
   down.as_stride = as_stride;
-  down.as32_off = act_w / 16;
   down.N = H;
   down.out = p.down_out;
   down.out_stride = H;

@@ -1,10 +1,8 @@
-// moe_mfma.hip -- the multi-token routed-MoE products on MFMA.
-//
-// Three kernels serve batches of two or more tokens:
+// moe_mfma.hip -- the routed-MoE products on MFMA.
 //
 //   split_rows_kernel   fp32 activation rows -> "split rows": every element
 //                       as two bf16 (hi + lo, |x - hi - lo| <= 2^-17 |x|) plus
-//                       the sums of each 16- and 32-element group of hi + lo.
+//                       the sum of each 16-element group of fl(hi) + fl(lo).
 //   router_mfma_kernel  the F32 router as a GEMM on v_mfma_f32_16x16x4_f32
 //                       (fp32 products, fp32 accumulation).
 //   moe_gemm_kernel     the grouped expert products over the chunk table
@@ -12,21 +10,36 @@
 //                       with silu(g)*u or relu(u)^2 fused, or down.
 //
 // Expert products.  The weights stay the tensor's GGUF super-blocks.  Each
-// wavefront stages the raw bytes of its rows for one 256-element K chunk in
-// LDS (global_load_lds_dwordx4 -- coalesced, no VGPR round trip), then every
-// lane turns its 8 (or 4) codes of one scale group into exact bf16 values
-// 128 + q (a v_perm_b32 with the filler byte 0x43) -- the B operand of a
-// 16x16x32 (or, for Q6_K's 16-weight groups, 16x16x16) bf16 MFMA whose A
-// operand is 16 tokens' hi, then lo, activations.  Per scale group g of row n
+// wavefront owns 16-row subtiles of one or two matrices (gate and up side by
+// side) and streams them through LDS in 256-element K chunks
+// (global_load_lds_dwordx4: coalesced, no VGPR round trip).  Per chunk every
+// lane first decodes the scales of its share of the chunk's scale groups into
+// a per-wave table (delta, -c), then, group by group, turns its 8 (or 4)
+// codes into exact bf16 values 128 + q (v_perm_b32 with the filler byte 0x43)
+// -- the B operand of a 16x16x32 (Q6_K's 16-weight groups: 16x16x16) bf16
+// MFMA whose A operand is 16 tokens' hi, then lo, activations.  Per scale
+// group g of row n
 //     sum_k w_k x_k = delta_g * sum_k (128 + q_k) x_k  -  c_g * sum_k x_k
 // with c_g = 128 delta_g + mu_g (Q4_K), 160 delta_g (Q6_K: q - 32),
 // 144 delta_g (Q5_0: q - 16), 128 delta_g (Q8_0: codes q ^ 0x80).  The first
-// term is one VALU fma per output per group (the MFMA result scaled by the
-// row's delta); the second is itself a product over groups, done at the end
-// of each chunk as a v_mfma_f32_16x16x4_f32 of the group sums (A) with -c (B).
-// The reference forms every weight first (w = fl(fl(q delta) - mu)) and
-// accumulates w x in fp32; both are fp32 evaluations of the same sum and
-// differ by rounding, inside the bound 1e-4 sum|w x| per output.
+// term is one VALU fma per output per group; the second is itself a product
+// over groups, done at the end of each chunk as v_mfma_f32_16x16x4_f32 of the
+// group sums (A) with -c (B).  The reference forms every weight first
+// (w = fl(fl(q delta) - mu)) and accumulates w x in fp32; both are fp32
+// evaluations of the same sum and differ by rounding, inside the bound
+// 1e-4 sum|w x| per output.
+//
+// Three pipelines share that arithmetic instruction for instruction, so a
+// token's output does not depend on the batch it runs in:
+//   kPipeWide    2-4 token tiles (chunks of up to 64 pairs): 4 waves x 64
+//                rows, one LDS stage per wave; latency is hidden by the
+//                other waves of the SIMD, the MFMA work per chunk is long.
+//   kPipeDouble  1 token tile: 4 waves x 32 rows, two LDS stages per wave;
+//                chunk kc + 1 (rows by DMA, activations and group sums into
+//                registers) loads while chunk kc computes.
+//   kPipeDecode  one token: 1 wave x 32 rows, a ring of up to 8 LDS stages
+//                holding rows, the token's activations and group sums, all
+//                loaded by DMA ahead of use.
 #include "activations.h"
 #include "mfma.h"
 #include "moe.h"
@@ -35,21 +48,27 @@
 
 namespace llhip {
 
+// s_waitcnt immediates (gfx9 encoding: vmcnt [3:0] and [15:14], expcnt
+// [6:4], lgkmcnt [11:8]).  Issued through the builtin so the compiler's own
+// wait insertion knows the counters were drained.
+constexpr int waitcnt_vm(int n) { return 0x0F70 | (n & 15) | ((n >> 4) << 14); }
+constexpr int kWaitLgkm0 = 0xC07F;
+
 // ---------------------------------------------------------------- split rows
 // Row r of K elements (K % 32 == 0):
 //   q + r * q_stride (u16): for each 32-group j, [64j, 64j + 32) = hi bf16 of
 //       elements 32j .. 32j + 31 and [64j + 32, 64j + 64) = their lo bf16.
-//   s + r * s_stride (f32): [0, K/16) = sums of the 16-groups, then
-//       [K/16, K/16 + K/32) = sums of the 32-groups, each of fl(hi) + fl(lo).
+//   s + r * s_stride (f32): [0, K/16) = sums of the 16-groups, each of
+//       fl(hi) + fl(lo) over the group.  A 32-group's sum is always formed as
+//       s[2j] + s[2j + 1].
 __global__ void __launch_bounds__(256) split_rows_kernel(const float* __restrict__ x, int rows,
                                                          int K, uint16_t* __restrict__ q,
                                                          int64_t q_stride, float* __restrict__ s,
                                                          int64_t s_stride) {
   const int octets = K >> 3;
   const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  // octets is a multiple of 4 and so is the block size: the four octets of
-  // a 32-group are all in range or all out, so the shuffles below stay
-  // within active lanes
+  // octets is even and so is the block size: both octets of a 16-group are
+  // in range or both out, so the shuffle below stays within active lanes
   if (gid >= (int64_t)rows * octets) return;
   const int row = (int)(gid / octets), o = (int)(gid - (int64_t)row * octets);
   const float4* xp = reinterpret_cast<const float4*>(x + (int64_t)row * K + 8 * o);
@@ -69,10 +88,7 @@ __global__ void __launch_bounds__(256) split_rows_kernel(const float* __restrict
   *reinterpret_cast<u32x4*>(dst + 32) = u32x4{lo[0] | (lo[1] << 16), lo[2] | (lo[3] << 16),
                                               lo[4] | (lo[5] << 16), lo[6] | (lo[7] << 16)};
   const float s16 = sum + __shfl_xor(sum, 1, 64);
-  const float s32 = s16 + __shfl_xor(s16, 2, 64);
-  float* srow = s + (int64_t)row * s_stride;
-  if ((o & 1) == 0) srow[o >> 1] = s16;
-  if ((o & 3) == 0) srow[(K >> 4) + (o >> 2)] = s32;
+  if ((o & 1) == 0) s[(int64_t)row * s_stride + (o >> 1)] = s16;
 }
 
 hipError_t split_rows_launch(const float* x, int rows, int K, uint16_t* q, int64_t q_stride,
@@ -130,34 +146,23 @@ hipError_t router_mfma_launch(const float* x, int T, const float* R, int Er, int
 }
 
 // ------------------------------------------------------ B operand per type
-// step(): for lane (n, g), its codes of scale group j of the chunk as bf16
-// 128 + q, the row's delta and offset c for that group.  `row` is the
-// dword-aligned LDS image of the row's chunk; the chunk's first byte is at
-// row + sh (sh < 4; 0 for Q4_K).
+// `row` is the dword-aligned LDS image of one row's chunk; the chunk's first
+// byte is at row + sh (sh < 4; 0 for Q4_K).  codes(): lane g's codes of
+// scale group j as bf16 128 + q.  scale(): that group's delta and c.
 
-__device__ __forceinline__ uint32_t lds_dword(const uint8_t* row, int i) {
+__device__ __forceinline__ uint32_t lds_dword(const uint8_t* row, uint32_t i) {
   return reinterpret_cast<const uint32_t*>(row)[i];
 }
-// Four bytes at byte offset o (o % 4 == 0) of a chunk that starts sh bytes
-// past the dword-aligned row image.
-__device__ __forceinline__ uint32_t lds_dword_at(const uint8_t* row, uint32_t sh, int o) {
-  return __builtin_amdgcn_alignbyte(lds_dword(row, (o >> 2) + 1), lds_dword(row, o >> 2), sh);
-}
-// Four bytes at byte offset o (o even, o % 4 unknown) of the dword-aligned image.
+// Four bytes at byte offset o (o even) of the dword-aligned image.
 __device__ __forceinline__ uint32_t lds_dword_even(const uint8_t* row, uint32_t o) {
   const uint32_t* q = reinterpret_cast<const uint32_t*>(row) + (o >> 2);
-  return __builtin_amdgcn_alignbyte(q[1], q[0], o & 3u);
+  return (o & 3u) ? __builtin_amdgcn_alignbyte(q[1], q[0], o & 3u) : q[0];
 }
 __device__ __forceinline__ uint32_t lds_u16_even(const uint8_t* row, uint32_t o) {
-  return (reinterpret_cast<const uint32_t*>(row)[o >> 2] >> (8 * (o & 3u))) & 0xFFFFu;
+  return (lds_dword(row, o >> 2) >> (8 * (o & 3u))) & 0xFFFFu;
 }
 __device__ __forceinline__ uint32_t lds_u8(const uint8_t* row, uint32_t o) {
-  return (reinterpret_cast<const uint32_t*>(row)[o >> 2] >> (8 * (o & 3u))) & 0xFFu;
-}
-
-// Bits 0..3 of b to bit 4 of bytes 0..3.
-__device__ __forceinline__ uint32_t spread4_bit4(uint32_t b) {
-  return (((b & 0xFu) * 0x00204081u) & 0x01010101u) << 4;
+  return (lds_dword(row, o >> 2) >> (8 * (o & 3u))) & 0xFFu;
 }
 
 template <int TYPE>
@@ -171,14 +176,17 @@ struct GemmB<kQ4_K> {
   static constexpr int kSpan = 144, kPitch = 144, kSteps = 8, kStepK = 32;
   static constexpr bool kWide = true;
   typedef bf16x8 Frag;
-  static __device__ __forceinline__ void step(const uint8_t* row, uint32_t, int j, int g, Frag& b,
-                                              float& delta, float& c) {
-    const uint4 h = *reinterpret_cast<const uint4*>(row);
+  static __device__ __forceinline__ Frag codes(const uint8_t* row, uint32_t, int j, int g,
+                                               const uint2*) {
     const uint2 q = *reinterpret_cast<const uint2*>(row + 16 + 32 * (j >> 1) + 8 * g);
     const uint32_t c0 = (j & 1) ? (q.x >> 4) & 0x0F0F0F0Fu : q.x & 0x0F0F0F0Fu;
     const uint32_t c1 = (j & 1) ? (q.y >> 4) & 0x0F0F0F0Fu : q.y & 0x0F0F0F0Fu;
-    b = codes_to_b(c0, c1);
-    // get-scale-min-k4-at (llambda.lisp:4316-4336)
+    return codes_to_b(c0, c1);
+  }
+  // get-scale-min-k4-at (llambda.lisp:4316-4336)
+  static __device__ __forceinline__ void scale(const uint8_t* row, uint32_t, int j, float& delta,
+                                               float& c) {
+    const uint4 h = *reinterpret_cast<const uint4*>(row);
     const int k = j & 3;
     const uint32_t B0 = (h.y >> (8 * k)) & 0xFFu, B4 = (h.z >> (8 * k)) & 0xFFu;
     uint32_t sc, m;
@@ -205,14 +213,18 @@ struct GemmB<kQ6_K> {
   static constexpr int kSpan = 210, kPitch = 224, kSteps = 16, kStepK = 16;
   static constexpr bool kWide = false;
   typedef shortx4 Frag;
-  static __device__ __forceinline__ void step(const uint8_t* row, uint32_t sh, int u, int g,
-                                              Frag& b, float& delta, float& c) {
+  static __device__ __forceinline__ Frag codes(const uint8_t* row, uint32_t sh, int u, int g,
+                                               const uint2*) {
     const int h = u >> 3, k = (u >> 1) & 3, s = u & 1;
-    const uint32_t ql = lds_dword_at(row, sh, 64 * h + 32 * (k & 1) + 16 * s + 4 * g);
-    const uint32_t qh = lds_dword_at(row, sh, 128 + 32 * h + 16 * s + 4 * g);
+    const uint32_t ol = 64 * h + 32 * (k & 1) + 16 * s + 4 * g, oh = 128 + 32 * h + 16 * s + 4 * g;
+    const uint32_t ql = __builtin_amdgcn_alignbyte(lds_dword(row, (ol >> 2) + 1), lds_dword(row, ol >> 2), sh);
+    const uint32_t qh = __builtin_amdgcn_alignbyte(lds_dword(row, (oh >> 2) + 1), lds_dword(row, oh >> 2), sh);
     const uint32_t nib = (ql >> (4 * (k >> 1))) & 0x0F0F0F0Fu;
     const uint32_t hb = ((qh >> (2 * k)) & 0x03030303u) << 4;
-    b = codes4_to_b(nib | hb);
+    return codes4_to_b(nib | hb);
+  }
+  static __device__ __forceinline__ void scale(const uint8_t* row, uint32_t sh, int u, float& delta,
+                                               float& c) {
     const int sc = (int)(int8_t)lds_u8(row, sh + 192u + (uint32_t)u);
     const float d = half_bits_to_float(lds_u16_even(row, sh + 208u));
     delta = d * (float)sc;
@@ -222,26 +234,25 @@ struct GemmB<kQ6_K> {
 
 // Q5_0: chunk = 8 blocks of 22 B (llambda.lisp:3965-3990, 4037-4066).
 // Lane g takes elements 8g .. 8g+7: qs bytes 8 (g & 1) .. +7, low nibbles
-// for g < 2, high for g >= 2, fifth bits from qh bits 8g .. 8g+7.
+// for g < 2, high for g >= 2, fifth bits from qh bits 8g .. 8g+7.  `hbits`
+// maps a qh byte to its eight bits at bit 4 of eight bytes.
 template <>
 struct GemmB<kQ5_0> {
   static constexpr int kSpan = 176, kPitch = 192, kSteps = 8, kStepK = 32;
   static constexpr bool kWide = true;
   typedef bf16x8 Frag;
-  static __device__ __forceinline__ void step(const uint8_t* row, uint32_t sh, int j, int g,
-                                              Frag& b, float& delta, float& c) {
+  static __device__ __forceinline__ Frag codes(const uint8_t* row, uint32_t sh, int j, int g,
+                                               const uint2* hbits) {
     const uint32_t o = sh + 22u * (uint32_t)j;
     const uint32_t os = o + 6u + 8u * (uint32_t)(g & 1);
-    uint32_t q0 = lds_dword_even(row, os), q1 = lds_dword_even(row, os + 4u);
-    if (g >= 2) {
-      q0 >>= 4;
-      q1 >>= 4;
-    }
-    const uint32_t hb = lds_u8(row, o + 2u + (uint32_t)g);
-    const uint32_t c0 = (q0 & 0x0F0F0F0Fu) | spread4_bit4(hb);
-    const uint32_t c1 = (q1 & 0x0F0F0F0Fu) | spread4_bit4(hb >> 4);
-    b = codes_to_b(c0, c1);
-    delta = half_bits_to_float(lds_u16_even(row, o));
+    const uint32_t shift = 4u * (uint32_t)(g >> 1);
+    const uint32_t q0 = lds_dword_even(row, os) >> shift, q1 = lds_dword_even(row, os + 4u) >> shift;
+    const uint2 hb = hbits[lds_u8(row, o + 2u + (uint32_t)g)];
+    return codes_to_b((q0 & 0x0F0F0F0Fu) | hb.x, (q1 & 0x0F0F0F0Fu) | hb.y);
+  }
+  static __device__ __forceinline__ void scale(const uint8_t* row, uint32_t sh, int j, float& delta,
+                                               float& c) {
+    delta = half_bits_to_float(lds_u16_even(row, sh + 22u * (uint32_t)j));
     c = 144.f * delta;
   }
 };
@@ -258,39 +269,51 @@ struct GemmB<kQ8_0> {
     return __builtin_amdgcn_perm(__builtin_bit_cast(uint32_t, f1), __builtin_bit_cast(uint32_t, f0),
                                  0x07060302u);
   }
-  static __device__ __forceinline__ void step(const uint8_t* row, uint32_t sh, int j, int g,
-                                              Frag& b, float& delta, float& c) {
-    const uint32_t o = sh + 34u * (uint32_t)j;
-    const uint32_t os = o + 2u + 8u * (uint32_t)g;
+  static __device__ __forceinline__ Frag codes(const uint8_t* row, uint32_t sh, int j, int g,
+                                               const uint2*) {
+    const uint32_t os = sh + 34u * (uint32_t)j + 2u + 8u * (uint32_t)g;
     const uint32_t u0 = lds_dword_even(row, os) ^ 0x80808080u;
     const uint32_t u1 = lds_dword_even(row, os + 4u) ^ 0x80808080u;
     u32x4 v = {pack2(u0, 0), pack2(u0, 2), pack2(u1, 0), pack2(u1, 2)};
-    b = __builtin_bit_cast(bf16x8, v);
-    delta = half_bits_to_float(lds_u16_even(row, o));
+    return __builtin_bit_cast(bf16x8, v);
+  }
+  static __device__ __forceinline__ void scale(const uint8_t* row, uint32_t sh, int j, float& delta,
+                                               float& c) {
+    delta = half_bits_to_float(lds_u16_even(row, sh + 34u * (uint32_t)j));
     c = 128.f * delta;
   }
 };
 
-// A fragments of lane (t, g) for group j of the chunk starting at element
-// 256 kc: hi then lo (8 bf16 each for 32-groups, 4 for 16-groups).
+// A fragments of lane (t, g) for group j of chunk kc: hi then lo (8 bf16
+// each for 32-groups, 4 for 16-groups).  `row` is the token's split row.
 template <bool WIDE>
 struct AFrag;
 template <>
 struct AFrag<true> {
   bf16x8 hi, lo;
-  __device__ __forceinline__ void load(const uint16_t* row, int kc, int j, int g) {
-    const uint16_t* p = row + 512 * kc + 64 * j + 8 * g;
+  static __device__ __forceinline__ int offset(int j, int g) { return 64 * j + 8 * g; }
+  __device__ __forceinline__ void load(const uint16_t* p) {
     hi = *reinterpret_cast<const bf16x8*>(p);
     lo = *reinterpret_cast<const bf16x8*>(p + 32);
+  }
+  __device__ __forceinline__ void zero() {
+    hi = __builtin_bit_cast(bf16x8, u32x4{0u, 0u, 0u, 0u});
+    lo = hi;
   }
 };
 template <>
 struct AFrag<false> {
   shortx4 hi, lo;
-  __device__ __forceinline__ void load(const uint16_t* row, int kc, int u, int g) {
-    const uint16_t* p = row + 512 * kc + 64 * (u >> 1) + 16 * (u & 1) + 4 * g;
+  static __device__ __forceinline__ int offset(int u, int g) {
+    return 64 * (u >> 1) + 16 * (u & 1) + 4 * g;
+  }
+  __device__ __forceinline__ void load(const uint16_t* p) {
     hi = *reinterpret_cast<const shortx4*>(p);
     lo = *reinterpret_cast<const shortx4*>(p + 32);
+  }
+  __device__ __forceinline__ void zero() {
+    hi = shortx4{0, 0, 0, 0};
+    lo = hi;
   }
 };
 
@@ -301,33 +324,47 @@ __device__ __forceinline__ floatx4 mfma_b(const shortx4& a, const shortx4& b, co
   return mfma16(a, b, c);
 }
 
-// ------------------------------------------------------------ grouped GEMM
-constexpr int kGemmWaves = 4;
+// ------------------------------------------------------------ tile shape
+enum GemmPipe : int { kPipeWide = 0, kPipeDouble = 1, kPipeDecode = 2 };
 
-template <int EPI>
-struct EpiShape {
-  static constexpr int kMats = EPI == kEpiSwiglu ? 2 : 1;  // gate and up rows side by side
-  static constexpr int kSub = EPI == kEpiSwiglu ? 2 : 4;   // 16-row subtiles per matrix
+template <int TYPE, int EPI, int PIPE>
+struct GemmShape {
+  using B = GemmB<TYPE>;
+  static constexpr int kWaves = PIPE == kPipeDecode ? 1 : 4;
+  static constexpr int NB = EPI == kEpiSwiglu ? 2 : 1;             // gate and up side by side
+  static constexpr int NS = (PIPE == kPipeWide ? 4 : 2) / NB;      // 16-row subtiles per matrix
+  static constexpr int ROWS = 16 * NS;                              // rows per matrix and wave
+  static constexpr int PPR = B::kPitch / 16;                        // 16-byte pieces per row
+  static constexpr int PIECES = ROWS * PPR;
+  static constexpr int LOADS = (PIECES + 63) / 64;                  // per matrix
+  static constexpr int ROWBUF = 1024 * LOADS * NB;                  // rows of one chunk
+  static constexpr int TABLE = NS * NB * B::kSteps * 16 * 8;        // (delta, -c) per group and row
+  static constexpr int A_OFF = ROWBUF;                              // decode: the token's chunk
+  static constexpr int S_OFF = ROWBUF + 1024;                       // decode: its 16 group sums
+  static constexpr int STAGE = PIPE == kPipeDecode ? ROWBUF + 1024 + 256 : ROWBUF;
+  static constexpr int DEPTH = PIPE == kPipeWide ? 1 : PIPE == kPipeDouble ? 2 : 8;
+  static constexpr int LUT = TYPE == kQ5_0 ? 256 * 8 : 0;          // Q5_0 fifth-bit table
+  static constexpr int WAVE_LDS = DEPTH * STAGE + TABLE;
+  static constexpr int LDS = LUT + kWaves * WAVE_LDS;
+  static constexpr int DMA = NB * LOADS + (PIPE == kPipeDecode ? 2 : 0);  // loads per stage
 };
 
-template <int TYPE, int EPI>
-constexpr int gemm_lds_bytes() {
-  using B = GemmB<TYPE>;
-  using S = EpiShape<EPI>;
-  constexpr int pieces = 16 * S::kSub * B::kPitch / 16;
-  return kGemmWaves * S::kMats * 1024 * ((pieces + 63) / 64);
+template <int TYPE, int EPI, int PIPE>
+constexpr int gemm_lds_bytes(int depth) {
+  using Sh = GemmShape<TYPE, EPI, PIPE>;
+  return Sh::LUT + Sh::kWaves * (depth * Sh::STAGE + Sh::TABLE);
 }
 
-template <int TYPE, int EPI, int MT>
-__global__ void __launch_bounds__(64 * kGemmWaves) moe_gemm_kernel(MoeGemmArgs a) {
+// ------------------------------------------------------------ the kernel
+// ALIGNED: row_bytes % 4 == 0, so every row's chunk starts at the same offset
+// from a dword (Q4_K, Q5_0, Q8_0: 0; Q6_K: 2 in odd chunks).
+template <int TYPE, int EPI, int MT, int PIPE, bool ALIGNED>
+__global__ void __launch_bounds__((64 * GemmShape<TYPE, EPI, PIPE>::kWaves))
+moe_gemm_kernel(MoeGemmArgs a) {
   using B = GemmB<TYPE>;
-  using S = EpiShape<EPI>;
-  constexpr int NB = S::kMats, NS = S::kSub, ROWS = 16 * NS;
-  constexpr int PPR = B::kPitch / 16;  // 16-byte pieces per row
-  constexpr int PIECES = ROWS * PPR;
-  constexpr int LOADS = (PIECES + 63) / 64;
-  constexpr int BUF = 1024 * LOADS;
-  constexpr int NQ = B::kSteps / 4;  // offset MFMAs per chunk
+  using Sh = GemmShape<TYPE, EPI, PIPE>;
+  constexpr int NB = Sh::NB, NS = Sh::NS, NQ = B::kSteps / 4, KS = B::kSteps;
+  typedef AFrag<B::kWide> AF;
   extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
 
   const int nchunks = a.chunk_counts[a.group];
@@ -336,40 +373,85 @@ __global__ void __launch_bounds__(64 * kGemmWaves) moe_gemm_kernel(MoeGemmArgs a
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int n = lane & 15, g = lane >> 4;
-  const int n0 = (blockIdx.y * kGemmWaves + wave) * ROWS;
-  if (n0 >= a.N) return;
 
-  // A rows of this lane's token (tile row t = n) in each token tile
+  // Q5_0: qh byte -> its bits at bit 4 of eight bytes
+  const uint2* hbits = reinterpret_cast<const uint2*>(lds);
+  if constexpr (TYPE == kQ5_0) {
+    uint2* lut = reinterpret_cast<uint2*>(lds);
+    for (int b = threadIdx.x; b < 256; b += 64 * Sh::kWaves) {
+      uint2 v = {0u, 0u};
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        v.x |= ((uint32_t)(b >> i) & 1u) << (8 * i + 4);
+        v.y |= ((uint32_t)(b >> (i + 4)) & 1u) << (8 * i + 4);
+      }
+      lut[b] = v;
+    }
+    if constexpr (Sh::kWaves > 1) __syncthreads();
+  }
+
+  const int n0 = (blockIdx.y * Sh::kWaves + wave) * Sh::ROWS;
+  if (n0 >= a.N) return;
+  const int depth = PIPE == kPipeDecode ? a.depth : Sh::DEPTH;
+  uint8_t* wlds = lds + Sh::LUT + wave * (depth * Sh::STAGE + Sh::TABLE);
+  float2* table = reinterpret_cast<float2*>(wlds + depth * Sh::STAGE);
+  const uint32_t wlds_addr = lds_address(wlds);
+
+  // split rows of this lane's tokens (tile row t = n of each token tile)
   const uint16_t* arow[MT];
   const float* srow[MT];
+  bool tok_ok[MT];
 #pragma unroll
   for (int i = 0; i < MT; ++i) {
     const int tk = 16 * i + n;
-    const int q = a.perm[ch.start + (tk < ch.count ? tk : 0)];
+    tok_ok[i] = tk < ch.count;
+    const int q = a.perm[ch.start + (tok_ok[i] ? tk : 0)];
     const int64_t r = a.a_by_token ? (q < a.pairs ? q / a.top_k : q - a.pairs) : q;
     arow[i] = a.aq + r * a.aq_stride;
-    srow[i] = a.as + r * a.as_stride + (B::kStepK == 32 ? a.as32_off : 0);
+    srow[i] = a.as + r * a.as_stride;
   }
   const uint8_t* base[NB];
   base[0] = uniform_ptr(a.w0 + (int64_t)ch.expert * a.expert_stride);
   if constexpr (NB == 2) base[NB - 1] = uniform_ptr(a.w1 + (int64_t)ch.expert * a.expert_stride);
-  uint8_t* buf = lds + wave * NB * BUF;
-  const uint32_t buf_lds = lds_address(buf);
   const uint32_t rb = (uint32_t)a.row_bytes;
 
   // this lane's DMA pieces: (row, piece) per load instruction
-  uint32_t prow[LOADS], ppc[LOADS];
+  uint32_t prow[Sh::LOADS], ppc[Sh::LOADS];
 #pragma unroll
-  for (int i = 0; i < LOADS; ++i) {
-    const int idx = min(64 * i + lane, PIECES - 1);
-    const int r = idx / PPR;
+  for (int i = 0; i < Sh::LOADS; ++i) {
+    const int idx = min(64 * i + lane, Sh::PIECES - 1);
+    const int r = idx / Sh::PPR;
     prow[i] = (uint32_t)min(n0 + r, a.N - 1) * rb;
-    ppc[i] = 16u * (uint32_t)(idx - r * PPR);
+    ppc[i] = 16u * (uint32_t)(idx - r * Sh::PPR);
   }
-  // this lane's B rows (one per subtile)
   uint32_t brow[NS];
 #pragma unroll
   for (int m = 0; m < NS; ++m) brow[m] = (uint32_t)min(n0 + 16 * m + n, a.N - 1) * rb;
+
+  const int groups = a.K / B::kStepK;
+  const int nchunk = (a.K + 255) >> 8;
+
+  // Issue chunk kc's loads into stage `slot`: the rows; for the decode
+  // pipeline also the token's 256 split elements (1 KB) and 16 group sums.
+  auto issue = [&](int kc, int slot) {
+    const uint32_t koff = (uint32_t)kc * (uint32_t)B::kSpan;
+    const uint32_t st = wlds_addr + (uint32_t)(slot * Sh::STAGE);
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+      for (int i = 0; i < Sh::LOADS; ++i)
+        load_lds16(base[nb], ((prow[i] + koff) & ~3u) + ppc[i],
+                   st + (uint32_t)(nb * Sh::LOADS * 1024 + 1024 * i));
+    if constexpr (PIPE == kPipeDecode) {
+      // lane l: 16 bytes [16 l, 16 l + 16) of the token's chunk; the sums
+      // (16 floats; lanes past them re-read the last one into slack)
+      const uint8_t* abase = uniform_ptr(reinterpret_cast<const uint8_t*>(arow[0] + 512 * kc));
+      load_lds16(abase, 16u * (uint32_t)lane, st + Sh::A_OFF);
+      const uint8_t* sbase = uniform_ptr(reinterpret_cast<const uint8_t*>(srow[0] + 16 * kc));
+      const int smax = min(16, (a.K >> 4) - 16 * kc) - 1;
+      load_lds4(sbase, 4u * (uint32_t)min(lane, smax), st + Sh::S_OFF);
+    }
+  };
 
   floatx4 tot[MT][NS][NB];
 #pragma unroll
@@ -379,43 +461,43 @@ __global__ void __launch_bounds__(64 * kGemmWaves) moe_gemm_kernel(MoeGemmArgs a
 #pragma unroll
       for (int nb = 0; nb < NB; ++nb) tot[i][m][nb] = floatx4{0.f, 0.f, 0.f, 0.f};
 
-  const int groups = a.K / B::kStepK;  // scale groups along K
-  const int nchunk = (a.K + 255) >> 8;
-  for (int kc = 0; kc < nchunk; ++kc) {
+  // ---- one chunk: scale table, then groups, then offsets
+  // get_a(i, j, af) fills tile i's fragments of group j; get_s(i, q)
+  // returns the sum of the group (4q + g) of tile i's lane token.
+  auto compute = [&](int kc, const uint8_t* stage, auto get_a, auto get_s) {
     const uint32_t koff = (uint32_t)kc * (uint32_t)B::kSpan;
-    // stage the wave's rows of this chunk
+    const int valid = min(KS, groups - kc * KS);
+    uint32_t sh[NS];
 #pragma unroll
-    for (int nb = 0; nb < NB; ++nb)
-#pragma unroll
-      for (int i = 0; i < LOADS; ++i)
-        load_lds16(base[nb], ((prow[i] + koff) & ~3u) + ppc[i],
-                   buf_lds + (uint32_t)(nb * BUF + 1024 * i));
-    wait_loads<0>();
-
-    const int gbase = kc * B::kSteps;  // first scale group of the chunk
-    float cq[NS][NB][NQ];
+    for (int m = 0; m < NS; ++m) sh[m] = ALIGNED ? (koff & 3u) : ((brow[m] + koff) & 3u);
+    // scale table: lane (n, g) decodes groups g*KS/4 .. +KS/4-1 of row n
 #pragma unroll
     for (int m = 0; m < NS; ++m)
 #pragma unroll
-      for (int nb = 0; nb < NB; ++nb)
+      for (int nb = 0; nb < NB; ++nb) {
+        const uint8_t* row = stage + nb * Sh::LOADS * 1024 + (16 * m + n) * B::kPitch;
 #pragma unroll
-        for (int q = 0; q < NQ; ++q) cq[m][nb][q] = 0.f;
-
+        for (int e = 0; e < KS / 4; ++e) {
+          const int j = g * (KS / 4) + e;
+          float delta, c;
+          B::scale(row, sh[m], j, delta, c);
+          const bool ok = j < valid;
+          table[((m * NB + nb) * KS + j) * 16 + n] = float2{ok ? delta : 0.f, ok ? -c : 0.f};
+        }
+      }
 #pragma unroll
-    for (int j = 0; j < B::kSteps; ++j) {
-      if (gbase + j < groups) {
-        AFrag<B::kWide> af[MT];
+    for (int j = 0; j < KS; ++j) {
+      if (j < valid) {
+        AF af[MT];
 #pragma unroll
-        for (int i = 0; i < MT; ++i) af[i].load(arow[i], kc, j, g);
+        for (int i = 0; i < MT; ++i) get_a(i, j, af[i]);
 #pragma unroll
-        for (int m = 0; m < NS; ++m) {
-          const uint32_t sh = (brow[m] + koff) & 3u;
+        for (int m = 0; m < NS; ++m)
 #pragma unroll
           for (int nb = 0; nb < NB; ++nb) {
-            typename B::Frag bf;
-            float delta, c;
-            B::step(buf + nb * BUF + (16 * m + n) * B::kPitch, sh, j, g, bf, delta, c);
-            if ((j & 3) == g) cq[m][nb][j >> 2] = -c;
+            const uint8_t* row = stage + nb * Sh::LOADS * 1024 + (16 * m + n) * B::kPitch;
+            const typename B::Frag bf = B::codes(row, sh[m], j, g, hbits);
+            const float delta = table[((m * NB + nb) * KS + j) * 16 + n].x;
 #pragma unroll
             for (int i = 0; i < MT; ++i) {
               floatx4 d = mfma_b(af[i].hi, bf, floatx4{0.f, 0.f, 0.f, 0.f});
@@ -427,25 +509,118 @@ __global__ void __launch_bounds__(64 * kGemmWaves) moe_gemm_kernel(MoeGemmArgs a
               t[3] = fmaf(delta, d[3], t[3]);
             }
           }
-        }
       }
     }
-    // offsets: sum over the chunk's groups of (-c) x (group sum), 4 groups
-    // per MFMA (K slice g = lane >> 4 is group 4q + g)
+    // offsets: group 4q + g of the chunk in K slice g of MFMA q
 #pragma unroll
-    for (int i = 0; i < MT; ++i) {
+    for (int q = 0; q < NQ; ++q) {
+      float cb[NS][NB];
 #pragma unroll
-      for (int q = 0; q < NQ; ++q) {
-        const int gi = min(gbase + 4 * q + g, groups - 1);
-        const float sv = srow[i][gi];
+      for (int m = 0; m < NS; ++m)
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb) cb[m][nb] = table[((m * NB + nb) * KS + 4 * q + g) * 16 + n].y;
+#pragma unroll
+      for (int i = 0; i < MT; ++i) {
+        const float sv = get_s(i, q);
 #pragma unroll
         for (int m = 0; m < NS; ++m)
 #pragma unroll
-          for (int nb = 0; nb < NB; ++nb) tot[i][m][nb] = mfma4f32(sv, cq[m][nb][q], tot[i][m][nb]);
+          for (int nb = 0; nb < NB; ++nb) tot[i][m][nb] = mfma4f32(sv, cb[m][nb], tot[i][m][nb]);
       }
     }
-    // every LDS read of this chunk has returned before the next DMA writes
-    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+  };
+
+  // group sum of element group gi of a split row (16-groups; a 32-group is
+  // the sum of its two halves)
+  auto row_sum = [&](const float* s, int gi) -> float {
+    if constexpr (B::kStepK == 32) return s[2 * gi] + s[2 * gi + 1];
+    else return s[gi];
+  };
+
+  if constexpr (PIPE == kPipeWide) {
+    for (int kc = 0; kc < nchunk; ++kc) {
+      issue(kc, 0);
+      __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
+      const int gbase = kc * KS;
+      compute(
+          kc, wlds,
+          [&](int i, int j, AF& af) {
+            if (tok_ok[i]) af.load(arow[i] + 512 * kc + AF::offset(j, g));
+            else af.zero();
+          },
+          [&](int i, int q) { return row_sum(srow[i], min(gbase + 4 * q + g, groups - 1)); });
+      __builtin_amdgcn_s_waitcnt(kWaitLgkm0);
+    }
+  } else if constexpr (PIPE == kPipeDouble) {
+    // chunk activations and sums in registers, one chunk ahead
+    AF acur[KS], anext[KS];
+    float scur[NQ], snext[NQ];
+    auto load_regs = [&](int kc, AF (&ar)[KS], float (&sr)[NQ]) {
+      const int valid = min(KS, groups - kc * KS);
+#pragma unroll
+      for (int j = 0; j < KS; ++j) {
+        if (tok_ok[0] && j < valid) ar[j].load(arow[0] + 512 * kc + AF::offset(j, g));
+        else ar[j].zero();
+      }
+#pragma unroll
+      for (int q = 0; q < NQ; ++q) sr[q] = row_sum(srow[0], min(kc * KS + 4 * q + g, groups - 1));
+    };
+    issue(0, 0);
+    load_regs(0, acur, scur);
+    __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
+    for (int kc = 0; kc < nchunk; ++kc) {
+      const bool more = kc + 1 < nchunk;
+      if (more) {
+        issue(kc + 1, (kc + 1) & 1);
+        load_regs(kc + 1, anext, snext);
+      }
+      compute(
+          kc, wlds + (kc & 1) * Sh::STAGE, [&](int, int j, AF& af) { af = acur[j]; },
+          [&](int, int q) { return scur[q]; });
+      __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
+      __builtin_amdgcn_s_waitcnt(kWaitLgkm0);
+      if (more) {
+#pragma unroll
+        for (int j = 0; j < KS; ++j) acur[j] = anext[j];
+#pragma unroll
+        for (int q = 0; q < NQ; ++q) scur[q] = snext[q];
+      }
+    }
+  } else {
+    // decode: one token, a ring of `depth` stages filled ahead of use
+    const int first = min(depth, nchunk);
+    for (int s = 0; s < first; ++s) issue(s, s);
+    for (int kc = 0; kc < nchunk; ++kc) {
+      const int ahead = min(nchunk, kc + depth) - kc - 1;  // stages issued after kc
+      // at most `ahead` stages (DMA loads each) may still be in flight; the
+      // counter holds 63, beyond which the wait is stricter than needed
+      switch (ahead) {
+        case 0: __builtin_amdgcn_s_waitcnt(waitcnt_vm(0)); break;
+        case 1: __builtin_amdgcn_s_waitcnt(waitcnt_vm(std::min(63, 1 * Sh::DMA))); break;
+        case 2: __builtin_amdgcn_s_waitcnt(waitcnt_vm(std::min(63, 2 * Sh::DMA))); break;
+        case 3: __builtin_amdgcn_s_waitcnt(waitcnt_vm(std::min(63, 3 * Sh::DMA))); break;
+        case 4: __builtin_amdgcn_s_waitcnt(waitcnt_vm(std::min(63, 4 * Sh::DMA))); break;
+        case 5: __builtin_amdgcn_s_waitcnt(waitcnt_vm(std::min(63, 5 * Sh::DMA))); break;
+        case 6: __builtin_amdgcn_s_waitcnt(waitcnt_vm(std::min(63, 6 * Sh::DMA))); break;
+        default: __builtin_amdgcn_s_waitcnt(waitcnt_vm(std::min(63, 7 * Sh::DMA))); break;
+      }
+      const int slot = kc % depth;
+      const uint8_t* stage = wlds + slot * Sh::STAGE;
+      const float* ssum = reinterpret_cast<const float*>(stage + Sh::S_OFF);
+      compute(
+          kc, stage,
+          [&](int, int j, AF& af) {
+            if (n == 0) af.load(reinterpret_cast<const uint16_t*>(stage + Sh::A_OFF) + AF::offset(j, g));
+            else af.zero();
+          },
+          [&](int, int q) {
+            const int gi = min(kc * KS + 4 * q + g, groups - 1) - kc * KS;
+            if constexpr (B::kStepK == 32) return ssum[2 * gi] + ssum[2 * gi + 1];
+            else return ssum[gi];
+          });
+      __builtin_amdgcn_s_waitcnt(kWaitLgkm0);
+      if (kc + depth < nchunk) issue(kc + depth, slot);
+    }
   }
 
   // ---------------------------------------------------------- epilogue
@@ -455,18 +630,17 @@ __global__ void __launch_bounds__(64 * kGemmWaves) moe_gemm_kernel(MoeGemmArgs a
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       const int tk = 16 * i + 4 * g + r;
-      const bool tok_ok = tk < ch.count;
-      const int q = tok_ok ? a.perm[ch.start + tk] : 0;
+      const bool ok_t = tk < ch.count;
+      const int q = ok_t ? a.perm[ch.start + tk] : 0;
       if constexpr (EPI == kEpiDown) {
 #pragma unroll
         for (int m = 0; m < NS; ++m) {
           const int row = n0 + 16 * m + n;
-          if (tok_ok && row < a.N) a.out[(int64_t)q * a.out_stride + row] = tot[i][m][0][r];
+          if (ok_t && row < a.N) a.out[(int64_t)q * a.out_stride + row] = tot[i][m][0][r];
         }
       } else {
         uint16_t* oq = a.oq + (int64_t)q * a.oq_stride;
         float* os = a.os + (int64_t)q * a.os_stride;
-        float s16[NS];
 #pragma unroll
         for (int m = 0; m < NS; ++m) {
           const int row = n0 + 16 * m + n;
@@ -480,23 +654,15 @@ __global__ void __launch_bounds__(64 * kGemmWaves) moe_gemm_kernel(MoeGemmArgs a
           uint32_t hb, lb;
           float sum;
           split_bf16(act, hb, lb, sum);
-          const bool ok = tok_ok && row < a.N;
+          const bool ok = ok_t && row < a.N;
           if (ok) {
             uint16_t* p = oq + 64 * (row >> 5) + (row & 31);
             p[0] = (uint16_t)hb;
             p[32] = (uint16_t)lb;
           }
-          s16[m] = group_sum(ok ? sum : 0.f, 4);
-        }
-        if (n == 0 && tok_ok) {
-#pragma unroll
-          for (int m = 0; m < NS; ++m) {
-            const int row = n0 + 16 * m;
-            if (row < a.N) {
-              os[row >> 4] = s16[m];
-              if ((m & 1) == 0) os[a.os32_off + (row >> 5)] = s16[m] + s16[m + 1];
-            }
-          }
+          // the 16 rows of the subtile are one 16-group of the activation row
+          const float s16 = group_sum(ok ? sum : 0.f, 4);
+          if (n == 0 && ok) os[row >> 4] = s16;
         }
       }
     }
@@ -505,39 +671,52 @@ __global__ void __launch_bounds__(64 * kGemmWaves) moe_gemm_kernel(MoeGemmArgs a
 
 // ------------------------------------------------------------------ host
 
-template <int TYPE, int EPI, int MT>
-static hipError_t launch_gemm_t(const MoeGemmArgs& a, int max_chunks, hipStream_t stream) {
-  constexpr int lds = gemm_lds_bytes<TYPE, EPI>();
-  const auto kernel = moe_gemm_kernel<TYPE, EPI, MT>;
+template <int TYPE, int EPI, int MT, int PIPE, bool ALIGNED>
+static hipError_t launch_gemm_t(const MoeGemmArgs& a_in, int max_chunks, hipStream_t stream) {
+  using Sh = GemmShape<TYPE, EPI, PIPE>;
+  MoeGemmArgs a = a_in;
+  const int nchunk = (a.K + 255) / 256;
+  a.depth = PIPE == kPipeDecode ? std::min(Sh::DEPTH, nchunk) : Sh::DEPTH;
+  const int lds = gemm_lds_bytes<TYPE, EPI, PIPE>(a.depth);
+  const auto kernel = moe_gemm_kernel<TYPE, EPI, MT, PIPE, ALIGNED>;
   if (lds > 65536) {
     hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kernel),
                                        hipFuncAttributeMaxDynamicSharedMemorySize, lds);
     if (e != hipSuccess) return e;
   }
-  constexpr int rows_per_block = kGemmWaves * 16 * EpiShape<EPI>::kSub;
+  constexpr int rows_per_block = Sh::kWaves * Sh::ROWS;
   const dim3 grid(max_chunks, (a.N + rows_per_block - 1) / rows_per_block);
-  hipLaunchKernelGGL(kernel, grid, dim3(64 * kGemmWaves), lds, stream, a);
+  hipLaunchKernelGGL(kernel, grid, dim3(64 * Sh::kWaves), lds, stream, a);
   return hipGetLastError();
 }
 
-template <int TYPE, int EPI>
+template <int TYPE, int EPI, bool ALIGNED>
 static hipError_t launch_gemm_mt(const MoeGemmArgs& a, int mt, int max_chunks, hipStream_t s) {
   switch (mt) {
-    case 1: return launch_gemm_t<TYPE, EPI, 1>(a, max_chunks, s);
-    case 2: return launch_gemm_t<TYPE, EPI, 2>(a, max_chunks, s);
-    case 4: return launch_gemm_t<TYPE, EPI, 4>(a, max_chunks, s);
+    case 0: return launch_gemm_t<TYPE, EPI, 1, kPipeDecode, ALIGNED>(a, max_chunks, s);
+    case 1: return launch_gemm_t<TYPE, EPI, 1, kPipeDouble, ALIGNED>(a, max_chunks, s);
+    case 2: return launch_gemm_t<TYPE, EPI, 2, kPipeWide, ALIGNED>(a, max_chunks, s);
+    case 4: return launch_gemm_t<TYPE, EPI, 4, kPipeWide, ALIGNED>(a, max_chunks, s);
     default: return hipErrorInvalidValue;
   }
+}
+
+template <int TYPE, int EPI>
+static hipError_t launch_gemm_al(const MoeGemmArgs& a, int mt, int max_chunks, hipStream_t s) {
+  // Q4_K rows are always whole 144-byte blocks (16-byte multiples)
+  if (TYPE == kQ4_K || a.row_bytes % 4 == 0) return launch_gemm_mt<TYPE, EPI, true>(a, mt, max_chunks, s);
+  if constexpr (TYPE != kQ4_K) return launch_gemm_mt<TYPE, EPI, false>(a, mt, max_chunks, s);
+  return hipErrorInvalidValue;
 }
 
 template <int EPI>
 static hipError_t launch_gemm_epi(int type, const MoeGemmArgs& a, int mt, int max_chunks,
                                   hipStream_t s) {
   switch (type) {
-    case kQ4_K: return launch_gemm_mt<kQ4_K, EPI>(a, mt, max_chunks, s);
-    case kQ6_K: return launch_gemm_mt<kQ6_K, EPI>(a, mt, max_chunks, s);
-    case kQ5_0: return launch_gemm_mt<kQ5_0, EPI>(a, mt, max_chunks, s);
-    case kQ8_0: return launch_gemm_mt<kQ8_0, EPI>(a, mt, max_chunks, s);
+    case kQ4_K: return launch_gemm_al<kQ4_K, EPI>(a, mt, max_chunks, s);
+    case kQ6_K: return launch_gemm_al<kQ6_K, EPI>(a, mt, max_chunks, s);
+    case kQ5_0: return launch_gemm_al<kQ5_0, EPI>(a, mt, max_chunks, s);
+    case kQ8_0: return launch_gemm_al<kQ8_0, EPI>(a, mt, max_chunks, s);
     default: return hipErrorInvalidValue;
   }
 }
