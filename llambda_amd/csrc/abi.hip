@@ -397,8 +397,8 @@ struct llambda_hip_moe_session {
   hipStream_t stream = nullptr;
   MoePlan plan{};
   DevBuf router, bias, gate, up, down, sh_gate, sh_up, sh_down;
-  DevBuf logits, top_idx, top_w, shared_w, counts, perm, chunks, chunk_counts, act, down_out,
-      error, xq, xsum, aq, asum;
+  DevBuf logits, top_idx, top_w, shared_w, counts, perm, chunks, chunk_counts, down_out, error,
+      xq, xsum, aq, asum;
   DevBuf x, y;
   int staged = 0;
   ~llambda_hip_moe_session() {
@@ -418,7 +418,6 @@ struct llambda_hip_moe_session {
     perm.alloc(pairs * sizeof(int), "permutation");
     p.capacity = tokens;
     chunks.alloc((size_t)moe_max_chunks(p, tokens, 1) * sizeof(MoeChunk), "chunk table");
-    act.alloc(pairs * act_w * sizeof(float), "activations");
     down_out.alloc(pairs * (size_t)p.hidden * sizeof(float), "expert outputs");
     const size_t H = (size_t)p.hidden;
     // the decode pipeline stages whole 256-element chunks (1 KB of split
@@ -437,7 +436,6 @@ struct llambda_hip_moe_session {
     p.shared_w = shared_w.as<float>();
     p.perm = perm.as<int>();
     p.chunks = chunks.as<MoeChunk>();
-    p.act = act.as<float>();
     p.down_out = down_out.as<float>();
   }
   void ensure_staging(int tokens) {
@@ -508,9 +506,10 @@ int llambda_hip_moe_session_create(const llambda_hip_moe_desc* d,
         failf("moe_session_create: expert tensors must be Q4_K, Q6_K, Q5_0 or Q8_0 (got tag %d)", t);
     const int64_t up_rb = checked_row_bytes(d->up_type, H, "ffn_up_exps");
     const int64_t down_rb = checked_row_bytes(d->down_type, F, "ffn_down_exps");
-    // LDS limit of the grouped kernels: kMoeChunkTokens rows of activations
-    if ((size_t)kMoeChunkTokens * (std::max(H, std::max(F, Fs)) * 17 / 16) * 4 > 160 * 1024)
-      failf("moe_session_create: hidden/ffn too large for the LDS tiles");
+    // the expert kernels address one expert's slab with 32-bit offsets
+    if (F * up_rb + (int64_t)kWeightPad >= ((int64_t)1 << 31) ||
+        H * down_rb + (int64_t)kWeightPad >= ((int64_t)1 << 31))
+      failf("moe_session_create: one expert's slab exceeds 2 GiB");
 
     auto* s = new llambda_hip_moe_session();
     try {
@@ -573,6 +572,13 @@ int llambda_hip_moe_session_create(const llambda_hip_moe_desc* d,
                        H * (Fs / block_weights(d->shared_down_type)), s->stream, "ffn_down_shexp");
         p.sh_up = s->sh_up.as<uint8_t>();
         p.sh_down = s->sh_down.as<uint8_t>();
+      }
+      {
+        auto dword_rows = [](int type, int64_t columns) {
+          return type == kQ4_K || (columns / block_weights(type) * block_bytes(type)) % 4 == 0;
+        };
+        p.wide4 = dword_rows(p.up_type, H) && dword_rows(p.down_type, F) &&
+                  (Fs == 0 || (dword_rows(p.sh_up_type, H) && dword_rows(p.sh_down_type, Fs)));
       }
       s->counts.alloc((size_t)E * sizeof(int), "expert histogram");
       s->chunk_counts.alloc(2 * sizeof(int), "chunk counts");
@@ -641,6 +647,8 @@ int llambda_hip_moe_session_run_device(llambda_hip_moe_session* s, const float* 
     if (!s) failf("moe_session_run_device: null session");
     if (!input || !output) failf("moe_session_run_device: null input or output");
     if (batch == 0 || batch > (1u << 20)) failf("moe_session_run_device: bad batch %zu", batch);
+    if (reinterpret_cast<uintptr_t>(input) & 15u)
+      failf("moe_session_run_device: input must be 16-byte aligned");
     std::lock_guard<std::mutex> lock(s->run_mutex);
     HIPC(hipSetDevice(s->device));
     const int T = (int)batch;

@@ -23,10 +23,9 @@ enum MoeVariant : int { kQwen3Next = 0, kNemotronH = 1 };
 struct MoeChunk {
   int expert;  // slab index within its group (routed: expert id; shared: 0)
   int start;   // first entry of the permutation
-  int count;   // pairs in this chunk (1..kMoeChunkTokens)
+  int count;   // pairs in this chunk (1..64)
 };
 
-constexpr int kMoeChunkTokens = 4;  // tokens per chunk (grouped kernels, batch > 1)
 constexpr int kMoeMaxExperts = 1024;
 constexpr int kMoeMaxTopK = 64;
 
@@ -36,6 +35,7 @@ struct MoePlan {
   int hidden, experts, top_k, ffn, shared_ffn;
   float weights_scale;
   int weights_norm;
+  int wide4;  // every expert tensor has dword-multiple rows: 4-tile chunks allowed
   // weights
   const float* router;   // [(experts + (variant == qwen3next && shared)) ][hidden]
   const float* bias;     // [experts], nemotron
@@ -57,7 +57,6 @@ struct MoePlan {
   int* perm;           // [capacity * (top_k + 1)]
   MoeChunk* chunks;    // [max_chunks(capacity)]
   int* chunk_counts;   // [2]: routed chunks, shared chunks
-  float* act;          // [capacity * (top_k + 1)][max(ffn, shared_ffn)]  (batch 1)
   // split rows (moe_mfma.hip) of the multi-token path
   uint16_t* xq;        // [capacity][2 hidden]           x as bf16 hi/lo
   float* xsum;         // [capacity][hidden/16]          16-group sums
@@ -105,10 +104,10 @@ struct MoeGemmArgs {
   int depth;  // LDS stages per wave (set by the launcher)
 };
 
-hipError_t split_rows_launch(const float* x, int rows, int K, uint16_t* q, int64_t q_stride,
-                             float* s, int64_t s_stride, hipStream_t stream);
+// Router logits of T tokens (fp32 MFMA) and the split rows of x (q, s).
 hipError_t router_mfma_launch(const float* x, int T, const float* R, int Er, int H, float* logits,
-                              int ld, hipStream_t stream);
+                              int ld, uint16_t* q, int64_t q_stride, float* s, int64_t s_stride,
+                              hipStream_t stream);
 // mt: token tiles per chunk (1, 2, 4), or 0 for a batch of one token.
 hipError_t moe_gemm_launch(int type, int epi, const MoeGemmArgs& a, int mt, int max_chunks,
                            hipStream_t stream);

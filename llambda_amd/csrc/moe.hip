@@ -1,4 +1,5 @@
-// moe.hip -- routed-MoE feed-forward kernels for gfx950 (see moe.h).
+// moe.hip -- routed-MoE feed-forward: routing, permutation, combine and the
+// forward's launch sequence (the expert products are in moe_mfma.hip).
 #include "moe.h"
 #include "activations.h"
 
@@ -13,11 +14,12 @@ namespace llhip {
 // order, the k largest logits strictly above most-negative-single-float,
 // lower index first among equal values, never NaN; unfilled slots stay
 // (-1, -FLT_MAX).  Here one wavefront holds JPL logits per lane and takes k
-// rounds of a wave-wide (value desc, index asc) arg-max.  `bias` (optional)
-// is added first and the biased logits are written back.
+// rounds of a wave-wide (value desc, index asc) arg-max; lane r keeps rank
+// r.  `bias` (optional) is added first and the biased logits are written
+// back.
 template <int JPL>
 __device__ __forceinline__ void wave_select(float* lg, const float* bias, int E, int K, int lane,
-                                            int* out_idx, float* out_val) {
+                                            int& my_idx, float& my_val) {
   float vals[JPL];
 #pragma unroll
   for (int j = 0; j < JPL; ++j) {
@@ -33,6 +35,8 @@ __device__ __forceinline__ void wave_select(float* lg, const float* bias, int E,
     }
     vals[j] = v;
   }
+  my_idx = -1;
+  my_val = -FLT_MAX;
   for (int r = 0; r < K; ++r) {
     float bv = -INFINITY;
     int bi = INT_MAX;
@@ -57,9 +61,9 @@ __device__ __forceinline__ void wave_select(float* lg, const float* bias, int E,
       for (int j = 0; j < JPL; ++j)
         if (j == (bi >> 6)) vals[j] = -INFINITY;
     }
-    if (lane == 0) {
-      out_idx[r] = bi == INT_MAX ? -1 : bi;
-      out_val[r] = bi == INT_MAX ? -FLT_MAX : bv;
+    if (lane == r && bi != INT_MAX) {
+      my_idx = bi;
+      my_val = bv;
     }
   }
 }
@@ -70,47 +74,72 @@ __global__ void __launch_bounds__(256) topk_kernel(const float* __restrict__ log
                                                    float* __restrict__ val) {
   const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
   if (t >= batch) return;
-  wave_select<JPL>(const_cast<float*>(logits + (int64_t)t * n), nullptr, n, k,
-                   threadIdx.x & 63, idx + (int64_t)t * k, val + (int64_t)t * k);
+  const int lane = threadIdx.x & 63;
+  int mi;
+  float mv;
+  wave_select<JPL>(const_cast<float*>(logits + (int64_t)t * n), nullptr, n, k, lane, mi, mv);
+  if (lane < k) {
+    idx[(int64_t)t * k + lane] = mi;
+    val[(int64_t)t * k + lane] = mv;
+  }
 }
 
 // Top-k plus the gating weights of llambda.lisp:5365-5379 (qwen3next:
 // sigmoid, renormalise, error when the sum is not positive) or 5894-5913
-// (nemotron: bias before selection, sigmoid, optional renormalise, scale);
-// then the expert histogram.
+// (nemotron: bias before selection, sigmoid, optional renormalise, scale).
+// The weight sum runs over the ranks in order, as the reference's loop does.
+// Then either the expert histogram (batches) or, for a single token, the
+// chunk table itself: one chunk per selected expert in rank order, then the
+// shared expert.
 template <int JPL>
-__global__ void __launch_bounds__(256) topk_gate_kernel(MoePlan p, int tokens) {
+__global__ void __launch_bounds__(256) topk_gate_kernel(MoePlan p, int tokens, int single) {
 #pragma clang fp contract(off)
   const int lane = threadIdx.x & 63;
   const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
   if (t >= tokens) return;
   const int E = p.experts, K = p.top_k;
   float* lg = p.logits + (int64_t)t * (E + 1);
-  int* ti = p.top_idx + (int64_t)t * K;
-  float* tw = p.top_w + (int64_t)t * K;
-  wave_select<JPL>(lg, p.variant == kNemotronH ? p.bias : nullptr, E, K, lane, ti, tw);
-  if (lane != 0) return;
-  int err = 0;
+  int mi;
+  float mv;
+  wave_select<JPL>(lg, p.variant == kNemotronH ? p.bias : nullptr, E, K, lane, mi, mv);
+  const bool has = lane < K;
+  float w = has ? sigmoid_ref(mv) : 0.f;
   float sum = 0.f;
-  for (int r = 0; r < K; ++r) {
-    if (ti[r] < 0) err |= 1;
-    const float w = sigmoid_ref(tw[r]);
-    tw[r] = w;
-    sum = sum + w;
-  }
+  for (int r = 0; r < K; ++r) sum = sum + __shfl(w, r, kWave);
+  int err = (has && mi < 0) ? 1 : 0;
   if (p.variant == kQwen3Next || p.weights_norm) {
-    if (!(sum > 0.f)) {
-      err |= 2;
-    } else {
-      for (int r = 0; r < K; ++r) tw[r] = tw[r] / sum;
-    }
+    if (!(sum > 0.f)) err |= 2;
+    else w = w / sum;
   }
-  if (p.variant == kNemotronH)
-    for (int r = 0; r < K; ++r) tw[r] = p.weights_scale * tw[r];
-  p.shared_w[t] = p.variant == kQwen3Next ? sigmoid_ref(lg[E]) : 1.f;
-  for (int r = 0; r < K; ++r)
-    if (ti[r] >= 0) atomicAdd(&p.counts[ti[r]], 1);
+  if (p.variant == kNemotronH) w = p.weights_scale * w;
+  if (has) {
+    p.top_idx[(int64_t)t * K + lane] = mi;
+    p.top_w[(int64_t)t * K + lane] = w;
+  }
+  if (lane == 0) p.shared_w[t] = p.variant == kQwen3Next ? sigmoid_ref(lg[E]) : 1.f;
   if (err) atomicOr(p.error, err);
+  const bool valid = has && mi >= 0 && mi < E;
+  if (!single) {
+    if (valid) atomicAdd(&p.counts[mi], 1);
+    return;
+  }
+  // single token: pair id of rank r is r; the shared pair is K
+  const uint64_t mask = __ballot(valid);
+  const int pos = __popcll(mask & ((1ull << lane) - 1ull));
+  const int nvalid = __popcll(mask);
+  if (valid) {
+    p.chunks[pos] = MoeChunk{mi, pos, 1};
+    p.perm[pos] = lane;
+  }
+  if (lane == 0) {
+    const int has_shared = p.shared_ffn > 0;
+    if (has_shared) {
+      p.chunks[nvalid] = MoeChunk{0, nvalid, 1};
+      p.perm[nvalid] = K;
+    }
+    p.chunk_counts[0] = nvalid;
+    p.chunk_counts[1] = has_shared;
+  }
 }
 
 // ------------------------------------------------------------ scan/scatter
@@ -202,175 +231,6 @@ __global__ void __launch_bounds__(kScanThreads) moe_scan_kernel(MoePlan p, int t
   }
 }
 
-// ------------------------------------------------------- grouped experts
-// One group is either the routed experts (slabs of E experts, chunk table
-// entries [0, chunk_counts[0])) or the shared expert (one slab, entries
-// after the routed ones).
-struct MoeGroup {
-  int group;              // 0 routed, 1 shared
-  const uint8_t* gate;    // qwen3next gate rows (null for nemotron)
-  const uint8_t* up;
-  int64_t up_row_bytes;
-  int64_t up_expert_stride;  // bytes between experts' gate/up slabs
-  int ffn;                   // rows per expert of gate/up = columns of down
-  const uint8_t* down;
-  int64_t down_row_bytes;
-  int64_t down_expert_stride;
-  int act_stride;            // floats per pair row of act
-  int up_iters;              // row iterations per workgroup (up kernel)
-  int down_iters;            // row iterations per workgroup (down kernel)
-};
-
-template <int NT>
-__device__ __forceinline__ bool load_chunk(const MoePlan& p, const MoeGroup& g, int tokens,
-                                           MoeChunk& c, int* pair_of) {
-  const int nchunks = p.chunk_counts[g.group];
-  if ((int)blockIdx.x >= nchunks) return false;
-  const int cbase = g.group == 0 ? 0 : p.chunk_counts[0];
-  c = p.chunks[cbase + blockIdx.x];
-  if (threadIdx.x < NT)
-    pair_of[threadIdx.x] = (int)threadIdx.x < c.count ? p.perm[c.start + threadIdx.x] : -1;
-  (void)tokens;
-  return true;
-}
-
-// gate/up rows of one expert against the chunk's tokens, activation fused:
-// qwen3next  act = fl(silu(g) * u)  (llambda.lisp:5386-5401)
-// nemotron   act = relu(u)^2        (llambda.lisp:5921-5926)
-template <int TU, int NT, int VARIANT>
-__global__ void __launch_bounds__(256) moe_up_kernel(MoePlan p, MoeGroup g,
-                                                     const float* __restrict__ x, int tokens) {
-#pragma clang fp contract(off)
-  __shared__ int pair_of[NT];
-  __shared__ const float* src[NT];
-  MoeChunk c;
-  if (!load_chunk<NT>(p, g, tokens, c, pair_of)) return;
-  const int H = p.hidden, K = p.top_k, P = tokens * K;
-  __syncthreads();
-  if (threadIdx.x < NT) {
-    const int q = pair_of[threadIdx.x];
-    src[threadIdx.x] = q < 0 ? nullptr : x + (int64_t)(q < P ? q / K : q - P) * H;
-  }
-  __syncthreads();
-  extern __shared__ float smem[];
-  float* xs = smem;
-  float* xg = smem + NT * H;
-  stage_rows<NT>(xs, xg, src, H);
-  __syncthreads();
-  const XView xv{xs, xg, H, H >> 4};
-
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int lpr_log2 = lanes_per_row_log2(H);
-  const int lpr = 1 << lpr_log2, slot = lane >> lpr_log2, l = lane & (lpr - 1);
-  const int slots = kWave >> lpr_log2;
-  const int units = H >> 5;
-  const uint8_t* gate_e = g.gate + (int64_t)c.expert * g.up_expert_stride;
-  const uint8_t* up_e = g.up + (int64_t)c.expert * g.up_expert_stride;
-  // rows handled per wave iteration: qwen3next 1 (gate+up), nemotron 2
-  constexpr int ITEMS = VARIANT == kQwen3Next ? 1 : 2;
-  const int per_iter = 4 * slots * ITEMS;
-  const int tile0 = blockIdx.y * per_iter * g.up_iters;
-  for (int it = 0; it < g.up_iters; ++it) {
-    const int f0 = tile0 + it * per_iter + (wave * slots + slot) * ITEMS;
-    const uint8_t* rp[2];
-    bool valid[2];
-    int f[2];
-    if constexpr (VARIANT == kQwen3Next) {
-      f[0] = f[1] = f0;
-      valid[0] = valid[1] = f0 < g.ffn;
-      rp[0] = gate_e + (int64_t)(valid[0] ? f0 : 0) * g.up_row_bytes;
-      rp[1] = up_e + (int64_t)(valid[1] ? f0 : 0) * g.up_row_bytes;
-    } else {
-#pragma unroll
-      for (int r = 0; r < 2; ++r) {
-        f[r] = f0 + r;
-        valid[r] = f[r] < g.ffn;
-        rp[r] = up_e + (int64_t)(valid[r] ? f[r] : 0) * g.up_row_bytes;
-      }
-    }
-    float acc[2][NT];
-    rows_dot<TU, NT, 2>(rp, valid, l, lpr, units, xv, acc);
-#pragma unroll
-    for (int r = 0; r < 2; ++r)
-#pragma unroll
-      for (int t = 0; t < NT; ++t) acc[r][t] = segment_sum_dyn(acc[r][t], lpr);
-    if (l == 0) {
-#pragma unroll
-      for (int t = 0; t < NT; ++t) {
-        const int q = pair_of[t];
-        if (q < 0) continue;
-        float* row = p.act + (int64_t)q * g.act_stride;
-        if constexpr (VARIANT == kQwen3Next) {
-          if (valid[0]) row[f0] = silu_ref(acc[0][t]) * acc[1][t];
-        } else {
-#pragma unroll
-          for (int r = 0; r < 2; ++r)
-            if (valid[r]) row[f[r]] = relu2_ref(acc[r][t]);
-        }
-      }
-    }
-  }
-}
-
-// down rows of one expert against the chunk's activations, one output row
-// per pair: down_out[pair][i] (llambda.lisp:5402-5408, 5927-5931).
-template <int TD, int NT>
-__global__ void __launch_bounds__(256) moe_down_kernel(MoePlan p, MoeGroup g, int tokens) {
-  __shared__ int pair_of[NT];
-  __shared__ const float* src[NT];
-  MoeChunk c;
-  if (!load_chunk<NT>(p, g, tokens, c, pair_of)) return;
-  const int H = p.hidden, F = g.ffn;
-  __syncthreads();
-  if (threadIdx.x < NT) {
-    const int q = pair_of[threadIdx.x];
-    src[threadIdx.x] = q < 0 ? nullptr : p.act + (int64_t)q * g.act_stride;
-  }
-  __syncthreads();
-  extern __shared__ float smem[];
-  float* xs = smem;
-  float* xg = smem + NT * F;
-  stage_rows<NT>(xs, xg, src, F);
-  __syncthreads();
-  const XView xv{xs, xg, F, F >> 4};
-
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int lpr_log2 = lanes_per_row_log2(F);
-  const int lpr = 1 << lpr_log2, slot = lane >> lpr_log2, l = lane & (lpr - 1);
-  const int slots = kWave >> lpr_log2;
-  const int units = F >> 5;
-  const uint8_t* down_e = g.down + (int64_t)c.expert * g.down_expert_stride;
-  constexpr int R = 2;
-  const int per_iter = 4 * slots * R;
-  const int tile0 = blockIdx.y * per_iter * g.down_iters;
-  for (int it = 0; it < g.down_iters; ++it) {
-    const int i0 = tile0 + it * per_iter + (wave * slots + slot) * R;
-    const uint8_t* rp[R];
-    bool valid[R];
-#pragma unroll
-    for (int r = 0; r < R; ++r) {
-      valid[r] = i0 + r < H;
-      rp[r] = down_e + (int64_t)(valid[r] ? i0 + r : 0) * g.down_row_bytes;
-    }
-    float acc[R][NT];
-    rows_dot<TD, NT, R>(rp, valid, l, lpr, units, xv, acc);
-#pragma unroll
-    for (int r = 0; r < R; ++r)
-#pragma unroll
-      for (int t = 0; t < NT; ++t) acc[r][t] = segment_sum_dyn(acc[r][t], lpr);
-    if (l == 0) {
-#pragma unroll
-      for (int t = 0; t < NT; ++t) {
-        const int q = pair_of[t];
-        if (q < 0) continue;
-#pragma unroll
-        for (int r = 0; r < R; ++r)
-          if (valid[r]) p.down_out[(int64_t)q * H + i0 + r] = acc[r][t];
-      }
-    }
-  }
-}
-
 // Weighted combine in rank order, then the shared expert, every product and
 // sum rounded separately as in vector-add-scaled-in-place /
 // vector-add-bias-in-place (llambda.lisp:3465-3489; 5359, 5409, 5426, 5914,
@@ -431,125 +291,52 @@ static int jpl_for(int E) {
   return j;
 }
 
-template <int NT, int VARIANT>
-static hipError_t launch_up(const MoePlan& p, const MoeGroup& g, int type, int chunks,
-                            const float* x, int tokens, hipStream_t s) {
-  const int slots = kWave >> lanes_per_row_log2(p.hidden);
-  const int items = VARIANT == kQwen3Next ? 1 : 2;
-  const int per_block = 4 * slots * items * g.up_iters;
-  const dim3 grid(chunks, (g.ffn + per_block - 1) / per_block);
-  const size_t lds = (size_t)NT * (p.hidden + (p.hidden >> 4)) * sizeof(float);
-  switch (type) {
-    case kQ4_K: return launch(moe_up_kernel<kQ4_K, NT, VARIANT>, grid, dim3(256), lds, s, p, g, x, tokens);
-    case kQ6_K: return launch(moe_up_kernel<kQ6_K, NT, VARIANT>, grid, dim3(256), lds, s, p, g, x, tokens);
-    case kQ5_0: return launch(moe_up_kernel<kQ5_0, NT, VARIANT>, grid, dim3(256), lds, s, p, g, x, tokens);
-    case kQ8_0: return launch(moe_up_kernel<kQ8_0, NT, VARIANT>, grid, dim3(256), lds, s, p, g, x, tokens);
-    default: return hipErrorInvalidValue;
-  }
-}
-
-template <int NT>
-static hipError_t launch_down(const MoePlan& p, const MoeGroup& g, int type, int chunks,
-                              int tokens, hipStream_t s) {
-  const int slots = kWave >> lanes_per_row_log2(g.ffn);
-  const int per_block = 4 * slots * 2 * g.down_iters;
-  const dim3 grid(chunks, (p.hidden + per_block - 1) / per_block);
-  const size_t lds = (size_t)NT * (g.ffn + (g.ffn >> 4)) * sizeof(float);
-  switch (type) {
-    case kQ4_K: return launch(moe_down_kernel<kQ4_K, NT>, grid, dim3(256), lds, s, p, g, tokens);
-    case kQ6_K: return launch(moe_down_kernel<kQ6_K, NT>, grid, dim3(256), lds, s, p, g, tokens);
-    case kQ5_0: return launch(moe_down_kernel<kQ5_0, NT>, grid, dim3(256), lds, s, p, g, tokens);
-    case kQ8_0: return launch(moe_down_kernel<kQ8_0, NT>, grid, dim3(256), lds, s, p, g, tokens);
-    default: return hipErrorInvalidValue;
-  }
-}
-
 static int64_t row_bytes_of(int type, int64_t columns) {
   return columns / block_weights(type) * block_bytes(type);
 }
 
-template <int NT>
-static hipError_t launch_groups(const MoePlan& p, const float* x, int tokens, hipStream_t s) {
-  const int has_shared = p.shared_ffn > 0;
-  const int act_stride = std::max(p.ffn, p.shared_ffn);
-  const int64_t pairs = (int64_t)tokens * p.top_k;
-  const int routed_chunks = (int)(pairs / NT + std::min<int64_t>(p.experts, pairs));
-  const int shared_chunks = (tokens + NT - 1) / NT;
-  MoeGroup routed{};
-  routed.group = 0;
-  routed.gate = p.gate;
-  routed.up = p.up;
-  routed.up_row_bytes = row_bytes_of(p.up_type, p.hidden);
-  routed.up_expert_stride = routed.up_row_bytes * p.ffn;
-  routed.ffn = p.ffn;
-  routed.down = p.down;
-  routed.down_row_bytes = row_bytes_of(p.down_type, p.ffn);
-  routed.down_expert_stride = routed.down_row_bytes * p.hidden;
-  routed.act_stride = act_stride;
-  routed.up_iters = 4;
-  routed.down_iters = 4;
-  MoeGroup shared = routed;
-  shared.group = 1;
-  shared.gate = p.sh_gate;
-  shared.up = p.sh_up;
-  shared.up_row_bytes = row_bytes_of(p.sh_up_type, p.hidden);
-  shared.up_expert_stride = 0;
-  shared.ffn = p.shared_ffn;
-  shared.down = p.sh_down;
-  shared.down_row_bytes = row_bytes_of(p.sh_down_type, p.shared_ffn);
-  shared.down_expert_stride = 0;
-
-  hipError_t e;
-  if (p.variant == kQwen3Next) {
-    e = launch_up<NT, kQwen3Next>(p, routed, p.up_type, routed_chunks, x, tokens, s);
-    if (e == hipSuccess && has_shared)
-      e = launch_up<NT, kQwen3Next>(p, shared, p.sh_up_type, shared_chunks, x, tokens, s);
-  } else {
-    e = launch_up<NT, kNemotronH>(p, routed, p.up_type, routed_chunks, x, tokens, s);
-    if (e == hipSuccess && has_shared)
-      e = launch_up<NT, kNemotronH>(p, shared, p.sh_up_type, shared_chunks, x, tokens, s);
-  }
-  if (e != hipSuccess) return e;
-  e = launch_down<NT>(p, routed, p.down_type, routed_chunks, tokens, s);
-  if (e == hipSuccess && has_shared)
-    e = launch_down<NT>(p, shared, p.sh_down_type, shared_chunks, tokens, s);
-  return e;
-}
-
 // Token-tile count (16 tokens each) of the grouped MFMA chunks: enough to
-// cover the average (token, rank) pairs per expert, at most 4.
+// cover the average (token, rank) pairs per expert, at most 4 (2 when some
+// expert tensor has rows that are not a whole number of dwords).  0 selects
+// the single-token pipeline.
 static int moe_mfma_tiles(const MoePlan& p, int tokens) {
-  if (tokens == 1) return 0;  // the decode pipeline: one token per chunk
+  if (tokens == 1) return 0;
   const int64_t avg = ((int64_t)tokens * p.top_k + p.experts - 1) / p.experts;
-  return avg <= 16 ? 1 : avg <= 40 ? 2 : 4;
+  return avg <= 16 ? 1 : (avg <= 40 || !p.wide4) ? 2 : 4;
 }
 
-// The multi-token forward on MFMA (moe_mfma.hip): split x, router GEMM,
-// top-k, scan, grouped gate/up and down products, combine.
-static hipError_t moe_forward_mfma(const MoePlan& p, const float* x, float* y, int tokens,
-                                   hipStream_t s) {
+// One forward: router GEMM (+ split x), top-k and gating, scan (batches),
+// grouped gate/up and down products, combine.
+hipError_t moe_forward_launch(const MoePlan& p, const float* x, float* y, int tokens,
+                              hipStream_t s) {
+  if (tokens <= 0) return hipSuccess;
+  if (tokens > p.capacity) return hipErrorInvalidValue;
+  // the router and the split read x with 16-byte loads
+  if (reinterpret_cast<uintptr_t>(x) & 15u) return hipErrorInvalidValue;
   const int has_shared = p.shared_ffn > 0;
   const int H = p.hidden, E = p.experts, K = p.top_k;
   const int act_w = std::max(p.ffn, p.shared_ffn);
   const int64_t xs_stride = H / 16, as_stride = act_w / 16;
-  hipError_t e = split_rows_launch(x, tokens, H, p.xq, 2 * (int64_t)H, p.xsum, xs_stride, s);
-  if (e != hipSuccess) return e;
   const int er = E + ((p.variant == kQwen3Next && has_shared) ? 1 : 0);
-  e = router_mfma_launch(x, tokens, p.router, er, H, p.logits, E + 1, s);
+  hipError_t e = router_mfma_launch(x, tokens, p.router, er, H, p.logits, E + 1, p.xq,
+                                    2 * (int64_t)H, p.xsum, xs_stride, s);
   if (e != hipSuccess) return e;
+  const int single = tokens == 1;
   const dim3 tgrid((tokens + 3) / 4);
   switch (jpl_for(E)) {
-    case 1: e = launch(topk_gate_kernel<1>, tgrid, dim3(256), 0, s, p, tokens); break;
-    case 2: e = launch(topk_gate_kernel<2>, tgrid, dim3(256), 0, s, p, tokens); break;
-    case 4: e = launch(topk_gate_kernel<4>, tgrid, dim3(256), 0, s, p, tokens); break;
-    case 8: e = launch(topk_gate_kernel<8>, tgrid, dim3(256), 0, s, p, tokens); break;
-    case 16: e = launch(topk_gate_kernel<16>, tgrid, dim3(256), 0, s, p, tokens); break;
+    case 1: e = launch(topk_gate_kernel<1>, tgrid, dim3(256), 0, s, p, tokens, single); break;
+    case 2: e = launch(topk_gate_kernel<2>, tgrid, dim3(256), 0, s, p, tokens, single); break;
+    case 4: e = launch(topk_gate_kernel<4>, tgrid, dim3(256), 0, s, p, tokens, single); break;
+    case 8: e = launch(topk_gate_kernel<8>, tgrid, dim3(256), 0, s, p, tokens, single); break;
+    case 16: e = launch(topk_gate_kernel<16>, tgrid, dim3(256), 0, s, p, tokens, single); break;
     default: return hipErrorInvalidValue;
   }
   if (e != hipSuccess) return e;
   const int mt = moe_mfma_tiles(p, tokens), nt = 16 * std::max(mt, 1);
-  e = launch(moe_scan_kernel, dim3(1), dim3(kScanThreads), 0, s, p, tokens, nt, has_shared);
-  if (e != hipSuccess) return e;
+  if (!single) {
+    e = launch(moe_scan_kernel, dim3(1), dim3(kScanThreads), 0, s, p, tokens, nt, has_shared);
+    if (e != hipSuccess) return e;
+  }
   const int64_t pairs = (int64_t)tokens * K;
   const int routed_chunks = (int)(pairs / nt + std::min<int64_t>(E, pairs));
   const int shared_chunks = (tokens + nt - 1) / nt;
@@ -627,51 +414,6 @@ static hipError_t moe_forward_mfma(const MoePlan& p, const float* x, float* y, i
   }
   return launch(moe_combine_kernel, dim3((H + 255) / 256, tokens), dim3(256), 0, s, p, y, tokens,
                 has_shared);
-}
-
-hipError_t moe_forward_launch(const MoePlan& p, const float* x, float* y, int tokens,
-                              hipStream_t s) {
-  if (tokens <= 0) return hipSuccess;
-  if (tokens > p.capacity) return hipErrorInvalidValue;
-  // the MFMA path reads x with 16-byte loads
-  if (p.xq && (reinterpret_cast<uintptr_t>(x) & 15u) == 0)
-    return moe_forward_mfma(p, x, y, tokens, s);
-  const int has_shared = p.shared_ffn > 0;
-  // 1 router (+ the shared-gate row for qwen3next)
-  GemvProblem r{};
-  r.type = kF32;
-  r.weights = reinterpret_cast<const uint8_t*>(p.router);
-  r.row_bytes = (int64_t)p.hidden * 4;
-  r.rows = p.experts + ((p.variant == kQwen3Next && has_shared) ? 1 : 0);
-  r.columns = p.hidden;
-  r.x = x;
-  r.x_stride = p.hidden;
-  r.tokens = tokens;
-  r.y = p.logits;
-  r.y_stride = p.experts + 1;
-  hipError_t e = gemv_launch(r, s);
-  if (e != hipSuccess) return e;
-  // 2 top-k + gating
-  const dim3 tgrid((tokens + 3) / 4);
-  switch (jpl_for(p.experts)) {
-    case 1: e = launch(topk_gate_kernel<1>, tgrid, dim3(256), 0, s, p, tokens); break;
-    case 2: e = launch(topk_gate_kernel<2>, tgrid, dim3(256), 0, s, p, tokens); break;
-    case 4: e = launch(topk_gate_kernel<4>, tgrid, dim3(256), 0, s, p, tokens); break;
-    case 8: e = launch(topk_gate_kernel<8>, tgrid, dim3(256), 0, s, p, tokens); break;
-    case 16: e = launch(topk_gate_kernel<16>, tgrid, dim3(256), 0, s, p, tokens); break;
-    default: return hipErrorInvalidValue;
-  }
-  if (e != hipSuccess) return e;
-  // 3 scan + scatter
-  const int nt = tokens == 1 ? 1 : kMoeChunkTokens;
-  e = launch(moe_scan_kernel, dim3(1), dim3(kScanThreads), 0, s, p, tokens, nt, has_shared);
-  if (e != hipSuccess) return e;
-  // 4, 5 grouped experts
-  e = nt == 1 ? launch_groups<1>(p, x, tokens, s) : launch_groups<kMoeChunkTokens>(p, x, tokens, s);
-  if (e != hipSuccess) return e;
-  // 6 combine
-  return launch(moe_combine_kernel, dim3((p.hidden + 255) / 256, tokens), dim3(256), 0, s, p, y,
-                tokens, has_shared);
 }
 
 hipError_t moe_reset_launch(const MoePlan& p, hipStream_t s) {

@@ -29,22 +29,27 @@
 // evaluations of the same sum and differ by rounding, inside the bound
 // 1e-4 sum|w x| per output.
 //
-// Three pipelines share that arithmetic instruction for instruction, so a
-// token's output does not depend on the batch it runs in:
+// The two batch pipelines share that arithmetic instruction for instruction,
+// so a token's output does not depend on the batch (of two or more) it runs
+// in:
 //   kPipeWide    2-4 token tiles (chunks of up to 64 pairs): 4 waves x 64
 //                rows, one LDS stage per wave; latency is hidden by the
 //                other waves of the SIMD, the MFMA work per chunk is long.
 //   kPipeDouble  1 token tile: 4 waves x 32 rows, two LDS stages per wave;
 //                chunk kc + 1 (rows by DMA, activations and group sums into
 //                registers) loads while chunk kc computes.
-//   kPipeDecode  one token: 1 wave x 32 rows, a ring of up to 8 LDS stages
-//                holding rows, the token's activations and group sums, all
-//                loaded by DMA ahead of use.
+//   kPipeDecode  one token: 4 waves share 32 rows and split K (wave w takes
+//                chunks w, w + 4, ...), each through a ring of up to 8 LDS
+//                stages of rows, the token's activations and group sums,
+//                loaded by DMA ahead of use; the four partial sums are added
+//                in wave order.  Its sums therefore run in another order than
+//                the batch pipelines' (same bound).
 #include "activations.h"
 #include "mfma.h"
 #include "moe.h"
 
 #include <algorithm>
+#include <type_traits>
 
 namespace llhip {
 
@@ -54,24 +59,17 @@ namespace llhip {
 constexpr int waitcnt_vm(int n) { return 0x0F70 | (n & 15) | ((n >> 4) << 14); }
 constexpr int kWaitLgkm0 = 0xC07F;
 
-// ---------------------------------------------------------------- split rows
+// ------------------------------------------------------------ split rows
 // Row r of K elements (K % 32 == 0):
 //   q + r * q_stride (u16): for each 32-group j, [64j, 64j + 32) = hi bf16 of
 //       elements 32j .. 32j + 31 and [64j + 32, 64j + 64) = their lo bf16.
 //   s + r * s_stride (f32): [0, K/16) = sums of the 16-groups, each of
 //       fl(hi) + fl(lo) over the group.  A 32-group's sum is always formed as
 //       s[2j] + s[2j + 1].
-__global__ void __launch_bounds__(256) split_rows_kernel(const float* __restrict__ x, int rows,
-                                                         int K, uint16_t* __restrict__ q,
-                                                         int64_t q_stride, float* __restrict__ s,
-                                                         int64_t s_stride) {
-  const int octets = K >> 3;
-  const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  // octets is even and so is the block size: both octets of a 16-group are
-  // in range or both out, so the shuffle below stays within active lanes
-  if (gid >= (int64_t)rows * octets) return;
-  const int row = (int)(gid / octets), o = (int)(gid - (int64_t)row * octets);
-  const float4* xp = reinterpret_cast<const float4*>(x + (int64_t)row * K + 8 * o);
+// Octet o (elements 8o .. 8o+7) of a row; lanes o and o ^ 1 must both run it.
+__device__ __forceinline__ void split_octet(const float* __restrict__ xrow, int o,
+                                            uint16_t* __restrict__ qrow, float* __restrict__ srow) {
+  const float4* xp = reinterpret_cast<const float4*>(xrow + 8 * o);
   const float4 a = xp[0], b = xp[1];
   const float v[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
   uint32_t hi[8], lo[8];
@@ -82,53 +80,68 @@ __global__ void __launch_bounds__(256) split_rows_kernel(const float* __restrict
     split_bf16(v[e], hi[e], lo[e], t);
     sum += t;
   }
-  uint16_t* dst = q + (int64_t)row * q_stride + 64 * (o >> 2) + 8 * (o & 3);
+  uint16_t* dst = qrow + 64 * (o >> 2) + 8 * (o & 3);
   *reinterpret_cast<u32x4*>(dst) = u32x4{hi[0] | (hi[1] << 16), hi[2] | (hi[3] << 16),
                                          hi[4] | (hi[5] << 16), hi[6] | (hi[7] << 16)};
   *reinterpret_cast<u32x4*>(dst + 32) = u32x4{lo[0] | (lo[1] << 16), lo[2] | (lo[3] << 16),
                                               lo[4] | (lo[5] << 16), lo[6] | (lo[7] << 16)};
   const float s16 = sum + __shfl_xor(sum, 1, 64);
-  if ((o & 1) == 0) s[(int64_t)row * s_stride + (o >> 1)] = s16;
-}
-
-hipError_t split_rows_launch(const float* x, int rows, int K, uint16_t* q, int64_t q_stride,
-                             float* s, int64_t s_stride, hipStream_t stream) {
-  if (rows <= 0) return hipSuccess;
-  const int64_t threads = (int64_t)rows * (K >> 3);
-  const int grid = (int)((threads + 255) / 256);
-  hipLaunchKernelGGL(split_rows_kernel, dim3(grid), dim3(256), 0, stream, x, rows, K, q, q_stride,
-                     s, s_stride);
-  return hipGetLastError();
+  if ((o & 1) == 0) srow[o >> 1] = s16;
 }
 
 // -------------------------------------------------------------------- router
 // logits[t * ld + e] = sum_h x[t][h] R[e][h] (dot-product-with-f32-tensor-data,
-// llambda.lisp:4096-4107, in another fp32 order).  A workgroup owns a 16 x 16
-// (token, expert) tile; its four wavefronts take interleaved 16-element K
-// slices and their partial tiles are added in wave order.
-__global__ void __launch_bounds__(256) router_mfma_kernel(const float* __restrict__ x, int T,
-                                                          const float* __restrict__ R, int Er,
-                                                          int H, float* __restrict__ logits,
-                                                          int ld) {
-  __shared__ floatx4 red[4][64];
+// llambda.lisp:4096-4107, in another fp32 order) for a 16 x 16 (token, expert)
+// tile per workgroup.  K is cut into 16-element pieces; piece p belongs to
+// chain p % 32, and each chain accumulates its pieces in order on
+// v_mfma_f32_16x16x4_f32.  Wave w (of 8) runs chains 4w .. 4w+3 side by side,
+// adds them as (c0 + c1) + (c2 + c3), and the eight wave sums are added as
+// ((w0 + w1) + (w2 + w3)) + ((w4 + w5) + (w6 + w7)): one fixed order for
+// every batch size.  The expert-tile-0 workgroups also write the split rows
+// of their 16 tokens for the expert products.
+constexpr int kRouterWaves = 8;
+
+__global__ void __launch_bounds__(64 * kRouterWaves)
+router_mfma_kernel(const float* __restrict__ x, int T, const float* __restrict__ R, int Er, int H,
+                   float* __restrict__ logits, int ld, uint16_t* __restrict__ q, int64_t q_stride,
+                   float* __restrict__ s, int64_t s_stride) {
+  __shared__ floatx4 red[kRouterWaves][64];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int i = lane & 15, kg = lane >> 4;
   const int t0 = blockIdx.y * 16, e0 = blockIdx.x * 16;
+  if (blockIdx.x == 0) {
+    const int octets = H >> 3;
+    for (int idx = threadIdx.x; idx < 16 * octets; idx += 64 * kRouterWaves) {
+      const int tt = idx / octets, o = idx - tt * octets;
+      if (t0 + tt < T)
+        split_octet(x + (int64_t)(t0 + tt) * H, o, q + (int64_t)(t0 + tt) * q_stride,
+                    s + (int64_t)(t0 + tt) * s_stride);
+    }
+  }
   const float* xr = x + (int64_t)min(t0 + i, T - 1) * H + 4 * kg;
   const float* rr = R + (int64_t)min(e0 + i, Er - 1) * H + 4 * kg;
-  floatx4 acc = {0.f, 0.f, 0.f, 0.f};
-  for (int k = 16 * wave; k < H; k += 64) {
-    const float4 xa = *reinterpret_cast<const float4*>(xr + k);
-    const float4 rb = *reinterpret_cast<const float4*>(rr + k);
-    acc = mfma4f32(xa.x, rb.x, acc);
-    acc = mfma4f32(xa.y, rb.y, acc);
-    acc = mfma4f32(xa.z, rb.z, acc);
-    acc = mfma4f32(xa.w, rb.w, acc);
+  floatx4 acc[4];
+#pragma unroll
+  for (int c = 0; c < 4; ++c) acc[c] = floatx4{0.f, 0.f, 0.f, 0.f};
+  for (int k0 = 64 * wave; k0 < H; k0 += 64 * kRouterWaves) {
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      const int k = k0 + 16 * c;
+      if (k < H) {
+        const float4 xa = *reinterpret_cast<const float4*>(xr + k);
+        const float4 rb = *reinterpret_cast<const float4*>(rr + k);
+        acc[c] = mfma4f32(xa.x, rb.x, acc[c]);
+        acc[c] = mfma4f32(xa.y, rb.y, acc[c]);
+        acc[c] = mfma4f32(xa.z, rb.z, acc[c]);
+        acc[c] = mfma4f32(xa.w, rb.w, acc[c]);
+      }
+    }
   }
-  red[wave][lane] = acc;
+  red[wave][lane] = (acc[0] + acc[1]) + (acc[2] + acc[3]);
   __syncthreads();
   if (wave != 0) return;
-  const floatx4 v = ((red[0][lane] + red[1][lane]) + red[2][lane]) + red[3][lane];
+  const floatx4 v = ((red[0][lane] + red[1][lane]) + (red[2][lane] + red[3][lane])) +
+                    ((red[4][lane] + red[5][lane]) + (red[6][lane] + red[7][lane]));
   const int e = e0 + i;
   if (e >= Er) return;
 #pragma unroll
@@ -139,9 +152,11 @@ __global__ void __launch_bounds__(256) router_mfma_kernel(const float* __restric
 }
 
 hipError_t router_mfma_launch(const float* x, int T, const float* R, int Er, int H, float* logits,
-                              int ld, hipStream_t stream) {
+                              int ld, uint16_t* q, int64_t q_stride, float* s, int64_t s_stride,
+                              hipStream_t stream) {
   const dim3 grid((Er + 15) / 16, (T + 15) / 16);
-  hipLaunchKernelGGL(router_mfma_kernel, grid, dim3(256), 0, stream, x, T, R, Er, H, logits, ld);
+  hipLaunchKernelGGL(router_mfma_kernel, grid, dim3(64 * kRouterWaves), 0, stream, x, T, R, Er, H,
+                     logits, ld, q, q_stride, s, s_stride);
   return hipGetLastError();
 }
 
@@ -330,7 +345,7 @@ enum GemmPipe : int { kPipeWide = 0, kPipeDouble = 1, kPipeDecode = 2 };
 template <int TYPE, int EPI, int PIPE>
 struct GemmShape {
   using B = GemmB<TYPE>;
-  static constexpr int kWaves = PIPE == kPipeDecode ? 1 : 4;
+  static constexpr int kWaves = 4;
   static constexpr int NB = EPI == kEpiSwiglu ? 2 : 1;             // gate and up side by side
   static constexpr int NS = (PIPE == kPipeWide ? 4 : 2) / NB;      // 16-row subtiles per matrix
   static constexpr int ROWS = 16 * NS;                              // rows per matrix and wave
@@ -344,15 +359,17 @@ struct GemmShape {
   static constexpr int STAGE = PIPE == kPipeDecode ? ROWBUF + 1024 + 256 : ROWBUF;
   static constexpr int DEPTH = PIPE == kPipeWide ? 1 : PIPE == kPipeDouble ? 2 : 8;
   static constexpr int LUT = TYPE == kQ5_0 ? 256 * 8 : 0;          // Q5_0 fifth-bit table
-  static constexpr int WAVE_LDS = DEPTH * STAGE + TABLE;
-  static constexpr int LDS = LUT + kWaves * WAVE_LDS;
   static constexpr int DMA = NB * LOADS + (PIPE == kPipeDecode ? 2 : 0);  // loads per stage
+  // decode: the waves' partial sums, added in wave order
+  static constexpr int RED = PIPE == kPipeDecode ? kWaves * NS * NB * 64 * 16 : 0;
+  // rows per workgroup: the decode waves share their rows and split K
+  static constexpr int WG_ROWS = PIPE == kPipeDecode ? ROWS : kWaves * ROWS;
 };
 
 template <int TYPE, int EPI, int PIPE>
 constexpr int gemm_lds_bytes(int depth) {
   using Sh = GemmShape<TYPE, EPI, PIPE>;
-  return Sh::LUT + Sh::kWaves * (depth * Sh::STAGE + Sh::TABLE);
+  return Sh::LUT + Sh::RED + Sh::kWaves * (depth * Sh::STAGE + Sh::TABLE);
 }
 
 // ------------------------------------------------------------ the kernel
@@ -390,22 +407,20 @@ moe_gemm_kernel(MoeGemmArgs a) {
     if constexpr (Sh::kWaves > 1) __syncthreads();
   }
 
-  const int n0 = (blockIdx.y * Sh::kWaves + wave) * Sh::ROWS;
-  if (n0 >= a.N) return;
+  const int n0 = PIPE == kPipeDecode ? blockIdx.y * Sh::ROWS : (blockIdx.y * Sh::kWaves + wave) * Sh::ROWS;
+  if (n0 >= a.N) return;  // uniform over the workgroup for the decode pipeline
   const int depth = PIPE == kPipeDecode ? a.depth : Sh::DEPTH;
-  uint8_t* wlds = lds + Sh::LUT + wave * (depth * Sh::STAGE + Sh::TABLE);
+  uint8_t* wlds = lds + Sh::LUT + Sh::RED + wave * (depth * Sh::STAGE + Sh::TABLE);
   float2* table = reinterpret_cast<float2*>(wlds + depth * Sh::STAGE);
   const uint32_t wlds_addr = lds_address(wlds);
 
   // split rows of this lane's tokens (tile row t = n of each token tile)
   const uint16_t* arow[MT];
   const float* srow[MT];
-  bool tok_ok[MT];
 #pragma unroll
   for (int i = 0; i < MT; ++i) {
     const int tk = 16 * i + n;
-    tok_ok[i] = tk < ch.count;
-    const int q = a.perm[ch.start + (tok_ok[i] ? tk : 0)];
+    const int q = a.perm[ch.start + (tk < ch.count ? tk : 0)];
     const int64_t r = a.a_by_token ? (q < a.pairs ? q / a.top_k : q - a.pairs) : q;
     arow[i] = a.aq + r * a.aq_stride;
     srow[i] = a.as + r * a.as_stride;
@@ -464,9 +479,13 @@ moe_gemm_kernel(MoeGemmArgs a) {
   // ---- one chunk: scale table, then groups, then offsets
   // get_a(i, j, af) fills tile i's fragments of group j; get_s(i, q)
   // returns the sum of the group (4q + g) of tile i's lane token.
-  auto compute = [&](int kc, const uint8_t* stage, auto get_a, auto get_s) {
+  // FULL: all KS groups of the chunk lie inside K (always for Q4_K and Q6_K,
+  // whose K is a multiple of 256); only the last chunk of a Q5_0 / Q8_0 row
+  // may be partial.
+  auto compute = [&](auto full, int kc, const uint8_t* stage, auto get_a, auto get_s) {
+    constexpr bool FULL = decltype(full)::value;
     const uint32_t koff = (uint32_t)kc * (uint32_t)B::kSpan;
-    const int valid = min(KS, groups - kc * KS);
+    const int valid = FULL ? KS : min(KS, groups - kc * KS);
     uint32_t sh[NS];
 #pragma unroll
     for (int m = 0; m < NS; ++m) sh[m] = ALIGNED ? (koff & 3u) : ((brow[m] + koff) & 3u);
@@ -487,7 +506,7 @@ moe_gemm_kernel(MoeGemmArgs a) {
       }
 #pragma unroll
     for (int j = 0; j < KS; ++j) {
-      if (j < valid) {
+      if (FULL || j < valid) {
         AF af[MT];
 #pragma unroll
         for (int i = 0; i < MT; ++i) get_a(i, j, af[i]);
@@ -530,6 +549,11 @@ moe_gemm_kernel(MoeGemmArgs a) {
     }
   };
 
+  auto run_chunk = [&](int kc, const uint8_t* stage, auto get_a, auto get_s) {
+    if (kc * KS + KS <= groups) compute(std::true_type{}, kc, stage, get_a, get_s);
+    else compute(std::false_type{}, kc, stage, get_a, get_s);
+  };
+
   // group sum of element group gi of a split row (16-groups; a 32-group is
   // the sum of its two halves)
   auto row_sum = [&](const float* s, int gi) -> float {
@@ -542,12 +566,9 @@ moe_gemm_kernel(MoeGemmArgs a) {
       issue(kc, 0);
       __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
       const int gbase = kc * KS;
-      compute(
-          kc, wlds,
-          [&](int i, int j, AF& af) {
-            if (tok_ok[i]) af.load(arow[i] + 512 * kc + AF::offset(j, g));
-            else af.zero();
-          },
+      // lanes of padding tokens read the chunk's first token (outputs dropped)
+      run_chunk(
+          kc, wlds, [&](int i, int j, AF& af) { af.load(arow[i] + 512 * kc + AF::offset(j, g)); },
           [&](int i, int q) { return row_sum(srow[i], min(gbase + 4 * q + g, groups - 1)); });
       __builtin_amdgcn_s_waitcnt(kWaitLgkm0);
     }
@@ -559,7 +580,7 @@ moe_gemm_kernel(MoeGemmArgs a) {
       const int valid = min(KS, groups - kc * KS);
 #pragma unroll
       for (int j = 0; j < KS; ++j) {
-        if (tok_ok[0] && j < valid) ar[j].load(arow[0] + 512 * kc + AF::offset(j, g));
+        if (j < valid) ar[j].load(arow[0] + 512 * kc + AF::offset(j, g));
         else ar[j].zero();
       }
 #pragma unroll
@@ -574,7 +595,7 @@ moe_gemm_kernel(MoeGemmArgs a) {
         issue(kc + 1, (kc + 1) & 1);
         load_regs(kc + 1, anext, snext);
       }
-      compute(
+      run_chunk(
           kc, wlds + (kc & 1) * Sh::STAGE, [&](int, int j, AF& af) { af = acur[j]; },
           [&](int, int q) { return scur[q]; });
       __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
@@ -587,11 +608,14 @@ moe_gemm_kernel(MoeGemmArgs a) {
       }
     }
   } else {
-    // decode: one token, a ring of `depth` stages filled ahead of use
-    const int first = min(depth, nchunk);
-    for (int s = 0; s < first; ++s) issue(s, s);
-    for (int kc = 0; kc < nchunk; ++kc) {
-      const int ahead = min(nchunk, kc + depth) - kc - 1;  // stages issued after kc
+    // decode: one token; wave w takes chunks w, w + 4, ... through a ring of
+    // `depth` stages filled ahead of use
+    const int mine = (nchunk - wave + Sh::kWaves - 1) / Sh::kWaves;
+    const int first = min(depth, mine);
+    for (int s = 0; s < first; ++s) issue(wave + Sh::kWaves * s, s);
+    for (int it = 0; it < mine; ++it) {
+      const int kc = wave + Sh::kWaves * it;
+      const int ahead = min(mine, it + depth) - it - 1;  // stages issued after this one
       // at most `ahead` stages (DMA loads each) may still be in flight; the
       // counter holds 63, beyond which the wait is stricter than needed
       switch (ahead) {
@@ -604,14 +628,14 @@ moe_gemm_kernel(MoeGemmArgs a) {
         case 6: __builtin_amdgcn_s_waitcnt(waitcnt_vm(std::min(63, 6 * Sh::DMA))); break;
         default: __builtin_amdgcn_s_waitcnt(waitcnt_vm(std::min(63, 7 * Sh::DMA))); break;
       }
-      const int slot = kc % depth;
+      const int slot = it % depth;
       const uint8_t* stage = wlds + slot * Sh::STAGE;
       const float* ssum = reinterpret_cast<const float*>(stage + Sh::S_OFF);
-      compute(
+      // every tile row reads the one token (rows t > 0 are dropped)
+      run_chunk(
           kc, stage,
           [&](int, int j, AF& af) {
-            if (n == 0) af.load(reinterpret_cast<const uint16_t*>(stage + Sh::A_OFF) + AF::offset(j, g));
-            else af.zero();
+            af.load(reinterpret_cast<const uint16_t*>(stage + Sh::A_OFF) + AF::offset(j, g));
           },
           [&](int, int q) {
             const int gi = min(kc * KS + 4 * q + g, groups - 1) - kc * KS;
@@ -619,8 +643,25 @@ moe_gemm_kernel(MoeGemmArgs a) {
             else return ssum[gi];
           });
       __builtin_amdgcn_s_waitcnt(kWaitLgkm0);
-      if (kc + depth < nchunk) issue(kc + depth, slot);
+      if (it + depth < mine) issue(kc + Sh::kWaves * depth, slot);
     }
+    // partial sums of the four K slices, added in wave order by wave 0
+    floatx4* red = reinterpret_cast<floatx4*>(lds + Sh::LUT);
+#pragma unroll
+    for (int m = 0; m < NS; ++m)
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb) red[((wave * NS + m) * NB + nb) * 64 + lane] = tot[0][m][nb];
+    __syncthreads();
+    if (wave != 0) return;
+#pragma unroll
+    for (int m = 0; m < NS; ++m)
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb) {
+        floatx4 v = red[(m * NB + nb) * 64 + lane];
+#pragma unroll
+        for (int w = 1; w < Sh::kWaves; ++w) v = v + red[((w * NS + m) * NB + nb) * 64 + lane];
+        tot[0][m][nb] = v;
+      }
   }
 
   // ---------------------------------------------------------- epilogue
@@ -676,7 +717,8 @@ static hipError_t launch_gemm_t(const MoeGemmArgs& a_in, int max_chunks, hipStre
   using Sh = GemmShape<TYPE, EPI, PIPE>;
   MoeGemmArgs a = a_in;
   const int nchunk = (a.K + 255) / 256;
-  a.depth = PIPE == kPipeDecode ? std::min(Sh::DEPTH, nchunk) : Sh::DEPTH;
+  const int per_wave = (nchunk + Sh::kWaves - 1) / Sh::kWaves;
+  a.depth = PIPE == kPipeDecode ? std::max(1, std::min(Sh::DEPTH, per_wave)) : Sh::DEPTH;
   const int lds = gemm_lds_bytes<TYPE, EPI, PIPE>(a.depth);
   const auto kernel = moe_gemm_kernel<TYPE, EPI, MT, PIPE, ALIGNED>;
   if (lds > 65536) {
@@ -684,8 +726,7 @@ static hipError_t launch_gemm_t(const MoeGemmArgs& a_in, int max_chunks, hipStre
                                        hipFuncAttributeMaxDynamicSharedMemorySize, lds);
     if (e != hipSuccess) return e;
   }
-  constexpr int rows_per_block = Sh::kWaves * Sh::ROWS;
-  const dim3 grid(max_chunks, (a.N + rows_per_block - 1) / rows_per_block);
+  const dim3 grid(max_chunks, (a.N + Sh::WG_ROWS - 1) / Sh::WG_ROWS);
   hipLaunchKernelGGL(kernel, grid, dim3(64 * Sh::kWaves), lds, stream, a);
   return hipGetLastError();
 }
@@ -696,7 +737,11 @@ static hipError_t launch_gemm_mt(const MoeGemmArgs& a, int mt, int max_chunks, h
     case 0: return launch_gemm_t<TYPE, EPI, 1, kPipeDecode, ALIGNED>(a, max_chunks, s);
     case 1: return launch_gemm_t<TYPE, EPI, 1, kPipeDouble, ALIGNED>(a, max_chunks, s);
     case 2: return launch_gemm_t<TYPE, EPI, 2, kPipeWide, ALIGNED>(a, max_chunks, s);
-    case 4: return launch_gemm_t<TYPE, EPI, 4, kPipeWide, ALIGNED>(a, max_chunks, s);
+    case 4:
+      // rows with 2-byte-aligned chunks run 2 token tiles per chunk pass:
+      // (the 4-tile variants of those do not build with this compiler)
+      if constexpr (ALIGNED) return launch_gemm_t<TYPE, EPI, 4, kPipeWide, ALIGNED>(a, max_chunks, s);
+      else return hipErrorInvalidValue;
     default: return hipErrorInvalidValue;
   }
 }

@@ -67,6 +67,13 @@ def output_bounds(layer, x, idx, w, shared_w):
     return S
 
 
+def _shared_weights(layer, x):
+    if layer.variant == QWEN3NEXT and layer.shared_ffn:
+        return np.array([oracle.sigmoid(float(oracle.dot_product(layer.shared_gate_inp, xt)))
+                         for xt in x], dtype=np.float64)
+    return np.ones(x.shape[0])
+
+
 def router_bound(layer, x):
     """K * 2^-24 * sum_i |w_i x_i| per token: a bound on the serial fp32 router
     sum's deviation from the exact dot (plus the GPU's own, same order)."""
@@ -97,11 +104,7 @@ def check_layer(layer, x, label):
             assert np.array_equal(idx[t], ref.top_indices[t]), f"{label} token {t}: order differs"
         margins.append(gap_k / max(rb[t], 1e-30))
     # outputs, against the oracle's routing
-    shared_w = np.ones(x.shape[0])
-    if layer.variant == QWEN3NEXT and layer.shared_ffn:
-        shared_w = np.array([oracle.sigmoid(float(oracle.dot_product(layer.shared_gate_inp, xt)))
-                             for xt in x], dtype=np.float64)
-    S = output_bounds(layer, x, ref.top_indices, ref.top_weights, shared_w)
+    S = output_bounds(layer, x, ref.top_indices, ref.top_weights, _shared_weights(layer, x))
     same = np.array([np.array_equal(idx[t], ref.top_indices[t]) for t in range(x.shape[0])])
     err = np.abs(y.astype(np.float64) - ref.y.astype(np.float64))
     bad = (err > REL * S) & same[:, None]
@@ -130,12 +133,20 @@ def test_qwen3next_prefill_256(hip):
     layer = synthetic_qwen3next(rng)
     x = synthetic.activations(rng, 256, layer.hidden)
     y, idx = check_layer(layer, x, "qwen3next prefill")
-    # batch invariance: every token of the batch equals its own decode run
+    # a token run alone (the single-token pipeline: K split over four
+    # wavefronts) routes exactly as inside the batch (the router's order is
+    # the same for every batch size) and agrees within the parity bound
+    sub = list(range(0, 256, 37))
+    ref = oracle.moe_forward(layer, x[sub], threads=THREADS)
+    S = output_bounds(layer, x[sub], ref.top_indices, ref.top_weights,
+                      _shared_weights(layer, x[sub]))
     session = HipMoeSession(layer)
     try:
-        for t in range(0, 256, 37):
-            y1 = session.run(x[t:t + 1])
-            np.testing.assert_array_equal(y1[0], y[t])
+        for j, t in enumerate(sub):
+            y1, i1, _, _ = session.run(x[t:t + 1], with_routing=True)
+            np.testing.assert_array_equal(i1[0], idx[t])
+            err = np.abs(y1[0].astype(np.float64) - y[t].astype(np.float64))
+            assert np.all(err <= 2 * REL * S[j]), f"token {t}: single run differs from the batch"
     finally:
         session.close()
 
