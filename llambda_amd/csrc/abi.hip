@@ -573,13 +573,6 @@ int llambda_hip_moe_session_create(const llambda_hip_moe_desc* d,
         p.sh_up = s->sh_up.as<uint8_t>();
         p.sh_down = s->sh_down.as<uint8_t>();
       }
-      {
-        auto dword_rows = [](int type, int64_t columns) {
-          return type == kQ4_K || (columns / block_weights(type) * block_bytes(type)) % 4 == 0;
-        };
-        p.wide4 = dword_rows(p.up_type, H) && dword_rows(p.down_type, F) &&
-                  (Fs == 0 || (dword_rows(p.sh_up_type, H) && dword_rows(p.sh_down_type, Fs)));
-      }
       s->counts.alloc((size_t)E * sizeof(int), "expert histogram");
       s->chunk_counts.alloc(2 * sizeof(int), "chunk counts");
       s->error.alloc(sizeof(int), "error flag");

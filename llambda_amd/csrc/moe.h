@@ -35,7 +35,6 @@ struct MoePlan {
   int hidden, experts, top_k, ffn, shared_ffn;
   float weights_scale;
   int weights_norm;
-  int wide4;  // every expert tensor has dword-multiple rows: 4-tile chunks allowed
   // weights
   const float* router;   // [(experts + (variant == qwen3next && shared)) ][hidden]
   const float* bias;     // [experts], nemotron
@@ -108,7 +107,8 @@ struct MoeGemmArgs {
 hipError_t router_mfma_launch(const float* x, int T, const float* R, int Er, int H, float* logits,
                               int ld, uint16_t* q, int64_t q_stride, float* s, int64_t s_stride,
                               hipStream_t stream);
-// mt: token tiles per chunk (1, 2, 4), or 0 for a batch of one token.
+// mt: 0 = one token (K split over four wavefronts), 1 = chunks of up to 16
+// pairs (double-buffered), 2 = chunks of up to 32 pairs.
 hipError_t moe_gemm_launch(int type, int epi, const MoeGemmArgs& a, int mt, int max_chunks,
                            hipStream_t stream);
 

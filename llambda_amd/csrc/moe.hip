@@ -295,15 +295,15 @@ static int64_t row_bytes_of(int type, int64_t columns) {
   return columns / block_weights(type) * block_bytes(type);
 }
 
-// Token-tile count (16 tokens each) of the grouped MFMA chunks: enough to
-// cover the average (token, rank) pairs per expert, at most 4 (2 when some
-// expert tensor has rows that are not a whole number of dwords).  0 selects
-// the single-token pipeline.
+// Pipeline of the grouped MFMA products and its chunk size: 0 = the
+// single-token pipeline, 1 = one 16-token tile per chunk (double-buffered),
+// 2 = two 16-token tiles per chunk (32 pairs).
 static int moe_mfma_tiles(const MoePlan& p, int tokens) {
   if (tokens == 1) return 0;
   const int64_t avg = ((int64_t)tokens * p.top_k + p.experts - 1) / p.experts;
-  return avg <= 16 ? 1 : (avg <= 40 || !p.wide4) ? 2 : 4;
+  return avg <= 16 ? 1 : 2;
 }
+static int moe_chunk_tokens(int mt) { return mt == 0 ? 1 : 16 * mt; }
 
 // One forward: router GEMM (+ split x), top-k and gating, scan (batches),
 // grouped gate/up and down products, combine.
@@ -332,7 +332,7 @@ hipError_t moe_forward_launch(const MoePlan& p, const float* x, float* y, int to
     default: return hipErrorInvalidValue;
   }
   if (e != hipSuccess) return e;
-  const int mt = moe_mfma_tiles(p, tokens), nt = 16 * std::max(mt, 1);
+  const int mt = moe_mfma_tiles(p, tokens), nt = moe_chunk_tokens(mt);
   if (!single) {
     e = launch(moe_scan_kernel, dim3(1), dim3(kScanThreads), 0, s, p, tokens, nt, has_shared);
     if (e != hipSuccess) return e;

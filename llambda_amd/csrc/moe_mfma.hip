@@ -32,7 +32,7 @@
 // The two batch pipelines share that arithmetic instruction for instruction,
 // so a token's output does not depend on the batch (of two or more) it runs
 // in:
-//   kPipeWide    2-4 token tiles (chunks of up to 64 pairs): 4 waves x 64
+//   kPipeWide    2 token tiles (chunks of up to 32 pairs): 4 waves x 64
 //                rows, one LDS stage per wave; latency is hidden by the
 //                other waves of the SIMD, the MFMA work per chunk is long.
 //   kPipeDouble  1 token tile: 4 waves x 32 rows, two LDS stages per wave;
@@ -376,7 +376,8 @@ constexpr int gemm_lds_bytes(int depth) {
 // ALIGNED: row_bytes % 4 == 0, so every row's chunk starts at the same offset
 // from a dword (Q4_K, Q5_0, Q8_0: 0; Q6_K: 2 in odd chunks).
 template <int TYPE, int EPI, int MT, int PIPE, bool ALIGNED>
-__global__ void __launch_bounds__((64 * GemmShape<TYPE, EPI, PIPE>::kWaves))
+__global__ void __launch_bounds__((64 * GemmShape<TYPE, EPI, PIPE>::kWaves),
+                                  (PIPE == kPipeWide ? 2 : 1))
 moe_gemm_kernel(MoeGemmArgs a) {
   using B = GemmB<TYPE>;
   using Sh = GemmShape<TYPE, EPI, PIPE>;
@@ -737,11 +738,6 @@ static hipError_t launch_gemm_mt(const MoeGemmArgs& a, int mt, int max_chunks, h
     case 0: return launch_gemm_t<TYPE, EPI, 1, kPipeDecode, ALIGNED>(a, max_chunks, s);
     case 1: return launch_gemm_t<TYPE, EPI, 1, kPipeDouble, ALIGNED>(a, max_chunks, s);
     case 2: return launch_gemm_t<TYPE, EPI, 2, kPipeWide, ALIGNED>(a, max_chunks, s);
-    case 4:
-      // rows with 2-byte-aligned chunks run 2 token tiles per chunk pass:
-      // (the 4-tile variants of those do not build with this compiler)
-      if constexpr (ALIGNED) return launch_gemm_t<TYPE, EPI, 4, kPipeWide, ALIGNED>(a, max_chunks, s);
-      else return hipErrorInvalidValue;
     default: return hipErrorInvalidValue;
   }
 }
