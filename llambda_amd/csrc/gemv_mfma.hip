@@ -241,20 +241,37 @@ struct MfmaType {
   static constexpr int kZero = 2048;  // zero lines read by A lanes without data
 };
 
-constexpr int kMfmaWaves = 4;
+// Waves per workgroup, blocks per staged chunk and LDS stages per wave of the
+// batch-1 GEMV, as measured best on the Q6_K output head and the 4096 x 4096
+// Q4_K projection (deeper rings and longer chunks read HBM more slowly).
+#ifndef LLHIP_GEMV_WAVES
+#define LLHIP_GEMV_WAVES 8
+#endif
+#ifndef LLHIP_GEMV_CHUNK
+#define LLHIP_GEMV_CHUNK 2
+#endif
+constexpr int kMfmaWaves = LLHIP_GEMV_WAVES;
 
-// LDS layout: [0, kZero) zeros | table (nblk * kTable) | group sums | stages.
+// s_waitcnt vmcnt(n) (gfx9 encoding, other counters left alone)
+constexpr int waitcnt_vm(int n) { return 0x0F70 | (n & 15) | ((n >> 4) << 14); }
+
+// LDS layout: [0, kZero) zeros | table (nblk * kTable) | group sums | stages
+// (D per wave) | split-K partial row sums.
 template <int TYPE, int C, bool ALIGNED>
-constexpr size_t mfma_lds_bytes(int nblk) {
+constexpr size_t mfma_lds_bytes(int nblk, int depth) {
   using T = MfmaType<TYPE>;
   using Ch = Chunk<T::kBB, C, ALIGNED>;
   return (size_t)T::kZero + (size_t)nblk * (T::kTable + 4 * T::kSums) +
-         (size_t)kMfmaWaves * 2 * Ch::kBuffer;
+         (size_t)kMfmaWaves * depth * Ch::kBuffer + kMfmaWaves * 64 * sizeof(float);
 }
 
 // ALIGNED: the weights, row_bytes and the chunk span are multiples of 4, so
-// every row's chunk starts on a dword.
-template <int TYPE, int C, bool ALIGNED>
+// every row's chunk starts on a dword.  D: LDS stages per wave (a ring, D - 1
+// chunks in flight while one computes).  SPLIT: the four waves share each
+// 16-row tile and take every fourth chunk of it (row counts too small to
+// give every wave its own tiles); their partial sums meet in LDS and are
+// added in wave order.
+template <int TYPE, int C, bool ALIGNED, int D, bool SPLIT>
 __global__ void __launch_bounds__(64 * kMfmaWaves)
 gemv_mfma_kernel(const uint8_t* __restrict__ w, int64_t row_bytes, int rows, int nblk,
                  const float* __restrict__ x, float* __restrict__ y) {
@@ -265,6 +282,7 @@ gemv_mfma_kernel(const uint8_t* __restrict__ w, int64_t row_bytes, int rows, int
   uint8_t* table = lds + table_off;
   float* gsum = reinterpret_cast<float*>(table + nblk * T::kTable);
   uint8_t* stages = reinterpret_cast<uint8_t*>(gsum + nblk * T::kSums);
+  float* partial = reinterpret_cast<float*>(stages + kMfmaWaves * D * Ch::kBuffer);
 
   for (int i = threadIdx.x; i < T::kZero / 16; i += blockDim.x)
     reinterpret_cast<u32x4*>(lds)[i] = u32x4{0u, 0u, 0u, 0u};
@@ -289,15 +307,24 @@ gemv_mfma_kernel(const uint8_t* __restrict__ w, int64_t row_bytes, int rows, int
   }
   const uint32_t a_stride = (TYPE == kQ4_K && a_base == 0u) ? 0u : (uint32_t)T::kTable;
 
-  const uint8_t* stage = stages + wave * 2 * Ch::kBuffer;
+  const uint8_t* stage = stages + wave * D * Ch::kBuffer;
   const uint32_t stage_lds = lds_address(stage);
   const int tiles = (rows + 15) >> 4;
   const int chunks = nblk / C;
-  const int first_tile = blockIdx.x * kMfmaWaves + wave;
-  const int tile_step = gridDim.x * kMfmaWaves;
+  // Step s of this wave: (tile, chunk).  Without SPLIT the wave walks whole
+  // tiles first_tile, first_tile + tile_step, ...; with SPLIT the workgroup
+  // owns tile blockIdx.x and the wave its chunks wave, wave + 4, ...
+  const int first_tile = SPLIT ? blockIdx.x : blockIdx.x * kMfmaWaves + wave;
+  const int tile_step = gridDim.x * (SPLIT ? 1 : kMfmaWaves);
+  const int cpt = SPLIT ? (chunks - wave + kMfmaWaves - 1) / kMfmaWaves : chunks;  // chunks per tile
   const int my_tiles = first_tile < tiles ? (tiles - first_tile + tile_step - 1) / tile_step : 0;
-  const int steps = my_tiles * chunks;
+  const int steps = my_tiles * cpt;
   const uint32_t rb = (uint32_t)row_bytes;
+  auto tile_of = [&](int s) { return first_tile + (s / cpt) * tile_step; };
+  auto chunk_of = [&](int s) {
+    const int c = s - (s / cpt) * cpt;
+    return SPLIT ? wave + kMfmaWaves * c : c;
+  };
 
   // per load instruction i: this lane's (row, piece) and byte offset in the tile
   uint32_t voff[Ch::kLoads];
@@ -312,13 +339,13 @@ gemv_mfma_kernel(const uint8_t* __restrict__ w, int64_t row_bytes, int rows, int
   // dword at or below that, i.e. from base_al + ((bsh + r * rb) & ~3) with
   // base_al = base & ~3 and bsh = base & 3 (offsets stay non-negative).
   auto issue = [&](int s) {
-    const int tile = first_tile + (s / chunks) * tile_step;
-    const int chunk = s - (s / chunks) * chunks;
+    const int tile = tile_of(s);
+    const int chunk = chunk_of(s);
     const uint8_t* base =
         uniform_ptr(w + (int64_t)tile * 16 * row_bytes + (int64_t)chunk * Ch::kSpan);
     const uint32_t bsh = ALIGNED ? 0u : (uint32_t)(reinterpret_cast<uintptr_t>(base) & 3u);
     const uint8_t* base_al = base - bsh;
-    const uint32_t dst = stage_lds + (uint32_t)((s & 1) * Ch::kBuffer);
+    const uint32_t dst = stage_lds + (uint32_t)((s % D) * Ch::kBuffer);
     const int rmax = rows - 1 - tile * 16;
     if (ALIGNED && rmax >= 15) {
 #pragma unroll
@@ -337,18 +364,28 @@ gemv_mfma_kernel(const uint8_t* __restrict__ w, int64_t row_bytes, int rows, int
     }
   };
 
-  if (steps > 0) issue(0);
+  const int first = min(D - 1, steps);
+  for (int s = 0; s < first; ++s) issue(s);
   float acc = 0.f;
   for (int s = 0; s < steps; ++s) {
-    const int tile = first_tile + (s / chunks) * tile_step;
-    const int chunk = s - (s / chunks) * chunks;
-    if (s + 1 < steps) {
-      issue(s + 1);
-      wait_loads<Ch::kLoads>();
+    const int tile = tile_of(s);
+    const int chunk = chunk_of(s);
+    if (s + D - 1 < steps) issue(s + D - 1);
+    // at most `ahead` later steps' loads may still be in flight (a y store
+    // in between only makes the wait stricter)
+    const int ahead = min(steps, s + D) - s - 1;
+    if constexpr (D <= 2) {
+      if (ahead == 0) __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
+      else __builtin_amdgcn_s_waitcnt(waitcnt_vm(Ch::kLoads));
     } else {
-      wait_loads<0>();
+      switch (ahead) {
+        case 0: __builtin_amdgcn_s_waitcnt(waitcnt_vm(0)); break;
+        case 1: __builtin_amdgcn_s_waitcnt(waitcnt_vm(Ch::kLoads)); break;
+        case 2: __builtin_amdgcn_s_waitcnt(waitcnt_vm(2 * Ch::kLoads)); break;
+        default: __builtin_amdgcn_s_waitcnt(waitcnt_vm(3 * Ch::kLoads)); break;
+      }
     }
-    const uint8_t* buf = stage + (s & 1) * Ch::kBuffer;
+    const uint8_t* buf = stage + (s % D) * Ch::kBuffer;
     const uint8_t* rowp = buf + n * Ch::kRow;
     if constexpr (!ALIGNED) {
       const int row = min(tile * 16 + n, rows - 1);
@@ -371,41 +408,67 @@ gemv_mfma_kernel(const uint8_t* __restrict__ w, int64_t row_bytes, int rows, int
     [&]<int... BL>(std::integer_sequence<int, BL...>) {
       (block.template operator()<BL>(), ...);
     }(std::make_integer_sequence<int, C>{});
-    if (chunk == chunks - 1) {
+    if (!SPLIT && chunk == chunks - 1) {
       const float v = sum_lane_groups(acc);
       const int row = tile * 16 + n;
       if (g == 0 && row < rows) y[row] = v;
       acc = 0.f;
     }
-    asm volatile("" ::: "memory");
+  }
+  if constexpr (SPLIT) {
+    // one tile per workgroup: the waves' row sums, in wave order
+    const float v = sum_lane_groups(acc);
+    if (g == 0) partial[wave * 16 + n] = v;
+    __syncthreads();
+    const int row = first_tile * 16 + n;
+    if (wave == 0 && g == 0 && first_tile < tiles && row < rows) {
+      float v = partial[n];
+#pragma unroll
+      for (int w = 1; w < kMfmaWaves; ++w) v = v + partial[16 * w + n];
+      y[row] = v;
+    }
   }
 }
 
 // ------------------------------------------------------------------ host
 
+#ifndef LLHIP_GEMV_DEPTH
+#define LLHIP_GEMV_DEPTH 2
+#endif
+constexpr int kGemvDepth = LLHIP_GEMV_DEPTH;
+
 template <int TYPE>
 struct MfmaChoice {
   int chunk;
   bool aligned;
+  int depth;   // 4 when the LDS holds it, else 2
+  bool split;  // too few tiles for one per wave
 };
+
+template <int TYPE>
+static size_t mfma_lds_for(const MfmaChoice<TYPE>& c, int nblk) {
+  if (c.chunk == 4)
+    return c.aligned ? mfma_lds_bytes<TYPE, 4, true>(nblk, c.depth)
+                     : mfma_lds_bytes<TYPE, 4, false>(nblk, c.depth);
+  if (c.chunk == 2)
+    return c.aligned ? mfma_lds_bytes<TYPE, 2, true>(nblk, c.depth)
+                     : mfma_lds_bytes<TYPE, 2, false>(nblk, c.depth);
+  return c.aligned ? mfma_lds_bytes<TYPE, 1, true>(nblk, c.depth)
+                   : mfma_lds_bytes<TYPE, 1, false>(nblk, c.depth);
+}
 
 template <int TYPE>
 static MfmaChoice<TYPE> mfma_choice(const GemvProblem& p) {
   const int64_t nblk = p.columns / 256;
   MfmaChoice<TYPE> c;
-  c.chunk = nblk % 2 == 0 ? 2 : 1;
+  c.chunk = nblk % LLHIP_GEMV_CHUNK == 0 ? LLHIP_GEMV_CHUNK : nblk % 2 == 0 ? 2 : 1;
   const int64_t span = (int64_t)c.chunk * MfmaType<TYPE>::kBB;
   c.aligned = p.row_bytes % 4 == 0 && span % 4 == 0;
+  c.depth = kGemvDepth;
+  if (mfma_lds_for(c, (int)nblk) > kMaxLdsBytes) c.depth = 2;
+  const int64_t tiles = (p.rows + 15) / 16;
+  c.split = tiles < (int64_t)device_cu_count() * 2 * kMfmaWaves && nblk / c.chunk >= kMfmaWaves;
   return c;
-}
-
-template <int TYPE>
-static size_t mfma_lds(const GemvProblem& p) {
-  const MfmaChoice<TYPE> c = mfma_choice<TYPE>(p);
-  const int nblk = (int)(p.columns / 256);
-  if (c.chunk == 2)
-    return c.aligned ? mfma_lds_bytes<TYPE, 2, true>(nblk) : mfma_lds_bytes<TYPE, 2, false>(nblk);
-  return c.aligned ? mfma_lds_bytes<TYPE, 1, true>(nblk) : mfma_lds_bytes<TYPE, 1, false>(nblk);
 }
 
 bool gemv_mfma_supported(const GemvProblem& p) {
@@ -415,42 +478,67 @@ bool gemv_mfma_supported(const GemvProblem& p) {
   // weights must start on a dword (Q4_K: rows 16-byte aligned, its blocks
   // are read from LDS with 16-byte loads)
   if (reinterpret_cast<uintptr_t>(p.weights) & 3u) return false;
-  if (p.type == kQ4_K)
+  if (p.type == kQ4_K) {
+    const MfmaChoice<kQ4_K> c = mfma_choice<kQ4_K>(p);
     return (reinterpret_cast<uintptr_t>(p.weights) & 15u) == 0 && p.row_bytes % 16 == 0 &&
-           mfma_lds<kQ4_K>(p) <= kMaxLdsBytes;
-  if (p.type == kQ6_K) return mfma_lds<kQ6_K>(p) <= kMaxLdsBytes;
+           mfma_lds_for(c, (int)(p.columns / 256)) <= kMaxLdsBytes;
+  }
+  if (p.type == kQ6_K) {
+    const MfmaChoice<kQ6_K> c = mfma_choice<kQ6_K>(p);
+    return mfma_lds_for(c, (int)(p.columns / 256)) <= kMaxLdsBytes;
+  }
   return false;
 }
 
-template <int TYPE, int C, bool ALIGNED>
+template <int TYPE, int C, bool ALIGNED, int D, bool SPLIT>
 static hipError_t launch_mfma(const GemvProblem& p, hipStream_t stream) {
   const int nblk = (int)(p.columns / 256);
-  const size_t lds = mfma_lds_bytes<TYPE, C, ALIGNED>(nblk);
-  const auto kernel = gemv_mfma_kernel<TYPE, C, ALIGNED>;
+  const size_t lds = mfma_lds_bytes<TYPE, C, ALIGNED>(nblk, D);
+  const auto kernel = gemv_mfma_kernel<TYPE, C, ALIGNED, D, SPLIT>;
   if (lds > 65536) {
     hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kernel),
                                        hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
     if (e != hipSuccess) return e;
   }
-  int per_cu = 0;
-  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, reinterpret_cast<const void*>(kernel),
-                                                   64 * kMfmaWaves, lds) != hipSuccess ||
-      per_cu < 1)
-    per_cu = 1;
   const int tiles = (int)((p.rows + 15) / 16);
-  const int needed = (tiles + kMfmaWaves - 1) / kMfmaWaves;
-  const int grid = std::max(1, std::min(needed, device_cu_count() * per_cu));
+  int grid;
+  if (SPLIT) {
+    grid = tiles;  // one tile per workgroup
+  } else {
+    int per_cu = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, reinterpret_cast<const void*>(kernel),
+                                                     64 * kMfmaWaves, lds) != hipSuccess ||
+        per_cu < 1)
+      per_cu = 1;
+    const int needed = (tiles + kMfmaWaves - 1) / kMfmaWaves;
+    grid = std::max(1, std::min(needed, device_cu_count() * per_cu));
+  }
   hipLaunchKernelGGL(kernel, dim3(grid), dim3(64 * kMfmaWaves), lds, stream, p.weights,
                      p.row_bytes, (int)p.rows, nblk, p.x, p.y);
   return hipGetLastError();
 }
 
+template <int TYPE, int C, bool ALIGNED>
+static hipError_t launch_mfma_ds(const MfmaChoice<TYPE>& c, const GemvProblem& p, hipStream_t s) {
+  if (c.split) return c.depth == kGemvDepth ? launch_mfma<TYPE, C, ALIGNED, kGemvDepth, true>(p, s)
+                                            : launch_mfma<TYPE, C, ALIGNED, 2, true>(p, s);
+  return c.depth == kGemvDepth ? launch_mfma<TYPE, C, ALIGNED, kGemvDepth, false>(p, s)
+                               : launch_mfma<TYPE, C, ALIGNED, 2, false>(p, s);
+}
+
 template <int TYPE>
 static hipError_t launch_mfma_type(const GemvProblem& p, hipStream_t stream) {
   const MfmaChoice<TYPE> c = mfma_choice<TYPE>(p);
+#if LLHIP_GEMV_CHUNK == 4
+  if (c.chunk == 4)
+    return c.aligned ? launch_mfma_ds<TYPE, 4, true>(c, p, stream)
+                     : launch_mfma_ds<TYPE, 4, false>(c, p, stream);
+#endif
   if (c.chunk == 2)
-    return c.aligned ? launch_mfma<TYPE, 2, true>(p, stream) : launch_mfma<TYPE, 2, false>(p, stream);
-  return c.aligned ? launch_mfma<TYPE, 1, true>(p, stream) : launch_mfma<TYPE, 1, false>(p, stream);
+    return c.aligned ? launch_mfma_ds<TYPE, 2, true>(c, p, stream)
+                     : launch_mfma_ds<TYPE, 2, false>(c, p, stream);
+  return c.aligned ? launch_mfma_ds<TYPE, 1, true>(c, p, stream)
+                   : launch_mfma_ds<TYPE, 1, false>(c, p, stream);
 }
 
 hipError_t gemv_mfma_launch(const GemvProblem& p, hipStream_t stream) {
