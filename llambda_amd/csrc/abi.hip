@@ -397,8 +397,8 @@ struct llambda_hip_moe_session {
   hipStream_t stream = nullptr;
   MoePlan plan{};
   DevBuf router, bias, gate, up, down, sh_gate, sh_up, sh_down;
-  DevBuf logits, top_idx, top_w, shared_w, counts, perm, chunks, chunk_counts, down_out, error,
-      xq, xsum, aq, asum;
+  DevBuf logits, router_part, top_idx, top_w, shared_w, counts, perm, chunks, chunk_counts,
+      down_out, error, xq, xsum, aq, asum, combine_counter;
   DevBuf x, y;
   int staged = 0;
   ~llambda_hip_moe_session() {
@@ -412,6 +412,9 @@ struct llambda_hip_moe_session {
     const size_t pairs = T * (K + 1);
     const size_t act_w = (size_t)std::max(p.ffn, p.shared_ffn);
     logits.alloc(T * (E + 1) * sizeof(float), "router logits");
+    p.router_ks = router_slices(p.hidden);
+    router_part.alloc((size_t)p.router_ks * T * (E + 1) * sizeof(float), "router slice sums");
+    p.router_part = router_part.as<float>();
     top_idx.alloc(T * K * sizeof(int), "top-k indices");
     top_w.alloc(T * K * sizeof(float), "top-k weights");
     shared_w.alloc(T * sizeof(float), "shared weights");
@@ -574,6 +577,8 @@ int llambda_hip_moe_session_create(const llambda_hip_moe_desc* d,
         p.sh_down = s->sh_down.as<uint8_t>();
       }
       s->counts.alloc((size_t)E * sizeof(int), "expert histogram");
+      s->combine_counter.alloc((size_t)moe_combine_tiles(p) * sizeof(int), "combine counters");
+      p.combine_counter = s->combine_counter.as<int>();
       s->chunk_counts.alloc(2 * sizeof(int), "chunk counts");
       s->error.alloc(sizeof(int), "error flag");
       p.counts = s->counts.as<int>();

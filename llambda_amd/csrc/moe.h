@@ -49,6 +49,8 @@ struct MoePlan {
   // scratch, sized for `capacity` tokens
   int capacity;
   float* logits;       // [capacity][experts + 1]
+  float* router_part;  // [router_ks][capacity][experts + 1]  router K-slice sums
+  int router_ks;
   int* top_idx;        // [capacity][top_k]
   float* top_w;        // [capacity][top_k]
   float* shared_w;     // [capacity]
@@ -63,6 +65,7 @@ struct MoePlan {
   float* asum;         // [capacity * (top_k + 1)][act_width/16]
   float* down_out;     // [capacity * (top_k + 1)][hidden]
   int* error;          // [1] nonzero after a run that hit a reference error
+  int* combine_counter;  // [hidden / 32 + 1] finished workgroups per row tile (one token)
 };
 
 // Grouped expert product over a chunk table (moe_mfma.hip).
@@ -101,16 +104,36 @@ struct MoeGemmArgs {
   float* out;
   int64_t out_stride;
   int depth;  // LDS stages per wave (set by the launcher)
+  // routed and shared chunks in one launch (same weight type): the shared
+  // expert's tensors, rows and K
+  int joint;
+  const uint8_t* s_w0;
+  const uint8_t* s_w1;
+  int64_t s_row_bytes;
+  int s_N, s_K;
+  // single token, down products: the combine of moe_combine_kernel, done by
+  // the last workgroup to finish each row tile (null y: not fused)
+  float* y;
+  const float* top_w;
+  const int* top_idx;
+  const float* shared_w;
+  int variant;
+  int* counter;  // [row tiles], zero between runs
 };
 
-// Router logits of T tokens (fp32 MFMA) and the split rows of x (q, s).
-hipError_t router_mfma_launch(const float* x, int T, const float* R, int Er, int H, float* logits,
+// Router logits of T tokens (fp32 MFMA) as router_slices(H) partial sums
+// part[slice][t][e] (row stride ld), and the split rows of x (q, s).
+int router_slices(int H);
+hipError_t router_mfma_launch(const float* x, int T, const float* R, int Er, int H, float* part,
                               int ld, uint16_t* q, int64_t q_stride, float* s, int64_t s_stride,
                               hipStream_t stream);
 // mt: 0 = one token (K split over four wavefronts), 1 = chunks of up to 16
 // pairs (double-buffered), 2 = chunks of up to 32 pairs.
 hipError_t moe_gemm_launch(int type, int epi, const MoeGemmArgs& a, int mt, int max_chunks,
                            hipStream_t stream);
+
+// Entries of MoePlan::combine_counter.
+int moe_combine_tiles(const MoePlan& p);
 
 // Upper bound of the chunk table for `tokens` tokens with chunk size nt.
 int64_t moe_max_chunks(const MoePlan& p, int64_t tokens, int nt);

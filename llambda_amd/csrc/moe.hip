@@ -18,55 +18,35 @@ namespace llhip {
 // r.  `bias` (optional) is added first and the biased logits are written
 // back.
 template <int JPL>
-__device__ __forceinline__ void wave_select(float* lg, const float* bias, int E, int K, int lane,
-                                            int& my_idx, float& my_val) {
-  float vals[JPL];
-#pragma unroll
-  for (int j = 0; j < JPL; ++j) {
-    const int e = lane + kWave * j;
-    float v = -INFINITY;
-    if (e < E) {
-      float raw = lg[e];
-      if (bias) {
-        raw = __fadd_rn(raw, bias[e]);
-        lg[e] = raw;
-      }
-      v = raw > -FLT_MAX ? raw : -INFINITY;  // NaN, -inf, -FLT_MAX never qualify
-    }
-    vals[j] = v;
-  }
+__device__ __forceinline__ void wave_select(float (&vals)[JPL], int K, int lane, int& my_idx,
+                                            float& my_val) {
   my_idx = -1;
   my_val = -FLT_MAX;
   for (int r = 0; r < K; ++r) {
-    float bv = -INFINITY;
-    int bi = INT_MAX;
+    // the lane's best (lowest index among equals), then the wave's
+    float lv = -INFINITY;
+    int li = INT_MAX;
 #pragma unroll
     for (int j = 0; j < JPL; ++j) {
-      if (vals[j] > bv) {
-        bv = vals[j];
-        bi = lane + kWave * j;
+      if (vals[j] > lv) {
+        lv = vals[j];
+        li = lane + kWave * j;
       }
     }
+    const float bv = wave_max(lv);
+    const int bi = wave_min(lv == bv ? li : INT_MAX);
+    const bool own = bi != INT_MAX && (bi & (kWave - 1)) == lane;
 #pragma unroll
-    for (int off = kWave / 2; off > 0; off >>= 1) {
-      const float ov = __shfl_xor(bv, off, kWave);
-      const int oi = __shfl_xor(bi, off, kWave);
-      if (ov > bv || (ov == bv && oi < bi)) {
-        bv = ov;
-        bi = oi;
-      }
-    }
-    if (bi != INT_MAX && (bi & (kWave - 1)) == lane) {
-#pragma unroll
-      for (int j = 0; j < JPL; ++j)
-        if (j == (bi >> 6)) vals[j] = -INFINITY;
-    }
+    for (int j = 0; j < JPL; ++j) vals[j] = (own && j == (bi >> 6)) ? -INFINITY : vals[j];
     if (lane == r && bi != INT_MAX) {
       my_idx = bi;
       my_val = bv;
     }
   }
 }
+
+// The selectable logits of one token: NaN, -inf and -FLT_MAX never qualify.
+__device__ __forceinline__ float selectable(float raw) { return raw > -FLT_MAX ? raw : -INFINITY; }
 
 template <int JPL>
 __global__ void __launch_bounds__(256) topk_kernel(const float* __restrict__ logits, int n, int k,
@@ -75,9 +55,15 @@ __global__ void __launch_bounds__(256) topk_kernel(const float* __restrict__ log
   const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
   if (t >= batch) return;
   const int lane = threadIdx.x & 63;
+  float vals[JPL];
+#pragma unroll
+  for (int j = 0; j < JPL; ++j) {
+    const int e = lane + kWave * j;
+    vals[j] = e < n ? selectable(logits[(int64_t)t * n + e]) : -INFINITY;
+  }
   int mi;
   float mv;
-  wave_select<JPL>(const_cast<float*>(logits + (int64_t)t * n), nullptr, n, k, lane, mi, mv);
+  wave_select<JPL>(vals, k, lane, mi, mv);
   if (lane < k) {
     idx[(int64_t)t * k + lane] = mi;
     val[(int64_t)t * k + lane] = mv;
@@ -98,10 +84,52 @@ __global__ void __launch_bounds__(256) topk_gate_kernel(MoePlan p, int tokens, i
   const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
   if (t >= tokens) return;
   const int E = p.experts, K = p.top_k;
-  float* lg = p.logits + (int64_t)t * (E + 1);
+  const int ld = E + 1;
+  float* lg = p.logits + (int64_t)t * ld;
+  // router logits: the K-slice partial sums in slice order (the router's
+  // fixed order), then nemotron's bias; written back for the caller.  The
+  // lane's JPL logits (and, on lane 0, the shared-gate logit in slot JPL)
+  // load slice by slice, all slots of a slice at once.
+  const bool has_shared_row = p.variant == kQwen3Next && p.shared_ffn > 0;
+  // (loads are unconditional from a clamped column -- rows have ld = E + 1
+  // entries -- and unused slots are dropped by the selects)
+  float acc[JPL + 1];
+  int col[JPL + 1];
+  bool use[JPL + 1];
+#pragma unroll
+  for (int j = 0; j <= JPL; ++j) {
+    const int e = j < JPL ? lane + kWave * j : E;
+    use[j] = j < JPL ? e < E : (lane == 0 && has_shared_row);
+    col[j] = min(e, E);
+    const float v = p.router_part[(int64_t)t * ld + col[j]];
+    acc[j] = use[j] ? v : 0.f;
+  }
+  for (int ks = 1; ks < p.router_ks; ++ks) {
+    const float* part = p.router_part + ((int64_t)ks * tokens + t) * ld;
+    float v[JPL + 1];
+#pragma unroll
+    for (int j = 0; j <= JPL; ++j) v[j] = part[col[j]];
+#pragma unroll
+    for (int j = 0; j <= JPL; ++j) acc[j] = use[j] ? acc[j] + v[j] : 0.f;
+  }
+  float vals[JPL];
+#pragma unroll
+  for (int j = 0; j < JPL; ++j) {
+    const int e = lane + kWave * j;
+    float v = -INFINITY;
+    if (e < E) {
+      float raw = acc[j];
+      if (p.variant == kNemotronH) raw = __fadd_rn(raw, p.bias[e]);
+      lg[e] = raw;
+      v = selectable(raw);
+    }
+    vals[j] = v;
+  }
+  const float shared_logit = acc[JPL];
+  if (lane == 0 && has_shared_row) lg[E] = shared_logit;
   int mi;
   float mv;
-  wave_select<JPL>(lg, p.variant == kNemotronH ? p.bias : nullptr, E, K, lane, mi, mv);
+  wave_select<JPL>(vals, K, lane, mi, mv);
   const bool has = lane < K;
   float w = has ? sigmoid_ref(mv) : 0.f;
   float sum = 0.f;
@@ -116,7 +144,7 @@ __global__ void __launch_bounds__(256) topk_gate_kernel(MoePlan p, int tokens, i
     p.top_idx[(int64_t)t * K + lane] = mi;
     p.top_w[(int64_t)t * K + lane] = w;
   }
-  if (lane == 0) p.shared_w[t] = p.variant == kQwen3Next ? sigmoid_ref(lg[E]) : 1.f;
+  if (lane == 0) p.shared_w[t] = has_shared_row ? sigmoid_ref(shared_logit) : 1.f;
   if (err) atomicOr(p.error, err);
   const bool valid = has && mi >= 0 && mi < E;
   if (!single) {
@@ -261,13 +289,17 @@ __global__ void __launch_bounds__(256) moe_combine_kernel(MoePlan p, float* __re
   y[(int64_t)t * H + i] = acc;
 }
 
-__global__ void moe_reset_kernel(int* counts, int n, int* error) {
+__global__ void moe_reset_kernel(int* counts, int n, int* combine, int ncombine, int* error) {
   for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x)
     counts[i] = 0;
+  for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < ncombine; i += gridDim.x * blockDim.x)
+    combine[i] = 0;
   if (blockIdx.x == 0 && threadIdx.x == 0) *error = 0;
 }
 
 // ------------------------------------------------------------------ host
+
+int moe_combine_tiles(const MoePlan& p) { return p.hidden / 32 + 1; }
 
 int64_t moe_max_chunks(const MoePlan& p, int64_t tokens, int nt) {
   const int64_t pairs = tokens * p.top_k;
@@ -318,7 +350,7 @@ hipError_t moe_forward_launch(const MoePlan& p, const float* x, float* y, int to
   const int act_w = std::max(p.ffn, p.shared_ffn);
   const int64_t xs_stride = H / 16, as_stride = act_w / 16;
   const int er = E + ((p.variant == kQwen3Next && has_shared) ? 1 : 0);
-  hipError_t e = router_mfma_launch(x, tokens, p.router, er, H, p.logits, E + 1, p.xq,
+  hipError_t e = router_mfma_launch(x, tokens, p.router, er, H, p.router_part, E + 1, p.xq,
                                     2 * (int64_t)H, p.xsum, xs_stride, s);
   if (e != hipSuccess) return e;
   const int single = tokens == 1;
@@ -359,6 +391,7 @@ hipError_t moe_forward_launch(const MoePlan& p, const float* x, float* y, int to
   up.os_stride = as_stride;
   const int epi = p.variant == kQwen3Next ? kEpiSwiglu : kEpiRelu2;
 
+  // routed, then shared, gate/up products: one launch when the types agree
   MoeGemmArgs a = up;
   a.group = 0;
   a.w0 = p.variant == kQwen3Next ? p.gate : p.up;
@@ -366,9 +399,18 @@ hipError_t moe_forward_launch(const MoePlan& p, const float* x, float* y, int to
   a.row_bytes = row_bytes_of(p.up_type, H);
   a.expert_stride = a.row_bytes * p.ffn;
   a.N = p.ffn;
-  e = moe_gemm_launch(p.up_type, epi, a, mt, routed_chunks, s);
+  const bool joint_up = has_shared && p.sh_up_type == p.up_type;
+  if (joint_up) {
+    a.joint = 1;
+    a.s_w0 = p.variant == kQwen3Next ? p.sh_gate : p.sh_up;
+    a.s_w1 = p.sh_up;
+    a.s_row_bytes = row_bytes_of(p.sh_up_type, H);
+    a.s_N = p.shared_ffn;
+    a.s_K = H;
+  }
+  e = moe_gemm_launch(p.up_type, epi, a, mt, routed_chunks + (joint_up ? shared_chunks : 0), s);
   if (e != hipSuccess) return e;
-  if (has_shared) {
+  if (has_shared && !joint_up) {
     a = up;
     a.group = 1;
     a.w0 = p.variant == kQwen3Next ? p.sh_gate : p.sh_up;
@@ -394,15 +436,32 @@ hipError_t moe_forward_launch(const MoePlan& p, const float* x, float* y, int to
   down.N = H;
   down.out = p.down_out;
   down.out_stride = H;
+  if (single) {
+    // the last workgroup of each row tile writes y
+    down.y = y;
+    down.top_w = p.top_w;
+    down.top_idx = p.top_idx;
+    down.shared_w = p.shared_w;
+    down.variant = p.variant;
+    down.counter = p.combine_counter;
+  }
   a = down;
   a.group = 0;
   a.K = p.ffn;
   a.w0 = p.down;
   a.row_bytes = row_bytes_of(p.down_type, p.ffn);
   a.expert_stride = a.row_bytes * H;
-  e = moe_gemm_launch(p.down_type, kEpiDown, a, mt, routed_chunks, s);
+  const bool joint_down = has_shared && p.sh_down_type == p.down_type;
+  if (joint_down) {
+    a.joint = 1;
+    a.s_w0 = p.sh_down;
+    a.s_row_bytes = row_bytes_of(p.sh_down_type, p.shared_ffn);
+    a.s_N = H;
+    a.s_K = p.shared_ffn;
+  }
+  e = moe_gemm_launch(p.down_type, kEpiDown, a, mt, routed_chunks + (joint_down ? shared_chunks : 0), s);
   if (e != hipSuccess) return e;
-  if (has_shared) {
+  if (has_shared && !joint_down) {
     a = down;
     a.group = 1;
     a.K = p.shared_ffn;
@@ -412,12 +471,14 @@ hipError_t moe_forward_launch(const MoePlan& p, const float* x, float* y, int to
     e = moe_gemm_launch(p.sh_down_type, kEpiDown, a, mt, shared_chunks, s);
     if (e != hipSuccess) return e;
   }
+  if (single) return hipSuccess;
   return launch(moe_combine_kernel, dim3((H + 255) / 256, tokens), dim3(256), 0, s, p, y, tokens,
                 has_shared);
 }
 
 hipError_t moe_reset_launch(const MoePlan& p, hipStream_t s) {
-  return launch(moe_reset_kernel, dim3(4), dim3(256), 0, s, p.counts, p.experts, p.error);
+  return launch(moe_reset_kernel, dim3(4), dim3(256), 0, s, p.counts, p.experts, p.combine_counter,
+                moe_combine_tiles(p), p.error);
 }
 
 hipError_t topk_launch(const float* logits, int n, int k, int batch, int* idx, float* val,

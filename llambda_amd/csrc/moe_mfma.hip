@@ -90,29 +90,30 @@ __device__ __forceinline__ void split_octet(const float* __restrict__ xrow, int 
 }
 
 // -------------------------------------------------------------------- router
-// logits[t * ld + e] = sum_h x[t][h] R[e][h] (dot-product-with-f32-tensor-data,
-// llambda.lisp:4096-4107, in another fp32 order) for a 16 x 16 (token, expert)
-// tile per workgroup.  K is cut into 16-element pieces; piece p belongs to
-// chain p % 32, and each chain accumulates its pieces in order on
-// v_mfma_f32_16x16x4_f32.  Wave w (of 8) runs chains 4w .. 4w+3 side by side,
-// adds them as (c0 + c1) + (c2 + c3), and the eight wave sums are added as
-// ((w0 + w1) + (w2 + w3)) + ((w4 + w5) + (w6 + w7)): one fixed order for
-// every batch size.  The expert-tile-0 workgroups also write the split rows
-// of their 16 tokens for the expert products.
+// Router logits sum_h x[t][h] R[e][h] (dot-product-with-f32-tensor-data,
+// llambda.lisp:4096-4107, in another fp32 order), in one fixed order for
+// every batch size: K is cut into slices of 512; workgroup (e-tile, t-tile,
+// slice) adds its slice's 32 pieces of 16 elements for a 16 x 16 tile on
+// v_mfma_f32_16x16x4_f32 -- wave w of 8 takes pieces 4w .. 4w+3, adds them as
+// (p0 + p1) + (p2 + p3), and the wave sums meet as ((w0 + w1) + (w2 + w3)) +
+// ((w4 + w5) + (w6 + w7)) -- and writes the slice's partial sum to
+// part[slice][t][e]; the top-k kernel adds the slices in order.  Expert-tile
+// 0 workgroups also write their tokens' split rows over their slice.
 constexpr int kRouterWaves = 8;
+constexpr int kRouterSlice = 512;
 
 __global__ void __launch_bounds__(64 * kRouterWaves)
 router_mfma_kernel(const float* __restrict__ x, int T, const float* __restrict__ R, int Er, int H,
-                   float* __restrict__ logits, int ld, uint16_t* __restrict__ q, int64_t q_stride,
+                   float* __restrict__ part, int ld, uint16_t* __restrict__ q, int64_t q_stride,
                    float* __restrict__ s, int64_t s_stride) {
   __shared__ floatx4 red[kRouterWaves][64];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int i = lane & 15, kg = lane >> 4;
-  const int t0 = blockIdx.y * 16, e0 = blockIdx.x * 16;
+  const int t0 = blockIdx.y * 16, e0 = blockIdx.x * 16, k0 = blockIdx.z * kRouterSlice;
   if (blockIdx.x == 0) {
-    const int octets = H >> 3;
+    const int octets = min(kRouterSlice, H - k0) >> 3, ofirst = k0 >> 3;
     for (int idx = threadIdx.x; idx < 16 * octets; idx += 64 * kRouterWaves) {
-      const int tt = idx / octets, o = idx - tt * octets;
+      const int tt = idx / octets, o = ofirst + idx - tt * octets;
       if (t0 + tt < T)
         split_octet(x + (int64_t)(t0 + tt) * H, o, q + (int64_t)(t0 + tt) * q_stride,
                     s + (int64_t)(t0 + tt) * s_stride);
@@ -122,19 +123,16 @@ router_mfma_kernel(const float* __restrict__ x, int T, const float* __restrict__
   const float* rr = R + (int64_t)min(e0 + i, Er - 1) * H + 4 * kg;
   floatx4 acc[4];
 #pragma unroll
-  for (int c = 0; c < 4; ++c) acc[c] = floatx4{0.f, 0.f, 0.f, 0.f};
-  for (int k0 = 64 * wave; k0 < H; k0 += 64 * kRouterWaves) {
-#pragma unroll
-    for (int c = 0; c < 4; ++c) {
-      const int k = k0 + 16 * c;
-      if (k < H) {
-        const float4 xa = *reinterpret_cast<const float4*>(xr + k);
-        const float4 rb = *reinterpret_cast<const float4*>(rr + k);
-        acc[c] = mfma4f32(xa.x, rb.x, acc[c]);
-        acc[c] = mfma4f32(xa.y, rb.y, acc[c]);
-        acc[c] = mfma4f32(xa.z, rb.z, acc[c]);
-        acc[c] = mfma4f32(xa.w, rb.w, acc[c]);
-      }
+  for (int c = 0; c < 4; ++c) {
+    acc[c] = floatx4{0.f, 0.f, 0.f, 0.f};
+    const int k = k0 + 64 * wave + 16 * c;
+    if (k < H) {
+      const float4 xa = *reinterpret_cast<const float4*>(xr + k);
+      const float4 rb = *reinterpret_cast<const float4*>(rr + k);
+      acc[c] = mfma4f32(xa.x, rb.x, acc[c]);
+      acc[c] = mfma4f32(xa.y, rb.y, acc[c]);
+      acc[c] = mfma4f32(xa.z, rb.z, acc[c]);
+      acc[c] = mfma4f32(xa.w, rb.w, acc[c]);
     }
   }
   red[wave][lane] = (acc[0] + acc[1]) + (acc[2] + acc[3]);
@@ -144,19 +142,22 @@ router_mfma_kernel(const float* __restrict__ x, int T, const float* __restrict__
                     ((red[4][lane] + red[5][lane]) + (red[6][lane] + red[7][lane]));
   const int e = e0 + i;
   if (e >= Er) return;
+  float* out = part + (int64_t)blockIdx.z * T * ld;
 #pragma unroll
   for (int r = 0; r < 4; ++r) {
     const int t = t0 + 4 * kg + r;
-    if (t < T) logits[(int64_t)t * ld + e] = v[r];
+    if (t < T) out[(int64_t)t * ld + e] = v[r];
   }
 }
 
-hipError_t router_mfma_launch(const float* x, int T, const float* R, int Er, int H, float* logits,
+int router_slices(int H) { return (H + kRouterSlice - 1) / kRouterSlice; }
+
+hipError_t router_mfma_launch(const float* x, int T, const float* R, int Er, int H, float* part,
                               int ld, uint16_t* q, int64_t q_stride, float* s, int64_t s_stride,
                               hipStream_t stream) {
-  const dim3 grid((Er + 15) / 16, (T + 15) / 16);
+  const dim3 grid((Er + 15) / 16, (T + 15) / 16, router_slices(H));
   hipLaunchKernelGGL(router_mfma_kernel, grid, dim3(64 * kRouterWaves), 0, stream, x, T, R, Er, H,
-                     logits, ld, q, q_stride, s, s_stride);
+                     part, ld, q, q_stride, s, s_stride);
   return hipGetLastError();
 }
 
@@ -378,16 +379,29 @@ constexpr int gemm_lds_bytes(int depth) {
 template <int TYPE, int EPI, int MT, int PIPE, bool ALIGNED>
 __global__ void __launch_bounds__((64 * GemmShape<TYPE, EPI, PIPE>::kWaves),
                                   (PIPE == kPipeWide ? 2 : 1))
-moe_gemm_kernel(MoeGemmArgs a) {
+moe_gemm_kernel(MoeGemmArgs args) {
   using B = GemmB<TYPE>;
   using Sh = GemmShape<TYPE, EPI, PIPE>;
   constexpr int NB = Sh::NB, NS = Sh::NS, NQ = B::kSteps / 4, KS = B::kSteps;
   typedef AFrag<B::kWide> AF;
   extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
 
-  const int nchunks = a.chunk_counts[a.group];
+  const int* cc = args.chunk_counts;
+  const int all_chunks = cc[0] + cc[1];
+  const int nchunks = args.joint ? all_chunks : cc[args.group];
   if ((int)blockIdx.x >= nchunks) return;
-  const MoeChunk ch = a.chunks[(a.group ? a.chunk_counts[0] : 0) + blockIdx.x];
+  // joint launches: routed chunks, then the shared expert's (their entries
+  // follow the routed ones in the table)
+  const MoeChunk ch = args.chunks[args.joint ? blockIdx.x : (args.group ? cc[0] : 0) + blockIdx.x];
+  MoeGemmArgs a = args;
+  if (args.joint && (int)blockIdx.x >= cc[0]) {
+    a.w0 = args.s_w0;
+    a.w1 = args.s_w1;
+    a.row_bytes = args.s_row_bytes;
+    a.expert_stride = 0;
+    a.N = args.s_N;
+    a.K = args.s_K;
+  }
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int n = lane & 15, g = lane >> 4;
@@ -709,6 +723,50 @@ moe_gemm_kernel(MoeGemmArgs a) {
       }
     }
   }
+
+  // single token: the last workgroup to finish a row tile combines it in
+  // rank order, then the shared expert (moe_combine_kernel's arithmetic)
+  if constexpr (PIPE == kPipeDecode && EPI == kEpiDown) {
+    if (a.y != nullptr) {
+      __threadfence();
+      int last = 0;
+      if (lane == 0) last = atomicAdd(&a.counter[blockIdx.y], 1) == all_chunks - 1;
+      last = __shfl(last, 0, kWave);
+      if (last) {
+#pragma clang fp contract(off)
+        __threadfence();
+        const int i = n0 + lane;
+        // (this workgroup has not read these rows before: plain loads see the
+        // other workgroups' writes once the fences above have ordered them)
+        if (lane < Sh::ROWS && i < a.N) {
+          float acc = 0.f;
+          for (int r0 = 0; r0 < a.top_k; r0 += 8) {
+            float d[8];
+#pragma unroll
+            for (int u = 0; u < 8; ++u)
+              d[u] = r0 + u < a.top_k ? a.out[(int64_t)(r0 + u) * a.out_stride + i] : 0.f;
+#pragma unroll
+            for (int u = 0; u < 8; ++u) {
+              if (r0 + u >= a.top_k || a.top_idx[r0 + u] < 0) continue;
+              const float prod = a.top_w[r0 + u] * d[u];
+              acc = acc + prod;
+            }
+          }
+          if (cc[1] > 0) {
+            const float d = a.out[(int64_t)a.top_k * a.out_stride + i];
+            if (a.variant == kQwen3Next) {
+              const float prod = a.shared_w[0] * d;
+              acc = acc + prod;
+            } else {
+              acc = acc + d;
+            }
+          }
+          a.y[i] = acc;
+        }
+        if (lane == 0) a.counter[blockIdx.y] = 0;
+      }
+    }
+  }
 }
 
 // ------------------------------------------------------------------ host
@@ -717,7 +775,7 @@ template <int TYPE, int EPI, int MT, int PIPE, bool ALIGNED>
 static hipError_t launch_gemm_t(const MoeGemmArgs& a_in, int max_chunks, hipStream_t stream) {
   using Sh = GemmShape<TYPE, EPI, PIPE>;
   MoeGemmArgs a = a_in;
-  const int nchunk = (a.K + 255) / 256;
+  const int nchunk = (std::max(a.K, a.joint ? a.s_K : 0) + 255) / 256;
   const int per_wave = (nchunk + Sh::kWaves - 1) / Sh::kWaves;
   a.depth = PIPE == kPipeDecode ? std::max(1, std::min(Sh::DEPTH, per_wave)) : Sh::DEPTH;
   const int lds = gemm_lds_bytes<TYPE, EPI, PIPE>(a.depth);
@@ -727,7 +785,8 @@ static hipError_t launch_gemm_t(const MoeGemmArgs& a_in, int max_chunks, hipStre
                                        hipFuncAttributeMaxDynamicSharedMemorySize, lds);
     if (e != hipSuccess) return e;
   }
-  const dim3 grid(max_chunks, (a.N + Sh::WG_ROWS - 1) / Sh::WG_ROWS);
+  const int rows = a.joint ? std::max(a.N, a.s_N) : a.N;
+  const dim3 grid(max_chunks, (rows + Sh::WG_ROWS - 1) / Sh::WG_ROWS);
   hipLaunchKernelGGL(kernel, grid, dim3(64 * Sh::kWaves), lds, stream, a);
   return hipGetLastError();
 }
@@ -744,8 +803,10 @@ static hipError_t launch_gemm_mt(const MoeGemmArgs& a, int mt, int max_chunks, h
 
 template <int TYPE, int EPI>
 static hipError_t launch_gemm_al(const MoeGemmArgs& a, int mt, int max_chunks, hipStream_t s) {
-  // Q4_K rows are always whole 144-byte blocks (16-byte multiples)
-  if (TYPE == kQ4_K || a.row_bytes % 4 == 0) return launch_gemm_mt<TYPE, EPI, true>(a, mt, max_chunks, s);
+  // Q4_K rows are always whole 144-byte blocks (16-byte multiples); a joint
+  // launch is aligned only if the shared expert's rows are too
+  const bool aligned = a.row_bytes % 4 == 0 && (!a.joint || a.s_row_bytes % 4 == 0);
+  if (TYPE == kQ4_K || aligned) return launch_gemm_mt<TYPE, EPI, true>(a, mt, max_chunks, s);
   if constexpr (TYPE != kQ4_K) return launch_gemm_mt<TYPE, EPI, false>(a, mt, max_chunks, s);
   return hipErrorInvalidValue;
 }
