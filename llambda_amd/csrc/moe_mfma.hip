@@ -1,10 +1,10 @@
 // moe_mfma.hip -- the routed-MoE products on MFMA.
 //
-//   split_rows_kernel   fp32 activation rows -> "split rows": every element
-//                       as two bf16 (hi + lo, |x - hi - lo| <= 2^-17 |x|) plus
-//                       the sum of each 16-element group of fl(hi) + fl(lo).
 //   router_mfma_kernel  the F32 router as a GEMM on v_mfma_f32_16x16x4_f32
-//                       (fp32 products, fp32 accumulation).
+//                       (fp32 products, fp32 accumulation) in K slices of 512,
+//                       and the tokens' "split rows": every element as two
+//                       bf16 (hi + lo, |x - hi - lo| <= 2^-17 |x|) plus the
+//                       sum of each 16-element group of fl(hi) + fl(lo).
 //   moe_gemm_kernel     the grouped expert products over the chunk table
 //                       (expert, up to 16*MT (token, rank) pairs): gate/up
 //                       with silu(g)*u or relu(u)^2 fused, or down.
