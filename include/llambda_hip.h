@@ -33,6 +33,7 @@ extern "C" {
 
 typedef struct llambda_hip_session llambda_hip_session;
 typedef struct llambda_hip_moe_session llambda_hip_moe_session;
+typedef struct llambda_hip_llama_session llambda_hip_llama_session;
 
 /* ---- probe, versions, errors -------------------------------------- */
 
@@ -193,6 +194,98 @@ int llambda_hip_moe_session_sync(llambda_hip_moe_session* session, void* stream)
  * unfilled slots (-1, -FLT_MAX).  Host pointers, synchronous, on the device. */
 int llambda_hip_select_top_k(const float* logits, size_t n, size_t k, size_t batch,
                              int64_t* top_indices, float* top_logits);
+
+/* ---- Llama-layout decode token ---------------------------------------- */
+
+/* One packed 2-D tensor: GGML type tag and its rows (rows * row_bytes bytes,
+ * host memory, or device memory when the descriptor says so). */
+typedef struct llambda_hip_tensor_ref {
+  int type;
+  const void* data;
+  size_t bytes;
+} llambda_hip_tensor_ref;
+
+/* Tensors of layer N (blk.N.<name>.weight, llambda.lisp:6294-6441). */
+typedef struct llambda_hip_llama_layer {
+  const float* attn_norm;             /* attn_norm, F32 [hidden], host */
+  llambda_hip_tensor_ref attn_q;      /* [heads * head_dim][hidden] */
+  llambda_hip_tensor_ref attn_k;      /* [kv_heads * head_dim][hidden] */
+  llambda_hip_tensor_ref attn_v;      /* [kv_heads * head_dim][hidden] */
+  llambda_hip_tensor_ref attn_output; /* [hidden][heads * head_dim] */
+  const float* ffn_norm;              /* ffn_norm, F32 [hidden], host */
+  llambda_hip_tensor_ref ffn_gate;    /* [ffn][hidden] */
+  llambda_hip_tensor_ref ffn_up;      /* [ffn][hidden] */
+  llambda_hip_tensor_ref ffn_down;    /* [hidden][ffn] */
+} llambda_hip_llama_layer;
+
+/* Model hyper-parameters as load-llama-model reads them
+ * (llambda.lisp:6269-6292) and its tensors.  Quantised tensors must be
+ * Q4_K or Q6_K with a column count divisible by 256; q and k (and gate and
+ * up) of a layer that share a type are stored side by side on the device. */
+typedef struct llambda_hip_llama_desc {
+  int64_t hidden;             /* llama.embedding_length */
+  int64_t layer_count;        /* llama.block_count */
+  int64_t head_count;         /* llama.attention.head_count */
+  int64_t kv_head_count;      /* llama.attention.head_count_kv */
+  int64_t ffn;                /* llama.feed_forward_length */
+  int64_t vocab;              /* rows of token_embd and output */
+  int64_t rope_dimension;     /* llama.rope.dimension_count */
+  float norm_epsilon;         /* llama.attention.layer_norm_rms_epsilon */
+  float rope_base;            /* llama.rope.freq_base */
+  const float* rope_factors;  /* rope_freqs.weight, host, NULL if absent */
+  int64_t rope_factor_count;
+  int64_t context;            /* KV cache slots (positions) to allocate */
+  int weights_on_device;      /* 1: tensor data pointers are device memory */
+  llambda_hip_tensor_ref token_embd;  /* [vocab][hidden] */
+  llambda_hip_tensor_ref output;      /* [vocab][hidden] */
+  const float* output_norm;           /* output_norm, F32 [hidden], host */
+  const llambda_hip_llama_layer* layers; /* [layer_count] */
+} llambda_hip_llama_desc;
+
+/* Upload a model for device-resident decoding, with a zeroed fp32 KV cache
+ * of `context` slots per layer.  No counterpart in the reference's bridge:
+ * this is the model-level hook for make-llama-step-function
+ * (llambda.lisp:6294-6441), whose step runs every projection, norm,
+ * rotation and attention of a token on the device. */
+int llambda_hip_llama_session_create(const llambda_hip_llama_desc* desc,
+                                     llambda_hip_llama_session** result);
+
+void llambda_hip_llama_session_destroy(llambda_hip_llama_session* session);
+
+/* vocab; 0 for null. */
+size_t llambda_hip_llama_session_vocab(const llambda_hip_llama_session* session);
+
+/* One decode step of the step function (token-id position) -> logits
+ * (llambda.lisp:6315-6441): the token's keys and values go to cache slot
+ * `position`, attention covers slots 0..position.  logits: host [vocab].
+ * Synchronous. */
+int llambda_hip_llama_session_step(llambda_hip_llama_session* session, int64_t token,
+                                   int64_t position, float* logits, size_t logits_count);
+
+/* Device-resident form: logits is device memory [vocab] (null = the
+ * session's own logits buffer, read back with llambda_hip_llama_session_logits);
+ * enqueued on `stream` (null = the session's stream).  use_graph = 1 replays
+ * a HIP graph of the step captured on the first call for these logits. */
+int llambda_hip_llama_session_step_device(llambda_hip_llama_session* session, int64_t token,
+                                          int64_t position, float* logits, void* stream,
+                                          int use_graph);
+
+/* Copy the session's own logits buffer (the last step_device with null
+ * logits) to host memory after waiting for the session's stream. */
+int llambda_hip_llama_session_logits(llambda_hip_llama_session* session, float* logits,
+                                     size_t logits_count);
+
+/* Copy cache slots [first, first + count) of `layer` in or out: keys and
+ * values are [kv_heads][count][head_dim] fp32 (host memory, or device
+ * memory for write when on_device = 1).  Synchronous. */
+int llambda_hip_llama_session_write_kv(llambda_hip_llama_session* session, int64_t layer,
+                                       int64_t first, int64_t count, const float* keys,
+                                       const float* values, int on_device);
+int llambda_hip_llama_session_read_kv(llambda_hip_llama_session* session, int64_t layer,
+                                      int64_t first, int64_t count, float* keys, float* values);
+
+/* Wait for `stream` (null = the session's stream). */
+int llambda_hip_llama_session_sync(llambda_hip_llama_session* session, void* stream);
 
 #ifdef __cplusplus
 }

@@ -13,12 +13,15 @@
 #include <climits>
 #include <cstdarg>
 #include <cstdio>
+#include <cmath>
 #include <cstring>
+#include <memory>
 #include <mutex>
 #include <stdexcept>
 #include <string>
 #include <vector>
 
+#include "decoder.h"
 #include "gemv.h"
 #include "moe.h"
 #include "sha256.h"
@@ -696,6 +699,409 @@ int llambda_hip_select_top_k(const float* logits, size_t n, size_t k, size_t bat
     HIPC(hipMemcpyAsync(top_logits, dv.ptr, batch * k * sizeof(float), hipMemcpyDeviceToHost, stream));
     HIPC(hipStreamSynchronize(stream));
     for (size_t i = 0; i < idx.size(); ++i) top_indices[i] = idx[i];
+  });
+}
+
+}  // extern "C"
+
+// ---------------------------------------------------------- Llama decoder
+
+struct llambda_hip_llama_session {
+  std::mutex run_mutex;
+  int device = 0;
+  hipStream_t stream = nullptr;
+  DecoderPlan plan{};
+  std::vector<DecoderLayer> layers;
+  std::vector<std::unique_ptr<DevBuf>> weights;
+  DevBuf norms, kv, state, rope_denom, rope_cs, x, q, ctx, h, att_part, att_max, att_sum,
+      att_counter, logits;
+  int64_t layer_count = 0;
+  hipGraph_t graph = nullptr;
+  hipGraphExec_t exec = nullptr;
+  float* graph_logits = nullptr;
+  ~llambda_hip_llama_session() {
+    if (exec) (void)hipGraphExecDestroy(exec);
+    if (graph) (void)hipGraphDestroy(graph);
+    if (stream) (void)hipStreamDestroy(stream);
+  }
+  DevBuf& new_weights() {
+    weights.emplace_back(new DevBuf());
+    return *weights.back();
+  }
+  float* kcache(int64_t l) const {
+    return kv.as<float>() + (size_t)(2 * l) * plan.kv_heads * plan.context * plan.head_dim;
+  }
+  float* vcache(int64_t l) const { return kcache(l) + (size_t)plan.kv_heads * plan.context * plan.head_dim; }
+};
+
+namespace {
+
+int64_t decoder_row_bytes(const llambda_hip_tensor_ref& t, int64_t rows, int64_t columns,
+                          bool gemv, const char* what) {
+  if (gemv && t.type != kQ4_K && t.type != kQ6_K)
+    failf("%s: tensor type %s is not supported by the decoder (Q4_K or Q6_K)", what,
+          type_name(t.type));
+  if (!gemv && t.type != kQ4_K && t.type != kQ6_K && t.type != kQ5_0 && t.type != kQ8_0)
+    failf("%s: tensor type %s is not supported for the token embedding", what, type_name(t.type));
+  const int64_t rb = checked_row_bytes(t.type, columns, what);
+  if (!t.data) failf("%s: null tensor data", what);
+  if ((uint64_t)rows * (uint64_t)rb != t.bytes)
+    failf("%s: %zu bytes do not hold %lld rows of %lld %s columns", what, t.bytes,
+          (long long)rows, (long long)columns, type_name(t.type));
+  return rb;
+}
+
+void validate_device(const DevBuf& b, int type, size_t bytes, hipStream_t s, const char* what) {
+  DevBuf flag;
+  flag.alloc(sizeof(unsigned long long), "validation flag");
+  const unsigned long long none = ULLONG_MAX;
+  HIPC(hipMemcpyAsync(flag.ptr, &none, sizeof none, hipMemcpyHostToDevice, s));
+  HIPC(validate_launch(type, b.as<uint8_t>(), (int64_t)(bytes / block_bytes(type)),
+                       flag.as<unsigned long long>(), s));
+  unsigned long long first_bad = 0;
+  HIPC(hipMemcpyAsync(&first_bad, flag.ptr, sizeof first_bad, hipMemcpyDeviceToHost, s));
+  HIPC(hipStreamSynchronize(s));
+  if (first_bad != ULLONG_MAX)
+    failf("%s: Unsupported fp16 special value (Inf/NaN scale) in block %llu.", what, first_bad);
+}
+
+// Copy `parts` tensors (same type and columns) into one slab, rows of part i
+// after those of part i - 1; with interleave8 (two parts) rows go in groups
+// of 8: part 0 rows 8t..8t+7, then part 1 rows 8t..8t+7.
+DecoderMatrix upload_slab(llambda_hip_llama_session* s, const llambda_hip_tensor_ref* parts,
+                          const int64_t* rows, int n, int64_t columns, bool interleave8,
+                          bool on_device, const char* what) {
+  DecoderMatrix m;
+  m.type = parts[0].type;
+  m.columns = columns;
+  int64_t total = 0;
+  for (int i = 0; i < n; ++i) {
+    if (parts[i].type != m.type) failf("%s: parts of one slab differ in type", what);
+    m.row_bytes = decoder_row_bytes(parts[i], rows[i], columns, true, what);
+    total += rows[i];
+  }
+  m.rows = total;
+  const size_t bytes = (size_t)total * m.row_bytes;
+  DevBuf& buf = s->new_weights();
+  buf.alloc(bytes + kWeightPad, what);
+  HIPC(hipMemsetAsync(buf.as<uint8_t>() + bytes, 0, kWeightPad, s->stream));
+  const hipMemcpyKind kind = on_device ? hipMemcpyDeviceToDevice : hipMemcpyHostToDevice;
+  if (interleave8) {
+    if (n != 2 || rows[0] != rows[1] || rows[0] % 8)
+      failf("%s: gate and up need equal row counts divisible by 8", what);
+    const size_t w = 8 * (size_t)m.row_bytes;
+    for (int i = 0; i < 2; ++i)
+      HIPC(hipMemcpy2DAsync(buf.as<uint8_t>() + i * w, 2 * w, parts[i].data, w, w,
+                            (size_t)(rows[i] / 8), kind, s->stream));
+  } else {
+    size_t off = 0;
+    for (int i = 0; i < n; ++i) {
+      HIPC(hipMemcpyAsync(buf.as<uint8_t>() + off, parts[i].data, parts[i].bytes, kind, s->stream));
+      off += parts[i].bytes;
+    }
+  }
+  validate_device(buf, m.type, bytes, s->stream, what);
+  m.w = buf.as<uint8_t>();
+  return m;
+}
+
+}  // namespace
+
+extern "C" {
+
+int llambda_hip_llama_session_create(const llambda_hip_llama_desc* d,
+                                     llambda_hip_llama_session** result) {
+  return guarded([&] {
+    if (!result) failf("llama session: null result pointer");
+    *result = nullptr;
+    if (!d) failf("llama session: null descriptor");
+    const int64_t H = d->hidden, NH = d->head_count, NKV = d->kv_head_count;
+    if (H <= 0 || NH <= 0 || NKV <= 0 || d->layer_count <= 0 || d->ffn <= 0 || d->vocab <= 0)
+      failf("llama session: non-positive dimension");
+    if (H % NH) failf("Llama hidden size %lld is not divisible by head count %lld.", (long long)H,
+                      (long long)NH);
+    if (NH % NKV)
+      failf("Llama head count %lld is not divisible by KV head count %lld.", (long long)NH,
+            (long long)NKV);
+    const int64_t D = H / NH;
+    if (!decoder_head_supported((int)D, (int)(NH / NKV)))
+      failf("llama session: head size %lld with %lld query heads per kv head is not supported "
+            "(head size 64 or 128, group 1, 2, 4 or 8)", (long long)D, (long long)(NH / NKV));
+    if (d->context <= 0 || d->context > kDecoderMaxContext)
+      failf("llama session: context %lld out of range (1..%d)", (long long)d->context,
+            kDecoderMaxContext);
+    if (d->ffn % 16) failf("llama session: ffn %lld must be a multiple of 16", (long long)d->ffn);
+    if (!d->layers || !d->output_norm) failf("llama session: null layer list or output_norm");
+    if (d->rope_factor_count < 0 || (d->rope_factor_count > 0 && !d->rope_factors))
+      failf("llama session: bad rope factors");
+    const bool dev = d->weights_on_device != 0;
+
+    std::unique_ptr<llambda_hip_llama_session> s(new llambda_hip_llama_session());
+    s->device = current_device_checked();
+    HIPC(hipStreamCreateWithFlags(&s->stream, hipStreamNonBlocking));
+    DecoderPlan& p = s->plan;
+    p.hidden = (int)H;
+    p.heads = (int)NH;
+    p.kv_heads = (int)NKV;
+    p.head_dim = (int)D;
+    p.ffn = (int)d->ffn;
+    p.vocab = (int)d->vocab;
+    p.context = (int)d->context;
+    p.eps = d->norm_epsilon;
+    // (coerce (/ (sqrt head-size)) 'single-float), llambda.lisp:6304
+    p.q_scale = 1.f / sqrtf((float)D);
+    s->layer_count = d->layer_count;
+
+    // rotation: apply-rope-head-in-place (llambda.lisp:3760-3795)
+    const int64_t factor_limit = d->rope_factor_count > 0 ? 2 * d->rope_factor_count
+                                                          : d->rope_dimension;
+    const int64_t eff = std::min(std::min(d->rope_dimension, factor_limit), D);
+    const int64_t even = 2 * (eff / 2);
+    p.rope_pairs = (int)(even / 2);
+    std::vector<double> denom((size_t)std::max<int64_t>(p.rope_pairs, 1), 1.0);
+    for (int64_t i = 0; i < p.rope_pairs; ++i) {
+      const double factor = (d->rope_factors && i < d->rope_factor_count)
+                                ? (double)d->rope_factors[i] : 1.0;
+      // (expt theta-base (/ (* 2 i) even)): single-float base, rational
+      // power -> single-float result
+      const float power = (float)pow((double)d->rope_base, (double)(2 * i) / (double)even);
+      denom[(size_t)i] = factor > 1.0e20 ? INFINITY : factor * (double)power;
+    }
+
+    // norms: attn and ffn per layer, then output
+    const size_t nvec = (size_t)(2 * d->layer_count + 1);
+    s->norms.alloc(nvec * (size_t)H * sizeof(float), "norm vectors");
+    for (int64_t l = 0; l < d->layer_count; ++l) {
+      const llambda_hip_llama_layer& L = d->layers[l];
+      if (!L.attn_norm || !L.ffn_norm) failf("llama session: layer %lld: null norm vector", (long long)l);
+      HIPC(hipMemcpyAsync(s->norms.as<float>() + (size_t)(2 * l) * H, L.attn_norm, H * sizeof(float),
+                          hipMemcpyHostToDevice, s->stream));
+      HIPC(hipMemcpyAsync(s->norms.as<float>() + (size_t)(2 * l + 1) * H, L.ffn_norm,
+                          H * sizeof(float), hipMemcpyHostToDevice, s->stream));
+    }
+    HIPC(hipMemcpyAsync(s->norms.as<float>() + (nvec - 1) * H, d->output_norm, H * sizeof(float),
+                        hipMemcpyHostToDevice, s->stream));
+    p.output_norm = s->norms.as<float>() + (nvec - 1) * H;
+
+    // KV cache, zeroed
+    const size_t kv_floats = (size_t)d->layer_count * 2 * NKV * d->context * D;
+    s->kv.alloc(kv_floats * sizeof(float), "KV cache");
+    HIPC(hipMemsetAsync(s->kv.ptr, 0, kv_floats * sizeof(float), s->stream));
+
+    // tensors
+    {
+      const int64_t rows[1] = {d->vocab};
+      char what[64];
+      snprintf(what, sizeof what, "token_embd");
+      decoder_row_bytes(d->token_embd, d->vocab, H, false, what);
+      DevBuf& buf = s->new_weights();
+      buf.alloc(d->token_embd.bytes + kWeightPad, what);
+      HIPC(hipMemsetAsync(buf.as<uint8_t>() + d->token_embd.bytes, 0, kWeightPad, s->stream));
+      HIPC(hipMemcpyAsync(buf.ptr, d->token_embd.data, d->token_embd.bytes,
+                          dev ? hipMemcpyDeviceToDevice : hipMemcpyHostToDevice, s->stream));
+      validate_device(buf, d->token_embd.type, d->token_embd.bytes, s->stream, what);
+      p.embd.type = d->token_embd.type;
+      p.embd.w = buf.as<uint8_t>();
+      p.embd.row_bytes = checked_row_bytes(p.embd.type, H, what);
+      p.embd.rows = d->vocab;
+      p.embd.columns = H;
+      p.output = upload_slab(s.get(), &d->output, rows, 1, H, false, dev, "output");
+    }
+    s->layers.resize((size_t)d->layer_count);
+    for (int64_t l = 0; l < d->layer_count; ++l) {
+      const llambda_hip_llama_layer& L = d->layers[l];
+      DecoderLayer& o = s->layers[(size_t)l];
+      char what[64];
+      o.attn_norm = s->norms.as<float>() + (size_t)(2 * l) * H;
+      o.ffn_norm = s->norms.as<float>() + (size_t)(2 * l + 1) * H;
+      const int64_t qr = NH * D, kr = NKV * D;
+      if (L.attn_q.type == L.attn_k.type) {
+        const llambda_hip_tensor_ref parts[2] = {L.attn_q, L.attn_k};
+        const int64_t rows[2] = {qr, kr};
+        snprintf(what, sizeof what, "blk.%lld.attn_q|attn_k", (long long)l);
+        o.qk = upload_slab(s.get(), parts, rows, 2, H, false, dev, what);
+      } else {
+        snprintf(what, sizeof what, "blk.%lld.attn_q", (long long)l);
+        o.q = upload_slab(s.get(), &L.attn_q, &qr, 1, H, false, dev, what);
+        snprintf(what, sizeof what, "blk.%lld.attn_k", (long long)l);
+        o.k = upload_slab(s.get(), &L.attn_k, &kr, 1, H, false, dev, what);
+      }
+      snprintf(what, sizeof what, "blk.%lld.attn_v", (long long)l);
+      o.v = upload_slab(s.get(), &L.attn_v, &kr, 1, H, false, dev, what);
+      snprintf(what, sizeof what, "blk.%lld.attn_output", (long long)l);
+      o.o = upload_slab(s.get(), &L.attn_output, &H, 1, qr, false, dev, what);
+      {
+        const llambda_hip_tensor_ref parts[2] = {L.ffn_gate, L.ffn_up};
+        const int64_t rows[2] = {d->ffn, d->ffn};
+        snprintf(what, sizeof what, "blk.%lld.ffn_gate|ffn_up", (long long)l);
+        o.gate_up = upload_slab(s.get(), parts, rows, 2, H, true, dev, what);
+      }
+      snprintf(what, sizeof what, "blk.%lld.ffn_down", (long long)l);
+      o.down = upload_slab(s.get(), &L.ffn_down, &H, 1, d->ffn, false, dev, what);
+      o.kcache = s->kcache(l);
+      o.vcache = s->vcache(l);
+    }
+    p.layers = s->layers.data();
+    p.layer_count = (int)d->layer_count;
+
+    // scratch
+    p.att_chunks = (p.context + kAttnChunk - 1) / kAttnChunk;
+    s->state.alloc(2 * sizeof(int), "decoder state");
+    s->rope_denom.alloc(denom.size() * sizeof(double), "rope denominators");
+    HIPC(hipMemcpyAsync(s->rope_denom.ptr, denom.data(), denom.size() * sizeof(double),
+                        hipMemcpyHostToDevice, s->stream));
+    s->rope_cs.alloc(denom.size() * 2 * sizeof(double), "rope table");
+    s->x.alloc((size_t)H * sizeof(float), "hidden state");
+    s->q.alloc((size_t)NH * D * sizeof(float), "queries");
+    s->ctx.alloc((size_t)NH * D * sizeof(float), "attention context");
+    s->h.alloc((size_t)d->ffn * sizeof(float), "ffn activations");
+    s->att_part.alloc((size_t)NH * p.att_chunks * D * sizeof(float), "attention partial sums");
+    s->att_max.alloc((size_t)NH * p.att_chunks * sizeof(float), "attention chunk maxima");
+    s->att_sum.alloc((size_t)NH * p.att_chunks * sizeof(float), "attention chunk sums");
+    s->att_counter.alloc((size_t)NKV * sizeof(int), "attention counters");
+    HIPC(hipMemsetAsync(s->att_counter.ptr, 0, (size_t)NKV * sizeof(int), s->stream));
+    s->logits.alloc((size_t)d->vocab * sizeof(float), "logits");
+    p.state = s->state.as<int>();
+    p.rope_denom = s->rope_denom.as<double>();
+    p.rope_cs = s->rope_cs.as<double>();
+    p.x = s->x.as<float>();
+    p.q = s->q.as<float>();
+    p.ctx = s->ctx.as<float>();
+    p.h = s->h.as<float>();
+    p.att_part = s->att_part.as<float>();
+    p.att_max = s->att_max.as<float>();
+    p.att_sum = s->att_sum.as<float>();
+    p.att_counter = s->att_counter.as<int>();
+    HIPC(hipStreamSynchronize(s->stream));
+    *result = s.release();
+  });
+}
+
+void llambda_hip_llama_session_destroy(llambda_hip_llama_session* session) { delete session; }
+
+size_t llambda_hip_llama_session_vocab(const llambda_hip_llama_session* session) {
+  return session ? (size_t)session->plan.vocab : 0;
+}
+
+static void check_token(const llambda_hip_llama_session* s, int64_t token, int64_t position) {
+  if (token < 0 || token >= s->plan.vocab)
+    failf("token id %lld out of range (vocab %d)", (long long)token, s->plan.vocab);
+  if (position < 0 || position >= s->plan.context)
+    failf("position %lld outside the KV cache (context %d)", (long long)position, s->plan.context);
+}
+
+int llambda_hip_llama_session_step(llambda_hip_llama_session* s, int64_t token, int64_t position,
+                                   float* logits, size_t logits_count) {
+  return guarded([&] {
+    if (!s) failf("llama step: null session");
+    if (!logits || logits_count != (size_t)s->plan.vocab)
+      failf("llama step: logits count %zu does not match vocab %d", logits_count, s->plan.vocab);
+    check_token(s, token, position);
+    std::lock_guard<std::mutex> lock(s->run_mutex);
+    HIPC(hipSetDevice(s->device));
+    HIPC(decoder_state_launch(s->plan.state, (int)token, (int)position, s->stream));
+    HIPC(decoder_step_launch(s->plan, s->logits.as<float>(), s->stream));
+    HIPC(hipMemcpyAsync(logits, s->logits.ptr, logits_count * sizeof(float), hipMemcpyDeviceToHost,
+                        s->stream));
+    HIPC(hipStreamSynchronize(s->stream));
+  });
+}
+
+int llambda_hip_llama_session_step_device(llambda_hip_llama_session* s, int64_t token,
+                                          int64_t position, float* logits, void* stream,
+                                          int use_graph) {
+  return guarded([&] {
+    if (!s) failf("llama step: null session");
+    check_token(s, token, position);
+    std::lock_guard<std::mutex> lock(s->run_mutex);
+    HIPC(hipSetDevice(s->device));
+    hipStream_t st = stream ? static_cast<hipStream_t>(stream) : s->stream;
+    if (!logits) logits = s->logits.as<float>();
+    if (use_graph && (!s->exec || s->graph_logits != logits)) {
+      if (s->exec) HIPC(hipGraphExecDestroy(s->exec));
+      if (s->graph) HIPC(hipGraphDestroy(s->graph));
+      s->exec = nullptr;
+      s->graph = nullptr;
+      // capture on the session's own stream, after whatever `st` holds
+      HIPC(hipStreamSynchronize(st));
+      HIPC(hipStreamBeginCapture(s->stream, hipStreamCaptureModeRelaxed));
+      const hipError_t e = decoder_step_launch(s->plan, logits, s->stream);
+      hipGraph_t g = nullptr;
+      const hipError_t e2 = hipStreamEndCapture(s->stream, &g);
+      HIPC(e);
+      HIPC(e2);
+      s->graph = g;
+      HIPC(hipGraphInstantiate(&s->exec, s->graph, nullptr, nullptr, 0));
+      s->graph_logits = logits;
+    }
+    HIPC(decoder_state_launch(s->plan.state, (int)token, (int)position, st));
+    if (use_graph) HIPC(hipGraphLaunch(s->exec, st));
+    else HIPC(decoder_step_launch(s->plan, logits, st));
+  });
+}
+
+int llambda_hip_llama_session_logits(llambda_hip_llama_session* s, float* logits,
+                                     size_t logits_count) {
+  return guarded([&] {
+    if (!s || !logits) failf("llama logits: null argument");
+    if (logits_count != (size_t)s->plan.vocab)
+      failf("llama logits: count %zu does not match vocab %d", logits_count, s->plan.vocab);
+    std::lock_guard<std::mutex> lock(s->run_mutex);
+    HIPC(hipSetDevice(s->device));
+    HIPC(hipMemcpyAsync(logits, s->logits.ptr, logits_count * sizeof(float), hipMemcpyDeviceToHost,
+                        s->stream));
+    HIPC(hipStreamSynchronize(s->stream));
+  });
+}
+
+int llambda_hip_llama_session_write_kv(llambda_hip_llama_session* s, int64_t layer, int64_t first,
+                                       int64_t count, const float* keys, const float* values,
+                                       int on_device) {
+  return guarded([&] {
+    if (!s || !keys || !values) failf("write_kv: null argument");
+    if (layer < 0 || layer >= s->layer_count) failf("write_kv: layer %lld out of range", (long long)layer);
+    if (first < 0 || count < 0 || first + count > s->plan.context)
+      failf("write_kv: slots [%lld, %lld) outside the context %d", (long long)first,
+            (long long)(first + count), s->plan.context);
+    if (count == 0) return;
+    std::lock_guard<std::mutex> lock(s->run_mutex);
+    HIPC(hipSetDevice(s->device));
+    const size_t D = (size_t)s->plan.head_dim, C = (size_t)s->plan.context;
+    const hipMemcpyKind kind = on_device ? hipMemcpyDeviceToDevice : hipMemcpyHostToDevice;
+    const size_t w = (size_t)count * D * sizeof(float);
+    HIPC(hipMemcpy2DAsync(s->kcache(layer) + first * D, C * D * sizeof(float), keys, w, w,
+                          (size_t)s->plan.kv_heads, kind, s->stream));
+    HIPC(hipMemcpy2DAsync(s->vcache(layer) + first * D, C * D * sizeof(float), values, w, w,
+                          (size_t)s->plan.kv_heads, kind, s->stream));
+    HIPC(hipStreamSynchronize(s->stream));
+  });
+}
+
+int llambda_hip_llama_session_read_kv(llambda_hip_llama_session* s, int64_t layer, int64_t first,
+                                      int64_t count, float* keys, float* values) {
+  return guarded([&] {
+    if (!s || !keys || !values) failf("read_kv: null argument");
+    if (layer < 0 || layer >= s->layer_count) failf("read_kv: layer %lld out of range", (long long)layer);
+    if (first < 0 || count < 0 || first + count > s->plan.context)
+      failf("read_kv: slots [%lld, %lld) outside the context %d", (long long)first,
+            (long long)(first + count), s->plan.context);
+    if (count == 0) return;
+    std::lock_guard<std::mutex> lock(s->run_mutex);
+    HIPC(hipSetDevice(s->device));
+    const size_t D = (size_t)s->plan.head_dim, C = (size_t)s->plan.context;
+    const size_t w = (size_t)count * D * sizeof(float);
+    HIPC(hipMemcpy2DAsync(keys, w, s->kcache(layer) + first * D, C * D * sizeof(float), w,
+                          (size_t)s->plan.kv_heads, hipMemcpyDeviceToHost, s->stream));
+    HIPC(hipMemcpy2DAsync(values, w, s->vcache(layer) + first * D, C * D * sizeof(float), w,
+                          (size_t)s->plan.kv_heads, hipMemcpyDeviceToHost, s->stream));
+    HIPC(hipStreamSynchronize(s->stream));
+  });
+}
+
+int llambda_hip_llama_session_sync(llambda_hip_llama_session* s, void* stream) {
+  return guarded([&] {
+    if (!s) failf("llama sync: null session");
+    HIPC(hipStreamSynchronize(stream ? static_cast<hipStream_t>(stream) : s->stream));
   });
 }
 

@@ -1,0 +1,349 @@
+// decoder.hip -- the Llama-layout decode token (decoder.h): state, rotation
+// table, grouped-query attention over the fp32 KV cache, and the step's
+// launch sequence over the fused batch-1 GEMV (gemv_mfma.hip).
+#include "decoder.h"
+
+#include <cmath>
+
+namespace llhip {
+
+__global__ void decoder_state_kernel(int* __restrict__ state, int token, int position) {
+  if (threadIdx.x == 0) {
+    state[0] = token;
+    state[1] = position;
+  }
+}
+
+hipError_t decoder_state_launch(int* state, int token, int position, hipStream_t stream) {
+  hipLaunchKernelGGL(decoder_state_kernel, dim3(1), dim3(64), 0, stream, state, token, position);
+  return hipGetLastError();
+}
+
+// cos and sin of angle = position / denom[i] per rotary pair
+// (apply-rope-head-in-place, llambda.lisp:3760-3795: the angle in double;
+// denom[i] = factor_i * theta^(2i/d) is formed on the host, +inf where the
+// factor exceeds 1e20 so that the angle is 0).
+__global__ void rope_table_kernel(const int* __restrict__ state, const double* __restrict__ denom,
+                                  int pairs, double* __restrict__ cs) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= pairs) return;
+  const double angle = (double)state[1] / denom[i];
+  cs[2 * i] = cos(angle);
+  cs[2 * i + 1] = sin(angle);
+}
+
+// ----------------------------------------------------------------- attention
+// compute-gemma4-attention-into as the llama step calls it
+// (llambda.lisp:5122-5167 with dot-product 3491-3500, softmax-into 5075-5096,
+// weighted-sum-head-into 5097-5115): for query head h of kv head h / G,
+// scores s_p = q_h . k_p over cache slots p = 0..position, probabilities
+// exp(s_p - max) / sum, context = sum_p prob_p v_p.
+//
+// Workgroup (chunk, kv head) takes slots [128 chunk, 128 chunk + 128) for
+// the G query heads of its kv head: scores (16 lanes per slot, DPP-free
+// xor reduction), the chunk's max m_c, e_p = exp(s_p - m_c) and their sum
+// S_c, and the unnormalised sum_p e_p v_p.  The last workgroup of the kv
+// head to finish combines the chunks in order: M = max m_c,
+// a_c = exp(m_c - M), context = (sum_c a_c pv_c) / (sum_c a_c S_c).  The
+// reference normalises every probability before the weighted sum; the two
+// agree to rounding (single-precision exp of each difference, computed in
+// double as SBCL does).
+constexpr int kAttnWaves = 8;
+
+__device__ __forceinline__ float wave_sum(float v) {
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+
+__device__ __forceinline__ float4 operator+(float4 a, float4 b) {
+  return make_float4(a.x + b.x, a.y + b.y, a.z + b.z, a.w + b.w);
+}
+__device__ __forceinline__ float4 scale4(float s, float4 a) {
+  return make_float4(s * a.x, s * a.y, s * a.z, s * a.w);
+}
+
+template <int D, int G>
+__global__ void __launch_bounds__(64 * kAttnWaves)
+attention_kernel(const float* __restrict__ q, const float* __restrict__ kc,
+                 const float* __restrict__ vc, int64_t head_stride, const int* __restrict__ state,
+                 float* __restrict__ part, float* __restrict__ pmax, float* __restrict__ psum,
+                 int* __restrict__ counter, int max_chunks, float* __restrict__ out) {
+  constexpr int P = kAttnChunk;
+  constexpr int T = 64 * kAttnWaves;
+  constexpr int DL = D / 16;  // dims per lane in the scores
+  constexpr int DQ = D / 4;   // float4 columns of a row
+  constexpr int NP = T / DQ;  // slot parts in the weighted sum
+  constexpr int PPP = P / NP;  // slots per part
+  constexpr int NQ = T / (G * DQ) > 0 ? T / (G * DQ) : 1;  // chunk parts in the combine
+  static_assert(P == 128 && D % 16 == 0 && G <= kAttnWaves && NP * PPP == P, "attention shape");
+  __shared__ float sc[G][P];
+  __shared__ float4 pv[NP][G][DQ];
+  __shared__ float alpha[G][kAttnMaxChunks];
+  __shared__ float ssum[G];
+  __shared__ int ticket;
+
+  const int n = state[1] + 1;
+  const int chunk = blockIdx.x, kvh = blockIdx.y;
+  const int nchunks = (n + P - 1) / P;
+  if (chunk >= nchunks) return;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const float* kh = kc + (int64_t)kvh * head_stride;
+  const float* vh = vc + (int64_t)kvh * head_stride;
+  const int p0 = chunk * P;
+
+  // scores: lane (grp, sub) holds dims [DL sub, DL sub + DL); wave w takes
+  // slots 16w .. 16w+15 of the chunk, four per step
+  {
+    const int sub = lane & 15, grp = lane >> 4;
+    float qr[G][DL];
+#pragma unroll
+    for (int h = 0; h < G; ++h)
+#pragma unroll
+      for (int j = 0; j < DL; j += 4) {
+        const float4 v =
+            *reinterpret_cast<const float4*>(q + (int64_t)(kvh * G + h) * D + DL * sub + j);
+        qr[h][j] = v.x; qr[h][j + 1] = v.y; qr[h][j + 2] = v.z; qr[h][j + 3] = v.w;
+      }
+    float kr[4][DL];
+#pragma unroll
+    for (int st = 0; st < 4; ++st) {
+      const int p = min(p0 + 16 * wave + 4 * st + grp, n - 1);
+#pragma unroll
+      for (int j = 0; j < DL; j += 4) {
+        const float4 v = *reinterpret_cast<const float4*>(kh + (int64_t)p * D + DL * sub + j);
+        kr[st][j] = v.x; kr[st][j + 1] = v.y; kr[st][j + 2] = v.z; kr[st][j + 3] = v.w;
+      }
+    }
+#pragma unroll
+    for (int st = 0; st < 4; ++st) {
+      const int pl = 16 * wave + 4 * st + grp;
+#pragma unroll
+      for (int h = 0; h < G; ++h) {
+        float s = 0.f;
+#pragma unroll
+        for (int j = 0; j < DL; ++j) s += qr[h][j] * kr[st][j];
+        s += __shfl_xor(s, 1, 64);
+        s += __shfl_xor(s, 2, 64);
+        s += __shfl_xor(s, 4, 64);
+        s += __shfl_xor(s, 8, 64);
+        if (sub == 0) sc[h][pl] = p0 + pl < n ? s : -INFINITY;
+      }
+    }
+  }
+  __syncthreads();
+
+  // chunk max, e_p = exp(s_p - m) rounded to single, and the chunk sum
+  if (wave < G) {
+    const int h = wave;
+    const float s0 = sc[h][lane], s1 = sc[h][lane + 64];
+    const float m = wave_max(fmaxf(s0, s1));
+    const float e0 = p0 + lane < n ? (float)exp((double)(s0 - m)) : 0.f;
+    const float e1 = p0 + lane + 64 < n ? (float)exp((double)(s1 - m)) : 0.f;
+    const float t = wave_sum(e0 + e1);
+    sc[h][lane] = e0;
+    sc[h][lane + 64] = e1;
+    if (lane == 0) {
+      pmax[((int64_t)kvh * max_chunks + chunk) * G + h] = m;
+      psum[((int64_t)kvh * max_chunks + chunk) * G + h] = t;
+    }
+  }
+  __syncthreads();
+
+  // unnormalised weighted sum of the chunk's value rows
+  {
+    const int col = threadIdx.x % DQ, prt = threadIdx.x / DQ;
+    float4 vr[PPP];
+#pragma unroll
+    for (int i = 0; i < PPP; ++i) {
+      const int p = min(p0 + prt + NP * i, n - 1);
+      vr[i] = *reinterpret_cast<const float4*>(vh + (int64_t)p * D + 4 * col);
+    }
+    float4 acc[G];
+#pragma unroll
+    for (int h = 0; h < G; ++h) acc[h] = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+    for (int i = 0; i < PPP; ++i) {
+      const int pl = prt + NP * i;
+      if (p0 + pl < n) {
+#pragma unroll
+        for (int h = 0; h < G; ++h) acc[h] = acc[h] + scale4(sc[h][pl], vr[i]);
+      }
+    }
+#pragma unroll
+    for (int h = 0; h < G; ++h) pv[prt][h][col] = acc[h];
+  }
+  __syncthreads();
+  for (int i = threadIdx.x; i < G * DQ; i += T) {
+    const int h = i / DQ, c = i % DQ;
+    float4 t = pv[0][h][c];
+    for (int r = 1; r < NP; ++r) t = t + pv[r][h][c];
+    *reinterpret_cast<float4*>(part + (((int64_t)kvh * max_chunks + chunk) * G + h) * D + 4 * c) = t;
+  }
+
+  // the last workgroup of this kv head combines the chunks
+  __threadfence();
+  __syncthreads();
+  if (threadIdx.x == 0) ticket = atomicAdd(counter + kvh, 1);
+  __syncthreads();
+  if (ticket != nchunks - 1) return;
+  __threadfence();
+  if (wave < G) {
+    const int h = wave;
+    const float* mx = pmax + (int64_t)kvh * max_chunks * G + h;
+    const float* sm = psum + (int64_t)kvh * max_chunks * G + h;
+    float m = -INFINITY;
+    for (int c = lane; c < nchunks; c += 64) m = fmaxf(m, mx[(int64_t)c * G]);
+    m = wave_max(m);
+    float t = 0.f;
+    for (int c = lane; c < nchunks; c += 64) {
+      const float a = (float)exp((double)(mx[(int64_t)c * G] - m));
+      alpha[h][c] = a;
+      t += a * sm[(int64_t)c * G];
+    }
+    t = wave_sum(t);
+    if (lane == 0) ssum[h] = t;
+  }
+  __syncthreads();
+  // thread (quarter, column): chunks quarter, quarter + NQ, ...; the NQ
+  // partial sums meet in LDS in quarter order
+  {
+    const int i = threadIdx.x % (G * DQ), quarter = threadIdx.x / (G * DQ);
+    const int h = i / DQ, c = i % DQ;
+    float4 t = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (quarter < NQ) {
+      const float* base = part + ((int64_t)kvh * max_chunks * G + h) * D + 4 * c;
+      for (int k = quarter; k < nchunks; k += NQ)
+        t = t + scale4(alpha[h][k], *reinterpret_cast<const float4*>(base + (int64_t)k * G * D));
+    }
+    __syncthreads();  // pv is free again
+    float4* qp = &pv[0][0][0];
+    if (quarter < NQ) qp[quarter * G * DQ + i] = t;
+    __syncthreads();
+    if (quarter == 0) {
+      float4 r = qp[i];
+      for (int k = 1; k < NQ; ++k) r = r + qp[k * G * DQ + i];
+      const float S = ssum[h];
+      *reinterpret_cast<float4*>(out + (int64_t)(kvh * G + h) * D + 4 * c) =
+          make_float4(r.x / S, r.y / S, r.z / S, r.w / S);
+    }
+  }
+  if (threadIdx.x == 0) counter[kvh] = 0;
+}
+
+bool decoder_head_supported(int head_dim, int group) {
+  return (head_dim == 64 || head_dim == 128) &&
+         (group == 1 || group == 2 || group == 4 || group == 8);
+}
+
+template <int D, int G>
+static hipError_t launch_attention_t(const DecoderPlan& p, const float* q, const float* kc,
+                                     const float* vc, float* out, hipStream_t stream) {
+  const dim3 grid(p.att_chunks, p.kv_heads);
+  hipLaunchKernelGGL((attention_kernel<D, G>), grid, dim3(64 * kAttnWaves), 0, stream, q, kc, vc,
+                     (int64_t)p.context * D, p.state, p.att_part, p.att_max, p.att_sum,
+                     p.att_counter, p.att_chunks, out);
+  return hipGetLastError();
+}
+
+template <int D>
+static hipError_t launch_attention_d(const DecoderPlan& p, const float* q, const float* kc,
+                                     const float* vc, float* out, hipStream_t s) {
+  switch (p.heads / p.kv_heads) {
+    case 1: return launch_attention_t<D, 1>(p, q, kc, vc, out, s);
+    case 2: return launch_attention_t<D, 2>(p, q, kc, vc, out, s);
+    case 4: return launch_attention_t<D, 4>(p, q, kc, vc, out, s);
+    case 8: return launch_attention_t<D, 8>(p, q, kc, vc, out, s);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+hipError_t decoder_attention_launch(const DecoderPlan& p, const float* q, const float* kc,
+                                    const float* vc, float* out, hipStream_t s) {
+  if (p.kv_heads <= 0 || p.heads % p.kv_heads || !decoder_head_supported(p.head_dim, p.heads / p.kv_heads) ||
+      p.att_chunks <= 0 || p.att_chunks > kAttnMaxChunks || (int64_t)p.att_chunks * kAttnChunk < p.context)
+    return hipErrorInvalidValue;
+  return p.head_dim == 64 ? launch_attention_d<64>(p, q, kc, vc, out, s)
+                          : launch_attention_d<128>(p, q, kc, vc, out, s);
+}
+
+// ---------------------------------------------------------------- the step
+static GemvProblem problem(const DecoderMatrix& m, const float* x, float* y) {
+  GemvProblem g{};
+  g.type = m.type;
+  g.weights = m.w;
+  g.row_bytes = m.row_bytes;
+  g.rows = m.rows;
+  g.columns = m.columns;
+  g.x = x;
+  g.x_stride = m.columns;
+  g.tokens = 1;
+  g.y = y;
+  g.y_stride = m.rows;
+  return g;
+}
+
+#define DEC_CHECK(expr)                 \
+  do {                                  \
+    const hipError_t e_ = (expr);       \
+    if (e_ != hipSuccess) return e_;    \
+  } while (0)
+
+hipError_t decoder_step_launch(const DecoderPlan& p, float* logits, hipStream_t st) {
+  const int D = p.head_dim;
+  // token row (gguf-model-token-row-into, llambda.lisp:4977-4982), rotation
+  DEC_CHECK(dequant_launch(p.embd.type, p.embd.w, p.embd.row_bytes, 1, p.hidden, p.x, st, p.state));
+  if (p.rope_pairs > 0) {
+    hipLaunchKernelGGL(rope_table_kernel, dim3((p.rope_pairs + 63) / 64), dim3(64), 0, st, p.state,
+                       p.rope_denom, p.rope_pairs, p.rope_cs);
+    DEC_CHECK(hipGetLastError());
+  }
+  for (int l = 0; l < p.layer_count; ++l) {
+    const DecoderLayer& L = p.layers[l];
+    GemvFuse rope;
+    rope.norm_w = L.attn_norm;
+    rope.norm_eps = p.eps;
+    rope.epi = kGemvRope;
+    rope.y1 = L.kcache;
+    rope.head_dim = D;
+    rope.rope_pairs = p.rope_pairs;
+    rope.rope_cs = p.rope_cs;
+    rope.q_scale = p.q_scale;
+    rope.pos = p.state + 1;
+    rope.head_stride = (int64_t)p.context * D;
+    if (L.qk.w) {
+      rope.split = p.heads * D;
+      DEC_CHECK(gemv_fused_launch(problem(L.qk, p.x, p.q), rope, st));
+    } else {
+      rope.split = p.heads * D;  // every row a query row
+      DEC_CHECK(gemv_fused_launch(problem(L.q, p.x, p.q), rope, st));
+      rope.split = 0;  // every row a key row
+      DEC_CHECK(gemv_fused_launch(problem(L.k, p.x, p.q), rope, st));
+    }
+    GemvFuse cache;
+    cache.norm_w = L.attn_norm;
+    cache.norm_eps = p.eps;
+    cache.epi = kGemvCache;
+    cache.head_dim = D;
+    cache.pos = p.state + 1;
+    cache.head_stride = (int64_t)p.context * D;
+    DEC_CHECK(gemv_fused_launch(problem(L.v, p.x, L.vcache), cache, st));
+    DEC_CHECK(decoder_attention_launch(p, p.q, L.kcache, L.vcache, p.ctx, st));
+    // x += o(context) (vector-add-into, llambda.lisp:6404)
+    GemvFuse add;
+    add.epi = kGemvAdd;
+    add.res = p.x;
+    DEC_CHECK(gemv_fused_launch(problem(L.o, p.ctx, p.x), add, st));
+    GemvFuse swiglu;
+    swiglu.norm_w = L.ffn_norm;
+    swiglu.norm_eps = p.eps;
+    swiglu.epi = kGemvSwiglu8;
+    DEC_CHECK(gemv_fused_launch(problem(L.gate_up, p.x, p.h), swiglu, st));
+    DEC_CHECK(gemv_fused_launch(problem(L.down, p.h, p.x), add, st));
+  }
+  GemvFuse head;
+  head.norm_w = p.output_norm;
+  head.norm_eps = p.eps;
+  return gemv_fused_launch(problem(p.output, p.x, logits), head, st);
+}
+
+}  // namespace llhip

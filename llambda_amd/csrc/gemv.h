@@ -30,6 +30,39 @@ constexpr int64_t kMaxColumns = 32768;
 
 hipError_t gemv_launch(const GemvProblem& p, hipStream_t stream);
 
+// Fused prologue and epilogue of the batch-1 MFMA GEMV, used by the decoder's
+// projections.  The default is the plain y[r] = dot(row r, x).
+enum GemvEpilogue : int {
+  kGemvStore = 0,    // y[r] = v
+  kGemvAdd = 1,      // y[r] = res[r] + v                       (vector-add-into)
+  kGemvSwiglu8 = 2,  // rows come in groups of 16: 8 gate rows, then the same
+                     // 8 up rows; y[8 (r / 16) + i] = silu(g_i) * u_i
+  kGemvRope = 3,     // rows < split: query rows, rotated then times q_scale,
+                     // to y[r]; rows >= split: key rows, rotated, to the cache
+                     // y1 (layout as kGemvCache)
+  kGemvCache = 4,    // row r -> y[(r / head_dim) * head_stride +
+                     //            pos * head_dim + r % head_dim]
+};
+
+struct GemvFuse {
+  const float* norm_w = nullptr;  // non-null: x -> rms-norm-into(x, norm_w)
+  float norm_eps = 0.f;
+  int epi = kGemvStore;
+  const float* res = nullptr;     // kGemvAdd (may alias y)
+  float* y1 = nullptr;            // kGemvRope key cache
+  int split = 0;                  // kGemvRope: first key row
+  int head_dim = 0;               // kGemvRope, kGemvCache
+  int rope_pairs = 0;             // rotated pairs per head
+  const double* rope_cs = nullptr;  // [rope_pairs][2]: cos, sin of this position
+  float q_scale = 1.f;
+  const int* pos = nullptr;       // device: the token's cache position
+  int64_t head_stride = 0;        // cache floats per kv head
+};
+
+// Batch-1 GEMV with a fused prologue / epilogue (Q4_K / Q6_K on MFMA only;
+// hipErrorInvalidValue for problems the MFMA kernel does not take).
+hipError_t gemv_fused_launch(const GemvProblem& p, const GemvFuse& f, hipStream_t stream);
+
 // Batch-1 Q4_K / Q6_K GEMV on MFMA (gemv_mfma.hip).
 bool gemv_mfma_supported(const GemvProblem& p);
 hipError_t gemv_mfma_launch(const GemvProblem& p, hipStream_t stream);
@@ -38,8 +71,10 @@ hipError_t gemv_mfma_launch(const GemvProblem& p, hipStream_t stream);
 int device_cu_count();
 
 // out[r * columns + k] = the reference's dequantised weight (bit-exact).
+// With row_sel (device int), the one row w + *row_sel * row_bytes (rows = 1).
 hipError_t dequant_launch(int type, const uint8_t* w, int64_t row_bytes, int64_t rows,
-                          int64_t columns, float* out, hipStream_t stream);
+                          int64_t columns, float* out, hipStream_t stream,
+                          const int* row_sel = nullptr);
 
 // *first_bad = min(*first_bad, index of the first block whose fp16 scale
 // field is Inf/NaN).

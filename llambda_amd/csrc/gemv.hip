@@ -208,8 +208,10 @@ gemv_f32_kernel(const float* __restrict__ w, int rows, int K, const float* __res
 // rounded separately.
 template <int TYPE>
 __global__ void dequant_kernel(const uint8_t* __restrict__ w, int64_t row_bytes, int rows, int K,
-                               float* __restrict__ out) {
+                               float* __restrict__ out, const int* __restrict__ row_sel) {
 #pragma clang fp contract(off)
+  // row_sel: one row, its index read from device memory (a token's embedding)
+  if (row_sel) w += (int64_t)(*row_sel) * row_bytes;
   const int units = K >> 5;
   const int64_t total = (int64_t)rows * units;
   for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < total;
@@ -432,25 +434,25 @@ hipError_t gemv_launch(const GemvProblem& p, hipStream_t stream) {
 }
 
 hipError_t dequant_launch(int type, const uint8_t* w, int64_t row_bytes, int64_t rows,
-                          int64_t columns, float* out, hipStream_t stream) {
+                          int64_t columns, float* out, hipStream_t stream, const int* row_sel) {
   const int64_t units = rows * (columns >> 5);
   const int grid = (int)std::min<int64_t>((units + 255) / 256, 65536);
   switch (type) {
     case kQ4_K:
       hipLaunchKernelGGL(dequant_kernel<kQ4_K>, dim3(grid), dim3(256), 0, stream, w, row_bytes,
-                         (int)rows, (int)columns, out);
+                         (int)rows, (int)columns, out, row_sel);
       break;
     case kQ6_K:
       hipLaunchKernelGGL(dequant_kernel<kQ6_K>, dim3(grid), dim3(256), 0, stream, w, row_bytes,
-                         (int)rows, (int)columns, out);
+                         (int)rows, (int)columns, out, row_sel);
       break;
     case kQ5_0:
       hipLaunchKernelGGL(dequant_kernel<kQ5_0>, dim3(grid), dim3(256), 0, stream, w, row_bytes,
-                         (int)rows, (int)columns, out);
+                         (int)rows, (int)columns, out, row_sel);
       break;
     case kQ8_0:
       hipLaunchKernelGGL(dequant_kernel<kQ8_0>, dim3(grid), dim3(256), 0, stream, w, row_bytes,
-                         (int)rows, (int)columns, out);
+                         (int)rows, (int)columns, out, row_sel);
       break;
     default: return hipErrorInvalidValue;
   }

@@ -24,6 +24,7 @@
 //              llambda.lisp:4203-4310; 4 MFMAs per half, MFMA m takes q_m of
 //              l = 8g .. 8g+7 from lane g's ql/qh bytes.
 // The row sums of the four G lanes meet by two cross-lane adds.
+#include "activations.h"
 #include "gemv.h"
 #include "mfma.h"
 
@@ -63,18 +64,25 @@ struct Chunk {
 constexpr int kQ4Table = 8 * 16 * 16;  // bytes per block
 constexpr int kQ6Table = 2 * 4 * 8 * 16;
 
+// Activation element i: x[i], or with a fused rms-norm-into
+// (llambda.lisp:859-879) x[i] * norm_w[i] * scale, rounded as the reference
+// rounds (x * w) then (* scale).
+__device__ __forceinline__ float act_at(const float* x, const float* nw, float nscale, int i) {
+  return nw ? (x[i] * nw[i]) * nscale : x[i];
+}
+
 __device__ __forceinline__ void build_q4k_table(uint8_t* table, float* gsum, const float* x,
-                                                int nblk) {
+                                                int nblk, const float* nw, float nscale) {
   // one thread per (block, sub-block, 4-element step)
   for (int i = threadIdx.x; i < nblk * 64; i += blockDim.x) {
     const int b = i >> 6, s = (i >> 3) & 7, m = i & 7;
-    const float* xp = x + b * 256 + 32 * s + 4 * m;
+    const int x0 = b * 256 + 32 * s + 4 * m;
     uint32_t hi[4], lo[4];
     float part = 0.f;
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
       float sum;
-      split_bf16(xp[e], hi[e], lo[e], sum);
+      split_bf16(act_at(x, nw, nscale, x0 + e), hi[e], lo[e], sum);
       part += sum;
     }
     // rows a = 2s (hi) and 2s+1 (lo); the data sits in half (s & 1) of the 8 slots
@@ -141,17 +149,17 @@ __device__ __forceinline__ float q4k_block(const uint8_t* p, const uint8_t* lds,
 // sums.  Entry (a & 3) * 2 + (g & 1) of MFMA m serves A row a = 4m + (a & 3)
 // for lane g when (a >> 1) & 1 == g >> 1.
 __device__ __forceinline__ void build_q6k_table(uint8_t* table, float* gsum, const float* x,
-                                                int nblk) {
+                                                int nblk, const float* nw, float nscale) {
   // one thread per (block, half, k, l-octet): 8 activations
   for (int i = threadIdx.x; i < nblk * 32; i += blockDim.x) {
     const int b = i >> 5, h = (i >> 4) & 1, k = (i >> 2) & 3, g = i & 3;
-    const float* xp = x + b * 256 + 128 * h + 32 * k + 8 * g;
+    const int x0 = b * 256 + 128 * h + 32 * k + 8 * g;
     uint32_t hi[8], lo[8];
     float part = 0.f;
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
       float sum;
-      split_bf16(xp[e], hi[e], lo[e], sum);
+      split_bf16(act_at(x, nw, nscale, x0 + e), hi[e], lo[e], sum);
       part += sum;
     }
     // slot = 2k + (g >> 1): A rows 4k + 2(g >> 1) (hi) and +1 (lo)
@@ -232,6 +240,74 @@ __device__ __forceinline__ float q6k_block(const uint8_t* p, const uint8_t* lds,
   return v;
 }
 
+// ------------------------------------------------------------- fusion
+// 1 / sqrt(mean(x^2) + eps) over K elements (rms-norm-into,
+// llambda.lisp:859-879; the sum of squares runs in another order than
+// sum-square-elements' serial loop).  red: kMfmaWaves floats of LDS.
+template <int WAVES>
+__device__ float rms_scale(const float* __restrict__ x, int K, float eps, float* red) {
+  float acc = 0.f;
+  for (int i = threadIdx.x; i < K; i += 64 * WAVES) acc += x[i] * x[i];
+  for (int o = 32; o > 0; o >>= 1) acc += __shfl_xor(acc, o, 64);
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = acc;
+  __syncthreads();
+  float sum = red[0];
+#pragma unroll
+  for (int w = 1; w < WAVES; ++w) sum += red[w];
+  __syncthreads();
+  const float mean = sum / (float)K;
+  return 1.f / sqrtf(mean + eps);
+}
+
+// Store the value v of row `row` (every lane of the wavefront calls this with
+// its own row; `writer` lanes store).  Pairs of rows for the rotation and
+// gate / up rows for SwiGLU are lanes n ^ 1 and n ^ 8 of the same 16 rows.
+__device__ __forceinline__ void store_row(const GemvFuse& f, float* __restrict__ y, int rows,
+                                          int row, float v, bool writer) {
+#pragma clang fp contract(off)
+  switch (f.epi) {
+    case kGemvAdd:
+      if (writer && row < rows) y[row] = f.res[row] + v;
+      return;
+    case kGemvSwiglu8: {
+      // apply-silu-into then vector-elementwise-multiply-into
+      // (llambda.lisp:6433-6441)
+      const float u = __shfl_xor(v, 8, 64);
+      if (writer && (row & 8) == 0 && row < rows) y[((row >> 4) << 3) | (row & 7)] = silu_ref(v) * u;
+      return;
+    }
+    case kGemvRope:
+    case kGemvCache: {
+      const int hd = f.head_dim;
+      float out = v;
+      if (f.epi == kGemvRope) {
+        // apply-rope-head-in-place (llambda.lisp:3760-3795): the pair
+        // (x0, x1) rotated in double, each result rounded to single
+        const float other = __shfl_xor(v, 1, 64);
+        const int local = (row < f.split ? row : row - f.split) % hd;
+        const int pair = local >> 1;
+        if (pair < f.rope_pairs) {
+          const double c = f.rope_cs[2 * pair], sn = f.rope_cs[2 * pair + 1];
+          const double x0 = (local & 1) ? other : v, x1 = (local & 1) ? v : other;
+          out = (local & 1) ? (float)(x0 * sn + x1 * c) : (float)(x0 * c - x1 * sn);
+        }
+        if (writer && row < rows && row < f.split) {
+          y[row] = out * f.q_scale;  // vector-scale-into (llambda.lisp:6391)
+          return;
+        }
+      }
+      if (!writer || row >= rows) return;
+      const int r = f.epi == kGemvRope ? row - f.split : row;
+      float* base = f.epi == kGemvRope ? f.y1 : y;
+      base[(int64_t)(r / hd) * f.head_stride + (int64_t)(*f.pos) * hd + r % hd] = out;
+      return;
+    }
+    default:
+      if (writer && row < rows) y[row] = v;
+      return;
+  }
+}
+
 // ------------------------------------------------------------------ kernel
 template <int TYPE>
 struct MfmaType {
@@ -274,7 +350,7 @@ constexpr size_t mfma_lds_bytes(int nblk, int depth) {
 template <int TYPE, int C, bool ALIGNED, int D, bool SPLIT>
 __global__ void __launch_bounds__(64 * kMfmaWaves)
 gemv_mfma_kernel(const uint8_t* __restrict__ w, int64_t row_bytes, int rows, int nblk,
-                 const float* __restrict__ x, float* __restrict__ y) {
+                 const float* __restrict__ x, float* __restrict__ y, const GemvFuse f) {
   using T = MfmaType<TYPE>;
   using Ch = Chunk<T::kBB, C, ALIGNED>;
   extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
@@ -286,8 +362,9 @@ gemv_mfma_kernel(const uint8_t* __restrict__ w, int64_t row_bytes, int rows, int
 
   for (int i = threadIdx.x; i < T::kZero / 16; i += blockDim.x)
     reinterpret_cast<u32x4*>(lds)[i] = u32x4{0u, 0u, 0u, 0u};
-  if constexpr (TYPE == kQ4_K) build_q4k_table(table, gsum, x, nblk);
-  else build_q6k_table(table, gsum, x, nblk);
+  const float nscale = f.norm_w ? rms_scale<kMfmaWaves>(x, nblk * 256, f.norm_eps, partial) : 1.f;
+  if constexpr (TYPE == kQ4_K) build_q4k_table(table, gsum, x, nblk, f.norm_w, nscale);
+  else build_q6k_table(table, gsum, x, nblk, f.norm_w, nscale);
   __syncthreads();
 
   const int lane = threadIdx.x & 63;
@@ -410,8 +487,7 @@ gemv_mfma_kernel(const uint8_t* __restrict__ w, int64_t row_bytes, int rows, int
     }(std::make_integer_sequence<int, C>{});
     if (!SPLIT && chunk == chunks - 1) {
       const float v = sum_lane_groups(acc);
-      const int row = tile * 16 + n;
-      if (g == 0 && row < rows) y[row] = v;
+      store_row(f, y, rows, tile * 16 + n, v, g == 0);
       acc = 0.f;
     }
   }
@@ -420,12 +496,11 @@ gemv_mfma_kernel(const uint8_t* __restrict__ w, int64_t row_bytes, int rows, int
     const float v = sum_lane_groups(acc);
     if (g == 0) partial[wave * 16 + n] = v;
     __syncthreads();
-    const int row = first_tile * 16 + n;
-    if (wave == 0 && g == 0 && first_tile < tiles && row < rows) {
-      float v = partial[n];
+    if (wave == 0 && first_tile < tiles) {
+      float t = partial[n];
 #pragma unroll
-      for (int w = 1; w < kMfmaWaves; ++w) v = v + partial[16 * w + n];
-      y[row] = v;
+      for (int w = 1; w < kMfmaWaves; ++w) t = t + partial[16 * w + n];
+      store_row(f, y, rows, first_tile * 16 + n, t, g == 0);
     }
   }
 }
@@ -462,10 +537,17 @@ static MfmaChoice<TYPE> mfma_choice(const GemvProblem& p) {
   const int64_t nblk = p.columns / 256;
   MfmaChoice<TYPE> c;
   c.chunk = nblk % LLHIP_GEMV_CHUNK == 0 ? LLHIP_GEMV_CHUNK : nblk % 2 == 0 ? 2 : 1;
-  const int64_t span = (int64_t)c.chunk * MfmaType<TYPE>::kBB;
-  c.aligned = p.row_bytes % 4 == 0 && span % 4 == 0;
   c.depth = kGemvDepth;
-  if (mfma_lds_for(c, (int)nblk) > kMaxLdsBytes) c.depth = 2;
+  // long rows: shorter chunks, then fewer stages, until the LDS holds the
+  // activation table and the stages
+  for (;;) {
+    const int64_t span = (int64_t)c.chunk * MfmaType<TYPE>::kBB;
+    c.aligned = p.row_bytes % 4 == 0 && span % 4 == 0;
+    if (mfma_lds_for(c, (int)nblk) <= kMaxLdsBytes) break;
+    if (c.chunk > 1) c.chunk /= 2;
+    else if (c.depth > 2) c.depth = 2;
+    else break;
+  }
   const int64_t tiles = (p.rows + 15) / 16;
   c.split = tiles < (int64_t)device_cu_count() * 2 * kMfmaWaves && nblk / c.chunk >= kMfmaWaves;
   return c;
@@ -491,7 +573,7 @@ bool gemv_mfma_supported(const GemvProblem& p) {
 }
 
 template <int TYPE, int C, bool ALIGNED, int D, bool SPLIT>
-static hipError_t launch_mfma(const GemvProblem& p, hipStream_t stream) {
+static hipError_t launch_mfma(const GemvProblem& p, const GemvFuse& f, hipStream_t stream) {
   const int nblk = (int)(p.columns / 256);
   const size_t lds = mfma_lds_bytes<TYPE, C, ALIGNED>(nblk, D);
   const auto kernel = gemv_mfma_kernel<TYPE, C, ALIGNED, D, SPLIT>;
@@ -514,35 +596,49 @@ static hipError_t launch_mfma(const GemvProblem& p, hipStream_t stream) {
     grid = std::max(1, std::min(needed, device_cu_count() * per_cu));
   }
   hipLaunchKernelGGL(kernel, dim3(grid), dim3(64 * kMfmaWaves), lds, stream, p.weights,
-                     p.row_bytes, (int)p.rows, nblk, p.x, p.y);
+                     p.row_bytes, (int)p.rows, nblk, p.x, p.y, f);
   return hipGetLastError();
 }
 
 template <int TYPE, int C, bool ALIGNED>
-static hipError_t launch_mfma_ds(const MfmaChoice<TYPE>& c, const GemvProblem& p, hipStream_t s) {
-  if (c.split) return c.depth == kGemvDepth ? launch_mfma<TYPE, C, ALIGNED, kGemvDepth, true>(p, s)
-                                            : launch_mfma<TYPE, C, ALIGNED, 2, true>(p, s);
-  return c.depth == kGemvDepth ? launch_mfma<TYPE, C, ALIGNED, kGemvDepth, false>(p, s)
-                               : launch_mfma<TYPE, C, ALIGNED, 2, false>(p, s);
+static hipError_t launch_mfma_ds(const MfmaChoice<TYPE>& c, const GemvProblem& p,
+                                 const GemvFuse& f, hipStream_t s) {
+  if (c.split)
+    return c.depth == kGemvDepth ? launch_mfma<TYPE, C, ALIGNED, kGemvDepth, true>(p, f, s)
+                                 : launch_mfma<TYPE, C, ALIGNED, 2, true>(p, f, s);
+  return c.depth == kGemvDepth ? launch_mfma<TYPE, C, ALIGNED, kGemvDepth, false>(p, f, s)
+                               : launch_mfma<TYPE, C, ALIGNED, 2, false>(p, f, s);
 }
 
 template <int TYPE>
-static hipError_t launch_mfma_type(const GemvProblem& p, hipStream_t stream) {
+static hipError_t launch_mfma_type(const GemvProblem& p, const GemvFuse& f, hipStream_t stream) {
   const MfmaChoice<TYPE> c = mfma_choice<TYPE>(p);
 #if LLHIP_GEMV_CHUNK == 4
   if (c.chunk == 4)
-    return c.aligned ? launch_mfma_ds<TYPE, 4, true>(c, p, stream)
-                     : launch_mfma_ds<TYPE, 4, false>(c, p, stream);
+    return c.aligned ? launch_mfma_ds<TYPE, 4, true>(c, p, f, stream)
+                     : launch_mfma_ds<TYPE, 4, false>(c, p, f, stream);
 #endif
   if (c.chunk == 2)
-    return c.aligned ? launch_mfma_ds<TYPE, 2, true>(c, p, stream)
-                     : launch_mfma_ds<TYPE, 2, false>(c, p, stream);
-  return c.aligned ? launch_mfma_ds<TYPE, 1, true>(c, p, stream)
-                   : launch_mfma_ds<TYPE, 1, false>(c, p, stream);
+    return c.aligned ? launch_mfma_ds<TYPE, 2, true>(c, p, f, stream)
+                     : launch_mfma_ds<TYPE, 2, false>(c, p, f, stream);
+  return c.aligned ? launch_mfma_ds<TYPE, 1, true>(c, p, f, stream)
+                   : launch_mfma_ds<TYPE, 1, false>(c, p, f, stream);
 }
 
 hipError_t gemv_mfma_launch(const GemvProblem& p, hipStream_t stream) {
-  return p.type == kQ4_K ? launch_mfma_type<kQ4_K>(p, stream) : launch_mfma_type<kQ6_K>(p, stream);
+  const GemvFuse plain;
+  return p.type == kQ4_K ? launch_mfma_type<kQ4_K>(p, plain, stream)
+                         : launch_mfma_type<kQ6_K>(p, plain, stream);
+}
+
+hipError_t gemv_fused_launch(const GemvProblem& p, const GemvFuse& f, hipStream_t stream) {
+  if (!gemv_mfma_supported(p)) return hipErrorInvalidValue;
+  if ((f.epi == kGemvRope || f.epi == kGemvCache) && (f.head_dim <= 0 || f.head_dim % 2 || !f.pos))
+    return hipErrorInvalidValue;
+  if (f.epi == kGemvSwiglu8 && p.rows % 16) return hipErrorInvalidValue;
+  if (f.epi == kGemvAdd && !f.res) return hipErrorInvalidValue;
+  return p.type == kQ4_K ? launch_mfma_type<kQ4_K>(p, f, stream)
+                         : launch_mfma_type<kQ6_K>(p, f, stream);
 }
 
 }  // namespace llhip

@@ -48,6 +48,37 @@ class MoeDesc(ctypes.Structure):
     ]
 
 
+class TensorRef(ctypes.Structure):
+    """llambda_hip_tensor_ref."""
+    _fields_ = [("type", c_int), ("data", c_void_p), ("bytes", c_size)]
+
+
+class LlamaLayer(ctypes.Structure):
+    """llambda_hip_llama_layer."""
+    _fields_ = [
+        ("attn_norm", c_void_p),
+        ("attn_q", TensorRef), ("attn_k", TensorRef), ("attn_v", TensorRef),
+        ("attn_output", TensorRef),
+        ("ffn_norm", c_void_p),
+        ("ffn_gate", TensorRef), ("ffn_up", TensorRef), ("ffn_down", TensorRef),
+    ]
+
+
+class LlamaDesc(ctypes.Structure):
+    """llambda_hip_llama_desc."""
+    _fields_ = [
+        ("hidden", c_i64), ("layer_count", c_i64), ("head_count", c_i64),
+        ("kv_head_count", c_i64), ("ffn", c_i64), ("vocab", c_i64), ("rope_dimension", c_i64),
+        ("norm_epsilon", ctypes.c_float), ("rope_base", ctypes.c_float),
+        ("rope_factors", c_void_p), ("rope_factor_count", c_i64),
+        ("context", c_i64),
+        ("weights_on_device", c_int),
+        ("token_embd", TensorRef), ("output", TensorRef),
+        ("output_norm", c_void_p),
+        ("layers", ctypes.POINTER(LlamaLayer)),
+    ]
+
+
 # name -> (restype, argtypes); the complete export list of include/llambda_hip.h
 SIGNATURES = {
     "llambda_hip_probe": (c_int, []),
@@ -73,6 +104,19 @@ SIGNATURES = {
     "llambda_hip_moe_session_run_device": (c_int, [c_void_p, c_void_p, c_void_p, c_size, c_void_p]),
     "llambda_hip_moe_session_sync": (c_int, [c_void_p, c_void_p]),
     "llambda_hip_select_top_k": (c_int, [c_void_p, c_size, c_size, c_size, c_void_p, c_void_p]),
+    "llambda_hip_llama_session_create": (c_int, [ctypes.POINTER(LlamaDesc),
+                                                 ctypes.POINTER(c_void_p)]),
+    "llambda_hip_llama_session_destroy": (None, [c_void_p]),
+    "llambda_hip_llama_session_vocab": (c_size, [c_void_p]),
+    "llambda_hip_llama_session_step": (c_int, [c_void_p, c_i64, c_i64, c_void_p, c_size]),
+    "llambda_hip_llama_session_step_device": (c_int, [c_void_p, c_i64, c_i64, c_void_p, c_void_p,
+                                                      c_int]),
+    "llambda_hip_llama_session_logits": (c_int, [c_void_p, c_void_p, c_size]),
+    "llambda_hip_llama_session_write_kv": (c_int, [c_void_p, c_i64, c_i64, c_i64, c_void_p,
+                                                   c_void_p, c_int]),
+    "llambda_hip_llama_session_read_kv": (c_int, [c_void_p, c_i64, c_i64, c_i64, c_void_p,
+                                                  c_void_p]),
+    "llambda_hip_llama_session_sync": (c_int, [c_void_p, c_void_p]),
 }
 
 

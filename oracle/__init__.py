@@ -62,6 +62,26 @@ class MoeDesc(ctypes.Structure):
     ]
 
 
+class OTensor(ctypes.Structure):
+    _fields_ = [("type", ctypes.c_int), ("data", ctypes.c_void_p)]
+
+
+class LlamaLayerDesc(ctypes.Structure):
+    _fields_ = [("attn_norm", ctypes.c_void_p), ("attn_q", OTensor), ("attn_k", OTensor),
+                ("attn_v", OTensor), ("attn_output", OTensor), ("ffn_norm", ctypes.c_void_p),
+                ("ffn_gate", OTensor), ("ffn_up", OTensor), ("ffn_down", OTensor)]
+
+
+class LlamaDesc(ctypes.Structure):
+    _fields_ = [("hidden", ctypes.c_int64), ("layer_count", ctypes.c_int64),
+                ("heads", ctypes.c_int64), ("kv_heads", ctypes.c_int64), ("ffn", ctypes.c_int64),
+                ("vocab", ctypes.c_int64), ("rope_dim", ctypes.c_int64),
+                ("norm_eps", ctypes.c_float), ("rope_base", ctypes.c_float),
+                ("rope_factors", ctypes.c_void_p), ("rope_factor_count", ctypes.c_int64),
+                ("token_embd", OTensor), ("output", OTensor), ("output_norm", ctypes.c_void_p),
+                ("layers", ctypes.POINTER(LlamaLayerDesc))]
+
+
 def lib():
     global _lib
     if _lib is None:
@@ -92,6 +112,18 @@ def lib():
         L.oracle_moe_forward.argtypes = [ctypes.POINTER(MoeDesc), ctypes.c_void_p,
                                          ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p,
                                          ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int]
+        L.oracle_rms_norm.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int64,
+                                      ctypes.c_float, ctypes.c_void_p]
+        L.oracle_rope_head.argtypes = [ctypes.c_void_p, ctypes.c_int64, ctypes.c_int64,
+                                       ctypes.c_int64, ctypes.c_float, ctypes.c_void_p,
+                                       ctypes.c_int64]
+        L.oracle_softmax.argtypes = [ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p]
+        L.oracle_attention.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p,
+                                       ctypes.c_int64, ctypes.c_int64, ctypes.c_int64,
+                                       ctypes.c_int64, ctypes.c_int64, ctypes.c_void_p]
+        L.oracle_llama_step.argtypes = [ctypes.POINTER(LlamaDesc), ctypes.c_void_p,
+                                        ctypes.c_int64, ctypes.c_int64, ctypes.c_int64,
+                                        ctypes.c_void_p, ctypes.c_int]
         _lib = L
     return _lib
 
@@ -236,3 +268,86 @@ def moe_forward(layer, x: np.ndarray, threads: int = 1) -> MoeResult:
                                     idx.ctypes.data, w.ctypes.data, logits.ctypes.data,
                                     threads))
     return MoeResult(y, idx, w, logits)
+
+
+def _f32(a) -> np.ndarray:
+    return np.ascontiguousarray(a, dtype=np.float32)
+
+
+def rms_norm(x, w, eps: float) -> np.ndarray:
+    x, w = _f32(x), _f32(w)
+    out = np.empty_like(x)
+    lib().oracle_rms_norm(x.ctypes.data, w.ctypes.data, x.size, eps, out.ctypes.data)
+    return out
+
+
+def rope_head(head, position: int, rope_dim: int, theta_base: float,
+              factors: Optional[np.ndarray] = None) -> np.ndarray:
+    out = _f32(head).copy()
+    f = None if factors is None else _f32(factors)
+    lib().oracle_rope_head(out.ctypes.data, out.size, position, rope_dim, theta_base,
+                           _ptr(f), 0 if f is None else f.size)
+    return out
+
+
+def softmax(logits) -> np.ndarray:
+    x = _f32(logits)
+    out = np.empty_like(x)
+    lib().oracle_softmax(x.ctypes.data, x.size, out.ctypes.data)
+    return out
+
+
+def attention(q, kcache, vcache, n: int) -> np.ndarray:
+    """q [heads][D]; caches [kv_heads][cap][D]; slots 0..n-1."""
+    q, kc, vc = _f32(q), _f32(kcache), _f32(vcache)
+    heads, D = q.shape
+    kv_heads, cap, _ = kc.shape
+    out = np.empty_like(q)
+    _check(lib().oracle_attention(q.ctypes.data, kc.ctypes.data, vc.ctypes.data, cap, n, heads,
+                                  kv_heads, D, out.ctypes.data))
+    return out
+
+
+def llama_step(weights, kv: np.ndarray, token: int, position: int, threads: int = 1) -> np.ndarray:
+    """One step of the Llama step function on host weights (an object with the
+    attributes of llambda_amd.llama.LlamaWeights).  kv: float32
+    [layers][2][kv_heads][cap][head_dim], updated in place (slot `position`)."""
+    c = weights.config
+    assert kv.dtype == np.float32 and kv.flags["C_CONTIGUOUS"]
+    cap = kv.shape[3]
+    keep = []
+
+    def vec(a):
+        a = _f32(a)
+        keep.append(a)
+        return a.ctypes.data
+
+    def ten(t):
+        a = np.ascontiguousarray(t[1], dtype=np.uint8)
+        keep.append(a)
+        o = OTensor()
+        o.type, o.data = t[0], a.ctypes.data
+        return o
+
+    layers = (LlamaLayerDesc * c.layer_count)()
+    for i, L in enumerate(weights.layers):
+        layers[i].attn_norm = vec(L.attn_norm)
+        layers[i].attn_q, layers[i].attn_k = ten(L.attn_q), ten(L.attn_k)
+        layers[i].attn_v, layers[i].attn_output = ten(L.attn_v), ten(L.attn_output)
+        layers[i].ffn_norm = vec(L.ffn_norm)
+        layers[i].ffn_gate, layers[i].ffn_up = ten(L.ffn_gate), ten(L.ffn_up)
+        layers[i].ffn_down = ten(L.ffn_down)
+    d = LlamaDesc()
+    d.hidden, d.layer_count, d.heads, d.kv_heads = c.hidden, c.layer_count, c.head_count, c.kv_head_count
+    d.ffn, d.vocab, d.rope_dim = c.ffn, c.vocab, c.rope_dimension
+    d.norm_eps, d.rope_base = c.norm_epsilon, c.rope_base
+    if weights.rope_factors is not None:
+        d.rope_factors = vec(weights.rope_factors)
+        d.rope_factor_count = len(weights.rope_factors)
+    d.token_embd, d.output = ten(weights.token_embd), ten(weights.output)
+    d.output_norm = vec(weights.output_norm)
+    d.layers = layers
+    logits = np.empty(c.vocab, dtype=np.float32)
+    _check(lib().oracle_llama_step(ctypes.byref(d), kv.ctypes.data, cap, token, position,
+                                   logits.ctypes.data, threads))
+    return logits

@@ -710,3 +710,165 @@ int oracle_moe_forward(const oracle_moe_desc* m, const float* x, float* y, int64
   free(w);
   return status;
 }
+
+/* ================================================== Llama decode token */
+
+/* sum-square-elements (llambda.lisp:819-828) and rms-norm-into (859-879):
+ * serial fp32 sum of squares, mean = sum / n, scale = 1 / sqrt(mean + eps),
+ * out = (x * w) * scale. */
+void oracle_rms_norm(const float* x, const float* w, int64_t n, float eps, float* out) {
+  float sum = 0.0f;
+  for (int64_t i = 0; i < n; ++i) sum += x[i] * x[i];
+  const float mean = sum / (float)n;
+  const float scale = 1.0f / sqrtf(mean + eps);
+  for (int64_t i = 0; i < n; ++i) out[i] = (x[i] * w[i]) * scale;
+}
+
+/* apply-rope-head-in-place (llambda.lisp:3760-3795).  The power
+ * (expt theta-base (/ (* 2 i) even)) has a single-float base and a rational
+ * exponent, so Common Lisp returns a single-float: pow in double, rounded.
+ * The angle, cos, sin and the rotation are double; results rounded. */
+void oracle_rope_head(float* head, int64_t len, int64_t position, int64_t rope_dim,
+                      float theta_base, const float* factors, int64_t n_factors) {
+  const int64_t factor_limit = factors ? 2 * n_factors : rope_dim;
+  int64_t eff = rope_dim < factor_limit ? rope_dim : factor_limit;
+  if (len < eff) eff = len;
+  const int64_t even = 2 * (eff / 2), pairs = even / 2;
+  for (int64_t i = 0; i < pairs; ++i) {
+    const double factor = (factors && i < n_factors) ? (double)factors[i] : 1.0;
+    double angle = 0.0;
+    if (!(factor > 1.0e20)) {
+      const float power = (float)pow((double)theta_base, (double)(2 * i) / (double)even);
+      angle = (double)position / (factor * (double)power);
+    }
+    const double c = cos(angle), s = sin(angle);
+    const float x0 = head[2 * i], x1 = head[2 * i + 1];
+    head[2 * i] = (float)((double)x0 * c - (double)x1 * s);
+    head[2 * i + 1] = (float)((double)x0 * s + (double)x1 * c);
+  }
+}
+
+/* softmax-into (llambda.lisp:5075-5096) with max-single-float-element
+ * (841-857): exp of the single-float difference (computed in double,
+ * rounded), serial sum, each value divided by the sum. */
+void oracle_softmax(const float* logits, int64_t n, float* out) {
+  float mx = logits[0];
+  for (int64_t i = 1; i < n; ++i)
+    if (logits[i] > mx) mx = logits[i];
+  float sum = 0.0f;
+  for (int64_t i = 0; i < n; ++i) {
+    const float v = (float)exp((double)(logits[i] - mx));
+    out[i] = v;
+    sum += v;
+  }
+  for (int64_t i = 0; i < n; ++i) out[i] = out[i] / sum;
+}
+
+/* compute-gemma4-attention-into as the llama step uses it
+ * (llambda.lisp:5122-5167): query head h reads kv head h / (heads / kv);
+ * scores by dot-product (3491-3500) over slots 0..n-1, softmax-into, then
+ * weighted-sum-head-into (5097-5115), slot by slot.  q: [heads][D],
+ * caches: [kv][cap][D], out: [heads][D]. */
+int oracle_attention(const float* q, const float* kc, const float* vc, int64_t cap, int64_t n,
+                     int64_t heads, int64_t kv_heads, int64_t D, float* out) {
+  if (n <= 0 || n > cap) return fail("attention: %lld slots outside the cache", (long long)n);
+  if (kv_heads <= 0 || heads % kv_heads) return fail("attention: bad head counts");
+  float* scores = (float*)malloc((size_t)n * 2 * sizeof(float));
+  if (!scores) return fail("attention: out of memory");
+  float* probs = scores + n;
+  const int64_t group = heads / kv_heads;
+  for (int64_t h = 0; h < heads; ++h) {
+    const int64_t kvh = h / group;
+    const float* qh = q + h * D;
+    for (int64_t s = 0; s < n; ++s)
+      scores[s] = oracle_dot_product(qh, kc + (kvh * cap + s) * D, D);
+    oracle_softmax(scores, n, probs);
+    float* dst = out + h * D;
+    for (int64_t e = 0; e < D; ++e) dst[e] = 0.0f;
+    for (int64_t s = 0; s < n; ++s) {
+      const float* vh = vc + (kvh * cap + s) * D;
+      for (int64_t e = 0; e < D; ++e) dst[e] += probs[s] * vh[e];
+    }
+  }
+  free(scores);
+  return 0;
+}
+
+/* One step of make-llama-step-function (llambda.lisp:6294-6441) for token
+ * `token` at `position`: the embedding row (gguf-model-token-row-into,
+ * 4977-4982, via the dequantisers), per layer rms-norm, q/k/v projections,
+ * rotation of every q and k head, q scaled by 1/sqrt(head size), k and v
+ * appended (here: written to cache slot `position`), attention over slots
+ * 0..position, x += o(context), rms-norm, silu(gate) * up, x += down(h);
+ * then rms-norm with output_norm and the output rows.
+ * kv: [layers][2][kv_heads][cap][head_dim]. */
+int oracle_llama_step(const oracle_llama_desc* m, float* kv, int64_t cap, int64_t token,
+                      int64_t position, float* logits, int threads) {
+  if (!m || !kv || !logits) return fail("llama step: null argument");
+  const int64_t H = m->hidden, NH = m->heads, NKV = m->kv_heads, F = m->ffn;
+  if (H <= 0 || NH <= 0 || NKV <= 0 || H % NH || NH % NKV) return fail("llama step: bad dims");
+  if (token < 0 || token >= m->vocab) return fail("llama step: token out of range");
+  if (position < 0 || position >= cap) return fail("llama step: position outside the cache");
+  const int64_t D = H / NH;
+  const float scale = 1.0f / sqrtf((float)D);
+  const size_t nbuf = (size_t)(5 * H + 2 * NKV * D + 2 * F + NH * D);
+  float* buf = (float*)malloc(nbuf * sizeof(float));
+  if (!buf) return fail("llama step: out of memory");
+  float *x = buf, *xin = x + H, *q = xin + H, *k = q + NH * D, *v = k + NKV * D;
+  float *ctx = v + NKV * D, *ao = ctx + NH * D, *g = ao + H, *u = g + F;
+  int status = 0;
+  const int64_t erb = oracle_row_bytes(m->token_embd.type, H);
+  if (erb < 0 || oracle_dequantize(m->token_embd.type, m->token_embd.data + token * erb, H, x))
+    status = fail("llama step: token row: %s", g_error);
+  for (int64_t l = 0; l < m->layer_count && status == 0; ++l) {
+    const oracle_llama_layer* L = m->layers + l;
+    float* kc = kv + (size_t)(2 * l) * NKV * cap * D;
+    float* vc = kc + (size_t)NKV * cap * D;
+    oracle_rms_norm(x, L->attn_norm, H, m->norm_eps, xin);
+    if (oracle_gemv(L->attn_q.type, L->attn_q.data, NH * D, H, xin, q, threads) ||
+        oracle_gemv(L->attn_k.type, L->attn_k.data, NKV * D, H, xin, k, threads) ||
+        oracle_gemv(L->attn_v.type, L->attn_v.data, NKV * D, H, xin, v, threads)) {
+      status = -1;
+      break;
+    }
+    for (int64_t h = 0; h < NH; ++h)
+      oracle_rope_head(q + h * D, D, position, m->rope_dim, m->rope_base, m->rope_factors,
+                       m->rope_factor_count);
+    for (int64_t h = 0; h < NKV; ++h)
+      oracle_rope_head(k + h * D, D, position, m->rope_dim, m->rope_base, m->rope_factors,
+                       m->rope_factor_count);
+    for (int64_t i = 0; i < NH * D; ++i) q[i] = q[i] * scale;
+    for (int64_t h = 0; h < NKV; ++h) {
+      memcpy(kc + (h * cap + position) * D, k + h * D, (size_t)D * sizeof(float));
+      memcpy(vc + (h * cap + position) * D, v + h * D, (size_t)D * sizeof(float));
+    }
+    if (oracle_attention(q, kc, vc, cap, position + 1, NH, NKV, D, ctx)) {
+      status = -1;
+      break;
+    }
+    if (oracle_gemv(L->attn_output.type, L->attn_output.data, H, NH * D, ctx, ao, threads)) {
+      status = -1;
+      break;
+    }
+    for (int64_t i = 0; i < H; ++i) x[i] = x[i] + ao[i];
+    oracle_rms_norm(x, L->ffn_norm, H, m->norm_eps, xin);
+    if (oracle_gemv(L->ffn_gate.type, L->ffn_gate.data, F, H, xin, g, threads) ||
+        oracle_gemv(L->ffn_up.type, L->ffn_up.data, F, H, xin, u, threads)) {
+      status = -1;
+      break;
+    }
+    for (int64_t i = 0; i < F; ++i) g[i] = oracle_silu(g[i]);
+    for (int64_t i = 0; i < F; ++i) g[i] = g[i] * u[i];
+    if (oracle_gemv(L->ffn_down.type, L->ffn_down.data, H, F, g, ao, threads)) {
+      status = -1;
+      break;
+    }
+    for (int64_t i = 0; i < H; ++i) x[i] = x[i] + ao[i];
+  }
+  if (status == 0) {
+    oracle_rms_norm(x, m->output_norm, H, m->norm_eps, xin);
+    if (oracle_gemv(m->output.type, m->output.data, m->vocab, H, xin, logits, threads)) status = -1;
+  }
+  free(buf);
+  return status;
+}

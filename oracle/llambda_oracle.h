@@ -25,6 +25,16 @@
  *   sigmoid/silu/relu2   float64 closed forms
  *   MoE layers           float64 restatement from dequantised weights
  *                        (independent of the fused kernels)
+ *   rms_norm, silu,      reference KATs tests.lisp:298-345 (rms-norm of
+ *   rope, softmax        (3 4) by (1 2), silu 2, rotation by cos/sin 1,
+ *                        softmax of (2 1 0)), plus closed forms: rotation
+ *                        preserves the pair's norm and is the identity at
+ *                        position 0, softmax sums to 1 and is shift
+ *                        invariant, rms of the output equals rms of w
+ *   attention            float64 restatement; one slot returns its value
+ *                        row, identical keys return the mean value row
+ *   llama step           float64 restatement of the layer from dequantised
+ *                        weights (tests)
  *   horizontal+ of the 8-lane accumulator: sb-simd's internal order is not
  *   published; this file sums lanes 0..7 left to right.  Parity unpinned for
  *   that order; it moves results by a few ulp, far inside the 1e-4 bound.
@@ -117,6 +127,45 @@ typedef struct oracle_moe_desc {
 int oracle_moe_forward(const oracle_moe_desc* desc, const float* x, float* y,
                        int64_t tokens, int64_t* top_indices, float* top_weights,
                        float* router_logits, int threads);
+
+/* ---- Llama decode token (llambda.lisp:6294-6441) ---------------------- */
+
+/* llambda.lisp:819-828, 859-879 */
+void oracle_rms_norm(const float* x, const float* w, int64_t n, float eps, float* out);
+/* llambda.lisp:3760-3795 */
+void oracle_rope_head(float* head, int64_t len, int64_t position, int64_t rope_dim,
+                      float theta_base, const float* factors, int64_t n_factors);
+/* llambda.lisp:5075-5096 */
+void oracle_softmax(const float* logits, int64_t n, float* out);
+/* llambda.lisp:5122-5167: q [heads][D], caches [kv_heads][cap][D], slots 0..n-1 */
+int oracle_attention(const float* q, const float* kc, const float* vc, int64_t cap, int64_t n,
+                     int64_t heads, int64_t kv_heads, int64_t D, float* out);
+
+typedef struct oracle_tensor {
+  int type;
+  const uint8_t* data;
+} oracle_tensor;
+
+typedef struct oracle_llama_layer {
+  const float* attn_norm;
+  oracle_tensor attn_q, attn_k, attn_v, attn_output;
+  const float* ffn_norm;
+  oracle_tensor ffn_gate, ffn_up, ffn_down;
+} oracle_llama_layer;
+
+typedef struct oracle_llama_desc {
+  int64_t hidden, layer_count, heads, kv_heads, ffn, vocab, rope_dim;
+  float norm_eps, rope_base;
+  const float* rope_factors;
+  int64_t rope_factor_count;
+  oracle_tensor token_embd, output;
+  const float* output_norm;
+  const oracle_llama_layer* layers;
+} oracle_llama_desc;
+
+/* llambda.lisp:6315-6441; kv: [layers][2][kv_heads][cap][head_dim] */
+int oracle_llama_step(const oracle_llama_desc* m, float* kv, int64_t cap, int64_t token,
+                      int64_t position, float* logits, int threads);
 
 #ifdef __cplusplus
 }

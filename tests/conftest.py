@@ -1,3 +1,4 @@
+import json
 import os
 import sys
 
@@ -20,3 +21,10 @@ def hip():
     status = lib.llambda_hip_probe()
     assert status == 1, f"no usable gfx950 device (probe={status}): {native.last_error()}"
     return lib
+
+
+@pytest.fixture(scope="session")
+def kats():
+    """Known answers of the reference's own tests (tests/golden/reference_kats.json)."""
+    with open(os.path.join(ROOT, "tests", "golden", "reference_kats.json")) as fh:
+        return json.load(fh)

@@ -7,6 +7,8 @@ the reference's own tests for this path (tests.lisp), as data.
   dot-product-with-q4-k-tensor-row tests.lisp:2257-2288
   dot-product-with-q6-k-tensor-row tests.lisp:2290-2322
   forward-primitives silu(2) tests.lisp:298-344
+  forward-primitives rms-norm, apply-rope tests.lisp:305-344
+  softmax of (2 1 0)        tests.lisp:1359-1361
 
 The reference cannot run here (no Common Lisp implementation), so the blocks
 are rebuilt from the byte assignments those tests make and the expected
@@ -75,6 +77,13 @@ def main():
             "tolerance": 1e-4,
         },
         "silu": {"cite": "tests.lisp:298-344", "x": 2.0, "expect": 1.7615942, "tolerance": 1e-5},
+        "rms_norm": {"cite": "tests.lisp:305-311, 323-328", "x": [3.0, 4.0], "weight": [1.0, 2.0],
+                     "epsilon": 0.0, "expect": [0.84852815, 2.2627418], "tolerance": 1e-5},
+        "rope": {"cite": "tests.lisp:338-344", "x": [1.0, 0.0, 5.0, 6.0], "position": 1,
+                 "rope_dimension": 2, "theta_base": 10000.0,
+                 "expect": ["cos 1", "sin 1", 5.0, 6.0], "tolerance": 1e-5},
+        "softmax": {"cite": "tests.lisp:1359-1361", "x": [2.0, 1.0, 0.0],
+                    "expect": "sums to 1 within 1e-5, strictly decreasing", "tolerance": 1e-5},
     }
     with open(os.path.join(HERE, "reference_kats.json"), "w") as fh:
         json.dump(kats, fh, indent=1)

@@ -1,24 +1,13 @@
 """CPU tests that pin the oracle: the reference's known-answer tests, closed
 forms, encoders written from the block layouts (round trips), and brute
 force.  No GPU needed."""
-import json
 import math
-import os
 
 import numpy as np
 import pytest
 
 import oracle
 from llambda_amd import ggml, synthetic
-
-GOLDEN = os.path.join(os.path.dirname(__file__), "golden", "reference_kats.json")
-
-
-@pytest.fixture(scope="module")
-def kats():
-    with open(GOLDEN) as fh:
-        return json.load(fh)
-
 
 # ---------------------------------------------------------------- KATs
 
