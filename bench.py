@@ -3,8 +3,8 @@
 Default line: the Q6_K output-head GEMV (W 128256 x 4096 Q6_K, batch 1) --
 algorithmic GB/s and fraction of the 8 TB/s HBM roofline -- plus, in
 "workloads", the Q4_K 4096 x 4096 GEMV (cold and hot), the Qwen3Next-shaped
-MoE layer at batch 1 and 256, and the Nemotron-H-shaped MoE layer at batch
-1024 (tokens/s).  Inputs are resident in HBM when timing starts; times are
+MoE layer at batch 1 and 256, the Nemotron-H-shaped MoE layer at batch 1024
+(tokens/s) and the Llama-3.1-8B-layout decode token at position 4096.  Inputs are resident in HBM when timing starts; times are
 HIP events around K launches on the stream the kernels run on.
 
 The CPU baseline is the oracle (a C restatement of the reference's CPU
@@ -152,6 +152,70 @@ def cpu_moe_baseline(layer, tokens_sample, seconds):
     return n / el, n
 
 
+LLAMA_CONTEXT = 4224  # cache slots: 4096 prefilled + the decoded token, rounded up
+
+
+def bench_llama(torch, timer, steps, warmup):
+    """Llama-3.1-8B-layout decode token at position 4096: random-init weights
+    drawn on the device (Q4_K_M mix), fp32 cache slots 0..4095 ~ N(0, 1)."""
+    from llambda_amd.llama import (LLAMA31_8B, HipLlamaSession, synthetic_llama_device,
+                                   weight_bytes)
+    c = LLAMA31_8B
+    log("generating Llama-3.1-8B-layout weights on the device")
+    w = synthetic_llama_device(31, c, np.random.default_rng(31))
+    wbytes = weight_bytes(w)
+    sess = HipLlamaSession(w, context=LLAMA_CONTEXT)
+    del w
+    torch.cuda.empty_cache()
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(32)
+    for layer in range(c.layer_count):
+        k = torch.randn((c.kv_head_count, 4096, c.head_dim), device="cuda", generator=gen)
+        v = torch.randn((c.kv_head_count, 4096, c.head_dim), device="cuda", generator=gen)
+        torch.cuda.synchronize()
+        sess.write_kv_device(layer, 0, 4096, k.data_ptr(), v.data_ptr())
+    del k, v
+    logits = torch.empty(c.vocab, device="cuda", dtype=torch.float32)
+    pos, token = 4096, 1234
+    res = {}
+    for graph in (True, False):
+        def step():
+            sess.step_device(token, pos, logits.data_ptr(), timer.handle, graph=graph)
+        res[graph] = timer.time(step, steps, warmup)
+    sess.close()
+    kv_bytes = 2 * c.layer_count * c.kv_head_count * (pos + 1) * c.head_dim * 4
+    return res[True], res[False], wbytes, kv_bytes
+
+
+def cpu_llama_baseline(seconds):
+    """Oracle step of one 8B-shaped layer (cache at 4096) plus the head GEMV
+    rate of the head workload: per-token = 32 layers + head."""
+    import oracle
+    from llambda_amd.llama import LLAMA31_8B, LlamaConfig, synthetic_llama
+    c = LLAMA31_8B
+    one = LlamaConfig(hidden=c.hidden, layer_count=1, head_count=c.head_count,
+                      kv_head_count=c.kv_head_count, ffn=c.ffn, vocab=256,
+                      rope_dimension=c.rope_dimension, context=4097)
+    rng = np.random.default_rng(33)
+    w = synthetic_llama(rng, one)
+    kv = np.zeros((1, 2, c.kv_head_count, 4097, c.head_dim), dtype=np.float32)
+    kv[:, :, :, :4096] = rng.standard_normal(size=kv[:, :, :, :4096].shape, dtype=np.float32)
+    oracle.llama_step(w, kv, 5, 4096, threads=CPU_THREADS)
+    n, t0 = 0, time.perf_counter()
+    while True:
+        oracle.llama_step(w, kv, 5, 4096, threads=CPU_THREADS)
+        n += 1
+        if time.perf_counter() - t0 >= seconds:
+            break
+    t_layer = (time.perf_counter() - t0) / n
+    head = synthetic.packed(ggml.Q6_K, rng, c.vocab, c.hidden)
+    x = synthetic.activations(rng, 1, c.hidden)[0]
+    t0 = time.perf_counter()
+    oracle.gemv(ggml.Q6_K, head, c.vocab, c.hidden, x, threads=CPU_THREADS)
+    t_head = time.perf_counter() - t0
+    return 1.0 / (c.layer_count * t_layer + t_head), n
+
+
 def load_traffic(name):
     """HBM bytes per launch measured with rocprofv3 counters (profiles/)."""
     path = os.path.join(ROOT, "profiles", "traffic.json")
@@ -167,7 +231,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--only", choices=["head", "q4k", "moe", "copy", "none"], default=None,
+    ap.add_argument("--only", choices=["head", "q4k", "moe", "llama", "copy", "none"], default=None,
                     help="run one workload group only (profiling)")
     ap.add_argument("--cpu-seconds", type=float, default=8.0,
                     help="bound on each CPU-baseline sample (0 disables)")
@@ -253,6 +317,28 @@ def main():
                  "GB/s": round(nbytes / (ms * 1e-3) / 1e9, 1)}
         workloads.append(entry)
         log(f"nemotron B=1024: {ms:.3f} ms, {entry['tokens_per_s']} tok/s")
+
+    if args.only in (None, "llama"):
+        ms_g, ms_e, wbytes, kv_bytes = bench_llama(torch, timer, max(20, steps // 4), min(warmup, 5))
+        total = wbytes + kv_bytes
+        entry = {"workload": "Llama-3.1-8B-layout decode token at position 4096 (32 layers, "
+                             "hidden 4096, 32/8 heads x 128, SwiGLU 14336, Q4_K_M mix, fp32 KV "
+                             "cache), random-init, one HIP graph per token",
+                 "ms_per_token": round(ms_g, 4), "tokens_per_s": round(1000.0 / ms_g, 1),
+                 "ms_per_token_eager": round(ms_e, 4),
+                 "weight_bytes": wbytes, "kv_bytes": kv_bytes,
+                 "GB/s": round(total / (ms_g * 1e-3) / 1e9, 1),
+                 "frac_hbm": round(total / (ms_g * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
+        if args.cpu_seconds > 0:
+            tps, n = cpu_llama_baseline(args.cpu_seconds)
+            entry["cpu_baseline"] = {"tokens_per_s": round(tps, 3), "cores": CPU_THREADS,
+                                     "kind": "port",
+                                     "sample": f"{n} oracle steps of one 8B-shaped layer at "
+                                               f"position 4096, x32, plus one Q6_K head GEMV"}
+            entry["speedup_vs_cpu"] = round(entry["tokens_per_s"] / tps, 1)
+        workloads.append(entry)
+        log(f"llama 8B token: {ms_g:.3f} ms (graph), {ms_e:.3f} ms (eager), "
+            f"{entry['GB/s']} GB/s")
 
     if args.only == "copy":
         # a plain device copy of known size: the HBM reference and the

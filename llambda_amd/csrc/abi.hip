@@ -713,8 +713,7 @@ struct llambda_hip_llama_session {
   DecoderPlan plan{};
   std::vector<DecoderLayer> layers;
   std::vector<std::unique_ptr<DevBuf>> weights;
-  DevBuf norms, kv, state, rope_denom, rope_cs, x, q, ctx, h, att_part, att_max, att_sum,
-      att_counter, logits;
+  DevBuf norms, kv, state, rope_denom, rope_cs, x, q, ctx, h, att_part, att_max, att_sum, logits;
   int64_t layer_count = 0;
   hipGraph_t graph = nullptr;
   hipGraphExec_t exec = nullptr;
@@ -958,8 +957,6 @@ int llambda_hip_llama_session_create(const llambda_hip_llama_desc* d,
     s->att_part.alloc((size_t)NH * p.att_chunks * D * sizeof(float), "attention partial sums");
     s->att_max.alloc((size_t)NH * p.att_chunks * sizeof(float), "attention chunk maxima");
     s->att_sum.alloc((size_t)NH * p.att_chunks * sizeof(float), "attention chunk sums");
-    s->att_counter.alloc((size_t)NKV * sizeof(int), "attention counters");
-    HIPC(hipMemsetAsync(s->att_counter.ptr, 0, (size_t)NKV * sizeof(int), s->stream));
     s->logits.alloc((size_t)d->vocab * sizeof(float), "logits");
     p.state = s->state.as<int>();
     p.rope_denom = s->rope_denom.as<double>();
@@ -971,7 +968,6 @@ int llambda_hip_llama_session_create(const llambda_hip_llama_desc* d,
     p.att_part = s->att_part.as<float>();
     p.att_max = s->att_max.as<float>();
     p.att_sum = s->att_sum.as<float>();
-    p.att_counter = s->att_counter.as<int>();
     HIPC(hipStreamSynchronize(s->stream));
     *result = s.release();
   });

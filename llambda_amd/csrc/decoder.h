@@ -8,7 +8,7 @@
 //                   keys written to the cache slot of this position
 //     v rows        rms-norm(x) fused in, values written to the cache slot
 //     attention     GQA over cache slots 0..position (split over position
-//                   chunks, the chunks combined by the last workgroup)
+//                   chunks of 128, the chunks combined by a second launch)
 //     o rows        x += o(context)
 //     gate|up rows  rms-norm(x) fused in, silu(g) * u fused out
 //     down rows     x += down(h)
@@ -59,7 +59,6 @@ struct DecoderPlan {
   float* att_part = nullptr;       // [kv_heads][att_chunks][group][head_dim]
   float* att_max = nullptr;        // [kv_heads][att_chunks][group]
   float* att_sum = nullptr;        // [kv_heads][att_chunks][group]
-  int* att_counter = nullptr;      // [kv_heads], zero between launches
   int att_chunks = 0;              // chunks of the context
 };
 

@@ -40,14 +40,14 @@ __global__ void rope_table_kernel(const int* __restrict__ state, const double* _
 // exp(s_p - max) / sum, context = sum_p prob_p v_p.
 //
 // Workgroup (chunk, kv head) takes slots [128 chunk, 128 chunk + 128) for
-// the G query heads of its kv head: scores (16 lanes per slot, DPP-free
-// xor reduction), the chunk's max m_c, e_p = exp(s_p - m_c) and their sum
-// S_c, and the unnormalised sum_p e_p v_p.  The last workgroup of the kv
-// head to finish combines the chunks in order: M = max m_c,
-// a_c = exp(m_c - M), context = (sum_c a_c pv_c) / (sum_c a_c S_c).  The
-// reference normalises every probability before the weighted sum; the two
-// agree to rounding (single-precision exp of each difference, computed in
-// double as SBCL does).
+// the G query heads of its kv head: scores (16 lanes per slot, xor-shuffle
+// reduction), the chunk's max m_c, e_p = exp(s_p - m_c) and their sum S_c,
+// and the unnormalised sum_p e_p v_p.  A second launch combines the chunks
+// in order: M = max m_c, a_c = exp(m_c - M),
+// context = (sum_c a_c pv_c) / (sum_c a_c S_c).  The reference normalises
+// every probability before the weighted sum; the two agree to rounding
+// (single-precision exp of each difference, computed in double as SBCL
+// does).
 constexpr int kAttnWaves = 8;
 
 __device__ __forceinline__ float wave_sum(float v) {
@@ -67,20 +67,16 @@ __global__ void __launch_bounds__(64 * kAttnWaves)
 attention_kernel(const float* __restrict__ q, const float* __restrict__ kc,
                  const float* __restrict__ vc, int64_t head_stride, const int* __restrict__ state,
                  float* __restrict__ part, float* __restrict__ pmax, float* __restrict__ psum,
-                 int* __restrict__ counter, int max_chunks, float* __restrict__ out) {
+                 int max_chunks) {
   constexpr int P = kAttnChunk;
   constexpr int T = 64 * kAttnWaves;
   constexpr int DL = D / 16;  // dims per lane in the scores
   constexpr int DQ = D / 4;   // float4 columns of a row
   constexpr int NP = T / DQ;  // slot parts in the weighted sum
   constexpr int PPP = P / NP;  // slots per part
-  constexpr int NQ = T / (G * DQ) > 0 ? T / (G * DQ) : 1;  // chunk parts in the combine
   static_assert(P == 128 && D % 16 == 0 && G <= kAttnWaves && NP * PPP == P, "attention shape");
   __shared__ float sc[G][P];
   __shared__ float4 pv[NP][G][DQ];
-  __shared__ float alpha[G][kAttnMaxChunks];
-  __shared__ float ssum[G];
-  __shared__ int ticket;
 
   const int n = state[1] + 1;
   const int chunk = blockIdx.x, kvh = blockIdx.y;
@@ -179,55 +175,44 @@ attention_kernel(const float* __restrict__ q, const float* __restrict__ kc,
     for (int r = 1; r < NP; ++r) t = t + pv[r][h][c];
     *reinterpret_cast<float4*>(part + (((int64_t)kvh * max_chunks + chunk) * G + h) * D + 4 * c) = t;
   }
+}
 
-  // the last workgroup of this kv head combines the chunks
-  __threadfence();
-  __syncthreads();
-  if (threadIdx.x == 0) ticket = atomicAdd(counter + kvh, 1);
-  __syncthreads();
-  if (ticket != nchunks - 1) return;
-  __threadfence();
-  if (wave < G) {
-    const int h = wave;
-    const float* mx = pmax + (int64_t)kvh * max_chunks * G + h;
-    const float* sm = psum + (int64_t)kvh * max_chunks * G + h;
-    float m = -INFINITY;
-    for (int c = lane; c < nchunks; c += 64) m = fmaxf(m, mx[(int64_t)c * G]);
-    m = wave_max(m);
-    float t = 0.f;
-    for (int c = lane; c < nchunks; c += 64) {
-      const float a = (float)exp((double)(mx[(int64_t)c * G] - m));
-      alpha[h][c] = a;
-      t += a * sm[(int64_t)c * G];
-    }
-    t = wave_sum(t);
-    if (lane == 0) ssum[h] = t;
+// Chunks of one query head combined in chunk order: M = max m_c,
+// a_c = exp(m_c - M) (single, computed in double), S = sum a_c S_c,
+// out = (sum a_c pv_c) / S.  Workgroup h, thread d = element d.
+template <int D, int G>
+__global__ void __launch_bounds__(D)
+attention_combine_kernel(const float* __restrict__ part, const float* __restrict__ pmax,
+                         const float* __restrict__ psum, const int* __restrict__ state,
+                         int max_chunks, float* __restrict__ out) {
+  __shared__ float alpha[kAttnMaxChunks];
+  __shared__ float red[D / 64];
+  const int h = blockIdx.x, d = threadIdx.x, lane = d & 63;
+  const int kvh = h / G, hh = h % G;
+  const int nchunks = (state[1] + kAttnChunk) / kAttnChunk;
+  const int64_t base = (int64_t)kvh * max_chunks * G + hh;  // chunk c at base + c * G
+  float m = -INFINITY;
+  for (int c = d; c < nchunks; c += D) {
+    const float v = pmax[base + (int64_t)c * G];
+    alpha[c] = v;
+    m = fmaxf(m, v);
   }
+  m = wave_max(m);
+  if (lane == 0) red[d >> 6] = m;
   __syncthreads();
-  // thread (quarter, column): chunks quarter, quarter + NQ, ...; the NQ
-  // partial sums meet in LDS in quarter order
-  {
-    const int i = threadIdx.x % (G * DQ), quarter = threadIdx.x / (G * DQ);
-    const int h = i / DQ, c = i % DQ;
-    float4 t = make_float4(0.f, 0.f, 0.f, 0.f);
-    if (quarter < NQ) {
-      const float* base = part + ((int64_t)kvh * max_chunks * G + h) * D + 4 * c;
-      for (int k = quarter; k < nchunks; k += NQ)
-        t = t + scale4(alpha[h][k], *reinterpret_cast<const float4*>(base + (int64_t)k * G * D));
-    }
-    __syncthreads();  // pv is free again
-    float4* qp = &pv[0][0][0];
-    if (quarter < NQ) qp[quarter * G * DQ + i] = t;
-    __syncthreads();
-    if (quarter == 0) {
-      float4 r = qp[i];
-      for (int k = 1; k < NQ; ++k) r = r + qp[k * G * DQ + i];
-      const float S = ssum[h];
-      *reinterpret_cast<float4*>(out + (int64_t)(kvh * G + h) * D + 4 * c) =
-          make_float4(r.x / S, r.y / S, r.z / S, r.w / S);
-    }
+  m = red[0];
+#pragma unroll
+  for (int w = 1; w < D / 64; ++w) m = fmaxf(m, red[w]);
+  for (int c = d; c < nchunks; c += D) alpha[c] = (float)exp((double)(alpha[c] - m));
+  __syncthreads();
+  float S = 0.f, acc = 0.f;
+  const float* pc = part + base * D + d;
+  for (int c = 0; c < nchunks; ++c) {
+    const float a = alpha[c];
+    S += a * psum[base + (int64_t)c * G];
+    acc += a * pc[(int64_t)c * G * D];
   }
-  if (threadIdx.x == 0) counter[kvh] = 0;
+  out[(int64_t)h * D + d] = acc / S;
 }
 
 bool decoder_head_supported(int head_dim, int group) {
@@ -241,7 +226,9 @@ static hipError_t launch_attention_t(const DecoderPlan& p, const float* q, const
   const dim3 grid(p.att_chunks, p.kv_heads);
   hipLaunchKernelGGL((attention_kernel<D, G>), grid, dim3(64 * kAttnWaves), 0, stream, q, kc, vc,
                      (int64_t)p.context * D, p.state, p.att_part, p.att_max, p.att_sum,
-                     p.att_counter, p.att_chunks, out);
+                     p.att_chunks);
+  hipLaunchKernelGGL((attention_combine_kernel<D, G>), dim3(p.heads), dim3(D), 0, stream,
+                     p.att_part, p.att_max, p.att_sum, p.state, p.att_chunks, out);
   return hipGetLastError();
 }
 

@@ -64,25 +64,24 @@ struct Chunk {
 constexpr int kQ4Table = 8 * 16 * 16;  // bytes per block
 constexpr int kQ6Table = 2 * 4 * 8 * 16;
 
-// Activation element i: x[i], or with a fused rms-norm-into
-// (llambda.lisp:859-879) x[i] * norm_w[i] * scale, rounded as the reference
-// rounds (x * w) then (* scale).
-__device__ __forceinline__ float act_at(const float* x, const float* nw, float nscale, int i) {
-  return nw ? (x[i] * nw[i]) * nscale : x[i];
-}
-
-__device__ __forceinline__ void build_q4k_table(uint8_t* table, float* gsum, const float* x,
-                                                int nblk, const float* nw, float nscale) {
-  // one thread per (block, sub-block, 4-element step)
-  for (int i = threadIdx.x; i < nblk * 64; i += blockDim.x) {
+// Table items: Q4_K item i = (block, sub-block s, 4-element step m); Q6_K
+// item i = (block, half, k, l-octet): 8 activations.  first(i) is the item's
+// first element; emit() writes the split values of its elements and, with
+// the lanes sharing its scale group, the group's sum.
+struct Q4Items {
+  static constexpr int kEl = 4, kPerBlock = 64;
+  __device__ static int first(int i) {
     const int b = i >> 6, s = (i >> 3) & 7, m = i & 7;
-    const int x0 = b * 256 + 32 * s + 4 * m;
+    return b * 256 + 32 * s + 4 * m;
+  }
+  __device__ static void emit(uint8_t* table, float* gsum, int i, const float* v) {
+    const int b = i >> 6, s = (i >> 3) & 7, m = i & 7;
     uint32_t hi[4], lo[4];
     float part = 0.f;
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
       float sum;
-      split_bf16(act_at(x, nw, nscale, x0 + e), hi[e], lo[e], sum);
+      split_bf16(v[e], hi[e], lo[e], sum);
       part += sum;
     }
     // rows a = 2s (hi) and 2s+1 (lo); the data sits in half (s & 1) of the 8 slots
@@ -101,7 +100,7 @@ __device__ __forceinline__ void build_q4k_table(uint8_t* table, float* gsum, con
     part += __shfl_xor(part, 4, 64);
     if (m == 0) gsum[b * 8 + s] = part;
   }
-}
+};
 
 // One Q4_K block of lane (n, g)'s row, p = the block's 144 bytes in LDS
 // (16-byte aligned); a = the lane's A address for this block (0 when its A
@@ -148,18 +147,20 @@ __device__ __forceinline__ float q4k_block(const uint8_t* p, const uint8_t* lds,
 // LDS table per block: 2 halves x 4 MFMAs x 8 entries x 16 B, then 16 group
 // sums.  Entry (a & 3) * 2 + (g & 1) of MFMA m serves A row a = 4m + (a & 3)
 // for lane g when (a >> 1) & 1 == g >> 1.
-__device__ __forceinline__ void build_q6k_table(uint8_t* table, float* gsum, const float* x,
-                                                int nblk, const float* nw, float nscale) {
-  // one thread per (block, half, k, l-octet): 8 activations
-  for (int i = threadIdx.x; i < nblk * 32; i += blockDim.x) {
+struct Q6Items {
+  static constexpr int kEl = 8, kPerBlock = 32;
+  __device__ static int first(int i) {
     const int b = i >> 5, h = (i >> 4) & 1, k = (i >> 2) & 3, g = i & 3;
-    const int x0 = b * 256 + 128 * h + 32 * k + 8 * g;
+    return b * 256 + 128 * h + 32 * k + 8 * g;
+  }
+  __device__ static void emit(uint8_t* table, float* gsum, int i, const float* v) {
+    const int b = i >> 5, h = (i >> 4) & 1, k = (i >> 2) & 3, g = i & 3;
     uint32_t hi[8], lo[8];
     float part = 0.f;
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
       float sum;
-      split_bf16(act_at(x, nw, nscale, x0 + e), hi[e], lo[e], sum);
+      split_bf16(v[e], hi[e], lo[e], sum);
       part += sum;
     }
     // slot = 2k + (g >> 1): A rows 4k + 2(g >> 1) (hi) and +1 (lo)
@@ -175,7 +176,7 @@ __device__ __forceinline__ void build_q6k_table(uint8_t* table, float* gsum, con
     part += __shfl_xor(part, 1, 64);
     if ((g & 1) == 0) gsum[b * 16 + h * 8 + 2 * k + (g >> 1)] = part;
   }
-}
+};
 
 // 8 bytes at byte offset o of the dword-aligned q (the block starts SH bytes
 // past q).
@@ -259,6 +260,66 @@ __device__ float rms_scale(const float* __restrict__ x, int K, float eps, float*
   return 1.f / sqrtf(mean + eps);
 }
 
+// The activation table of one workgroup: every thread loads the elements of
+// its items (up to kMaxI items, 16 floats, at once: one memory latency),
+// with a fused rms-norm-into (llambda.lisp:859-879) also their norm weights
+// and the sum of squares; then splits x (or (x * w) * scale, rounded as the
+// reference rounds) into the table.  x is 16-byte aligned.  red: kMfmaWaves
+// floats of LDS.
+template <typename IT, int WAVES>
+__device__ void build_table(uint8_t* table, float* gsum, const float* __restrict__ x, int nblk,
+                            const float* __restrict__ nw, float eps, float* red) {
+  constexpr int T = 64 * WAVES, EL = IT::kEl, kMaxI = 16 / EL;
+  const int items = nblk * IT::kPerBlock;
+  const bool one_batch = items <= T * kMaxI;
+  float nscale = 1.f;
+  if (nw && !one_batch) nscale = rms_scale<WAVES>(x, nblk * 256, eps, red);
+  for (int base = 0; base < items; base += T * kMaxI) {
+    float v[kMaxI][EL], wv[kMaxI][EL];
+#pragma unroll
+    for (int j = 0; j < kMaxI; ++j) {
+      const int i = base + threadIdx.x + j * T;
+      const int x0 = IT::first(min(i, items - 1));
+#pragma unroll
+      for (int e = 0; e < EL; e += 4) {
+        const float4 a = *reinterpret_cast<const float4*>(x + x0 + e);
+        v[j][e] = a.x; v[j][e + 1] = a.y; v[j][e + 2] = a.z; v[j][e + 3] = a.w;
+        if (nw) {
+          const float4 c = *reinterpret_cast<const float4*>(nw + x0 + e);
+          wv[j][e] = c.x; wv[j][e + 1] = c.y; wv[j][e + 2] = c.z; wv[j][e + 3] = c.w;
+        }
+      }
+    }
+    if (nw && one_batch) {
+      float acc = 0.f;
+#pragma unroll
+      for (int j = 0; j < kMaxI; ++j)
+        if (base + threadIdx.x + j * T < items)
+#pragma unroll
+          for (int e = 0; e < EL; ++e) acc += v[j][e] * v[j][e];
+      for (int o = 32; o > 0; o >>= 1) acc += __shfl_xor(acc, o, 64);
+      if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = acc;
+      __syncthreads();
+      float sum = red[0];
+#pragma unroll
+      for (int w = 1; w < WAVES; ++w) sum += red[w];
+      __syncthreads();
+      nscale = 1.f / sqrtf(sum / (float)(nblk * 256) + eps);
+    }
+#pragma unroll
+    for (int j = 0; j < kMaxI; ++j) {
+      const int i = base + threadIdx.x + j * T;
+      if (i < items) {
+        if (nw) {
+#pragma unroll
+          for (int e = 0; e < EL; ++e) v[j][e] = (v[j][e] * wv[j][e]) * nscale;
+        }
+        IT::emit(table, gsum, i, v[j]);
+      }
+    }
+  }
+}
+
 // Store the value v of row `row` (every lane of the wavefront calls this with
 // its own row; `writer` lanes store).  Pairs of rows for the rotation and
 // gate / up rows for SwiGLU are lanes n ^ 1 and n ^ 8 of the same 16 rows.
@@ -328,29 +389,34 @@ struct MfmaType {
 #endif
 constexpr int kMfmaWaves = LLHIP_GEMV_WAVES;
 
-// s_waitcnt vmcnt(n) (gfx9 encoding, other counters left alone)
+// s_waitcnt vmcnt(n) and lgkmcnt(0) (gfx9 encoding, other counters left alone)
 constexpr int waitcnt_vm(int n) { return 0x0F70 | (n & 15) | ((n >> 4) << 14); }
+constexpr int kWaitLgkm0 = 0xC07F;
 
 // LDS layout: [0, kZero) zeros | table (nblk * kTable) | group sums | stages
-// (D per wave) | split-K partial row sums.
+// (nbuf per wave) | split-K partial row sums.
 template <int TYPE, int C, bool ALIGNED>
-constexpr size_t mfma_lds_bytes(int nblk, int depth) {
+constexpr size_t mfma_lds_bytes(int nblk, int nbuf) {
   using T = MfmaType<TYPE>;
   using Ch = Chunk<T::kBB, C, ALIGNED>;
   return (size_t)T::kZero + (size_t)nblk * (T::kTable + 4 * T::kSums) +
-         (size_t)kMfmaWaves * depth * Ch::kBuffer + kMfmaWaves * 64 * sizeof(float);
+         (size_t)kMfmaWaves * nbuf * Ch::kBuffer + kMfmaWaves * 64 * sizeof(float);
 }
 
 // ALIGNED: the weights, row_bytes and the chunk span are multiples of 4, so
-// every row's chunk starts on a dword.  D: LDS stages per wave (a ring, D - 1
-// chunks in flight while one computes).  SPLIT: the four waves share each
-// 16-row tile and take every fourth chunk of it (row counts too small to
-// give every wave its own tiles); their partial sums meet in LDS and are
-// added in wave order.
-template <int TYPE, int C, bool ALIGNED, int D, bool SPLIT>
+// every row's chunk starts on a dword.  D: depth of the ring of stages per
+// wave; nbuf = min(D, steps of any wave) stages are allocated, step s uses
+// stage s % nbuf, all of them are filled before the activation table is
+// built, and each is refilled as soon as it has been read.  S: waves
+// per 16-row tile.  S = 1: every wave walks whole tiles of its own (a
+// persistent grid).  S > 1: the workgroup owns kMfmaWaves / S tiles, one per
+// group of S waves; wave k of a group takes chunks k, k + S, ... of the tile
+// (row counts too small to give every wave its own tiles); the group's
+// partial sums meet in LDS and are added in wave order.
+template <int TYPE, int C, bool ALIGNED, int D, int S>
 __global__ void __launch_bounds__(64 * kMfmaWaves)
 gemv_mfma_kernel(const uint8_t* __restrict__ w, int64_t row_bytes, int rows, int nblk,
-                 const float* __restrict__ x, float* __restrict__ y, const GemvFuse f) {
+                 const float* __restrict__ x, float* __restrict__ y, const GemvFuse f, int nbuf) {
   using T = MfmaType<TYPE>;
   using Ch = Chunk<T::kBB, C, ALIGNED>;
   extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
@@ -358,14 +424,7 @@ gemv_mfma_kernel(const uint8_t* __restrict__ w, int64_t row_bytes, int rows, int
   uint8_t* table = lds + table_off;
   float* gsum = reinterpret_cast<float*>(table + nblk * T::kTable);
   uint8_t* stages = reinterpret_cast<uint8_t*>(gsum + nblk * T::kSums);
-  float* partial = reinterpret_cast<float*>(stages + kMfmaWaves * D * Ch::kBuffer);
-
-  for (int i = threadIdx.x; i < T::kZero / 16; i += blockDim.x)
-    reinterpret_cast<u32x4*>(lds)[i] = u32x4{0u, 0u, 0u, 0u};
-  const float nscale = f.norm_w ? rms_scale<kMfmaWaves>(x, nblk * 256, f.norm_eps, partial) : 1.f;
-  if constexpr (TYPE == kQ4_K) build_q4k_table(table, gsum, x, nblk, f.norm_w, nscale);
-  else build_q6k_table(table, gsum, x, nblk, f.norm_w, nscale);
-  __syncthreads();
+  float* partial = reinterpret_cast<float*>(stages + kMfmaWaves * nbuf * Ch::kBuffer);
 
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -384,23 +443,25 @@ gemv_mfma_kernel(const uint8_t* __restrict__ w, int64_t row_bytes, int rows, int
   }
   const uint32_t a_stride = (TYPE == kQ4_K && a_base == 0u) ? 0u : (uint32_t)T::kTable;
 
-  const uint8_t* stage = stages + wave * D * Ch::kBuffer;
+  const uint8_t* stage = stages + wave * nbuf * Ch::kBuffer;
   const uint32_t stage_lds = lds_address(stage);
   const int tiles = (rows + 15) >> 4;
   const int chunks = nblk / C;
-  // Step s of this wave: (tile, chunk).  Without SPLIT the wave walks whole
-  // tiles first_tile, first_tile + tile_step, ...; with SPLIT the workgroup
-  // owns tile blockIdx.x and the wave its chunks wave, wave + 4, ...
-  const int first_tile = SPLIT ? blockIdx.x : blockIdx.x * kMfmaWaves + wave;
-  const int tile_step = gridDim.x * (SPLIT ? 1 : kMfmaWaves);
-  const int cpt = SPLIT ? (chunks - wave + kMfmaWaves - 1) / kMfmaWaves : chunks;  // chunks per tile
+  // Step s of this wave: (tile, chunk).  S = 1: whole tiles first_tile,
+  // first_tile + tile_step, ...; S > 1: the group's one tile, chunks sw,
+  // sw + S, ...
+  constexpr int kGroups = kMfmaWaves / S;
+  const int grp = wave / S, sw = wave - grp * S;
+  const int first_tile = S == 1 ? blockIdx.x * kMfmaWaves + wave : blockIdx.x * kGroups + grp;
+  const int tile_step = S == 1 ? gridDim.x * kMfmaWaves : tiles;
+  const int cpt = S == 1 ? chunks : (chunks - sw + S - 1) / S;  // chunks per tile
   const int my_tiles = first_tile < tiles ? (tiles - first_tile + tile_step - 1) / tile_step : 0;
   const int steps = my_tiles * cpt;
   const uint32_t rb = (uint32_t)row_bytes;
   auto tile_of = [&](int s) { return first_tile + (s / cpt) * tile_step; };
   auto chunk_of = [&](int s) {
     const int c = s - (s / cpt) * cpt;
-    return SPLIT ? wave + kMfmaWaves * c : c;
+    return S == 1 ? c : sw + S * c;
   };
 
   // per load instruction i: this lane's (row, piece) and byte offset in the tile
@@ -422,7 +483,7 @@ gemv_mfma_kernel(const uint8_t* __restrict__ w, int64_t row_bytes, int rows, int
         uniform_ptr(w + (int64_t)tile * 16 * row_bytes + (int64_t)chunk * Ch::kSpan);
     const uint32_t bsh = ALIGNED ? 0u : (uint32_t)(reinterpret_cast<uintptr_t>(base) & 3u);
     const uint8_t* base_al = base - bsh;
-    const uint32_t dst = stage_lds + (uint32_t)((s % D) * Ch::kBuffer);
+    const uint32_t dst = stage_lds + (uint32_t)((s % nbuf) * Ch::kBuffer);
     const int rmax = rows - 1 - tile * 16;
     if (ALIGNED && rmax >= 15) {
 #pragma unroll
@@ -441,16 +502,27 @@ gemv_mfma_kernel(const uint8_t* __restrict__ w, int64_t row_bytes, int rows, int
     }
   };
 
-  const int first = min(D - 1, steps);
+  // every stage is filled before the table is built
+  const int first = min(nbuf, steps);
   for (int s = 0; s < first; ++s) issue(s);
+
+  // activation table (the loads above are in flight meanwhile)
+  for (int i = threadIdx.x; i < T::kZero / 16; i += blockDim.x)
+    reinterpret_cast<u32x4*>(lds)[i] = u32x4{0u, 0u, 0u, 0u};
+  if constexpr (TYPE == kQ4_K)
+    build_table<Q4Items, kMfmaWaves>(table, gsum, x, nblk, f.norm_w, f.norm_eps, partial);
+  else
+    build_table<Q6Items, kMfmaWaves>(table, gsum, x, nblk, f.norm_w, f.norm_eps, partial);
+  __syncthreads();
+
   float acc = 0.f;
   for (int s = 0; s < steps; ++s) {
     const int tile = tile_of(s);
     const int chunk = chunk_of(s);
-    if (s + D - 1 < steps) issue(s + D - 1);
-    // at most `ahead` later steps' loads may still be in flight (a y store
-    // in between only makes the wait stricter)
-    const int ahead = min(steps, s + D) - s - 1;
+    // steps up to s + nbuf - 1 are issued; at most `ahead` later steps' loads
+    // may still be in flight (a y store in between only makes the wait
+    // stricter)
+    const int ahead = min(steps, s + nbuf) - s - 1;
     if constexpr (D <= 2) {
       if (ahead == 0) __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
       else __builtin_amdgcn_s_waitcnt(waitcnt_vm(Ch::kLoads));
@@ -462,7 +534,7 @@ gemv_mfma_kernel(const uint8_t* __restrict__ w, int64_t row_bytes, int rows, int
         default: __builtin_amdgcn_s_waitcnt(waitcnt_vm(3 * Ch::kLoads)); break;
       }
     }
-    const uint8_t* buf = stage + (s % D) * Ch::kBuffer;
+    const uint8_t* buf = stage + (s % nbuf) * Ch::kBuffer;
     const uint8_t* rowp = buf + n * Ch::kRow;
     if constexpr (!ALIGNED) {
       const int row = min(tile * 16 + n, rows - 1);
@@ -485,21 +557,26 @@ gemv_mfma_kernel(const uint8_t* __restrict__ w, int64_t row_bytes, int rows, int
     [&]<int... BL>(std::integer_sequence<int, BL...>) {
       (block.template operator()<BL>(), ...);
     }(std::make_integer_sequence<int, C>{});
-    if (!SPLIT && chunk == chunks - 1) {
+    if (S == 1 && chunk == chunks - 1) {
       const float v = sum_lane_groups(acc);
       store_row(f, y, rows, tile * 16 + n, v, g == 0);
       acc = 0.f;
     }
+    // refill the stage just read (its LDS reads drained first)
+    if (s + nbuf < steps) {
+      __builtin_amdgcn_s_waitcnt(kWaitLgkm0);
+      issue(s + nbuf);
+    }
   }
-  if constexpr (SPLIT) {
-    // one tile per workgroup: the waves' row sums, in wave order
+  if constexpr (S > 1) {
+    // one tile per group: its waves' row sums, in wave order
     const float v = sum_lane_groups(acc);
     if (g == 0) partial[wave * 16 + n] = v;
     __syncthreads();
-    if (wave == 0 && first_tile < tiles) {
-      float t = partial[n];
+    if (sw == 0 && first_tile < tiles) {
+      float t = partial[wave * 16 + n];
 #pragma unroll
-      for (int w = 1; w < kMfmaWaves; ++w) t = t + partial[16 * w + n];
+      for (int k = 1; k < S; ++k) t = t + partial[(wave + k) * 16 + n];
       store_row(f, y, rows, first_tile * 16 + n, t, g == 0);
     }
   }
@@ -516,20 +593,43 @@ template <int TYPE>
 struct MfmaChoice {
   int chunk;
   bool aligned;
-  int depth;   // 4 when the LDS holds it, else 2
-  bool split;  // too few tiles for one per wave
+  int depth;  // ring depth per wave
+  int waves;  // waves per tile (S)
 };
+
+// Stages a wave needs: the ring depth, or fewer when no wave has that many
+// steps (S > 1: one tile's chunks shared by S waves).
+static int mfma_nbuf(int depth, int waves, int chunks) {
+  if (waves == 1) return depth;
+  return std::max(1, std::min(depth, (chunks + waves - 1) / waves));
+}
+template <int TYPE>
+static int mfma_nbuf(const MfmaChoice<TYPE>& c, int nblk) {
+  return mfma_nbuf(c.depth, c.waves, nblk / c.chunk);
+}
+
+// Waves per tile: enough waves in flight to cover the device
+// (LLHIP_GEMV_TARGET_WAVES of them), as long as every wave keeps a chunk.
+#ifndef LLHIP_GEMV_TARGET_WAVES
+#define LLHIP_GEMV_TARGET_WAVES 4096
+#endif
+static int mfma_waves_per_tile(int64_t tiles, int64_t chunks) {
+  int S = 1;
+  while (S < kMfmaWaves && tiles * S < LLHIP_GEMV_TARGET_WAVES && chunks >= 2 * S) S *= 2;
+  return S;
+}
 
 template <int TYPE>
 static size_t mfma_lds_for(const MfmaChoice<TYPE>& c, int nblk) {
+  const int nb = mfma_nbuf(c, nblk);
   if (c.chunk == 4)
-    return c.aligned ? mfma_lds_bytes<TYPE, 4, true>(nblk, c.depth)
-                     : mfma_lds_bytes<TYPE, 4, false>(nblk, c.depth);
+    return c.aligned ? mfma_lds_bytes<TYPE, 4, true>(nblk, nb)
+                     : mfma_lds_bytes<TYPE, 4, false>(nblk, nb);
   if (c.chunk == 2)
-    return c.aligned ? mfma_lds_bytes<TYPE, 2, true>(nblk, c.depth)
-                     : mfma_lds_bytes<TYPE, 2, false>(nblk, c.depth);
-  return c.aligned ? mfma_lds_bytes<TYPE, 1, true>(nblk, c.depth)
-                   : mfma_lds_bytes<TYPE, 1, false>(nblk, c.depth);
+    return c.aligned ? mfma_lds_bytes<TYPE, 2, true>(nblk, nb)
+                     : mfma_lds_bytes<TYPE, 2, false>(nblk, nb);
+  return c.aligned ? mfma_lds_bytes<TYPE, 1, true>(nblk, nb)
+                   : mfma_lds_bytes<TYPE, 1, false>(nblk, nb);
 }
 
 template <int TYPE>
@@ -538,18 +638,18 @@ static MfmaChoice<TYPE> mfma_choice(const GemvProblem& p) {
   MfmaChoice<TYPE> c;
   c.chunk = nblk % LLHIP_GEMV_CHUNK == 0 ? LLHIP_GEMV_CHUNK : nblk % 2 == 0 ? 2 : 1;
   c.depth = kGemvDepth;
+  const int64_t tiles = (p.rows + 15) / 16;
   // long rows: shorter chunks, then fewer stages, until the LDS holds the
   // activation table and the stages
   for (;;) {
     const int64_t span = (int64_t)c.chunk * MfmaType<TYPE>::kBB;
     c.aligned = p.row_bytes % 4 == 0 && span % 4 == 0;
+    c.waves = mfma_waves_per_tile(tiles, nblk / c.chunk);
     if (mfma_lds_for(c, (int)nblk) <= kMaxLdsBytes) break;
     if (c.chunk > 1) c.chunk /= 2;
     else if (c.depth > 2) c.depth = 2;
     else break;
   }
-  const int64_t tiles = (p.rows + 15) / 16;
-  c.split = tiles < (int64_t)device_cu_count() * 2 * kMfmaWaves && nblk / c.chunk >= kMfmaWaves;
   return c;
 }
 
@@ -560,6 +660,8 @@ bool gemv_mfma_supported(const GemvProblem& p) {
   // weights must start on a dword (Q4_K: rows 16-byte aligned, its blocks
   // are read from LDS with 16-byte loads)
   if (reinterpret_cast<uintptr_t>(p.weights) & 3u) return false;
+  // activations are read as float4
+  if (reinterpret_cast<uintptr_t>(p.x) & 15u) return false;
   if (p.type == kQ4_K) {
     const MfmaChoice<kQ4_K> c = mfma_choice<kQ4_K>(p);
     return (reinterpret_cast<uintptr_t>(p.weights) & 15u) == 0 && p.row_bytes % 16 == 0 &&
@@ -572,11 +674,12 @@ bool gemv_mfma_supported(const GemvProblem& p) {
   return false;
 }
 
-template <int TYPE, int C, bool ALIGNED, int D, bool SPLIT>
+template <int TYPE, int C, bool ALIGNED, int D, int S>
 static hipError_t launch_mfma(const GemvProblem& p, const GemvFuse& f, hipStream_t stream) {
   const int nblk = (int)(p.columns / 256);
-  const size_t lds = mfma_lds_bytes<TYPE, C, ALIGNED>(nblk, D);
-  const auto kernel = gemv_mfma_kernel<TYPE, C, ALIGNED, D, SPLIT>;
+  const int nbuf = mfma_nbuf(D, S, nblk / C);
+  const size_t lds = mfma_lds_bytes<TYPE, C, ALIGNED>(nblk, nbuf);
+  const auto kernel = gemv_mfma_kernel<TYPE, C, ALIGNED, D, S>;
   if (lds > 65536) {
     hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kernel),
                                        hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
@@ -584,8 +687,8 @@ static hipError_t launch_mfma(const GemvProblem& p, const GemvFuse& f, hipStream
   }
   const int tiles = (int)((p.rows + 15) / 16);
   int grid;
-  if (SPLIT) {
-    grid = tiles;  // one tile per workgroup
+  if (S > 1) {
+    grid = (tiles + kMfmaWaves / S - 1) / (kMfmaWaves / S);  // one tile per group
   } else {
     int per_cu = 0;
     if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, reinterpret_cast<const void*>(kernel),
@@ -596,18 +699,20 @@ static hipError_t launch_mfma(const GemvProblem& p, const GemvFuse& f, hipStream
     grid = std::max(1, std::min(needed, device_cu_count() * per_cu));
   }
   hipLaunchKernelGGL(kernel, dim3(grid), dim3(64 * kMfmaWaves), lds, stream, p.weights,
-                     p.row_bytes, (int)p.rows, nblk, p.x, p.y, f);
+                     p.row_bytes, (int)p.rows, nblk, p.x, p.y, f, nbuf);
   return hipGetLastError();
 }
 
 template <int TYPE, int C, bool ALIGNED>
 static hipError_t launch_mfma_ds(const MfmaChoice<TYPE>& c, const GemvProblem& p,
                                  const GemvFuse& f, hipStream_t s) {
-  if (c.split)
-    return c.depth == kGemvDepth ? launch_mfma<TYPE, C, ALIGNED, kGemvDepth, true>(p, f, s)
-                                 : launch_mfma<TYPE, C, ALIGNED, 2, true>(p, f, s);
-  return c.depth == kGemvDepth ? launch_mfma<TYPE, C, ALIGNED, kGemvDepth, false>(p, f, s)
-                               : launch_mfma<TYPE, C, ALIGNED, 2, false>(p, f, s);
+  static_assert(kGemvDepth == 2, "one ring depth is instantiated");
+  switch (c.waves) {
+    case 8: return launch_mfma<TYPE, C, ALIGNED, kGemvDepth, 8>(p, f, s);
+    case 4: return launch_mfma<TYPE, C, ALIGNED, kGemvDepth, 4>(p, f, s);
+    case 2: return launch_mfma<TYPE, C, ALIGNED, kGemvDepth, 2>(p, f, s);
+    default: return launch_mfma<TYPE, C, ALIGNED, kGemvDepth, 1>(p, f, s);
+  }
 }
 
 template <int TYPE>
