@@ -34,6 +34,7 @@ extern "C" {
 typedef struct llambda_hip_session llambda_hip_session;
 typedef struct llambda_hip_moe_session llambda_hip_moe_session;
 typedef struct llambda_hip_llama_session llambda_hip_llama_session;
+typedef struct llambda_hip_sampler llambda_hip_sampler;
 
 /* ---- probe, versions, errors -------------------------------------- */
 
@@ -286,6 +287,42 @@ int llambda_hip_llama_session_read_kv(llambda_hip_llama_session* session, int64_
 
 /* Wait for `stream` (null = the session's stream). */
 int llambda_hip_llama_session_sync(llambda_hip_llama_session* session, void* stream);
+
+/* ---- sampling ------------------------------------------------------------ */
+
+/* Keyword arguments of sample-token-id-from-logits (llambda.lisp:1272-1317),
+ * with the random value explicit (the reference's :random-value). */
+typedef struct llambda_hip_sampling {
+  const int64_t* history;     /* host, token ids already generated (may repeat) */
+  size_t history_count;
+  float repetition_penalty;   /* reference default 1.15 */
+  int64_t top_k;              /* reference default 40; 0 disables */
+  float top_p;                /* reference default 0.95; 1 disables */
+  float temperature;          /* reference default 1.0 */
+  float random_value;         /* in [0, 1) */
+} llambda_hip_sampling;
+
+/* Device scratch for logits rows of up to `vocab` entries.  No counterpart in
+ * the reference's bridge: sampling runs in Lisp there (llambda.lisp:1036-1317). */
+int llambda_hip_sampler_create(size_t vocab, llambda_hip_sampler** result);
+void llambda_hip_sampler_destroy(llambda_hip_sampler* sampler);
+
+/* The token sample-token-id-from-logits draws from logits[count] (host
+ * memory, or device memory when logits_on_device = 1); the logits are not
+ * modified.  With top-k (1 <= top_k < count) the token is the reference's bit
+ * for bit; without top-k, top_p must be 1 and the token matches wherever the
+ * random value is not within rounding of a cumulative boundary.  Errors: the
+ * reference's argument errors, NaN logits, more than 4096 logits tied at or
+ * above the top-k cutoff, top-p without top-k.  Synchronous. */
+int llambda_hip_sampler_sample(llambda_hip_sampler* sampler, const float* logits, size_t count,
+                               int logits_on_device, const llambda_hip_sampling* params,
+                               int64_t* token);
+
+/* Sample from a llama session's own logits buffer (after
+ * llambda_hip_llama_session_step_device with null logits). */
+int llambda_hip_llama_session_sample(llambda_hip_llama_session* session,
+                                     llambda_hip_sampler* sampler,
+                                     const llambda_hip_sampling* params, int64_t* token);
 
 #ifdef __cplusplus
 }

@@ -24,6 +24,7 @@
 #include "decoder.h"
 #include "gemv.h"
 #include "moe.h"
+#include "sample.h"
 #include "sha256.h"
 
 using namespace llhip;
@@ -1098,6 +1099,148 @@ int llambda_hip_llama_session_sync(llambda_hip_llama_session* s, void* stream) {
   return guarded([&] {
     if (!s) failf("llama sync: null session");
     HIPC(hipStreamSynchronize(stream ? static_cast<hipStream_t>(stream) : s->stream));
+  });
+}
+
+}  // extern "C"
+
+// ---------------------------------------------------------------- sampling
+
+struct llambda_hip_sampler {
+  std::mutex run_mutex;
+  int device = 0;
+  hipStream_t stream = nullptr;
+  int64_t vocab = 0;
+  DevBuf work, logits, history, result;
+  size_t history_cap = 0;
+  ~llambda_hip_sampler() {
+    if (stream) (void)hipStreamDestroy(stream);
+  }
+};
+
+namespace {
+
+// Validate the arguments as sample-token-id-from-logits does and enqueue the
+// sampling kernel on the sampler's stream; returns the token.
+int64_t run_sampler(llambda_hip_sampler* s, const float* dev_logits, int64_t n,
+                    const llambda_hip_sampling* a) {
+  if (!a) failf("sample: null parameters");
+  if (n <= 0 || n > s->vocab) failf("sample: %lld logits do not fit the sampler (vocab %lld)",
+                                    (long long)n, (long long)s->vocab);
+  if (!(a->random_value >= 0.0f && a->random_value < 1.0f))
+    failf("RANDOM-VALUE must satisfy 0.0 <= value < 1.0, got %g.", (double)a->random_value);
+  if (a->top_k < 0) failf("TOP-K must be a nonnegative fixnum or NIL, got %lld.", (long long)a->top_k);
+  if (!(a->top_p > 0.0f && a->top_p <= 1.0f))
+    failf("TOP-P must satisfy 0.0 < p <= 1.0, got %g.", (double)a->top_p);
+  if (!(a->temperature > 0.0f)) failf("TEMPERATURE must be positive, got %g.", (double)a->temperature);
+  if (a->temperature > 1.0e20f)
+    failf("sample: temperature %g is outside the device path (masked logits must underflow)",
+          (double)a->temperature);
+  // distinct history tokens, checked in the reference's order
+  std::vector<int> distinct;
+  if (a->history_count > 0) {
+    if (!a->history) failf("sample: null history");
+    if (!(a->repetition_penalty > 0.0f))
+      failf("PENALTY must be positive, got %g.", (double)a->repetition_penalty);
+    std::vector<int64_t> seen;
+    for (size_t i = 0; i < a->history_count; ++i) {
+      const int64_t t = a->history[i];
+      bool dup = false;
+      for (int64_t u : seen)
+        if (u == t) {
+          dup = true;
+          break;
+        }
+      if (dup) continue;
+      if (t < 0 || t >= n)
+        failf("History token id %lld is out of bounds for logits length %lld.", (long long)t,
+              (long long)n);
+      seen.push_back(t);
+      distinct.push_back((int)t);
+    }
+  }
+  const bool topk = a->top_k > 0 && a->top_k < n;
+  if (!topk && a->top_p < 1.0f)
+    failf("sample: top-p without top-k is not supported on the device (it needs a sort of the "
+          "whole row)");
+  if (distinct.size() > s->history_cap) {
+    s->history.alloc(distinct.size() * sizeof(int), "sampling history");
+    s->history_cap = distinct.size();
+  }
+  if (!distinct.empty())
+    HIPC(hipMemcpyAsync(s->history.ptr, distinct.data(), distinct.size() * sizeof(int),
+                        hipMemcpyHostToDevice, s->stream));
+  SampleParams p;
+  p.n = (int)n;
+  p.history = s->history.as<int>();
+  p.nh = (int)distinct.size();
+  p.penalty = a->repetition_penalty;
+  p.top_k = (int)std::min<int64_t>(a->top_k, n);
+  p.top_p = a->top_p;
+  p.temperature = a->temperature;
+  p.roll = a->random_value;
+  HIPC(sample_launch(dev_logits, s->work.as<float>(), p, s->result.as<int>(), s->stream));
+  int res[2] = {0, 0};
+  HIPC(hipMemcpyAsync(res, s->result.ptr, sizeof res, hipMemcpyDeviceToHost, s->stream));
+  HIPC(hipStreamSynchronize(s->stream));
+  if (res[1] == kSampleErrNaN) failf("sample: NaN logit");
+  if (res[1] == kSampleErrTies)
+    failf("sample: more than %d logits tie at or above the top-k cutoff", kSampleMaxSurvivors);
+  if (res[1] != 0 || res[0] < 0) failf("sample: device error %d", res[1]);
+  return res[0];
+}
+
+}  // namespace
+
+extern "C" {
+
+int llambda_hip_sampler_create(size_t vocab, llambda_hip_sampler** result) {
+  return guarded([&] {
+    if (!result) failf("sampler: null result pointer");
+    *result = nullptr;
+    if (vocab == 0 || vocab > (size_t)INT_MAX) failf("sampler: vocab %zu out of range", vocab);
+    std::unique_ptr<llambda_hip_sampler> s(new llambda_hip_sampler());
+    s->device = current_device_checked();
+    s->vocab = (int64_t)vocab;
+    HIPC(hipStreamCreateWithFlags(&s->stream, hipStreamNonBlocking));
+    s->work.alloc(vocab * sizeof(float), "sampling row");
+    s->logits.alloc(vocab * sizeof(float), "sampling input");
+    s->result.alloc(2 * sizeof(int), "sampling result");
+    *result = s.release();
+  });
+}
+
+void llambda_hip_sampler_destroy(llambda_hip_sampler* sampler) { delete sampler; }
+
+int llambda_hip_sampler_sample(llambda_hip_sampler* s, const float* logits, size_t count,
+                               int logits_on_device, const llambda_hip_sampling* params,
+                               int64_t* token) {
+  return guarded([&] {
+    if (!s || !logits || !token) failf("sample: null argument");
+    std::lock_guard<std::mutex> lock(s->run_mutex);
+    HIPC(hipSetDevice(s->device));
+    if (count == 0 || count > (size_t)s->vocab)
+      failf("sample: %zu logits do not fit the sampler (vocab %lld)", count, (long long)s->vocab);
+    const float* dev = logits;
+    if (!logits_on_device) {
+      HIPC(hipMemcpyAsync(s->logits.ptr, logits, count * sizeof(float), hipMemcpyHostToDevice,
+                          s->stream));
+      dev = s->logits.as<float>();
+    }
+    *token = run_sampler(s, dev, (int64_t)count, params);
+  });
+}
+
+int llambda_hip_llama_session_sample(llambda_hip_llama_session* session,
+                                     llambda_hip_sampler* s, const llambda_hip_sampling* params,
+                                     int64_t* token) {
+  return guarded([&] {
+    if (!session || !s || !token) failf("sample: null argument");
+    std::lock_guard<std::mutex> lock(s->run_mutex);
+    HIPC(hipSetDevice(s->device));
+    // the session's stream holds the step that wrote the logits
+    HIPC(hipStreamSynchronize(session->stream));
+    *token = run_sampler(s, session->logits.as<float>(), session->plan.vocab, params);
   });
 }
 

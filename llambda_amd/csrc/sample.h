@@ -1,0 +1,33 @@
+// sample.h -- sample-token-id-from-logits (llambda.lisp:1272-1317) on the
+// device (sample.hip).
+#pragma once
+
+#include "common.h"
+
+namespace llhip {
+
+// Survivors of top-k (ties included) the exact path holds in LDS.
+constexpr int kSampleMaxSurvivors = 4096;
+
+enum SampleError : int {
+  kSampleErrNaN = 1,   // a NaN logit
+  kSampleErrTies = 2,  // more than kSampleMaxSurvivors logits tie at or above the cutoff
+};
+
+struct SampleParams {
+  int n;               // logits
+  const int* history;  // device, distinct token ids < n (host-validated)
+  int nh;
+  float penalty;       // repetition penalty (> 0)
+  int top_k;           // 0 or >= n: no top-k (top_p must then be 1)
+  float top_p;         // (0, 1]
+  float temperature;   // > 0
+  float roll;          // random value in [0, 1)
+};
+
+// result[0] = token (-1 on error), result[1] = SampleError or 0.  work: [n]
+// floats of scratch.  One workgroup.
+hipError_t sample_launch(const float* logits, float* work, const SampleParams& p, int* result,
+                         hipStream_t stream);
+
+}  // namespace llhip

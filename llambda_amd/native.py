@@ -79,6 +79,14 @@ class LlamaDesc(ctypes.Structure):
     ]
 
 
+class Sampling(ctypes.Structure):
+    """llambda_hip_sampling."""
+    _fields_ = [("history", c_void_p), ("history_count", c_size),
+                ("repetition_penalty", ctypes.c_float), ("top_k", c_i64),
+                ("top_p", ctypes.c_float), ("temperature", ctypes.c_float),
+                ("random_value", ctypes.c_float)]
+
+
 # name -> (restype, argtypes); the complete export list of include/llambda_hip.h
 SIGNATURES = {
     "llambda_hip_probe": (c_int, []),
@@ -117,6 +125,12 @@ SIGNATURES = {
     "llambda_hip_llama_session_read_kv": (c_int, [c_void_p, c_i64, c_i64, c_i64, c_void_p,
                                                   c_void_p]),
     "llambda_hip_llama_session_sync": (c_int, [c_void_p, c_void_p]),
+    "llambda_hip_sampler_create": (c_int, [c_size, ctypes.POINTER(c_void_p)]),
+    "llambda_hip_sampler_destroy": (None, [c_void_p]),
+    "llambda_hip_sampler_sample": (c_int, [c_void_p, c_void_p, c_size, c_int,
+                                           ctypes.POINTER(Sampling), ctypes.POINTER(c_i64)]),
+    "llambda_hip_llama_session_sample": (c_int, [c_void_p, c_void_p, ctypes.POINTER(Sampling),
+                                                 ctypes.POINTER(c_i64)]),
 }
 
 

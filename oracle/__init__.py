@@ -124,6 +124,18 @@ def lib():
         L.oracle_llama_step.argtypes = [ctypes.POINTER(LlamaDesc), ctypes.c_void_p,
                                         ctypes.c_int64, ctypes.c_int64, ctypes.c_int64,
                                         ctypes.c_void_p, ctypes.c_int]
+        i64p = ctypes.c_void_p
+        L.oracle_repetition_penalty.argtypes = [ctypes.c_void_p, ctypes.c_int64, i64p,
+                                                ctypes.c_int64, ctypes.c_float]
+        L.oracle_top_k.argtypes = [ctypes.c_void_p, ctypes.c_int64, ctypes.c_int64]
+        L.oracle_top_p.argtypes = [ctypes.c_void_p, ctypes.c_int64, ctypes.c_float,
+                                   ctypes.c_float]
+        L.oracle_sample_from_probabilities.restype = ctypes.c_int64
+        L.oracle_sample_from_probabilities.argtypes = [ctypes.c_void_p, ctypes.c_int64,
+                                                       ctypes.c_float]
+        L.oracle_sample_token.argtypes = [ctypes.c_void_p, ctypes.c_int64, i64p, ctypes.c_int64,
+                                          ctypes.c_float, ctypes.c_int64, ctypes.c_float,
+                                          ctypes.c_float, ctypes.c_float, ctypes.c_void_p]
         _lib = L
     return _lib
 
@@ -351,3 +363,42 @@ def llama_step(weights, kv: np.ndarray, token: int, position: int, threads: int 
     _check(lib().oracle_llama_step(ctypes.byref(d), kv.ctypes.data, cap, token, position,
                                    logits.ctypes.data, threads))
     return logits
+
+
+def repetition_penalty(logits, history, penalty: float) -> np.ndarray:
+    out = _f32(logits).copy()
+    h = np.ascontiguousarray(history, dtype=np.int64)
+    _check(lib().oracle_repetition_penalty(out.ctypes.data, out.size, h.ctypes.data, h.size,
+                                           penalty))
+    return out
+
+
+def top_k(logits, k: int) -> np.ndarray:
+    out = _f32(logits).copy()
+    _check(lib().oracle_top_k(out.ctypes.data, out.size, k))
+    return out
+
+
+def top_p(logits, p: float, temperature: float = 1.0) -> np.ndarray:
+    out = _f32(logits).copy()
+    _check(lib().oracle_top_p(out.ctypes.data, out.size, p, temperature))
+    return out
+
+
+def sample_from_probabilities(probs, roll: float) -> int:
+    p = _f32(probs)
+    return int(lib().oracle_sample_from_probabilities(p.ctypes.data, p.size, roll))
+
+
+def sample_token(logits, *, history=None, repetition_penalty: float = 1.15, top_k: int = 40,
+                 top_p: float = 0.95, temperature: float = 1.0, random_value: float) -> int:
+    """sample-token-id-from-logits (llambda.lisp:1272-1317) on a copy of logits;
+    top_k=None -> 40 and top_p=None -> 0.95 as the reference defaults them."""
+    x = _f32(logits).copy()
+    h = np.ascontiguousarray(history if history is not None else [], dtype=np.int64)
+    tok = ctypes.c_int64()
+    _check(lib().oracle_sample_token(x.ctypes.data, x.size, h.ctypes.data, h.size,
+                                     repetition_penalty, 40 if top_k is None else top_k,
+                                     0.95 if top_p is None else top_p, temperature,
+                                     random_value, ctypes.byref(tok)))
+    return tok.value

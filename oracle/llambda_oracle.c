@@ -872,3 +872,159 @@ int oracle_llama_step(const oracle_llama_desc* m, float* kv, int64_t cap, int64_
   free(buf);
   return status;
 }
+
+/* ========================================================== sampling */
+
+#define MASKED_LOGIT (-1.0e30f) /* llambda.lisp:1098, 1172 */
+
+/* apply-repetition-penalty (llambda.lisp:1036-1086): every distinct history
+ * token once, positive logits divided by the penalty, negative multiplied. */
+int oracle_repetition_penalty(float* logits, int64_t n, const int64_t* history, int64_t nh,
+                              float penalty) {
+  if (!(penalty > 0.0f)) return fail("PENALTY must be positive, got %g.", (double)penalty);
+  for (int64_t i = 0; i < nh; ++i) {
+    const int64_t t = history[i];
+    int seen = 0;
+    for (int64_t j = 0; j < i; ++j)
+      if (history[j] == t) {
+        seen = 1;
+        break;
+      }
+    if (seen) continue;
+    if (t < 0 || t >= n)
+      return fail("History token id %lld is out of bounds for logits length %lld.", (long long)t,
+                  (long long)n);
+    const float l = logits[t];
+    if (l > 0.0f) logits[t] = l / penalty;
+    else if (l < 0.0f) logits[t] = l * penalty;
+  }
+  return 0;
+}
+
+static void heapify_down(float* heap, int64_t k, int64_t start) {
+  const float value = heap[start];
+  int64_t index = start;
+  for (;;) {
+    const int64_t left = 2 * index + 1;
+    if (left >= k) break;
+    const int64_t right = left + 1;
+    const int64_t smaller = (right < k && heap[right] < heap[left]) ? right : left;
+    if (value <= heap[smaller]) break;
+    heap[index] = heap[smaller];
+    index = smaller;
+  }
+  heap[index] = value;
+}
+
+/* apply-top-k-with-workspace (llambda.lisp:1088-1150): a min-heap of the
+ * first k logits, each later logit greater than the root replaces it; every
+ * logit below the final root is masked (ties with the root survive). */
+int oracle_top_k(float* logits, int64_t n, int64_t k) {
+  if (k < 0) return fail("TOP-K must be non-negative, got %lld.", (long long)k);
+  if (k == 0 || k >= n) return 0;
+  float* heap = (float*)malloc((size_t)k * sizeof(float));
+  if (!heap) return fail("top-k: out of memory");
+  memcpy(heap, logits, (size_t)k * sizeof(float));
+  for (int64_t i = (k - 2) / 2; i >= 0; --i) heapify_down(heap, k, i);
+  for (int64_t i = k; i < n; ++i)
+    if (logits[i] > heap[0]) {
+      heap[0] = logits[i];
+      heapify_down(heap, k, 0);
+    }
+  const float cutoff = heap[0];
+  for (int64_t i = 0; i < n; ++i)
+    if (logits[i] < cutoff) logits[i] = MASKED_LOGIT;
+  free(heap);
+  return 0;
+}
+
+/* apply-top-p-with-workspace (llambda.lisp:1163-1240): the unmasked logits
+ * in index order, insertion-sorted descending (stable), softmax of
+ * logit / temperature accumulated in that order until the cumulative
+ * probability reaches p; logits below the cutoff are masked. */
+int oracle_top_p(float* logits, int64_t n, float p, float temperature) {
+  if (!(p > 0.0f) || p > 1.0f) return fail("TOP-P must satisfy 0.0 < p <= 1.0, got %g.", (double)p);
+  if (!(temperature > 0.0f))
+    return fail("TEMPERATURE must be positive, got %g.", (double)temperature);
+  if (p == 1.0f) return 0;
+  float* val = (float*)malloc((size_t)n * sizeof(float));
+  int64_t* idx = (int64_t*)malloc((size_t)n * sizeof(int64_t));
+  if (!val || !idx) {
+    free(val);
+    free(idx);
+    return fail("top-p: out of memory");
+  }
+  int64_t active = 0;
+  for (int64_t i = 0; i < n; ++i)
+    if (logits[i] > MASKED_LOGIT) {
+      val[active] = logits[i];
+      idx[active] = i;
+      ++active;
+    }
+  if (active > 1) {
+    for (int64_t i = 1; i < active; ++i) {
+      const float v = val[i];
+      const int64_t t = idx[i];
+      int64_t j = i;
+      while (j > 0 && !(val[j - 1] >= v)) {
+        val[j] = val[j - 1];
+        idx[j] = idx[j - 1];
+        --j;
+      }
+      val[j] = v;
+      idx[j] = t;
+    }
+    const float max_scaled = val[0] / temperature;
+    float sum = 0.0f;
+    for (int64_t i = 0; i < active; ++i) sum += (float)exp((double)(val[i] / temperature - max_scaled));
+    float cumulative = 0.0f, cutoff = val[active - 1];
+    for (int64_t i = 0; i < active; ++i) {
+      cumulative += (float)exp((double)(val[i] / temperature - max_scaled)) / sum;
+      if (cumulative >= p) {
+        cutoff = val[i];
+        break;
+      }
+    }
+    for (int64_t i = 0; i < n; ++i)
+      if (logits[i] < cutoff) logits[i] = MASKED_LOGIT;
+  }
+  free(val);
+  free(idx);
+  return 0;
+}
+
+/* sample-from-probabilities (llambda.lisp:1253-1270): the first index whose
+ * running total reaches the roll, else the last index. */
+int64_t oracle_sample_from_probabilities(const float* probs, int64_t n, float roll) {
+  float running = 0.0f;
+  for (int64_t i = 0; i < n; ++i) {
+    running += probs[i];
+    if (roll <= running) return i;
+  }
+  return n - 1;
+}
+
+/* sample-token-id-from-logits (llambda.lisp:1272-1317) with an explicit
+ * random value: repetition penalty (when history is given), top-k, top-p,
+ * apply-temperature (1009-1015), softmax (1017-1034), the draw.  logits are
+ * modified in place as the reference modifies them. */
+int oracle_sample_token(float* logits, int64_t n, const int64_t* history, int64_t nh,
+                        float penalty, int64_t top_k, float top_p, float temperature, float roll,
+                        int64_t* token) {
+  if (n <= 0 || !token) return fail("sample: empty logits");
+  if (!(roll >= 0.0f && roll < 1.0f))
+    return fail("RANDOM-VALUE must satisfy 0.0 <= value < 1.0, got %g.", (double)roll);
+  if (!(top_p > 0.0f) || top_p > 1.0f)
+    return fail("TOP-P must satisfy 0.0 < p <= 1.0, got %g.", (double)top_p);
+  if (top_k < 0) return fail("TOP-K must be a nonnegative fixnum or NIL, got %lld.", (long long)top_k);
+  if (nh > 0 && oracle_repetition_penalty(logits, n, history, nh, penalty)) return -1;
+  if (oracle_top_k(logits, n, top_k)) return -1;
+  if (oracle_top_p(logits, n, top_p, temperature)) return -1;
+  float* probs = (float*)malloc((size_t)n * sizeof(float));
+  if (!probs) return fail("sample: out of memory");
+  for (int64_t i = 0; i < n; ++i) probs[i] = logits[i] / temperature;
+  oracle_softmax(probs, n, probs);
+  *token = oracle_sample_from_probabilities(probs, n, roll);
+  free(probs);
+  return 0;
+}

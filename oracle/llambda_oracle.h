@@ -35,6 +35,10 @@
  *                        row, identical keys return the mean value row
  *   llama step           float64 restatement of the layer from dequantised
  *                        weights (tests)
+ *   sampling             reference KATs tests.lisp:1258-1375 (penalty, top-k,
+ *                        top-p, draw, the default top-k of 40); top-k against
+ *                        a sort (the k-th largest value, ties kept); top-p
+ *                        against a float64 cumulative on a stable sort
  *   horizontal+ of the 8-lane accumulator: sb-simd's internal order is not
  *   published; this file sums lanes 0..7 left to right.  Parity unpinned for
  *   that order; it moves results by a few ulp, far inside the 1e-4 bound.
@@ -166,6 +170,16 @@ typedef struct oracle_llama_desc {
 /* llambda.lisp:6315-6441; kv: [layers][2][kv_heads][cap][head_dim] */
 int oracle_llama_step(const oracle_llama_desc* m, float* kv, int64_t cap, int64_t token,
                       int64_t position, float* logits, int threads);
+
+/* ---- sampling (llambda.lisp:1036-1317) ------------------------------ */
+int oracle_repetition_penalty(float* logits, int64_t n, const int64_t* history, int64_t nh,
+                              float penalty);                       /* 1036-1086 */
+int oracle_top_k(float* logits, int64_t n, int64_t k);              /* 1088-1150 */
+int oracle_top_p(float* logits, int64_t n, float p, float temperature); /* 1163-1240 */
+int64_t oracle_sample_from_probabilities(const float* probs, int64_t n, float roll); /* 1253-1270 */
+int oracle_sample_token(float* logits, int64_t n, const int64_t* history, int64_t nh,
+                        float penalty, int64_t top_k, float top_p, float temperature, float roll,
+                        int64_t* token);                            /* 1272-1317 */
 
 #ifdef __cplusplus
 }

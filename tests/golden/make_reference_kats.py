@@ -9,6 +9,7 @@ the reference's own tests for this path (tests.lisp), as data.
   forward-primitives silu(2) tests.lisp:298-344
   forward-primitives rms-norm, apply-rope tests.lisp:305-344
   softmax of (2 1 0)        tests.lisp:1359-1361
+  sampling-primitives       tests.lisp:1258-1375
 
 The reference cannot run here (no Common Lisp implementation), so the blocks
 are rebuilt from the byte assignments those tests make and the expected
@@ -84,6 +85,36 @@ def main():
                  "expect": ["cos 1", "sin 1", 5.0, 6.0], "tolerance": 1e-5},
         "softmax": {"cite": "tests.lisp:1359-1361", "x": [2.0, 1.0, 0.0],
                     "expect": "sums to 1 within 1e-5, strictly decreasing", "tolerance": 1e-5},
+        "sampling": {
+            "cite": "tests.lisp:1258-1375",
+            "tolerance": 1e-5,
+            "masked": -1.0e30,
+            "temperature": {"x": [2.0, 1.0, -2.0], "t": 0.5, "expect": [4.0, 2.0, -4.0]},
+            "repetition_penalty": {"x": [2.0, -3.0, 4.0, 1.0], "history": [2, 1, 2, 1],
+                                   "penalty": 1.25, "expect": [2.0, -3.75, 3.2, 1.0]},
+            "top_k": {"x": [0.5, 3.0, 2.0, 1.0, 2.0], "k": 2,
+                      "expect": [-1.0e30, 3.0, 2.0, -1.0e30, 2.0]},
+            "top_p": {"x": [3.0, 2.0, 1.0, -1.0e30], "p": 0.60, "t": 1.0,
+                      "expect": [3.0, -1.0e30, -1.0e30, -1.0e30]},
+            "probabilities": {"p": [0.7, 0.2, 0.1],
+                              "draws": [[0.1, 0], [0.75, 1], [0.95, 2]]},
+            # (logits, keyword arguments, random value, expected token)
+            "tokens": [
+                [[2.0, 1.95, 0.0], {"top_k": 0, "top_p": 1.0, "temperature": 1.0}, 0.45, 0],
+                [[2.0, 1.95, 0.0], {"history": [0], "repetition_penalty": 1.15, "top_k": 0,
+                                    "top_p": 1.0, "temperature": 1.0}, 0.45, 1],
+                [[3.0, 2.9, 0.1], {"top_k": 2, "top_p": 1.0, "temperature": 1.0}, 0.9, 1],
+                [[3.0, 2.0, 1.0], {"top_k": 0, "top_p": 0.60, "temperature": 1.0}, 0.95, 0],
+                [[3.0, 1.0, 0.0], {"top_p": 1.0, "temperature": 1.0}, 0.1, 0],
+                [[3.0, 1.0, 0.0], {"top_p": 1.0, "temperature": 1.0}, 0.9, 1],
+            ],
+            # pairs that must draw the same token: top-k nil = 40, top-p nil = 0.95
+            "same": [
+                [[float(v) for v in range(50, 0, -1)], {"top_k": None, "top_p": 1.0},
+                 {"top_k": 40, "top_p": 1.0}, 0.9],
+                [[3.0, 2.0, 1.0], {"top_k": 0, "top_p": None}, {"top_k": 0, "top_p": 0.95}, 0.9],
+            ],
+        },
     }
     with open(os.path.join(HERE, "reference_kats.json"), "w") as fh:
         json.dump(kats, fh, indent=1)

@@ -146,6 +146,31 @@ def test_llama_graph_replay_matches_eager(hip):
         sess.close()
 
 
+def test_llama_step_then_sample_on_device(hip):
+    """step_device into the session's logits, then the sampler reads them on
+    the device: the oracle's token for the same logits."""
+    from llambda_amd.sampling import HipSampler
+    c, _ = CONFIGS["g4d128"]
+    w = synthetic_llama(np.random.default_rng(14), c)
+    sess = HipLlamaSession(w)
+    sampler = HipSampler(c.vocab)
+    rng = np.random.default_rng(15)
+    history = []
+    try:
+        token = 1
+        for pos in range(6):
+            sess.step_device(token, pos, graph=True)
+            roll = float(np.float32(rng.random()))
+            kw = dict(history=history, top_k=40, top_p=0.9, temperature=0.8, random_value=roll)
+            got = sampler.sample_session(sess, **kw)
+            assert got == oracle.sample_token(sess.logits(), **kw), pos
+            history.append(got)
+            token = got
+    finally:
+        sampler.close()
+        sess.close()
+
+
 def test_llama_8b_layer_shapes_at_4096(hip):
     """Two layers of the Llama-3.1-8B layout (hidden 4096, 32 query / 8 kv
     heads of 128, SwiGLU 14336, Q4_K_M mix, Llama-3.1 rotation factors) with

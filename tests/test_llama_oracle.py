@@ -198,3 +198,64 @@ def test_llama_step_rejects_bad_token_and_position():
         oracle.llama_step(w, kv, TINY.vocab, 0)
     with pytest.raises(oracle.OracleError):
         oracle.llama_step(w, kv, 0, 16)
+
+
+# ------------------------------------------------------------------ sampling
+def test_reference_sampling_kats(kats):
+    k = kats["sampling"]
+    tol = k["tolerance"]
+    t = k["temperature"]
+    assert np.allclose(np.float32(t["x"]) / np.float32(t["t"]), t["expect"], atol=tol)
+    r = k["repetition_penalty"]
+    assert np.allclose(oracle.repetition_penalty(r["x"], r["history"], r["penalty"]), r["expect"],
+                       atol=tol)
+    r = k["top_k"]
+    assert np.allclose(oracle.top_k(r["x"], r["k"]), r["expect"], atol=tol)
+    r = k["top_p"]
+    assert np.allclose(oracle.top_p(r["x"], r["p"], r["t"]), r["expect"], atol=tol)
+    r = k["probabilities"]
+    for roll, want in r["draws"]:
+        assert oracle.sample_from_probabilities(r["p"], roll) == want
+    for logits, kw, roll, want in k["tokens"]:
+        assert oracle.sample_token(logits, random_value=roll, **kw) == want, (logits, kw)
+    for logits, kw1, kw2, roll in k["same"]:
+        assert oracle.sample_token(logits, random_value=roll, **kw1) == \
+            oracle.sample_token(logits, random_value=roll, **kw2)
+
+
+def test_top_k_is_the_kth_largest_with_ties():
+    rng = np.random.default_rng(21)
+    for trial in range(30):
+        n = int(rng.integers(2, 400))
+        x = rng.integers(-20, 20, size=n).astype(np.float32) * np.float32(0.5)  # many ties
+        k = int(rng.integers(1, n))
+        out = oracle.top_k(x, k)
+        cutoff = np.sort(x)[::-1][k - 1]
+        assert np.array_equal(out, np.where(x < cutoff, np.float32(-1e30), x))
+    x = np.arange(10, dtype=np.float32)
+    assert np.array_equal(oracle.top_k(x, 0), x) and np.array_equal(oracle.top_k(x, 10), x)
+
+
+def test_top_p_against_float64_cumulative():
+    rng = np.random.default_rng(22)
+    for trial in range(30):
+        n = int(rng.integers(2, 300))
+        x = (rng.normal(size=n) * 3).astype(np.float32)
+        x[rng.random(n) < 0.2] = np.float32(-1e30)
+        p = float(rng.uniform(0.05, 0.99))
+        T = float(rng.uniform(0.5, 2.0))
+        out = oracle.top_p(x, p, T)
+        act = np.flatnonzero(x > np.float32(-1e30))
+        if act.size <= 1:
+            assert np.array_equal(out, x)
+            continue
+        order = act[np.argsort(-x[act], kind="stable")]
+        v = x[order].astype(np.float64) / T
+        pr = np.exp(v - v[0])
+        pr /= pr.sum()
+        cum = np.cumsum(pr)
+        j = int(np.argmax(cum >= p)) if (cum >= p).any() else order.size - 1
+        # away from rounding ties the cutoff is the value at the first crossing
+        if abs(cum[j] - p) > 1e-5 and (j == 0 or abs(cum[j - 1] - p) > 1e-5):
+            cutoff = x[order[j]]
+            assert np.array_equal(out, np.where(x < cutoff, np.float32(-1e30), x)), trial

@@ -1,0 +1,109 @@
+"""Device sampling (llambda_hip_sampler_*) against the oracle's restatement of
+sample-token-id-from-logits (llambda.lisp:1272-1317): the token is identical
+for every case with top-k (the reference's serial sums over the survivors
+are reproduced in order); without top-k, wherever the random value is not
+within the rounding of the reference's serial cumulative sum (n * 2^-24)."""
+import numpy as np
+import pytest
+
+import oracle
+from llambda_amd.sampling import HipSampler, SamplingError
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def sampler(hip):
+    s = HipSampler(128256)
+    yield s
+    s.close()
+
+
+def test_reference_sampling_kats_on_device(sampler, kats):
+    k = kats["sampling"]
+    for logits, kw, roll, want in k["tokens"]:
+        kw = dict(kw)
+        if kw.get("top_k", 40) == 0 and kw.get("top_p", 0.95) < 1.0:
+            # top-p without top-k runs on the host only
+            with pytest.raises(SamplingError, match="top-p without top-k"):
+                sampler.sample(logits, random_value=roll, **kw)
+            continue
+        assert sampler.sample(logits, random_value=roll, **kw) == want, (logits, kw)
+    for logits, kw1, kw2, roll in k["same"]:
+        if (kw1.get("top_k") == 0) and (kw1.get("top_p") is None or kw1.get("top_p", 1.0) < 1):
+            continue
+        assert sampler.sample(logits, random_value=roll, **kw1) == \
+            sampler.sample(logits, random_value=roll, **kw2)
+
+
+def _head_like(rng, n):
+    # logits of an output head: N(0, 3) with a few large values
+    x = (rng.normal(size=n) * 3).astype(np.float32)
+    x[rng.integers(0, n, size=20)] += np.float32(8.0)
+    return x
+
+
+@pytest.mark.parametrize("top_k,top_p,temperature", [(40, 0.9, 1.0), (40, 1.0, 1.0),
+                                                     (1, 0.9, 1.0), (1000, 0.5, 0.7),
+                                                     (40, 0.95, 1.3), (7, 0.3, 2.0)])
+def test_full_vocab_matches_oracle(sampler, top_k, top_p, temperature):
+    rng = np.random.default_rng(top_k * 7 + int(top_p * 100))
+    n = 128256
+    for trial in range(6):
+        x = _head_like(rng, n)
+        hist = rng.integers(0, n, size=int(rng.integers(0, 30))).tolist()
+        hist += hist[:3]  # repeats
+        roll = float(np.float32(rng.random()))
+        kw = dict(history=hist, repetition_penalty=1.15, top_k=top_k, top_p=top_p,
+                  temperature=temperature, random_value=roll)
+        got = sampler.sample(x, **kw)
+        want = oracle.sample_token(x, **kw)
+        assert got == want, (trial, got, want)
+
+
+def test_ties_at_the_cutoff(sampler):
+    rng = np.random.default_rng(5)
+    n = 50000
+    x = rng.integers(-5, 6, size=n).astype(np.float32)  # thousands of ties
+    for k in (1, 3, 40):
+        for roll in (0.0, 0.3, 0.999):
+            x2 = x.copy()
+            x2[:500] = np.float32(9.0)  # 500 tied maxima: every one survives top-k
+            kw = dict(top_k=k, top_p=0.9, temperature=1.0, random_value=roll)
+            assert sampler.sample(x2, **kw) == oracle.sample_token(x2, **kw)
+    # more tied survivors than the device path holds
+    with pytest.raises(SamplingError, match="tie"):
+        sampler.sample(np.zeros(n, dtype=np.float32), top_k=5, top_p=0.9, random_value=0.5)
+
+
+def test_without_top_k(sampler):
+    rng = np.random.default_rng(6)
+    n = 128256
+    for trial in range(8):
+        x = _head_like(rng, n)
+        roll = float(np.float32(rng.random()))
+        got = sampler.sample(x, top_k=0, top_p=1.0, random_value=roll)
+        want = oracle.sample_token(x, top_k=0, top_p=1.0, random_value=roll)
+        if got != want:
+            # only where the roll is within the rounding of a cumulative sum:
+            # a serial fp32 sum over n terms is within n * 2^-24 of the exact one
+            p = np.exp(x.astype(np.float64) - x.max())
+            c = np.cumsum(p / p.sum())
+            tol = n * 2.0 ** -24
+            a, b = min(got, want), max(got, want)
+            # every cumulative between the two draws lies within the window
+            assert c[a] >= roll - tol and c[b - 1] <= roll + tol, (trial, got, want)
+
+
+def test_errors(sampler):
+    x = np.array([3.0, np.nan, 1.0], dtype=np.float32)
+    with pytest.raises(SamplingError, match="NaN"):
+        sampler.sample(x, top_k=2, top_p=1.0, random_value=0.5)
+    with pytest.raises(SamplingError, match="RANDOM-VALUE"):
+        sampler.sample([1.0, 2.0], random_value=1.0)
+    with pytest.raises(SamplingError, match="TOP-P"):
+        sampler.sample([1.0, 2.0], top_p=0.0, random_value=0.5)
+    with pytest.raises(SamplingError, match="out of bounds"):
+        sampler.sample([1.0, 2.0], history=[2], random_value=0.5)
+    with pytest.raises(SamplingError, match="PENALTY"):
+        sampler.sample([1.0, 2.0], history=[1], repetition_penalty=0.0, random_value=0.5)
