@@ -100,6 +100,48 @@ def bench_gemv(torch, timer, type_tag, rows, columns, steps, warmup, seed=1, cop
     return ms, nbytes
 
 
+def bench_head_sampling(torch, timer, rows, columns, steps, warmup):
+    """Output head then sample-token-id-from-logits on the device (top-k 40,
+    top-p 0.9, temperature 1, repetition penalty over a 64-token history,
+    random values from a seeded stream), one token per step, synchronous
+    (the token reaches the host each step)."""
+    from llambda_amd.sampling import HipSampler
+    rng = np.random.default_rng(3)
+    w = synthetic.packed(ggml.Q6_K, rng, rows, columns)
+    sess = make_hip_session_packed(w, ggml.Q6_K, rows, columns)
+    sampler = HipSampler(rows)
+    x = torch.randn(columns, device="cuda", dtype=torch.float32)
+    y = torch.empty(rows, device="cuda", dtype=torch.float32)
+    history = rng.integers(0, rows, size=64).tolist()
+    rolls = rng.random(steps + warmup).astype(np.float32)
+    state = {"i": 0}
+
+    def one(with_gemv):
+        if with_gemv:
+            sess.run_device(x.data_ptr(), y.data_ptr(), 1, timer.handle)
+            timer.stream.synchronize()
+        roll = float(rolls[state["i"] % len(rolls)])
+        state["i"] += 1
+        return sampler.sample(y.data_ptr(), device_count=rows, history=history, top_k=40,
+                              top_p=0.9, temperature=1.0, random_value=roll)
+
+    res = {}
+    for with_gemv in (True, False):
+        for _ in range(warmup):
+            one(with_gemv)
+        t0 = time.perf_counter()
+        for _ in range(steps):
+            one(with_gemv)
+        res[with_gemv] = (time.perf_counter() - t0) / steps * 1e6
+    sampler.close()
+    sess.close()
+    return {"workload": "Q6_K output head 128256x4096 + sampling (top-k 40, top-p 0.9, "
+                        "temperature 1, 64-token repetition history, seeded random values), "
+                        "token returned to the host every step",
+            "us_per_token": round(res[True], 1), "us_sampling": round(res[False], 1),
+            "tokens_per_s": round(1e6 / res[True], 1)}
+
+
 def cpu_gemv_baseline(type_tag, rows, columns, seconds):
     import oracle
     rng = np.random.default_rng(99)
@@ -261,6 +303,10 @@ def main():
                              f"CPU loop (8-lane fma accumulator, row partition over "
                              f"{CPU_THREADS} threads); not the Lisp reference itself"}
             log(f"CPU baseline: {cpu_gbs:.2f} GB/s over {n} runs")
+        samp = bench_head_sampling(torch, timer, rows, cols, max(20, steps // 4), min(warmup, 5))
+        workloads.append(samp)
+        log(f"Q6_K head + sampling: {samp['us_per_token']} us per token "
+            f"(sampling alone {samp['us_sampling']} us)")
         traffic = load_traffic("q6k_head")
         line = {
             "metric": METRIC, "value": round(gbs, 1), "unit": "GB/s", "n_gpus": 1,

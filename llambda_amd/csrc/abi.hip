@@ -10,6 +10,7 @@
 #include <sys/stat.h>
 #include <unistd.h>
 
+#include <algorithm>
 #include <climits>
 #include <cstdarg>
 #include <cstdio>
@@ -1113,7 +1114,13 @@ struct llambda_hip_sampler {
   int64_t vocab = 0;
   DevBuf work, logits, history, result;
   size_t history_cap = 0;
+  // pinned host staging of the history and the result (small synchronous
+  // copies without a pageable bounce)
+  int* host_history = nullptr;
+  int* host_result = nullptr;
   ~llambda_hip_sampler() {
+    if (host_history) (void)hipHostFree(host_history);
+    if (host_result) (void)hipHostFree(host_result);
     if (stream) (void)hipStreamDestroy(stream);
   }
 };
@@ -1160,16 +1167,25 @@ int64_t run_sampler(llambda_hip_sampler* s, const float* dev_logits, int64_t n,
     }
   }
   const bool topk = a->top_k > 0 && a->top_k < n;
+  if (topk && a->top_k > kSampleMaxSurvivors)
+    failf("sample: top-k %lld above %d is not supported on the device", (long long)a->top_k,
+          kSampleMaxSurvivors);
   if (!topk && a->top_p < 1.0f)
     failf("sample: top-p without top-k is not supported on the device (it needs a sort of the "
           "whole row)");
   if (distinct.size() > s->history_cap) {
-    s->history.alloc(distinct.size() * sizeof(int), "sampling history");
-    s->history_cap = distinct.size();
+    const size_t cap = std::max<size_t>(distinct.size(), 2 * s->history_cap);
+    s->history.alloc(cap * sizeof(int), "sampling history");
+    if (s->host_history) HIPC(hipHostFree(s->host_history));
+    s->host_history = nullptr;
+    HIPC(hipHostMalloc((void**)&s->host_history, cap * sizeof(int), hipHostMallocDefault));
+    s->history_cap = cap;
   }
-  if (!distinct.empty())
-    HIPC(hipMemcpyAsync(s->history.ptr, distinct.data(), distinct.size() * sizeof(int),
+  if (!distinct.empty()) {
+    std::copy(distinct.begin(), distinct.end(), s->host_history);
+    HIPC(hipMemcpyAsync(s->history.ptr, s->host_history, distinct.size() * sizeof(int),
                         hipMemcpyHostToDevice, s->stream));
+  }
   SampleParams p;
   p.n = (int)n;
   p.history = s->history.as<int>();
@@ -1180,8 +1196,8 @@ int64_t run_sampler(llambda_hip_sampler* s, const float* dev_logits, int64_t n,
   p.temperature = a->temperature;
   p.roll = a->random_value;
   HIPC(sample_launch(dev_logits, s->work.as<float>(), p, s->result.as<int>(), s->stream));
-  int res[2] = {0, 0};
-  HIPC(hipMemcpyAsync(res, s->result.ptr, sizeof res, hipMemcpyDeviceToHost, s->stream));
+  int* res = s->host_result;
+  HIPC(hipMemcpyAsync(res, s->result.ptr, 2 * sizeof(int), hipMemcpyDeviceToHost, s->stream));
   HIPC(hipStreamSynchronize(s->stream));
   if (res[1] == kSampleErrNaN) failf("sample: NaN logit");
   if (res[1] == kSampleErrTies)
@@ -1198,7 +1214,8 @@ int llambda_hip_sampler_create(size_t vocab, llambda_hip_sampler** result) {
   return guarded([&] {
     if (!result) failf("sampler: null result pointer");
     *result = nullptr;
-    if (vocab == 0 || vocab > (size_t)INT_MAX) failf("sampler: vocab %zu out of range", vocab);
+    if (vocab == 0 || vocab > (size_t)kSampleMaxVocab)
+      failf("sampler: vocab %zu out of range (1..%d)", vocab, kSampleMaxVocab);
     std::unique_ptr<llambda_hip_sampler> s(new llambda_hip_sampler());
     s->device = current_device_checked();
     s->vocab = (int64_t)vocab;
@@ -1206,6 +1223,7 @@ int llambda_hip_sampler_create(size_t vocab, llambda_hip_sampler** result) {
     s->work.alloc(vocab * sizeof(float), "sampling row");
     s->logits.alloc(vocab * sizeof(float), "sampling input");
     s->result.alloc(2 * sizeof(int), "sampling result");
+    HIPC(hipHostMalloc((void**)&s->host_result, 2 * sizeof(int), hipHostMallocDefault));
     *result = s.release();
   });
 }
@@ -1222,6 +1240,8 @@ int llambda_hip_sampler_sample(llambda_hip_sampler* s, const float* logits, size
     if (count == 0 || count > (size_t)s->vocab)
       failf("sample: %zu logits do not fit the sampler (vocab %lld)", count, (long long)s->vocab);
     const float* dev = logits;
+    if (logits_on_device && (reinterpret_cast<uintptr_t>(logits) & 15u))
+      failf("sample: device logits must be 16-byte aligned");
     if (!logits_on_device) {
       HIPC(hipMemcpyAsync(s->logits.ptr, logits, count * sizeof(float), hipMemcpyHostToDevice,
                           s->stream));

@@ -8,6 +8,8 @@ namespace llhip {
 
 // Survivors of top-k (ties included) the exact path holds in LDS.
 constexpr int kSampleMaxSurvivors = 4096;
+// Longest logits row (the history bitmap lives in LDS).
+constexpr int kSampleMaxVocab = 262144;
 
 enum SampleError : int {
   kSampleErrNaN = 1,   // a NaN logit
@@ -19,14 +21,15 @@ struct SampleParams {
   const int* history;  // device, distinct token ids < n (host-validated)
   int nh;
   float penalty;       // repetition penalty (> 0)
-  int top_k;           // 0 or >= n: no top-k (top_p must then be 1)
+  int top_k;           // 0 or >= n: no top-k (top_p must then be 1); at most
+                       // kSampleMaxSurvivors
   float top_p;         // (0, 1]
   float temperature;   // > 0
   float roll;          // random value in [0, 1)
 };
 
 // result[0] = token (-1 on error), result[1] = SampleError or 0.  work: [n]
-// floats of scratch.  One workgroup.
+// floats of scratch.  logits and work 16-byte aligned.  One workgroup.
 hipError_t sample_launch(const float* logits, float* work, const SampleParams& p, int* result,
                          hipStream_t stream);
 

@@ -2,13 +2,16 @@
 // device, for an output head's logits (sample.h).
 //
 // One workgroup of 1024 threads:
-//   1 copy the logits to the scratch row (NaN rejected), repetition penalty
-//     on the distinct history tokens (apply-repetition-penalty, 1036-1086)
+//   1 copy the logits to the scratch row with the repetition penalty applied
+//     to the distinct history tokens (apply-repetition-penalty, 1036-1086;
+//     the tokens marked in an LDS bitmap), NaN rejected
 //   2 top-k (apply-top-k-with-workspace, 1088-1150): the reference keeps every
 //     logit >= the root of a min-heap of the k largest, i.e. the k-th largest
-//     value; here that value by a 4-pass radix select (8 bits per pass) over
-//     order-preserving keys of the floats
-//   3 the survivors (logit >= cutoff) compacted in index order
+//     value; here: a threshold T0 (the k-th largest of the 1024 threads'
+//     maxima, so at least k logits are >= T0), the logits >= T0 compacted
+//     into LDS, and the k-th largest of those by a 4-pass radix select
+//     (8 bits per pass) over order-preserving keys of the floats
+//   3 the survivors (logit >= cutoff) ordered by index
 //   4 top-p (apply-top-p-with-workspace, 1163-1240) on the survivors: a
 //     stable descending order by rank, then the reference's serial
 //     single-precision sums in that order
@@ -27,6 +30,7 @@
 namespace llhip {
 
 constexpr int kSampleThreads = 1024;
+constexpr int kSampleBitmapWords = kSampleMaxVocab / 32;
 constexpr float kMaskedLogit = -1.0e30f;  // llambda.lisp:1098, 1172
 
 // Order-preserving key of a float (larger float -> larger key; -0 < +0).
@@ -37,31 +41,6 @@ __device__ __forceinline__ uint32_t float_key(float f) {
 __device__ __forceinline__ float key_float(uint32_t k) {
   const uint32_t u = (k & 0x80000000u) ? (k & 0x7FFFFFFFu) : ~k;
   return __builtin_bit_cast(float, u);
-}
-
-// Inclusive prefix sum over the block (int); red: kSampleThreads / 64 ints.
-__device__ int block_scan(int v, int* red, int* total) {
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  for (int o = 1; o < 64; o <<= 1) {
-    const int t = __shfl_up(v, o, 64);
-    if (lane >= o) v += t;
-  }
-  if (lane == 63) red[wave] = v;
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    int acc = 0;
-    for (int w = 0; w < kSampleThreads / 64; ++w) {
-      const int t = red[w];
-      red[w] = acc;
-      acc += t;
-    }
-    red[kSampleThreads / 64] = acc;
-  }
-  __syncthreads();
-  const int out = v + red[wave];
-  *total = red[kSampleThreads / 64];
-  __syncthreads();
-  return out;
 }
 
 // Sum over the block in a fixed order (waves' sums added in wave order).
@@ -99,29 +78,142 @@ __device__ float block_exclusive_scan(float v, float* red) {
   return out;
 }
 
+// The key of the k-th largest of vals[0..m) (generic pointer: LDS or global),
+// by a 4-pass radix select over order-preserving keys; every thread calls.
+// hist: 256 ints of LDS, sel: 3 words of LDS.  The bins of each pass are
+// scanned from the top by wavefront 0 (four bins per lane, a lane prefix sum
+// and a ballot).
+__device__ uint32_t radix_select(const float* vals, int m, int k, int* hist, uint32_t* sel) {
+  const int tid = threadIdx.x;
+  if (tid == 0) {
+    sel[0] = 0u;
+    sel[1] = 0u;
+    sel[2] = (uint32_t)k;
+  }
+  for (int pass = 0; pass < 4; ++pass) {
+    const int shift = 24 - 8 * pass;
+    for (int b = tid; b < 256; b += kSampleThreads) hist[b] = 0;
+    __syncthreads();
+    const uint32_t prefix = sel[0], mask = sel[1];
+    for (int i = tid; i < m; i += kSampleThreads) {
+      const uint32_t key = float_key(vals[i]);
+      if ((key & mask) == prefix) atomicAdd(&hist[(key >> shift) & 255u], 1);
+    }
+    __syncthreads();
+    if (tid < 64) {
+      const int lane = tid;
+      const uint32_t r = sel[2];
+      uint32_t c[4], sum = 0;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        c[j] = (uint32_t)hist[255 - 4 * lane - j];
+        sum += c[j];
+      }
+      uint32_t inc = sum;
+      for (int o = 1; o < 64; o <<= 1) {
+        const uint32_t t = __shfl_up(inc, o, 64);
+        if (lane >= o) inc += t;
+      }
+      const unsigned long long hit = __ballot(inc >= r);
+      const int first = hit ? __ffsll(hit) - 1 : 63;
+      if (lane == first) {
+        uint32_t acc = inc - sum;
+        int bin = 255 - 4 * lane - 3;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          if (acc + c[j] >= r) {
+            bin = 255 - 4 * lane - j;
+            break;
+          }
+          acc += c[j];
+        }
+        sel[0] = prefix | ((uint32_t)bin << shift);
+        sel[1] = mask | (255u << shift);
+        sel[2] = r - acc;
+      }
+    }
+    __syncthreads();
+  }
+  return sel[0];
+}
+
 __global__ void __launch_bounds__(kSampleThreads)
 sample_kernel(const float* __restrict__ logits, float* __restrict__ work, SampleParams p,
               int* __restrict__ result) {
 #pragma clang fp contract(off)
   __shared__ int hist[256];
   __shared__ int red[kSampleThreads / 64 + 1];
-  __shared__ uint32_t sel[3];  // prefix, mask, remaining rank
-  __shared__ int flag;
+  __shared__ float fred[kSampleThreads / 64 + 1];
+  __shared__ uint32_t sel[3];
+  __shared__ int flag, ncand;
+  __shared__ float s_tmax[kSampleThreads];
+  __shared__ uint32_t bitmap[kSampleBitmapWords];
+  __shared__ int c_idx[kSampleMaxSurvivors];
+  __shared__ float c_val[kSampleMaxSurvivors];
   __shared__ int s_idx[kSampleMaxSurvivors];
   __shared__ float s_val[kSampleMaxSurvivors];
   __shared__ float s_e[kSampleMaxSurvivors];
   __shared__ int s_order[kSampleMaxSurvivors];
-  __shared__ float fred[kSampleThreads / 64 + 1];
   const int n = p.n, tid = threadIdx.x;
 
-  // 1. copy, NaN check, penalty
-  if (tid == 0) flag = 0;
-  __syncthreads();
-  for (int i = tid; i < n; i += kSampleThreads) {
-    const float v = logits[i];
-    if (v != v) flag = 1;
-    work[i] = v;
+  // 1. copy with the repetition penalty applied (history tokens marked in an
+  // LDS bitmap), NaN rejected; each thread's maximum over its float4s
+  if (tid == 0) {
+    flag = 0;
+    ncand = 0;
   }
+  for (int w = tid; w < kSampleBitmapWords; w += kSampleThreads) bitmap[w] = 0u;
+  __syncthreads();
+  for (int i = tid; i < p.nh; i += kSampleThreads) {
+    const int t = p.history[i];
+    atomicOr(&bitmap[t >> 5], 1u << (t & 31));
+  }
+  __syncthreads();
+  auto penalized = [&](int i, float v) {
+    if (bitmap[i >> 5] & (1u << (i & 31))) {
+      if (v > 0.0f) return v / p.penalty;
+      if (v < 0.0f) return v * p.penalty;
+    }
+    return v;
+  };
+  float tmax = -INFINITY;
+  int nan = 0;
+  {
+    const int n4 = n >> 2;
+    const float4* src = reinterpret_cast<const float4*>(logits);
+    float4* dst = reinterpret_cast<float4*>(work);
+    constexpr int U = 4;
+    for (int base = tid; base < n4; base += U * kSampleThreads) {
+      float4 a[U];
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int j = base + u * kSampleThreads;
+        a[u] = j < n4 ? src[j] : make_float4(0.f, 0.f, 0.f, 0.f);
+      }
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int j = base + u * kSampleThreads;
+        if (j < n4) {
+          float4 v = a[u];
+          v.x = penalized(4 * j, v.x);
+          v.y = penalized(4 * j + 1, v.y);
+          v.z = penalized(4 * j + 2, v.z);
+          v.w = penalized(4 * j + 3, v.w);
+          nan |= (v.x != v.x) | (v.y != v.y) | (v.z != v.z) | (v.w != v.w);
+          tmax = fmaxf(fmaxf(tmax, fmaxf(v.x, v.y)), fmaxf(v.z, v.w));
+          dst[j] = v;
+        }
+      }
+    }
+    for (int i = 4 * n4 + tid; i < n; i += kSampleThreads) {
+      const float v = penalized(i, logits[i]);
+      nan |= v != v;
+      tmax = fmaxf(tmax, v);
+      work[i] = v;
+    }
+  }
+  if (nan) flag = 1;
+  s_tmax[tid] = tmax;
   __syncthreads();
   if (flag) {
     if (tid == 0) {
@@ -130,58 +222,14 @@ sample_kernel(const float* __restrict__ logits, float* __restrict__ work, Sample
     }
     return;
   }
-  for (int i = tid; i < p.nh; i += kSampleThreads) {
-    const int t = p.history[i];
-    const float l = work[t];
-    if (l > 0.0f) work[t] = l / p.penalty;
-    else if (l < 0.0f) work[t] = l * p.penalty;
-  }
-  __syncthreads();
 
-  // 2. top-k cutoff: the k-th largest key
   const bool topk = p.top_k > 0 && p.top_k < n;
-  float cutoff = -INFINITY;
-  if (topk) {
-    if (tid == 0) {
-      sel[0] = 0u;
-      sel[1] = 0u;
-      sel[2] = (uint32_t)p.top_k;
-    }
-    for (int pass = 0; pass < 4; ++pass) {
-      const int shift = 24 - 8 * pass;
-      for (int b = tid; b < 256; b += kSampleThreads) hist[b] = 0;
-      __syncthreads();
-      const uint32_t prefix = sel[0], mask = sel[1];
-      for (int i = tid; i < n; i += kSampleThreads) {
-        const uint32_t key = float_key(work[i]);
-        if ((key & mask) == prefix) atomicAdd(&hist[(key >> shift) & 255u], 1);
-      }
-      __syncthreads();
-      if (tid == 0) {
-        uint32_t r = sel[2], acc = 0;
-        int b = 255;
-        for (; b > 0; --b) {
-          if (acc + (uint32_t)hist[b] >= r) break;
-          acc += (uint32_t)hist[b];
-        }
-        sel[0] = prefix | ((uint32_t)b << shift);
-        sel[1] = mask | (255u << shift);
-        sel[2] = r - acc;
-      }
-      __syncthreads();
-    }
-    cutoff = key_float(sel[0]);
-  }
-
-  // 3. survivors in index order: thread t owns [t * per, (t + 1) * per)
-  const int per = (n + kSampleThreads - 1) / kSampleThreads;
-  const int lo = min(n, tid * per), hi = min(n, lo + per);
-  int count = 0;
-  for (int i = lo; i < hi; ++i) count += !(work[i] < cutoff);
-  int total = 0;
-  const int end = block_scan(count, red, &total);
   if (!topk) {
-    // every logit survives: the tree path (top-p must be 1)
+    // every logit survives: the tree path (top-p must be 1); thread t owns
+    // the contiguous range [t * per, (t + 1) * per) so that its prefix sums
+    // follow index order
+    const int per = (n + kSampleThreads - 1) / kSampleThreads;
+    const int lo = min(n, tid * per), hi = min(n, lo + per);
     float m = -INFINITY;
     for (int i = lo; i < hi; ++i) m = fmaxf(m, work[i] / p.temperature);
     for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
@@ -212,23 +260,79 @@ sample_kernel(const float* __restrict__ logits, float* __restrict__ work, Sample
     }
     return;
   }
-  if (total > kSampleMaxSurvivors) {
+
+  // 2. top-k cutoff.  T0 = the k-th largest of the per-thread maxima: at
+  // least k logits are >= T0, so the k-th largest logit is >= T0 and lies
+  // among the candidates (logits >= T0), which are compacted into LDS.
+  // (k above the thread count: the k-th largest of the whole row itself)
+  float t0 = key_float(p.top_k <= kSampleThreads
+                           ? radix_select(s_tmax, kSampleThreads, p.top_k, hist, sel)
+                           : radix_select(work, n, p.top_k, hist, sel));
+  auto candidate = [&](int i, float v) {
+    if (!(v < t0)) {
+      const int slot = atomicAdd(&ncand, 1);
+      if (slot < kSampleMaxSurvivors) {
+        c_val[slot] = v;
+        c_idx[slot] = i;
+      }
+    }
+  };
+  for (int attempt = 0; attempt < 2; ++attempt) {
+    const int n4 = n >> 2;
+    const float4* w4 = reinterpret_cast<const float4*>(work);
+    constexpr int U = 4;
+    for (int base = tid; base < n4; base += U * kSampleThreads) {
+      float4 a[U];
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int j = base + u * kSampleThreads;
+        a[u] = j < n4 ? w4[j] : make_float4(0.f, 0.f, 0.f, 0.f);
+      }
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int j = base + u * kSampleThreads;
+        if (j < n4) {
+          candidate(4 * j, a[u].x);
+          candidate(4 * j + 1, a[u].y);
+          candidate(4 * j + 2, a[u].z);
+          candidate(4 * j + 3, a[u].w);
+        }
+      }
+    }
+    for (int i = 4 * n4 + tid; i < n; i += kSampleThreads) candidate(i, work[i]);
+    __syncthreads();
+    if (ncand <= kSampleMaxSurvivors || attempt == 1) break;
+    // too many candidates above the threshold: the k-th largest of the whole
+    // row is the threshold instead (only ties at it can then overflow)
+    t0 = key_float(radix_select(work, n, p.top_k, hist, sel));
+    __syncthreads();
+    if (tid == 0) ncand = 0;
+    __syncthreads();
+  }
+  const int cand = ncand;
+  if (cand > kSampleMaxSurvivors) {
     if (tid == 0) {
       result[0] = -1;
       result[1] = kSampleErrTies;
     }
     return;
   }
-  {
-    int o = end - count;
-    for (int i = lo; i < hi; ++i)
-      if (!(work[i] < cutoff)) {
-        s_idx[o] = i;
-        s_val[o] = work[i];
-        ++o;
-      }
+  const float cutoff = key_float(radix_select(c_val, cand, p.top_k, hist, sel));
+
+  // 3. survivors (candidates >= cutoff) in index order
+  if (tid == 0) flag = 0;
+  __syncthreads();
+  for (int c = tid; c < cand; c += kSampleThreads) {
+    if (c_val[c] < cutoff) continue;
+    const int idx = c_idx[c];
+    int pos = 0;
+    for (int d = 0; d < cand; ++d) pos += !(c_val[d] < cutoff) && c_idx[d] < idx;
+    s_idx[pos] = idx;
+    s_val[pos] = c_val[c];
+    atomicAdd(&flag, 1);
   }
   __syncthreads();
+  const int total = flag;
 
   // 4. top-p over the survivors above the mask value
   if (p.top_p < 1.0f) {

@@ -45,7 +45,9 @@ def _head_like(rng, n):
 
 @pytest.mark.parametrize("top_k,top_p,temperature", [(40, 0.9, 1.0), (40, 1.0, 1.0),
                                                      (1, 0.9, 1.0), (1000, 0.5, 0.7),
-                                                     (40, 0.95, 1.3), (7, 0.3, 2.0)])
+                                                     (40, 0.95, 1.3), (7, 0.3, 2.0),
+                                                     (1024, 0.9, 1.0), (1500, 0.8, 1.0),
+                                                     (4096, 0.99, 1.0)])
 def test_full_vocab_matches_oracle(sampler, top_k, top_p, temperature):
     rng = np.random.default_rng(top_k * 7 + int(top_p * 100))
     n = 128256
