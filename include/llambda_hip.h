@@ -35,6 +35,7 @@ typedef struct llambda_hip_session llambda_hip_session;
 typedef struct llambda_hip_moe_session llambda_hip_moe_session;
 typedef struct llambda_hip_llama_session llambda_hip_llama_session;
 typedef struct llambda_hip_sampler llambda_hip_sampler;
+typedef struct llambda_hip_gguf llambda_hip_gguf;
 
 /* ---- probe, versions, errors -------------------------------------- */
 
@@ -323,6 +324,71 @@ int llambda_hip_sampler_sample(llambda_hip_sampler* sampler, const float* logits
 int llambda_hip_llama_session_sample(llambda_hip_llama_session* session,
                                      llambda_hip_sampler* sampler,
                                      const llambda_hip_sampling* params, int64_t* token);
+
+/* ---- GGUF files ------------------------------------------------------------ */
+
+/* One tensor info of read-gguf-tensor-infos (llambda.lisp:2147-2238).  name
+ * and data point into the mapping (valid until close; name is not
+ * NUL-terminated). */
+typedef struct llambda_hip_gguf_tensor {
+  const char* name;
+  size_t name_length;
+  uint32_t dimension_count;    /* 1..4 */
+  uint64_t dimensions[4];      /* GGUF order: dimensions[0] = columns */
+  uint32_t type;               /* GGML type tag */
+  uint64_t offset;             /* relative to the tensor data start */
+  uint64_t element_count;
+  int supported;               /* supported-ggml-type-p */
+  uint64_t byte_size;          /* 0 when unsupported */
+  uint64_t data_offset;        /* absolute file offset */
+  const void* data;            /* mapping + data_offset */
+} llambda_hip_gguf_tensor;
+
+/* One metadata value (read-gguf-value, llambda.lisp:1985-2045): the key
+ * (metadata entries only), the GGUF value type (0 u8, 1 i8, 2 u16, 3 i16,
+ * 4 u32, 5 i32, 6 f32, 7 bool, 8 string, 9 array, 10 u64, 11 i64, 12 f64),
+ * integers in u / i, floats in f, booleans as u = 0 / 1, strings as bytes
+ * in the mapping (not NUL-terminated), arrays as element_type and count. */
+typedef struct llambda_hip_gguf_value {
+  const char* key;
+  size_t key_length;
+  uint32_t type;
+  uint32_t element_type;
+  uint64_t count;
+  uint64_t u;
+  int64_t i;
+  double f;
+  const char* string;
+  size_t string_length;
+} llambda_hip_gguf_value;
+
+/* Open and map a GGUF file read-only and parse its header, metadata and
+ * tensor infos with every read bounded by the file length; errors carry the
+ * reference's texts ("... exceeds mapped file length ...", "Invalid GGUF
+ * magic", "... invalid dimension count ...").  Replaces call-with-file and
+ * with-mapped-file (llambda.lisp:489-675, Win32) with open/fstat/mmap. */
+int llambda_hip_gguf_open(const char* path, llambda_hip_gguf** result);
+void llambda_hip_gguf_close(llambda_hip_gguf* file);
+
+/* read-gguf-header (llambda.lisp:2047-2059) plus the alignment
+ * (general.alignment, default 32) and the tensor data start. */
+int llambda_hip_gguf_header(const llambda_hip_gguf* file, uint32_t* version,
+                            uint64_t* tensor_count, uint64_t* kv_count, uint64_t* alignment,
+                            uint64_t* data_start);
+
+/* The mapping (size in *size); tensor data for zero-copy uploads. */
+const void* llambda_hip_gguf_mapping(const llambda_hip_gguf* file, size_t* size);
+
+int llambda_hip_gguf_tensor_info(const llambda_hip_gguf* file, uint64_t index,
+                                 llambda_hip_gguf_tensor* out);
+/* Index of the first tensor named `name`, -1 when absent (find-gguf-tensor-info). */
+int64_t llambda_hip_gguf_find_tensor(const llambda_hip_gguf* file, const char* name);
+
+/* Metadata entry `index` in file order; array elements by
+ * llambda_hip_gguf_kv_element. */
+int llambda_hip_gguf_kv(const llambda_hip_gguf* file, uint64_t index, llambda_hip_gguf_value* out);
+int llambda_hip_gguf_kv_element(const llambda_hip_gguf* file, uint64_t index, uint64_t element,
+                                llambda_hip_gguf_value* out);
 
 #ifdef __cplusplus
 }

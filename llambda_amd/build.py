@@ -31,7 +31,7 @@ HIP_FLAGS = [
 CXX_FLAGS = ["-O2", "-std=c++17", "-fPIC", "-Wall"]
 
 HIP_SOURCES = ["gemv.hip", "gemv_mfma.hip", "moe.hip", "moe_mfma.hip", "decoder.hip", "sample.hip", "abi.hip"]
-CXX_SOURCES = ["sha256.cpp"]
+CXX_SOURCES = ["sha256.cpp", "gguf.cpp"]
 
 
 def _run(cmd):

@@ -24,6 +24,7 @@
 
 #include "decoder.h"
 #include "gemv.h"
+#include "gguf.h"
 #include "moe.h"
 #include "sample.h"
 #include "sha256.h"
@@ -1261,6 +1262,112 @@ int llambda_hip_llama_session_sample(llambda_hip_llama_session* session,
     // the session's stream holds the step that wrote the logits
     HIPC(hipStreamSynchronize(session->stream));
     *token = run_sampler(s, session->logits.as<float>(), session->plan.vocab, params);
+  });
+}
+
+}  // extern "C"
+
+// -------------------------------------------------------------------- GGUF
+
+struct llambda_hip_gguf {
+  std::unique_ptr<GgufFile> file;
+};
+
+static void fill_value(const GgufValue& v, llambda_hip_gguf_value* out) {
+  out->type = v.type;
+  out->element_type = v.elem_type;
+  out->count = v.type == 9 ? v.items.size() : 0;
+  out->u = v.u;
+  out->i = v.i;
+  out->f = v.f;
+  out->string = v.str;
+  out->string_length = v.str_len;
+}
+
+extern "C" {
+
+int llambda_hip_gguf_open(const char* path, llambda_hip_gguf** result) {
+  return guarded([&] {
+    if (!result) failf("gguf: null result pointer");
+    *result = nullptr;
+    std::unique_ptr<llambda_hip_gguf> g(new llambda_hip_gguf());
+    g->file.reset(gguf_open(path));
+    *result = g.release();
+  });
+}
+
+void llambda_hip_gguf_close(llambda_hip_gguf* file) { delete file; }
+
+int llambda_hip_gguf_header(const llambda_hip_gguf* g, uint32_t* version, uint64_t* tensor_count,
+                            uint64_t* kv_count, uint64_t* alignment, uint64_t* data_start) {
+  return guarded([&] {
+    if (!g) failf("gguf: null file");
+    if (version) *version = g->file->version;
+    if (tensor_count) *tensor_count = g->file->tensor_count;
+    if (kv_count) *kv_count = g->file->kv_count;
+    if (alignment) *alignment = g->file->alignment;
+    if (data_start) *data_start = g->file->data_start;
+  });
+}
+
+const void* llambda_hip_gguf_mapping(const llambda_hip_gguf* g, size_t* size) {
+  if (!g) return nullptr;
+  if (size) *size = (size_t)g->file->size;
+  return g->file->base;
+}
+
+int llambda_hip_gguf_tensor_info(const llambda_hip_gguf* g, uint64_t index,
+                                 llambda_hip_gguf_tensor* out) {
+  return guarded([&] {
+    if (!g || !out) failf("gguf: null argument");
+    if (index >= g->file->tensors.size()) failf("gguf: tensor index %llu out of range", (unsigned long long)index);
+    const GgufTensor& t = g->file->tensors[index];
+    out->name = t.name;
+    out->name_length = (size_t)t.name_len;
+    out->dimension_count = t.dimension_count;
+    for (int d = 0; d < 4; ++d) out->dimensions[d] = t.dimensions[d];
+    out->type = t.type;
+    out->offset = t.offset;
+    out->element_count = t.element_count;
+    out->supported = t.supported;
+    out->byte_size = t.byte_size;
+    out->data_offset = t.data_offset;
+    out->data = g->file->base + t.data_offset;
+  });
+}
+
+int64_t llambda_hip_gguf_find_tensor(const llambda_hip_gguf* g, const char* name) {
+  if (!g || !name) return -1;
+  const size_t n = strlen(name);
+  for (size_t i = 0; i < g->file->tensors.size(); ++i) {
+    const GgufTensor& t = g->file->tensors[i];
+    if (t.name_len == n && memcmp(t.name, name, n) == 0) return (int64_t)i;
+  }
+  return -1;
+}
+
+int llambda_hip_gguf_kv(const llambda_hip_gguf* g, uint64_t index, llambda_hip_gguf_value* out) {
+  return guarded([&] {
+    if (!g || !out) failf("gguf: null argument");
+    if (index >= g->file->kv.size()) failf("gguf: metadata index %llu out of range", (unsigned long long)index);
+    const GgufKv& kv = g->file->kv[index];
+    fill_value(kv.value, out);
+    out->key = kv.key;
+    out->key_length = (size_t)kv.key_len;
+  });
+}
+
+int llambda_hip_gguf_kv_element(const llambda_hip_gguf* g, uint64_t index, uint64_t element,
+                                llambda_hip_gguf_value* out) {
+  return guarded([&] {
+    if (!g || !out) failf("gguf: null argument");
+    if (index >= g->file->kv.size()) failf("gguf: metadata index %llu out of range", (unsigned long long)index);
+    const GgufValue& v = g->file->kv[index].value;
+    if (v.type != 9 || element >= v.items.size())
+      failf("gguf: metadata %llu has no element %llu", (unsigned long long)index, (unsigned long long)element);
+    fill_value(v.items[element], out);
+    out->key = nullptr;
+    out->key_length = 0;
   });
 }
 

@@ -87,6 +87,23 @@ class Sampling(ctypes.Structure):
                 ("random_value", ctypes.c_float)]
 
 
+class GgufTensor(ctypes.Structure):
+    """llambda_hip_gguf_tensor."""
+    _fields_ = [("name", c_void_p), ("name_length", c_size), ("dimension_count", ctypes.c_uint32),
+                ("dimensions", ctypes.c_uint64 * 4), ("type", ctypes.c_uint32),
+                ("offset", ctypes.c_uint64), ("element_count", ctypes.c_uint64),
+                ("supported", c_int), ("byte_size", ctypes.c_uint64),
+                ("data_offset", ctypes.c_uint64), ("data", c_void_p)]
+
+
+class GgufValue(ctypes.Structure):
+    """llambda_hip_gguf_value."""
+    _fields_ = [("key", c_void_p), ("key_length", c_size), ("type", ctypes.c_uint32),
+                ("element_type", ctypes.c_uint32), ("count", ctypes.c_uint64),
+                ("u", ctypes.c_uint64), ("i", ctypes.c_int64), ("f", ctypes.c_double),
+                ("string", c_void_p), ("string_length", c_size)]
+
+
 # name -> (restype, argtypes); the complete export list of include/llambda_hip.h
 SIGNATURES = {
     "llambda_hip_probe": (c_int, []),
@@ -131,6 +148,20 @@ SIGNATURES = {
                                            ctypes.POINTER(Sampling), ctypes.POINTER(c_i64)]),
     "llambda_hip_llama_session_sample": (c_int, [c_void_p, c_void_p, ctypes.POINTER(Sampling),
                                                  ctypes.POINTER(c_i64)]),
+    "llambda_hip_gguf_open": (c_int, [c_char_p, ctypes.POINTER(c_void_p)]),
+    "llambda_hip_gguf_close": (None, [c_void_p]),
+    "llambda_hip_gguf_header": (c_int, [c_void_p, ctypes.POINTER(ctypes.c_uint32),
+                                        ctypes.POINTER(ctypes.c_uint64),
+                                        ctypes.POINTER(ctypes.c_uint64),
+                                        ctypes.POINTER(ctypes.c_uint64),
+                                        ctypes.POINTER(ctypes.c_uint64)]),
+    "llambda_hip_gguf_mapping": (c_void_p, [c_void_p, ctypes.POINTER(c_size)]),
+    "llambda_hip_gguf_tensor_info": (c_int, [c_void_p, ctypes.c_uint64,
+                                             ctypes.POINTER(GgufTensor)]),
+    "llambda_hip_gguf_find_tensor": (c_i64, [c_void_p, c_char_p]),
+    "llambda_hip_gguf_kv": (c_int, [c_void_p, ctypes.c_uint64, ctypes.POINTER(GgufValue)]),
+    "llambda_hip_gguf_kv_element": (c_int, [c_void_p, ctypes.c_uint64, ctypes.c_uint64,
+                                            ctypes.POINTER(GgufValue)]),
 }
 
 

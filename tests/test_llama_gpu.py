@@ -171,6 +171,26 @@ def test_llama_step_then_sample_on_device(hip):
         sess.close()
 
 
+def test_llama_from_gguf_file(hip, tmp_path):
+    """A model written to a GGUF file, mapped, parsed and uploaded straight
+    from the mapping (the file is closed before the steps run)."""
+    from llambda_amd.gguf import GgufFile, load_llama, save_llama
+    c, _ = CONFIGS["g4d128"]
+    w = synthetic_llama(np.random.default_rng(16), c)
+    path = str(tmp_path / "model.gguf")
+    save_llama(path, w)
+    with GgufFile(path) as f:
+        sess = HipLlamaSession(load_llama(f, context=c.context))
+    kv = _kv(c)
+    try:
+        for pos, token in enumerate([2, 7, 11]):
+            got = sess.step(token, pos)
+            ref = oracle.llama_step(w, kv, token, pos, threads=8)
+            _check_logits(got, ref, f"gguf pos {pos}")
+    finally:
+        sess.close()
+
+
 def test_llama_8b_layer_shapes_at_4096(hip):
     """Two layers of the Llama-3.1-8B layout (hidden 4096, 32 query / 8 kv
     heads of 128, SwiGLU 14336, Q4_K_M mix, Llama-3.1 rotation factors) with
