@@ -407,12 +407,9 @@ constexpr size_t mfma_lds_bytes(int nblk, int nbuf) {
 // every row's chunk starts on a dword.  D: depth of the ring of stages per
 // wave; nbuf = min(D, steps of any wave) stages are allocated, step s uses
 // stage s % nbuf, all of them are filled before the activation table is
-// built, and each is refilled as soon as it has been read.  S: waves
-// per 16-row tile.  S = 1: every wave walks whole tiles of its own (a
-// persistent grid).  S > 1: the workgroup owns kMfmaWaves / S tiles, one per
-// group of S waves; wave k of a group takes chunks k, k + S, ... of the tile
-// (row counts too small to give every wave its own tiles); the group's
-// partial sums meet in LDS and are added in wave order.
+// built, and each is refilled as soon as it has been read.  S: waves per
+// 16-row tile (rows are taken in rounds; see the step mapping below); with
+// S > 1 a tile's partial sums meet in LDS and are added in wave order.
 template <int TYPE, int C, bool ALIGNED, int D, int S>
 __global__ void __launch_bounds__(64 * kMfmaWaves)
 gemv_mfma_kernel(const uint8_t* __restrict__ w, int64_t row_bytes, int rows, int nblk,
@@ -447,15 +444,22 @@ gemv_mfma_kernel(const uint8_t* __restrict__ w, int64_t row_bytes, int rows, int
   const uint32_t stage_lds = lds_address(stage);
   const int tiles = (rows + 15) >> 4;
   const int chunks = nblk / C;
-  // Step s of this wave: (tile, chunk).  S = 1: whole tiles first_tile,
-  // first_tile + tile_step, ...; S > 1: the group's one tile, chunks sw,
-  // sw + S, ...
+  // Step s of this wave: (tile, chunk).  The workgroup owns a contiguous
+  // range of tiles (HBM streams each workgroup's own region faster than
+  // interleaved ones), taken in rounds of kGroups tiles: group grp (S waves)
+  // takes tile first + r * kGroups + grp of round r, wave sw of the group its
+  // chunks sw, sw + S, ...  With S = kMfmaWaves a round is one tile whose
+  // bytes the whole workgroup loads at once.
   constexpr int kGroups = kMfmaWaves / S;
   const int grp = wave / S, sw = wave - grp * S;
-  const int first_tile = S == 1 ? blockIdx.x * kMfmaWaves + wave : blockIdx.x * kGroups + grp;
-  const int tile_step = S == 1 ? gridDim.x * kMfmaWaves : tiles;
+  const int wg_first = (int)(((int64_t)blockIdx.x * tiles) / gridDim.x);
+  const int wg_end = (int)(((int64_t)(blockIdx.x + 1) * tiles) / gridDim.x);
+  const int rounds = (wg_end - wg_first + kGroups - 1) / kGroups;  // same for every group
+  const int first_tile = wg_first + grp;
+  const int tile_step = kGroups;
   const int cpt = S == 1 ? chunks : (chunks - sw + S - 1) / S;  // chunks per tile
-  const int my_tiles = first_tile < tiles ? (tiles - first_tile + tile_step - 1) / tile_step : 0;
+  const int my_tiles =
+      first_tile < wg_end ? (wg_end - first_tile + tile_step - 1) / tile_step : 0;
   const int steps = my_tiles * cpt;
   const uint32_t rb = (uint32_t)row_bytes;
   auto tile_of = [&](int s) { return first_tile + (s / cpt) * tile_step; };
@@ -516,7 +520,10 @@ gemv_mfma_kernel(const uint8_t* __restrict__ w, int64_t row_bytes, int rows, int
   __syncthreads();
 
   float acc = 0.f;
-  for (int s = 0; s < steps; ++s) {
+  int s = 0;
+  for (int r = 0; r < rounds; ++r) {
+  const int round_end = S == 1 ? steps : (r < my_tiles ? s + cpt : s);
+  for (; s < round_end; ++s) {
     const int tile = tile_of(s);
     const int chunk = chunk_of(s);
     // steps up to s + nbuf - 1 are issued; at most `ahead` later steps' loads
@@ -569,16 +576,22 @@ gemv_mfma_kernel(const uint8_t* __restrict__ w, int64_t row_bytes, int rows, int
     }
   }
   if constexpr (S > 1) {
-    // one tile per group: its waves' row sums, in wave order
+    // the round's tiles: each group's row sums, in wave order
     const float v = sum_lane_groups(acc);
+    acc = 0.f;
     if (g == 0) partial[wave * 16 + n] = v;
     __syncthreads();
-    if (sw == 0 && first_tile < tiles) {
+    const int tile = first_tile + r * tile_step;
+    if (sw == 0 && r < my_tiles) {
       float t = partial[wave * 16 + n];
 #pragma unroll
       for (int k = 1; k < S; ++k) t = t + partial[(wave + k) * 16 + n];
-      store_row(f, y, rows, first_tile * 16 + n, t, g == 0);
+      store_row(f, y, rows, tile * 16 + n, t, g == 0);
     }
+    __syncthreads();
+  } else {
+    break;  // S = 1: every step of the wave ran in the one pass
+  }
   }
 }
 
@@ -608,14 +621,15 @@ static int mfma_nbuf(const MfmaChoice<TYPE>& c, int nblk) {
   return mfma_nbuf(c.depth, c.waves, nblk / c.chunk);
 }
 
-// Waves per tile: enough waves in flight to cover the device
-// (LLHIP_GEMV_TARGET_WAVES of them), as long as every wave keeps a chunk.
-#ifndef LLHIP_GEMV_TARGET_WAVES
-#define LLHIP_GEMV_TARGET_WAVES 4096
+// Waves per tile: as many as the tile has chunks, up to the workgroup (a
+// round of a workgroup then loads one contiguous tile at once; measured best
+// for every decode shape, 4096..128256 rows).
+#ifndef LLHIP_GEMV_WAVES_PER_TILE
+#define LLHIP_GEMV_WAVES_PER_TILE 8
 #endif
-static int mfma_waves_per_tile(int64_t tiles, int64_t chunks) {
+static int mfma_waves_per_tile(int64_t chunks) {
   int S = 1;
-  while (S < kMfmaWaves && tiles * S < LLHIP_GEMV_TARGET_WAVES && chunks >= 2 * S) S *= 2;
+  while (S < LLHIP_GEMV_WAVES_PER_TILE && S < kMfmaWaves && chunks >= 2 * S) S *= 2;
   return S;
 }
 
@@ -638,13 +652,12 @@ static MfmaChoice<TYPE> mfma_choice(const GemvProblem& p) {
   MfmaChoice<TYPE> c;
   c.chunk = nblk % LLHIP_GEMV_CHUNK == 0 ? LLHIP_GEMV_CHUNK : nblk % 2 == 0 ? 2 : 1;
   c.depth = kGemvDepth;
-  const int64_t tiles = (p.rows + 15) / 16;
   // long rows: shorter chunks, then fewer stages, until the LDS holds the
   // activation table and the stages
   for (;;) {
     const int64_t span = (int64_t)c.chunk * MfmaType<TYPE>::kBB;
     c.aligned = p.row_bytes % 4 == 0 && span % 4 == 0;
-    c.waves = mfma_waves_per_tile(tiles, nblk / c.chunk);
+    c.waves = mfma_waves_per_tile(nblk / c.chunk);
     if (mfma_lds_for(c, (int)nblk) <= kMaxLdsBytes) break;
     if (c.chunk > 1) c.chunk /= 2;
     else if (c.depth > 2) c.depth = 2;
@@ -686,18 +699,14 @@ static hipError_t launch_mfma(const GemvProblem& p, const GemvFuse& f, hipStream
     if (e != hipSuccess) return e;
   }
   const int tiles = (int)((p.rows + 15) / 16);
-  int grid;
-  if (S > 1) {
-    grid = (tiles + kMfmaWaves / S - 1) / (kMfmaWaves / S);  // one tile per group
-  } else {
-    int per_cu = 0;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, reinterpret_cast<const void*>(kernel),
-                                                     64 * kMfmaWaves, lds) != hipSuccess ||
-        per_cu < 1)
-      per_cu = 1;
-    const int needed = (tiles + kMfmaWaves - 1) / kMfmaWaves;
-    grid = std::max(1, std::min(needed, device_cu_count() * per_cu));
-  }
+  // persistent: at most the resident workgroups, each a contiguous tile range
+  int per_cu = 0;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, reinterpret_cast<const void*>(kernel),
+                                                   64 * kMfmaWaves, lds) != hipSuccess ||
+      per_cu < 1)
+    per_cu = 1;
+  const int needed = (tiles + kMfmaWaves / S - 1) / (kMfmaWaves / S);
+  const int grid = std::max(1, std::min(needed, device_cu_count() * per_cu));
   hipLaunchKernelGGL(kernel, dim3(grid), dim3(64 * kMfmaWaves), lds, stream, p.weights,
                      p.row_bytes, (int)p.rows, nblk, p.x, p.y, f, nbuf);
   return hipGetLastError();
@@ -706,10 +715,17 @@ static hipError_t launch_mfma(const GemvProblem& p, const GemvFuse& f, hipStream
 template <int TYPE, int C, bool ALIGNED>
 static hipError_t launch_mfma_ds(const MfmaChoice<TYPE>& c, const GemvProblem& p,
                                  const GemvFuse& f, hipStream_t s) {
-  static_assert(kGemvDepth == 2, "one ring depth is instantiated");
+  if (c.depth != kGemvDepth) {  // shallower ring where the LDS is short
+    switch (c.waves) {
+      case 8: return launch_mfma<TYPE, C, ALIGNED, 2, (kMfmaWaves >= 8 ? 8 : kMfmaWaves)>(p, f, s);
+      case 4: return launch_mfma<TYPE, C, ALIGNED, 2, (kMfmaWaves >= 4 ? 4 : kMfmaWaves)>(p, f, s);
+      case 2: return launch_mfma<TYPE, C, ALIGNED, 2, 2>(p, f, s);
+      default: return launch_mfma<TYPE, C, ALIGNED, 2, 1>(p, f, s);
+    }
+  }
   switch (c.waves) {
-    case 8: return launch_mfma<TYPE, C, ALIGNED, kGemvDepth, 8>(p, f, s);
-    case 4: return launch_mfma<TYPE, C, ALIGNED, kGemvDepth, 4>(p, f, s);
+    case 8: return launch_mfma<TYPE, C, ALIGNED, kGemvDepth, (kMfmaWaves >= 8 ? 8 : kMfmaWaves)>(p, f, s);
+    case 4: return launch_mfma<TYPE, C, ALIGNED, kGemvDepth, (kMfmaWaves >= 4 ? 4 : kMfmaWaves)>(p, f, s);
     case 2: return launch_mfma<TYPE, C, ALIGNED, kGemvDepth, 2>(p, f, s);
     default: return launch_mfma<TYPE, C, ALIGNED, kGemvDepth, 1>(p, f, s);
   }
