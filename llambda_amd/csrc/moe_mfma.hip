@@ -386,15 +386,26 @@ moe_gemm_kernel(MoeGemmArgs args) {
   typedef AFrag<B::kWide> AF;
   extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
 
+  // (chunk, row tile) of this workgroup.  Batch pipelines: a 1-D grid in
+  // which the row tiles of chunk c take the workgroup ids
+  // (c / 8) * 8 T + 8 k + c % 8 (k < T tiles): workgroups are dealt to the
+  // eight XCDs by id modulo 8, so every row tile of a chunk runs on one XCD,
+  // close in time, and the chunk's activations are fetched into its L2 once.
+  int bx = blockIdx.x, by = blockIdx.y;
+  if constexpr (PIPE != kPipeDecode) {
+    const int T = args.row_tiles, L = blockIdx.x;
+    bx = (L / (8 * T)) * 8 + (L & 7);
+    by = (L >> 3) % T;
+  }
   const int* cc = args.chunk_counts;
   const int all_chunks = cc[0] + cc[1];
   const int nchunks = args.joint ? all_chunks : cc[args.group];
-  if ((int)blockIdx.x >= nchunks) return;
+  if (bx >= nchunks) return;
   // joint launches: routed chunks, then the shared expert's (their entries
   // follow the routed ones in the table)
-  const MoeChunk ch = args.chunks[args.joint ? blockIdx.x : (args.group ? cc[0] : 0) + blockIdx.x];
+  const MoeChunk ch = args.chunks[args.joint ? bx : (args.group ? cc[0] : 0) + bx];
   MoeGemmArgs a = args;
-  if (args.joint && (int)blockIdx.x >= cc[0]) {
+  if (args.joint && bx >= cc[0]) {
     a.w0 = args.s_w0;
     a.w1 = args.s_w1;
     a.row_bytes = args.s_row_bytes;
@@ -422,7 +433,7 @@ moe_gemm_kernel(MoeGemmArgs args) {
     if constexpr (Sh::kWaves > 1) __syncthreads();
   }
 
-  const int n0 = PIPE == kPipeDecode ? blockIdx.y * Sh::ROWS : (blockIdx.y * Sh::kWaves + wave) * Sh::ROWS;
+  const int n0 = PIPE == kPipeDecode ? by * Sh::ROWS : (by * Sh::kWaves + wave) * Sh::ROWS;
   if (n0 >= a.N) return;  // uniform over the workgroup for the decode pipeline
   const int depth = PIPE == kPipeDecode ? a.depth : Sh::DEPTH;
   uint8_t* wlds = lds + Sh::LUT + Sh::RED + wave * (depth * Sh::STAGE + Sh::TABLE);
@@ -786,7 +797,11 @@ static hipError_t launch_gemm_t(const MoeGemmArgs& a_in, int max_chunks, hipStre
     if (e != hipSuccess) return e;
   }
   const int rows = a.joint ? std::max(a.N, a.s_N) : a.N;
-  const dim3 grid(max_chunks, (rows + Sh::WG_ROWS - 1) / Sh::WG_ROWS);
+  const int tiles = (rows + Sh::WG_ROWS - 1) / Sh::WG_ROWS;
+  a.row_tiles = tiles;
+  // batch pipelines: the XCD-grouped 1-D grid (chunks padded to a multiple of 8)
+  const dim3 grid = PIPE == kPipeDecode ? dim3(max_chunks, tiles)
+                                        : dim3(((max_chunks + 7) / 8) * 8 * tiles);
   hipLaunchKernelGGL(kernel, grid, dim3(64 * Sh::kWaves), lds, stream, a);
   return hipGetLastError();
 }
