@@ -29,6 +29,7 @@
 #include "mfma.h"
 
 #include <algorithm>
+#include <type_traits>
 #include <utility>
 
 namespace llhip {
@@ -102,14 +103,22 @@ struct Q4Items {
   }
 };
 
-// One Q4_K block of lane (n, g)'s row, p = the block's 144 bytes in LDS
-// (16-byte aligned); a = the lane's A address for this block (0 when its A
-// row carries no data: LDS [0, 2 KB) is zero).
-__device__ __forceinline__ float q4k_block(const uint8_t* p, const uint8_t* lds, uint32_t a,
+// The bytes of one Q4_K block that lane (n, g) uses: the 16-byte header and
+// its 32 qs bytes, read from the block's 144 bytes in LDS (16-byte aligned).
+struct Q4Raw {
+  uint4 h, c0, c1;
+};
+__device__ __forceinline__ Q4Raw q4k_fetch(const uint8_t* p, int g) {
+  return {*reinterpret_cast<const uint4*>(p), *reinterpret_cast<const uint4*>(p + 16 + 32 * g),
+          *reinterpret_cast<const uint4*>(p + 32 + 32 * g)};
+}
+
+// One Q4_K block of lane (n, g)'s row from its fetched bytes; a = the lane's
+// A address for this block (0 when its A row carries no data: LDS [0, 2 KB)
+// is zero).
+__device__ __forceinline__ float q4k_block(const Q4Raw& r, const uint8_t* lds, uint32_t a,
                                            const float* gs, int g) {
-  const uint4 h = *reinterpret_cast<const uint4*>(p);
-  const uint4 c0 = *reinterpret_cast<const uint4*>(p + 16 + 32 * g);
-  const uint4 c1 = *reinterpret_cast<const uint4*>(p + 32 + 32 * g);
+  const uint4 h = r.h, c0 = r.c0, c1 = r.c1;
   const uint32_t qw[8] = {c0.x, c0.y, c0.z, c0.w, c1.x, c1.y, c1.z, c1.w};
   floatx4 d = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -194,28 +203,46 @@ __device__ __forceinline__ uint2 read8(const uint32_t* q, int o, uint32_t sh) {
   return make_uint2(__builtin_amdgcn_alignbyte(r1, r0, sh), __builtin_amdgcn_alignbyte(r2, r1, sh));
 }
 
-// One Q6_K block of lane (n, g)'s row: p = its 210 bytes in LDS (2-byte
-// aligned), SH = p & 3 when known at compile time (-1: read it from p).
-// am[m] = the lane's A address for MFMA m of the block (0: zero line).
+// The bytes of one Q6_K block that lane (n, g) uses, read from the block's
+// 210 bytes p in LDS (2-byte aligned; SH = p & 3 when known at compile time,
+// -1: read it from p): per half its 8 ql bytes of each 32-lane run, its 8 qh
+// bytes and its two scales, and the block's d.
+struct Q6Raw {
+  uint2 la[2], lb[2], qh[2];
+  uint32_t sv[2];
+  uint32_t d;
+};
 template <int SH>
-__device__ __forceinline__ float q6k_block(const uint8_t* p, const uint8_t* lds, const uint32_t am[4],
-                                           const float* gs, int g) {
+__device__ __forceinline__ Q6Raw q6k_fetch(const uint8_t* p, int g) {
   const uint32_t sh = SH >= 0 ? (uint32_t)SH : (uint32_t)(reinterpret_cast<uintptr_t>(p) & 3u);
   const uint32_t* q = reinterpret_cast<const uint32_t*>(p - sh);
-  const float dd = half_bits_to_float(*reinterpret_cast<const uint16_t*>(p + 208));
+  Q6Raw r;
+  r.d = *reinterpret_cast<const uint16_t*>(p + 208);
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    if constexpr (SH >= 0) {
+      r.la[h] = read8<SH>(q, 64 * h + 8 * g);
+      r.lb[h] = read8<SH>(q, 64 * h + 32 + 8 * g);
+      r.qh[h] = read8<SH>(q, 128 + 32 * h + 8 * g);
+    } else {
+      r.la[h] = read8(q, 64 * h + 8 * g + 0, sh);
+      r.lb[h] = read8(q, 64 * h + 32 + 8 * g, sh);
+      r.qh[h] = read8(q, 128 + 32 * h + 8 * g, sh);
+    }
+    r.sv[h] = *reinterpret_cast<const uint16_t*>(p + 192 + 8 * h + 2 * g);
+  }
+  return r;
+}
+
+// One Q6_K block of lane (n, g)'s row from its fetched bytes.  am[m] = the
+// lane's A address for MFMA m of the block (0: zero line).
+__device__ __forceinline__ float q6k_block(const Q6Raw& r, const uint8_t* lds, const uint32_t am[4],
+                                           const float* gs, int g) {
+  const float dd = half_bits_to_float(r.d);
   float v = 0.f;
 #pragma unroll
   for (int h = 0; h < 2; ++h) {
-    uint2 la, lb, qh;
-    if constexpr (SH >= 0) {
-      la = read8<SH>(q, 64 * h + 8 * g);
-      lb = read8<SH>(q, 64 * h + 32 + 8 * g);
-      qh = read8<SH>(q, 128 + 32 * h + 8 * g);
-    } else {
-      la = read8(q, 64 * h + 8 * g + 0, sh);
-      lb = read8(q, 64 * h + 32 + 8 * g, sh);
-      qh = read8(q, 128 + 32 * h + 8 * g, sh);
-    }
+    const uint2 la = r.la[h], lb = r.lb[h], qh = r.qh[h];
     floatx4 d = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int m = 0; m < 4; ++m) {
@@ -231,7 +258,7 @@ __device__ __forceinline__ float q6k_block(const uint8_t* p, const uint8_t* lds,
     }
     // D rows 4g .. 4g+3 of column n: groups (k = g, l-half 0 / 1) of half h,
     // i.e. scales sc[8h + 2g] and sc[8h + 2g + 1] (llambda.lisp:4203-4310)
-    const uint32_t sv = *reinterpret_cast<const uint16_t*>(p + 192 + 8 * h + 2 * g);
+    const uint32_t sv = r.sv[h];
     const float delta0 = dd * (float)(int)(int8_t)(sv & 0xFFu);
     const float delta1 = dd * (float)(int)(int8_t)(sv >> 8);
     const float2 gsv = *reinterpret_cast<const float2*>(gs + h * 8 + 2 * g);
@@ -547,48 +574,58 @@ gemv_mfma_kernel(const uint8_t* __restrict__ w, int64_t row_bytes, int rows, int
       const int row = min(tile * 16 + n, rows - 1);
       rowp += (reinterpret_cast<uintptr_t>(w + (int64_t)row * row_bytes + (int64_t)chunk * Ch::kSpan) & 3u);
     }
-    auto block = [&]<int BL>() {
-      const int b = chunk * C + BL;
+    // this lane's bytes of the stage into registers, then the stage is
+    // refilled (its LDS reads drained first) while the blocks compute
+    using Raw = std::conditional_t<TYPE == kQ4_K, Q4Raw, Q6Raw>;
+    Raw raw[C];
+    [&]<int... BL>(std::integer_sequence<int, BL...>) {
+      ((raw[BL] = [&] {
+         const uint8_t* p = rowp + BL * T::kBB;
+         if constexpr (TYPE == kQ4_K) return q4k_fetch(p, g);
+         else if constexpr (ALIGNED) return q6k_fetch<(BL * 210) & 3>(p, g);
+         else return q6k_fetch<-1>(p, g);
+       }()), ...);
+    }(std::make_integer_sequence<int, C>{});
+    if (s + nbuf < steps) {
+      __builtin_amdgcn_s_waitcnt(kWaitLgkm0);
+      issue(s + nbuf);
+    }
+#pragma unroll
+    for (int bl = 0; bl < C; ++bl) {
+      const int b = chunk * C + bl;
       const float* gs = gsum + b * T::kSums;
-      const uint8_t* p = rowp + BL * T::kBB;
       if constexpr (TYPE == kQ4_K) {
-        acc += q4k_block(p, lds, a_base + (uint32_t)b * a_stride, gs, g);
+        acc += q4k_block(raw[bl], lds, a_base + (uint32_t)b * a_stride, gs, g);
       } else {
         const uint32_t ab = a_base + (uint32_t)b * (uint32_t)T::kTable;
         const uint32_t am[4] = {a_m[0] ? ab : 0u, a_m[1] ? ab : 0u, a_m[2] ? ab : 0u,
                                 a_m[3] ? ab : 0u};
-        if constexpr (ALIGNED) acc += q6k_block<(BL * 210) & 3>(p, lds, am, gs, g);
-        else acc += q6k_block<-1>(p, lds, am, gs, g);
+        acc += q6k_block(raw[bl], lds, am, gs, g);
       }
-    };
-    [&]<int... BL>(std::integer_sequence<int, BL...>) {
-      (block.template operator()<BL>(), ...);
-    }(std::make_integer_sequence<int, C>{});
+    }
     if (S == 1 && chunk == chunks - 1) {
       const float v = sum_lane_groups(acc);
       store_row(f, y, rows, tile * 16 + n, v, g == 0);
       acc = 0.f;
     }
-    // refill the stage just read (its LDS reads drained first)
-    if (s + nbuf < steps) {
-      __builtin_amdgcn_s_waitcnt(kWaitLgkm0);
-      issue(s + nbuf);
-    }
   }
   if constexpr (S > 1) {
     // the round's tiles: each group's row sums, in wave order
+    // (partial sums alternate between two halves by round, so one barrier
+    // per round suffices: a half is written again two rounds later, after
+    // the next round's barrier, which its readers reach only when done)
+    float* part = partial + (r & 1) * (kMfmaWaves * 16);
     const float v = sum_lane_groups(acc);
     acc = 0.f;
-    if (g == 0) partial[wave * 16 + n] = v;
+    if (g == 0) part[wave * 16 + n] = v;
     __syncthreads();
     const int tile = first_tile + r * tile_step;
     if (sw == 0 && r < my_tiles) {
-      float t = partial[wave * 16 + n];
+      float t = part[wave * 16 + n];
 #pragma unroll
-      for (int k = 1; k < S; ++k) t = t + partial[(wave + k) * 16 + n];
+      for (int k = 1; k < S; ++k) t = t + part[(wave + k) * 16 + n];
       store_row(f, y, rows, tile * 16 + n, t, g == 0);
     }
-    __syncthreads();
   } else {
     break;  // S = 1: every step of the wave ran in the one pass
   }
@@ -612,8 +649,11 @@ struct MfmaChoice {
 
 // Stages a wave needs: the ring depth, or fewer when no wave has that many
 // steps (S > 1: one tile's chunks shared by S waves).
+#ifndef LLHIP_GEMV_NBUF_CAP
+#define LLHIP_GEMV_NBUF_CAP 1
+#endif
 static int mfma_nbuf(int depth, int waves, int chunks) {
-  if (waves == 1) return depth;
+  if (waves == 1 || !LLHIP_GEMV_NBUF_CAP) return depth;
   return std::max(1, std::min(depth, (chunks + waves - 1) / waves));
 }
 template <int TYPE>
