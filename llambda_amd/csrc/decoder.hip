@@ -110,6 +110,7 @@ attention_kernel(const float* __restrict__ q, const float* __restrict__ kc,
         kr[st][j] = v.x; kr[st][j + 1] = v.y; kr[st][j + 2] = v.z; kr[st][j + 3] = v.w;
       }
     }
+
 #pragma unroll
     for (int st = 0; st < 4; ++st) {
       const int pl = 16 * wave + 4 * st + grp;
@@ -185,12 +186,24 @@ __global__ void __launch_bounds__(D)
 attention_combine_kernel(const float* __restrict__ part, const float* __restrict__ pmax,
                          const float* __restrict__ psum, const int* __restrict__ state,
                          int max_chunks, float* __restrict__ out) {
+  // the partials were just written by workgroups on other XCDs, so every
+  // dependent round of loads is slow: the chunk maxima, sums and this
+  // thread's partial values of up to U chunks are all loaded at once
+  constexpr int U = 64;
   __shared__ float alpha[kAttnMaxChunks];
   __shared__ float red[D / 64];
   const int h = blockIdx.x, d = threadIdx.x, lane = d & 63;
   const int kvh = h / G, hh = h % G;
   const int nchunks = (state[1] + kAttnChunk) / kAttnChunk;
   const int64_t base = (int64_t)kvh * max_chunks * G + hh;  // chunk c at base + c * G
+  const float* pc = part + base * D + d;
+  float ps[U], pv[U];
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    const int c = min(u, nchunks - 1);
+    ps[u] = psum[base + (int64_t)c * G];
+    pv[u] = pc[(int64_t)c * G * D];
+  }
   float m = -INFINITY;
   for (int c = d; c < nchunks; c += D) {
     const float v = pmax[base + (int64_t)c * G];
@@ -205,12 +218,26 @@ attention_combine_kernel(const float* __restrict__ part, const float* __restrict
   for (int w = 1; w < D / 64; ++w) m = fmaxf(m, red[w]);
   for (int c = d; c < nchunks; c += D) alpha[c] = (float)exp((double)(alpha[c] - m));
   __syncthreads();
+  // M = max m_c, a_c = exp(m_c - M), S = sum a_c S_c, out = (sum a_c pv_c) / S,
+  // the sums in chunk order
   float S = 0.f, acc = 0.f;
-  const float* pc = part + base * D + d;
-  for (int c = 0; c < nchunks; ++c) {
-    const float a = alpha[c];
-    S += a * psum[base + (int64_t)c * G];
-    acc += a * pc[(int64_t)c * G * D];
+  for (int c0 = 0; c0 < nchunks; c0 += U) {
+    if (c0 > 0) {
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int c = min(c0 + u, nchunks - 1);
+        ps[u] = psum[base + (int64_t)c * G];
+        pv[u] = pc[(int64_t)c * G * D];
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      if (c0 + u < nchunks) {
+        const float a = alpha[c0 + u];
+        S += a * ps[u];
+        acc += a * pv[u];
+      }
+    }
   }
   out[(int64_t)h * D + d] = acc / S;
 }
