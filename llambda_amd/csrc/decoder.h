@@ -7,6 +7,7 @@
 //     q|k rows      rms-norm(x) fused in, rotation (+ query scale) fused out,
 //                   keys written to the cache slot of this position
 //     v rows        rms-norm(x) fused in, values written to the cache slot
+//                   (one launch with the q|k rows where their shapes allow)
 //     attention     GQA over cache slots 0..position (split over position
 //                   chunks of 128, the chunks combined by a second launch)
 //     o rows        x += o(context)

@@ -324,15 +324,6 @@ hipError_t decoder_step_launch(const DecoderPlan& p, float* logits, hipStream_t 
     rope.q_scale = p.q_scale;
     rope.pos = p.state + 1;
     rope.head_stride = (int64_t)p.context * D;
-    if (L.qk.w) {
-      rope.split = p.heads * D;
-      DEC_CHECK(gemv_fused_launch(problem(L.qk, p.x, p.q), rope, st));
-    } else {
-      rope.split = p.heads * D;  // every row a query row
-      DEC_CHECK(gemv_fused_launch(problem(L.q, p.x, p.q), rope, st));
-      rope.split = 0;  // every row a key row
-      DEC_CHECK(gemv_fused_launch(problem(L.k, p.x, p.q), rope, st));
-    }
     GemvFuse cache;
     cache.norm_w = L.attn_norm;
     cache.norm_eps = p.eps;
@@ -340,7 +331,18 @@ hipError_t decoder_step_launch(const DecoderPlan& p, float* logits, hipStream_t 
     cache.head_dim = D;
     cache.pos = p.state + 1;
     cache.head_stride = (int64_t)p.context * D;
-    DEC_CHECK(gemv_fused_launch(problem(L.v, p.x, L.vcache), cache, st));
+    if (L.qk.w) {
+      // q|k and v rows in one launch where their shapes allow
+      rope.split = p.heads * D;
+      DEC_CHECK(gemv_fused_pair_launch(problem(L.qk, p.x, p.q), rope,
+                                       problem(L.v, p.x, L.vcache), cache, st));
+    } else {
+      rope.split = p.heads * D;  // every row a query row
+      DEC_CHECK(gemv_fused_launch(problem(L.q, p.x, p.q), rope, st));
+      rope.split = 0;  // every row a key row
+      DEC_CHECK(gemv_fused_launch(problem(L.k, p.x, p.q), rope, st));
+      DEC_CHECK(gemv_fused_launch(problem(L.v, p.x, L.vcache), cache, st));
+    }
     DEC_CHECK(decoder_attention_launch(p, p.q, L.kcache, L.vcache, p.ctx, st));
     // x += o(context) (vector-add-into, llambda.lisp:6404)
     GemvFuse add;

@@ -63,6 +63,11 @@ struct GemvFuse {
 // hipErrorInvalidValue for problems the MFMA kernel does not take).
 hipError_t gemv_fused_launch(const GemvProblem& p, const GemvFuse& f, hipStream_t stream);
 
+// Two independent fused GEMVs (no shared outputs) in one launch where the
+// pair's shapes allow it (Q4_K then Q6_K), else two launches.
+hipError_t gemv_fused_pair_launch(const GemvProblem& pa, const GemvFuse& fa, const GemvProblem& pb,
+                                  const GemvFuse& fb, hipStream_t stream);
+
 // Batch-1 Q4_K / Q6_K GEMV on MFMA (gemv_mfma.hip).
 bool gemv_mfma_supported(const GemvProblem& p);
 hipError_t gemv_mfma_launch(const GemvProblem& p, hipStream_t stream);

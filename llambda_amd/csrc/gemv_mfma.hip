@@ -415,6 +415,10 @@ struct MfmaType {
 #define LLHIP_GEMV_CHUNK 2
 #endif
 constexpr int kMfmaWaves = LLHIP_GEMV_WAVES;
+#ifndef LLHIP_GEMV_DEPTH
+#define LLHIP_GEMV_DEPTH 2
+#endif
+constexpr int kGemvDepth = LLHIP_GEMV_DEPTH;
 
 // s_waitcnt vmcnt(n) and lgkmcnt(0) (gfx9 encoding, other counters left alone)
 constexpr int waitcnt_vm(int n) { return 0x0F70 | (n & 15) | ((n >> 4) << 14); }
@@ -437,13 +441,30 @@ constexpr size_t mfma_lds_bytes(int nblk, int nbuf) {
 // built, and each is refilled as soon as it has been read.  S: waves per
 // 16-row tile (rows are taken in rounds; see the step mapping below); with
 // S > 1 a tile's partial sums meet in LDS and are added in wave order.
+// The arguments of one batch-1 GEMV launch.
+struct MfmaArgs {
+  const uint8_t* w;
+  int64_t row_bytes;
+  int rows, nblk;
+  const float* x;
+  float* y;
+  GemvFuse f;
+  int nbuf;
+};
+
+// Workgroup `wg` of `nwg` working on one GEMV (the body of gemv_mfma_kernel
+// and of each half of gemv_mfma_pair_kernel).
 template <int TYPE, int C, bool ALIGNED, int D, int S>
-__global__ void __launch_bounds__(64 * kMfmaWaves)
-gemv_mfma_kernel(const uint8_t* __restrict__ w, int64_t row_bytes, int rows, int nblk,
-                 const float* __restrict__ x, float* __restrict__ y, const GemvFuse f, int nbuf) {
+__device__ __forceinline__ void gemv_mfma_body(uint8_t* lds, int wg, int nwg, const MfmaArgs& args) {
+  const uint8_t* __restrict__ w = args.w;
+  const int64_t row_bytes = args.row_bytes;
+  const int rows = args.rows, nblk = args.nblk;
+  const float* __restrict__ x = args.x;
+  float* __restrict__ y = args.y;
+  const GemvFuse& f = args.f;
+  const int nbuf = args.nbuf;
   using T = MfmaType<TYPE>;
   using Ch = Chunk<T::kBB, C, ALIGNED>;
-  extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
   const uint32_t table_off = T::kZero;
   uint8_t* table = lds + table_off;
   float* gsum = reinterpret_cast<float*>(table + nblk * T::kTable);
@@ -479,8 +500,8 @@ gemv_mfma_kernel(const uint8_t* __restrict__ w, int64_t row_bytes, int rows, int
   // bytes the whole workgroup loads at once.
   constexpr int kGroups = kMfmaWaves / S;
   const int grp = wave / S, sw = wave - grp * S;
-  const int wg_first = (int)(((int64_t)blockIdx.x * tiles) / gridDim.x);
-  const int wg_end = (int)(((int64_t)(blockIdx.x + 1) * tiles) / gridDim.x);
+  const int wg_first = (int)(((int64_t)wg * tiles) / nwg);
+  const int wg_end = (int)(((int64_t)(wg + 1) * tiles) / nwg);
   const int rounds = (wg_end - wg_first + kGroups - 1) / kGroups;  // same for every group
   const int first_tile = wg_first + grp;
   const int tile_step = kGroups;
@@ -633,12 +654,29 @@ gemv_mfma_kernel(const uint8_t* __restrict__ w, int64_t row_bytes, int rows, int
   }
 }
 
+template <int TYPE, int C, bool ALIGNED, int D, int S>
+__global__ void __launch_bounds__(64 * kMfmaWaves) gemv_mfma_kernel(const MfmaArgs args) {
+  extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+  gemv_mfma_body<TYPE, C, ALIGNED, D, S>(lds, blockIdx.x, gridDim.x, args);
+}
+
+// Two independent GEMVs in one launch (the decoder's q|k and v rows): the
+// first `grid_a` workgroups run the first, the rest the second, so the
+// second's fixed latency (table, first loads, epilogue) overlaps the first's
+// instead of following it.
+template <int TA, int CA, bool AA, int TB, int CB, bool AB>
+__global__ void __launch_bounds__(64 * kMfmaWaves)
+gemv_mfma_pair_kernel(const MfmaArgs a, const MfmaArgs b, int grid_a) {
+  extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+  if ((int)blockIdx.x < grid_a)
+    gemv_mfma_body<TA, CA, AA, kGemvDepth, kMfmaWaves>(lds, blockIdx.x, grid_a, a);
+  else
+    gemv_mfma_body<TB, CB, AB, kGemvDepth, kMfmaWaves>(lds, blockIdx.x - grid_a,
+                                                        gridDim.x - grid_a, b);
+}
+
 // ------------------------------------------------------------------ host
 
-#ifndef LLHIP_GEMV_DEPTH
-#define LLHIP_GEMV_DEPTH 2
-#endif
-constexpr int kGemvDepth = LLHIP_GEMV_DEPTH;
 
 template <int TYPE>
 struct MfmaChoice {
@@ -748,8 +786,8 @@ static hipError_t launch_mfma(const GemvProblem& p, const GemvFuse& f, hipStream
     per_cu = 1;
   const int needed = (tiles + kMfmaWaves / S - 1) / (kMfmaWaves / S);
   const int grid = std::max(1, std::min(needed, device_cu_count() * per_cu));
-  hipLaunchKernelGGL(kernel, dim3(grid), dim3(64 * kMfmaWaves), lds, stream, p.weights,
-                     p.row_bytes, (int)p.rows, nblk, p.x, p.y, f, nbuf);
+  const MfmaArgs args{p.weights, p.row_bytes, (int)p.rows, nblk, p.x, p.y, f, nbuf};
+  hipLaunchKernelGGL(kernel, dim3(grid), dim3(64 * kMfmaWaves), lds, stream, args);
   return hipGetLastError();
 }
 
@@ -793,14 +831,62 @@ hipError_t gemv_mfma_launch(const GemvProblem& p, hipStream_t stream) {
                          : launch_mfma_type<kQ6_K>(p, plain, stream);
 }
 
-hipError_t gemv_fused_launch(const GemvProblem& p, const GemvFuse& f, hipStream_t stream) {
-  if (!gemv_mfma_supported(p)) return hipErrorInvalidValue;
+static bool fuse_ok(const GemvProblem& p, const GemvFuse& f) {
+  if (!gemv_mfma_supported(p)) return false;
   if ((f.epi == kGemvRope || f.epi == kGemvCache) && (f.head_dim <= 0 || f.head_dim % 2 || !f.pos))
-    return hipErrorInvalidValue;
-  if (f.epi == kGemvSwiglu8 && p.rows % 16) return hipErrorInvalidValue;
-  if (f.epi == kGemvAdd && !f.res) return hipErrorInvalidValue;
+    return false;
+  if (f.epi == kGemvSwiglu8 && p.rows % 16) return false;
+  if (f.epi == kGemvAdd && !f.res) return false;
+  return true;
+}
+
+hipError_t gemv_fused_launch(const GemvProblem& p, const GemvFuse& f, hipStream_t stream) {
+  if (!fuse_ok(p, f)) return hipErrorInvalidValue;
   return p.type == kQ4_K ? launch_mfma_type<kQ4_K>(p, f, stream)
                          : launch_mfma_type<kQ6_K>(p, f, stream);
+}
+
+// The pair kernel is instantiated for the shape of the Llama-style q|k (Q4_K)
+// and v (Q6_K) rows whose K is a multiple of 512 (two-block chunks, dword
+// aligned rows, whole workgroups on a tile); other pairs run as two launches.
+template <int TYPE>
+static bool pair_shape(const GemvProblem& p) {
+  const MfmaChoice<TYPE> c = mfma_choice<TYPE>(p);
+  return c.chunk == 2 && c.aligned && c.depth == kGemvDepth && c.waves == kMfmaWaves;
+}
+
+hipError_t gemv_fused_pair_launch(const GemvProblem& pa, const GemvFuse& fa, const GemvProblem& pb,
+                                  const GemvFuse& fb, hipStream_t stream) {
+  if (!fuse_ok(pa, fa) || !fuse_ok(pb, fb)) return hipErrorInvalidValue;
+  if (!(pa.type == kQ4_K && pb.type == kQ6_K && pair_shape<kQ4_K>(pa) && pair_shape<kQ6_K>(pb))) {
+    const hipError_t e = gemv_fused_launch(pa, fa, stream);
+    return e != hipSuccess ? e : gemv_fused_launch(pb, fb, stream);
+  }
+  const int na = (int)(pa.columns / 256), nb = (int)(pb.columns / 256);
+  const int bufa = mfma_nbuf(kGemvDepth, kMfmaWaves, na / 2);
+  const int bufb = mfma_nbuf(kGemvDepth, kMfmaWaves, nb / 2);
+  const size_t lds = std::max(mfma_lds_bytes<kQ4_K, 2, true>(na, bufa),
+                              mfma_lds_bytes<kQ6_K, 2, true>(nb, bufb));
+  const auto kernel = gemv_mfma_pair_kernel<kQ4_K, 2, true, kQ6_K, 2, true>;
+  if (lds > 65536) {
+    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kernel),
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    if (e != hipSuccess) return e;
+  }
+  int per_cu = 0;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, reinterpret_cast<const void*>(kernel),
+                                                   64 * kMfmaWaves, lds) != hipSuccess ||
+      per_cu < 1)
+    per_cu = 1;
+  const int slots = device_cu_count() * per_cu;
+  const int ta = (int)((pa.rows + 15) / 16), tb = (int)((pb.rows + 15) / 16);
+  // resident slots shared in proportion to the tiles (each part >= 1)
+  int ga = std::min(ta, std::max(1, (int)((int64_t)slots * ta / (ta + tb))));
+  int gb = std::min(tb, std::max(1, slots - ga));
+  const MfmaArgs a{pa.weights, pa.row_bytes, (int)pa.rows, na, pa.x, pa.y, fa, bufa};
+  const MfmaArgs b{pb.weights, pb.row_bytes, (int)pb.rows, nb, pb.x, pb.y, fb, bufb};
+  hipLaunchKernelGGL(kernel, dim3(ga + gb), dim3(64 * kMfmaWaves), lds, stream, a, b, ga);
+  return hipGetLastError();
 }
 
 }  // namespace llhip
