@@ -64,8 +64,11 @@ struct DecoderPlan {
 };
 
 // Positions per attention workgroup and the longest context.
-constexpr int kAttnChunk = 128;
-constexpr int kAttnMaxChunks = 256;
+#ifndef LLHIP_ATTN_CHUNK
+#define LLHIP_ATTN_CHUNK 128
+#endif
+constexpr int kAttnChunk = LLHIP_ATTN_CHUNK;
+constexpr int kAttnMaxChunks = 32768 / kAttnChunk;
 constexpr int kDecoderMaxContext = kAttnChunk * kAttnMaxChunks;
 
 bool decoder_head_supported(int head_dim, int group);

@@ -39,11 +39,11 @@ __global__ void rope_table_kernel(const int* __restrict__ state, const double* _
 // scores s_p = q_h . k_p over cache slots p = 0..position, probabilities
 // exp(s_p - max) / sum, context = sum_p prob_p v_p.
 //
-// Workgroup (chunk, kv head) takes slots [128 chunk, 128 chunk + 128) for
-// the G query heads of its kv head: scores (16 lanes per slot, xor-shuffle
-// reduction), the chunk's max m_c, e_p = exp(s_p - m_c) and their sum S_c,
-// and the unnormalised sum_p e_p v_p.  A second launch combines the chunks
-// in order: M = max m_c, a_c = exp(m_c - M),
+// Workgroup (chunk, kv head) takes slots [P chunk, P chunk + P), P =
+// kAttnChunk, for the G query heads of its kv head: scores (16 lanes per
+// slot, xor-shuffle reduction), the chunk's max m_c, e_p = exp(s_p - m_c) and
+// their sum S_c, and the unnormalised sum_p e_p v_p.  A second launch
+// combines the chunks in order: M = max m_c, a_c = exp(m_c - M),
 // context = (sum_c a_c pv_c) / (sum_c a_c S_c).  The reference normalises
 // every probability before the weighted sum; the two agree to rounding
 // (single-precision exp of each difference, computed in double as SBCL
@@ -74,7 +74,12 @@ attention_kernel(const float* __restrict__ q, const float* __restrict__ kc,
   constexpr int DQ = D / 4;   // float4 columns of a row
   constexpr int NP = T / DQ;  // slot parts in the weighted sum
   constexpr int PPP = P / NP;  // slots per part
-  static_assert(P == 128 && D % 16 == 0 && G <= kAttnWaves && NP * PPP == P, "attention shape");
+  constexpr int SPW = P / kAttnWaves;  // slots per wave in the scores
+  constexpr int ST = SPW / 4;          // four slots per step
+  constexpr int E = P / 64;            // slots per lane in the softmax
+  static_assert((P == 64 || P == 128) && D % 16 == 0 && G <= kAttnWaves && NP * PPP == P &&
+                    ST * 4 * kAttnWaves == P,
+                "attention shape");
   __shared__ float sc[G][P];
   __shared__ float4 pv[NP][G][DQ];
 
@@ -100,10 +105,10 @@ attention_kernel(const float* __restrict__ q, const float* __restrict__ kc,
             *reinterpret_cast<const float4*>(q + (int64_t)(kvh * G + h) * D + DL * sub + j);
         qr[h][j] = v.x; qr[h][j + 1] = v.y; qr[h][j + 2] = v.z; qr[h][j + 3] = v.w;
       }
-    float kr[4][DL];
+    float kr[ST][DL];
 #pragma unroll
-    for (int st = 0; st < 4; ++st) {
-      const int p = min(p0 + 16 * wave + 4 * st + grp, n - 1);
+    for (int st = 0; st < ST; ++st) {
+      const int p = min(p0 + SPW * wave + 4 * st + grp, n - 1);
 #pragma unroll
       for (int j = 0; j < DL; j += 4) {
         const float4 v = *reinterpret_cast<const float4*>(kh + (int64_t)p * D + DL * sub + j);
@@ -112,8 +117,8 @@ attention_kernel(const float* __restrict__ q, const float* __restrict__ kc,
     }
 
 #pragma unroll
-    for (int st = 0; st < 4; ++st) {
-      const int pl = 16 * wave + 4 * st + grp;
+    for (int st = 0; st < ST; ++st) {
+      const int pl = SPW * wave + 4 * st + grp;
 #pragma unroll
       for (int h = 0; h < G; ++h) {
         float s = 0.f;
@@ -132,13 +137,22 @@ attention_kernel(const float* __restrict__ q, const float* __restrict__ kc,
   // chunk max, e_p = exp(s_p - m) rounded to single, and the chunk sum
   if (wave < G) {
     const int h = wave;
-    const float s0 = sc[h][lane], s1 = sc[h][lane + 64];
-    const float m = wave_max(fmaxf(s0, s1));
-    const float e0 = p0 + lane < n ? (float)exp((double)(s0 - m)) : 0.f;
-    const float e1 = p0 + lane + 64 < n ? (float)exp((double)(s1 - m)) : 0.f;
-    const float t = wave_sum(e0 + e1);
-    sc[h][lane] = e0;
-    sc[h][lane + 64] = e1;
+    float sv[E];
+    float m = -INFINITY;
+#pragma unroll
+    for (int e = 0; e < E; ++e) {
+      sv[e] = sc[h][lane + 64 * e];
+      m = fmaxf(m, sv[e]);
+    }
+    m = wave_max(m);
+    float t = 0.f;
+#pragma unroll
+    for (int e = 0; e < E; ++e) {
+      const float ev = p0 + lane + 64 * e < n ? (float)exp((double)(sv[e] - m)) : 0.f;
+      sc[h][lane + 64 * e] = ev;
+      t += ev;
+    }
+    t = wave_sum(t);
     if (lane == 0) {
       pmax[((int64_t)kvh * max_chunks + chunk) * G + h] = m;
       psum[((int64_t)kvh * max_chunks + chunk) * G + h] = t;
@@ -148,6 +162,7 @@ attention_kernel(const float* __restrict__ q, const float* __restrict__ kc,
 
   // unnormalised weighted sum of the chunk's value rows
   {
+    // thread (prt, col) takes float4 column col of slots prt, prt + NP, ...
     const int col = threadIdx.x % DQ, prt = threadIdx.x / DQ;
     float4 vr[PPP];
 #pragma unroll
