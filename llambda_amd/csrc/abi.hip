@@ -404,7 +404,7 @@ struct llambda_hip_moe_session {
   MoePlan plan{};
   DevBuf router, bias, gate, up, down, sh_gate, sh_up, sh_down;
   DevBuf logits, router_part, top_idx, top_w, shared_w, counts, perm, chunks, chunk_counts,
-      down_out, error, xq, xsum, aq, asum, combine_counter;
+      down_out, error, xq, xsum, aq, asum;
   DevBuf x, y;
   int staged = 0;
   ~llambda_hip_moe_session() {
@@ -583,8 +583,6 @@ int llambda_hip_moe_session_create(const llambda_hip_moe_desc* d,
         p.sh_down = s->sh_down.as<uint8_t>();
       }
       s->counts.alloc((size_t)E * sizeof(int), "expert histogram");
-      s->combine_counter.alloc((size_t)moe_combine_tiles(p) * sizeof(int), "combine counters");
-      p.combine_counter = s->combine_counter.as<int>();
       s->chunk_counts.alloc(2 * sizeof(int), "chunk counts");
       s->error.alloc(sizeof(int), "error flag");
       p.counts = s->counts.as<int>();

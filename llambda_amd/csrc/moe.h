@@ -65,7 +65,6 @@ struct MoePlan {
   float* asum;         // [capacity * (top_k + 1)][act_width/16]
   float* down_out;     // [capacity * (top_k + 1)][hidden]
   int* error;          // [1] nonzero after a run that hit a reference error
-  int* combine_counter;  // [hidden / 32 + 1] finished workgroups per row tile (one token)
 };
 
 // Grouped expert product over a chunk table (moe_mfma.hip).
@@ -112,14 +111,6 @@ struct MoeGemmArgs {
   const uint8_t* s_w1;
   int64_t s_row_bytes;
   int s_N, s_K;
-  // single token, down products: the combine of moe_combine_kernel, done by
-  // the last workgroup to finish each row tile (null y: not fused)
-  float* y;
-  const float* top_w;
-  const int* top_idx;
-  const float* shared_w;
-  int variant;
-  int* counter;  // [row tiles], zero between runs
 };
 
 // Router logits of T tokens (fp32 MFMA) as router_slices(H) partial sums
@@ -132,9 +123,6 @@ hipError_t router_mfma_launch(const float* x, int T, const float* R, int Er, int
 // pairs (double-buffered), 2 = chunks of up to 32 pairs.
 hipError_t moe_gemm_launch(int type, int epi, const MoeGemmArgs& a, int mt, int max_chunks,
                            hipStream_t stream);
-
-// Entries of MoePlan::combine_counter.
-int moe_combine_tiles(const MoePlan& p);
 
 // Upper bound of the chunk table for `tokens` tokens with chunk size nt.
 int64_t moe_max_chunks(const MoePlan& p, int64_t tokens, int nt);

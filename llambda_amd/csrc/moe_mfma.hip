@@ -734,50 +734,6 @@ moe_gemm_kernel(MoeGemmArgs args) {
       }
     }
   }
-
-  // single token: the last workgroup to finish a row tile combines it in
-  // rank order, then the shared expert (moe_combine_kernel's arithmetic)
-  if constexpr (PIPE == kPipeDecode && EPI == kEpiDown) {
-    if (a.y != nullptr) {
-      __threadfence();
-      int last = 0;
-      if (lane == 0) last = atomicAdd(&a.counter[blockIdx.y], 1) == all_chunks - 1;
-      last = __shfl(last, 0, kWave);
-      if (last) {
-#pragma clang fp contract(off)
-        __threadfence();
-        const int i = n0 + lane;
-        // (this workgroup has not read these rows before: plain loads see the
-        // other workgroups' writes once the fences above have ordered them)
-        if (lane < Sh::ROWS && i < a.N) {
-          float acc = 0.f;
-          for (int r0 = 0; r0 < a.top_k; r0 += 8) {
-            float d[8];
-#pragma unroll
-            for (int u = 0; u < 8; ++u)
-              d[u] = r0 + u < a.top_k ? a.out[(int64_t)(r0 + u) * a.out_stride + i] : 0.f;
-#pragma unroll
-            for (int u = 0; u < 8; ++u) {
-              if (r0 + u >= a.top_k || a.top_idx[r0 + u] < 0) continue;
-              const float prod = a.top_w[r0 + u] * d[u];
-              acc = acc + prod;
-            }
-          }
-          if (cc[1] > 0) {
-            const float d = a.out[(int64_t)a.top_k * a.out_stride + i];
-            if (a.variant == kQwen3Next) {
-              const float prod = a.shared_w[0] * d;
-              acc = acc + prod;
-            } else {
-              acc = acc + d;
-            }
-          }
-          a.y[i] = acc;
-        }
-        if (lane == 0) a.counter[blockIdx.y] = 0;
-      }
-    }
-  }
 }
 
 // ------------------------------------------------------------------ host
