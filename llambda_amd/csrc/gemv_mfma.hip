@@ -688,11 +688,8 @@ struct MfmaChoice {
 
 // Stages a wave needs: the ring depth, or fewer when no wave has that many
 // steps (S > 1: one tile's chunks shared by S waves).
-#ifndef LLHIP_GEMV_NBUF_CAP
-#define LLHIP_GEMV_NBUF_CAP 1
-#endif
 static int mfma_nbuf(int depth, int waves, int chunks) {
-  if (waves == 1 || !LLHIP_GEMV_NBUF_CAP) return depth;
+  if (waves == 1) return depth;
   return std::max(1, std::min(depth, (chunks + waves - 1) / waves));
 }
 template <int TYPE>
