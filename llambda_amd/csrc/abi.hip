@@ -1219,7 +1219,7 @@ int llambda_hip_sampler_create(size_t vocab, llambda_hip_sampler** result) {
     s->device = current_device_checked();
     s->vocab = (int64_t)vocab;
     HIPC(hipStreamCreateWithFlags(&s->stream, hipStreamNonBlocking));
-    s->work.alloc(vocab * sizeof(float), "sampling row");
+    s->work.alloc(sample_work_floats((int)vocab) * sizeof(float), "sampling row");
     s->logits.alloc(vocab * sizeof(float), "sampling input");
     s->result.alloc(2 * sizeof(int), "sampling result");
     HIPC(hipHostMalloc((void**)&s->host_result, 2 * sizeof(int), hipHostMallocDefault));

@@ -28,8 +28,13 @@ struct SampleParams {
   float roll;          // random value in [0, 1)
 };
 
-// result[0] = token (-1 on error), result[1] = SampleError or 0.  work: [n]
-// floats of scratch.  logits and work 16-byte aligned.  One workgroup.
+// Scratch floats sample_launch needs for n logits: the penalised row, the
+// first pass's candidates and its per-workgroup counts.
+size_t sample_work_floats(int n);
+
+// result[0] = token (-1 on error), result[1] = SampleError or 0.  work:
+// sample_work_floats(n) floats of scratch.  logits and work 16-byte aligned.
+// Two launches: a multi-workgroup pass over the row, then one workgroup.
 hipError_t sample_launch(const float* logits, float* work, const SampleParams& p, int* result,
                          hipStream_t stream);
 

@@ -1,16 +1,23 @@
 // sample.hip -- sample-token-id-from-logits (llambda.lisp:1272-1317) on the
 // device, for an output head's logits (sample.h).
 //
-// One workgroup of 1024 threads:
+// A first launch of kPrepGroups workgroups, each over one contiguous slice
+// of the row:
 //   1 copy the logits to the scratch row with the repetition penalty applied
 //     to the distinct history tokens (apply-repetition-penalty, 1036-1086;
-//     the tokens marked in an LDS bitmap), NaN rejected
+//     the slice's tokens marked in an LDS bitmap), NaN flagged; and, for
+//     k <= kPrepCap, the slice's candidates: every logit >= the slice's k-th
+//     largest (ties included; more than kPrepCap of them is an overflow).
+//     The k largest of the row are among the union of the slices'.
+// Then one workgroup of 1024 threads:
 //   2 top-k (apply-top-k-with-workspace, 1088-1150): the reference keeps every
 //     logit >= the root of a min-heap of the k largest, i.e. the k-th largest
-//     value; here: a threshold T0 (the k-th largest of the 1024 threads'
-//     maxima, so at least k logits are >= T0), the logits >= T0 compacted
-//     into LDS, and the k-th largest of those by a 4-pass radix select
-//     (8 bits per pass) over order-preserving keys of the floats
+//     value; here the k-th largest of the slices' candidates by a 4-pass
+//     radix select (8 bits per pass) over order-preserving keys of the
+//     floats.  Larger k, or a slice overflow: a threshold T0 (the k-th
+//     largest of the 1024 threads' maxima over the scratch row, so at least
+//     k logits are >= T0), the logits >= T0 compacted into LDS, and their
+//     k-th largest by the radix select
 //   3 the survivors (logit >= cutoff) ordered by index
 //   4 top-p (apply-top-p-with-workspace, 1163-1240) on the survivors: a
 //     stable descending order by rank, then the reference's serial
@@ -30,7 +37,11 @@
 namespace llhip {
 
 constexpr int kSampleThreads = 1024;
-constexpr int kSampleBitmapWords = kSampleMaxVocab / 32;
+constexpr int kPrepGroups = 64;    // first-pass workgroups (row slices)
+constexpr int kPrepThreads = 256;
+constexpr int kPrepCap = 64;       // candidates a slice may pass on
+constexpr int kPrepSlice = kSampleMaxVocab / kPrepGroups;  // longest slice
+static_assert(kPrepGroups * kPrepCap <= kSampleMaxSurvivors, "candidates must fit the LDS lists");
 constexpr float kMaskedLogit = -1.0e30f;  // llambda.lisp:1098, 1172
 
 // Order-preserving key of a float (larger float -> larger key; -0 < +0).
@@ -83,6 +94,7 @@ __device__ float block_exclusive_scan(float v, float* red) {
 // hist: 256 ints of LDS, sel: 3 words of LDS.  The bins of each pass are
 // scanned from the top by wavefront 0 (four bins per lane, a lane prefix sum
 // and a ballot).
+template <int THREADS = kSampleThreads>
 __device__ uint32_t radix_select(const float* vals, int m, int k, int* hist, uint32_t* sel) {
   const int tid = threadIdx.x;
   if (tid == 0) {
@@ -92,10 +104,10 @@ __device__ uint32_t radix_select(const float* vals, int m, int k, int* hist, uin
   }
   for (int pass = 0; pass < 4; ++pass) {
     const int shift = 24 - 8 * pass;
-    for (int b = tid; b < 256; b += kSampleThreads) hist[b] = 0;
+    for (int b = tid; b < 256; b += THREADS) hist[b] = 0;
     __syncthreads();
     const uint32_t prefix = sel[0], mask = sel[1];
-    for (int i = tid; i < m; i += kSampleThreads) {
+    for (int i = tid; i < m; i += THREADS) {
       const uint32_t key = float_key(vals[i]);
       if ((key & mask) == prefix) atomicAdd(&hist[(key >> shift) & 255u], 1);
     }
@@ -137,9 +149,106 @@ __device__ uint32_t radix_select(const float* vals, int m, int k, int* hist, uin
   return sel[0];
 }
 
+// Scratch layout after the row (n rounded up to 4 floats): candidates
+// [kPrepGroups][kPrepCap] values, then their indices, then per slice
+// (count, nan, cutoff key).  A count above kPrepCap is an overflow; the
+// cutoff key is 0 for a slice of at most k logits.
+struct PrepScratch {
+  float* val;
+  int* idx;
+  int* count;
+  int* nan;
+  uint32_t* cut;
+};
+__device__ __host__ inline PrepScratch prep_scratch(float* work, int n) {
+  float* base = work + ((n + 3) & ~3);
+  PrepScratch ps;
+  ps.val = base;
+  ps.idx = reinterpret_cast<int*>(base + kPrepGroups * kPrepCap);
+  ps.count = ps.idx + kPrepGroups * kPrepCap;
+  ps.nan = ps.count + kPrepGroups;
+  ps.cut = reinterpret_cast<uint32_t*>(ps.nan + kPrepGroups);
+  return ps;
+}
+
+size_t sample_work_floats(int n) {
+  return (size_t)((n + 3) & ~3) + 2 * kPrepGroups * kPrepCap + 3 * kPrepGroups;
+}
+
+__global__ void __launch_bounds__(kPrepThreads)
+sample_prep_kernel(const float* __restrict__ logits, float* __restrict__ work, SampleParams p) {
+#pragma clang fp contract(off)
+  __shared__ uint32_t bitmap[kPrepSlice / 32];
+  __shared__ float vals[kPrepSlice];
+  __shared__ int hist[256];
+  __shared__ uint32_t sel[3];
+  __shared__ int nan_flag, count;
+  const int g = blockIdx.x, tid = threadIdx.x, n = p.n;
+  const int lo = (int)((int64_t)g * n / kPrepGroups), hi = (int)((int64_t)(g + 1) * n / kPrepGroups);
+  const int m = hi - lo;
+  const PrepScratch ps = prep_scratch(work, n);
+  for (int w = tid; w < kPrepSlice / 32; w += kPrepThreads) bitmap[w] = 0u;
+  if (tid == 0) {
+    nan_flag = 0;
+    count = 0;
+  }
+  __syncthreads();
+  for (int i = tid; i < p.nh; i += kPrepThreads) {
+    const int t = p.history[i] - lo;
+    if (t >= 0 && t < m) atomicOr(&bitmap[t >> 5], 1u << (t & 31));
+  }
+  __syncthreads();
+  // the slice's logits in one round of loads (they were just written by
+  // another launch), then the penalty
+  constexpr int kPer = kPrepSlice / kPrepThreads;
+  float lv[kPer];
+#pragma unroll
+  for (int j = 0; j < kPer; ++j) {
+    const int i = tid + kPrepThreads * j;
+    lv[j] = i < m ? logits[lo + i] : 0.f;
+  }
+  int nan = 0;
+#pragma unroll
+  for (int j = 0; j < kPer; ++j) {
+    const int i = tid + kPrepThreads * j;
+    if (i < m) {
+      float v = lv[j];
+      if (bitmap[i >> 5] & (1u << (i & 31))) {
+        if (v > 0.0f) v = v / p.penalty;
+        else if (v < 0.0f) v = v * p.penalty;
+      }
+      nan |= v != v;
+      work[lo + i] = v;
+      vals[i] = v;
+    }
+  }
+  if (nan) nan_flag = 1;
+  __syncthreads();
+  const bool topk = p.top_k > 0 && p.top_k < n;
+  uint32_t ck = 0u;
+  if (topk && p.top_k <= kPrepCap && !nan_flag) {
+    // every logit >= the slice's k-th largest (all of them when m <= k)
+    ck = m > p.top_k ? radix_select<kPrepThreads>(vals, m, p.top_k, hist, sel) : 0u;
+    for (int i = tid; i < m; i += kPrepThreads) {
+      if (float_key(vals[i]) >= ck) {
+        const int slot = atomicAdd(&count, 1);
+        if (slot < kPrepCap) {
+          ps.val[g * kPrepCap + slot] = vals[i];
+          ps.idx[g * kPrepCap + slot] = lo + i;
+        }
+      }
+    }
+    __syncthreads();
+  }
+  if (tid == 0) {
+    ps.count[g] = count;
+    ps.nan[g] = nan_flag;
+    ps.cut[g] = ck;
+  }
+}
+
 __global__ void __launch_bounds__(kSampleThreads)
-sample_kernel(const float* __restrict__ logits, float* __restrict__ work, SampleParams p,
-              int* __restrict__ result) {
+sample_kernel(float* __restrict__ work, SampleParams p, int* __restrict__ result) {
 #pragma clang fp contract(off)
   __shared__ int hist[256];
   __shared__ int red[kSampleThreads / 64 + 1];
@@ -147,7 +256,8 @@ sample_kernel(const float* __restrict__ logits, float* __restrict__ work, Sample
   __shared__ uint32_t sel[3];
   __shared__ int flag, ncand;
   __shared__ float s_tmax[kSampleThreads];
-  __shared__ uint32_t bitmap[kSampleBitmapWords];
+  __shared__ int s_cnt[kPrepGroups], s_nan[kPrepGroups];
+  __shared__ uint32_t s_cut[kPrepGroups];
   __shared__ int c_idx[kSampleMaxSurvivors];
   __shared__ float c_val[kSampleMaxSurvivors];
   __shared__ int s_idx[kSampleMaxSurvivors];
@@ -156,64 +266,22 @@ sample_kernel(const float* __restrict__ logits, float* __restrict__ work, Sample
   __shared__ int s_order[kSampleMaxSurvivors];
   const int n = p.n, tid = threadIdx.x;
 
-  // 1. copy with the repetition penalty applied (history tokens marked in an
-  // LDS bitmap), NaN rejected; each thread's maximum over its float4s
+  // the slices' words, one thread each (they were just written on other
+  // XCDs: one round of loads, not one per slice); NaN in any slice is the
+  // reference's error
+  const PrepScratch ps = prep_scratch(work, n);
+  if (tid < kPrepGroups) {
+    s_cnt[tid] = ps.count[tid];
+    s_cut[tid] = ps.cut[tid];
+    s_nan[tid] = ps.nan[tid];
+  }
+  __syncthreads();
   if (tid == 0) {
-    flag = 0;
+    int any = 0;
+    for (int g = 0; g < kPrepGroups; ++g) any |= s_nan[g];
+    flag = any;
     ncand = 0;
   }
-  for (int w = tid; w < kSampleBitmapWords; w += kSampleThreads) bitmap[w] = 0u;
-  __syncthreads();
-  for (int i = tid; i < p.nh; i += kSampleThreads) {
-    const int t = p.history[i];
-    atomicOr(&bitmap[t >> 5], 1u << (t & 31));
-  }
-  __syncthreads();
-  auto penalized = [&](int i, float v) {
-    if (bitmap[i >> 5] & (1u << (i & 31))) {
-      if (v > 0.0f) return v / p.penalty;
-      if (v < 0.0f) return v * p.penalty;
-    }
-    return v;
-  };
-  float tmax = -INFINITY;
-  int nan = 0;
-  {
-    const int n4 = n >> 2;
-    const float4* src = reinterpret_cast<const float4*>(logits);
-    float4* dst = reinterpret_cast<float4*>(work);
-    constexpr int U = 4;
-    for (int base = tid; base < n4; base += U * kSampleThreads) {
-      float4 a[U];
-#pragma unroll
-      for (int u = 0; u < U; ++u) {
-        const int j = base + u * kSampleThreads;
-        a[u] = j < n4 ? src[j] : make_float4(0.f, 0.f, 0.f, 0.f);
-      }
-#pragma unroll
-      for (int u = 0; u < U; ++u) {
-        const int j = base + u * kSampleThreads;
-        if (j < n4) {
-          float4 v = a[u];
-          v.x = penalized(4 * j, v.x);
-          v.y = penalized(4 * j + 1, v.y);
-          v.z = penalized(4 * j + 2, v.z);
-          v.w = penalized(4 * j + 3, v.w);
-          nan |= (v.x != v.x) | (v.y != v.y) | (v.z != v.z) | (v.w != v.w);
-          tmax = fmaxf(fmaxf(tmax, fmaxf(v.x, v.y)), fmaxf(v.z, v.w));
-          dst[j] = v;
-        }
-      }
-    }
-    for (int i = 4 * n4 + tid; i < n; i += kSampleThreads) {
-      const float v = penalized(i, logits[i]);
-      nan |= v != v;
-      tmax = fmaxf(tmax, v);
-      work[i] = v;
-    }
-  }
-  if (nan) flag = 1;
-  s_tmax[tid] = tmax;
   __syncthreads();
   if (flag) {
     if (tid == 0) {
@@ -261,13 +329,91 @@ sample_kernel(const float* __restrict__ logits, float* __restrict__ work, Sample
     return;
   }
 
-  // 2. top-k cutoff.  T0 = the k-th largest of the per-thread maxima: at
-  // least k logits are >= T0, so the k-th largest logit is >= T0 and lies
-  // among the candidates (logits >= T0), which are compacted into LDS.
+  // 2. top-k cutoff.  The slices' candidates when every slice passed all
+  // of its own (k <= kPrepCap, no overflow).  Two lower bounds of the row's
+  // k-th largest prune them: each slice's k-th largest (the slice alone holds
+  // k logits >= it), and the k-th largest of the slices' maxima (k slices
+  // each hold a logit >= it; k <= kPrepCap = kPrepGroups).  The larger one
+  // keeps about k candidates, and at least k.
+  if (tid == 0) {
+    int ok = p.top_k <= kPrepCap;
+    uint32_t cmax = 0u;
+    for (int g = 0; g < kPrepGroups; ++g) {
+      ok &= s_cnt[g] <= kPrepCap;
+      cmax = max(cmax, s_cut[g]);
+    }
+    red[0] = ok;
+    sel[0] = cmax;
+    sel[1] = 0u;
+  }
+  __syncthreads();
+  const bool gathered = red[0] != 0;
+  if (gathered) {
+    // every slot's value and index into LDS in one round of loads (s_val /
+    // s_idx are free until the survivors)
+    constexpr int kSlots = kPrepGroups * kPrepCap / kSampleThreads;
+    static_assert(kSlots * kSampleThreads == kPrepGroups * kPrepCap, "slot split");
+    float sv[kSlots];
+    int si[kSlots];
+#pragma unroll
+    for (int j = 0; j < kSlots; ++j) {
+      sv[j] = ps.val[tid + kSampleThreads * j];
+      si[j] = ps.idx[tid + kSampleThreads * j];
+    }
+#pragma unroll
+    for (int j = 0; j < kSlots; ++j) {
+      s_val[tid + kSampleThreads * j] = sv[j];
+      s_idx[tid + kSampleThreads * j] = si[j];
+    }
+    __syncthreads();
+    // slice maxima (key 0: an empty slice), then the k-th largest of them by
+    // counting: the g with #{> key_g} < k <= #{>= key_g}
+    if (tid < kPrepGroups) {
+      uint32_t mx = 0u;
+      for (int slot = 0; slot < s_cnt[tid]; ++slot)
+        mx = max(mx, float_key(s_val[tid * kPrepCap + slot]));
+      s_cut[tid] = mx;
+    }
+    __syncthreads();
+    if (tid < kPrepGroups) {
+      const uint32_t v = s_cut[tid];
+      int gt = 0, ge = 0;
+      for (int h = 0; h < kPrepGroups; ++h) {
+        gt += s_cut[h] > v;
+        ge += s_cut[h] >= v;
+      }
+      if (gt < p.top_k && p.top_k <= ge) sel[1] = v;  // equal keys write equal values
+    }
+    __syncthreads();
+    // (compared as floats, as the reference compares: -0 >= +0)
+    const float tlow = key_float(max(sel[0], sel[1]));
+    for (int c = tid; c < kPrepGroups * kPrepCap; c += kSampleThreads) {
+      const int g = c / kPrepCap, slot = c - g * kPrepCap;
+      if (slot < s_cnt[g]) {
+        const float v = s_val[c];
+        if (!(v < tlow)) {
+          const int pos = atomicAdd(&ncand, 1);
+          c_val[pos] = v;
+          c_idx[pos] = s_idx[c];
+        }
+      }
+    }
+    __syncthreads();
+  }
+  // ... else T0 = the k-th largest of the per-thread maxima over the scratch
+  // row: at least k logits are >= T0, so the k-th largest logit is >= T0 and
+  // lies among the candidates (logits >= T0), which are compacted into LDS.
   // (k above the thread count: the k-th largest of the whole row itself)
-  float t0 = key_float(p.top_k <= kSampleThreads
-                           ? radix_select(s_tmax, kSampleThreads, p.top_k, hist, sel)
-                           : radix_select(work, n, p.top_k, hist, sel));
+  float t0 = 0.f;
+  if (!gathered) {
+    float tmax = -INFINITY;
+    for (int i = tid; i < n; i += kSampleThreads) tmax = fmaxf(tmax, work[i]);
+    s_tmax[tid] = tmax;
+    __syncthreads();
+    t0 = key_float(p.top_k <= kSampleThreads
+                       ? radix_select(s_tmax, kSampleThreads, p.top_k, hist, sel)
+                       : radix_select(work, n, p.top_k, hist, sel));
+  }
   auto candidate = [&](int i, float v) {
     if (!(v < t0)) {
       const int slot = atomicAdd(&ncand, 1);
@@ -277,7 +423,7 @@ sample_kernel(const float* __restrict__ logits, float* __restrict__ work, Sample
       }
     }
   };
-  for (int attempt = 0; attempt < 2; ++attempt) {
+  for (int attempt = 0; attempt < 2 && !gathered; ++attempt) {
     const int n4 = n >> 2;
     const float4* w4 = reinterpret_cast<const float4*>(work);
     constexpr int U = 4;
@@ -317,7 +463,25 @@ sample_kernel(const float* __restrict__ logits, float* __restrict__ work, Sample
     }
     return;
   }
-  const float cutoff = key_float(radix_select(c_val, cand, p.top_k, hist, sel));
+  // the k-th largest candidate: by counting when they fit one per thread
+  // (the c with #{> v_c} < k <= #{>= v_c}), else the radix select
+  float cutoff;
+  if (cand <= kSampleThreads) {
+    if (tid < cand) {
+      const float v = c_val[tid];
+      int gt = 0, ge = 0;
+      for (int d = 0; d < cand; ++d) {
+        gt += c_val[d] > v;
+        ge += c_val[d] >= v;
+      }
+      if (gt < p.top_k && p.top_k <= ge) fred[0] = v;  // equal values write equal values
+    }
+    __syncthreads();
+    cutoff = fred[0];
+    __syncthreads();
+  } else {
+    cutoff = key_float(radix_select(c_val, cand, p.top_k, hist, sel));
+  }
 
   // 3. survivors (candidates >= cutoff) in index order
   if (tid == 0) flag = 0;
@@ -412,8 +576,10 @@ sample_kernel(const float* __restrict__ logits, float* __restrict__ work, Sample
 
 hipError_t sample_launch(const float* logits, float* work, const SampleParams& p, int* result,
                          hipStream_t stream) {
-  hipLaunchKernelGGL(sample_kernel, dim3(1), dim3(kSampleThreads), 0, stream, logits, work, p,
-                     result);
+  if (p.n <= 0 || p.n > kSampleMaxVocab) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(sample_prep_kernel, dim3(kPrepGroups), dim3(kPrepThreads), 0, stream, logits,
+                     work, p);
+  hipLaunchKernelGGL(sample_kernel, dim3(1), dim3(kSampleThreads), 0, stream, work, p, result);
   return hipGetLastError();
 }
 
