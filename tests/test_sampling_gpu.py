@@ -78,6 +78,31 @@ def test_ties_at_the_cutoff(sampler):
         sampler.sample(np.zeros(n, dtype=np.float32), top_k=5, top_p=0.9, random_value=0.5)
 
 
+def test_ties_within_the_slices(sampler):
+    """Ties at the top-k cutoff that every row slice can still pass on in
+    full (at most 64 candidates a slice), and a cutoff at zero where -0.0 and
+    +0.0 tie (the reference keeps every logit >= the k-th largest)."""
+    rng = np.random.default_rng(11)
+    n = 128256
+    for trial in range(4):
+        x = (rng.standard_normal(n) * 2.0).astype(np.float32)
+        top = np.float32(x.max() + 1.0)
+        spots = rng.choice(n, size=20, replace=False)  # spread over the slices
+        x[spots] = top
+        for k in (5, 20, 25):
+            roll = float(np.float32(rng.random()))
+            kw = dict(top_k=k, top_p=0.9, temperature=1.0, random_value=roll)
+            assert sampler.sample(x, **kw) == oracle.sample_token(x, **kw), (trial, k)
+    x = -np.abs(rng.standard_normal(n)).astype(np.float32) - 1.0
+    zeros = rng.choice(n, size=12, replace=False)
+    x[zeros[:6]] = np.float32(0.0)
+    x[zeros[6:]] = np.float32(-0.0)
+    for k in (3, 6, 12):
+        for roll in (0.1, 0.6, 0.95):
+            kw = dict(top_k=k, top_p=1.0, temperature=1.0, random_value=roll)
+            assert sampler.sample(x, **kw) == oracle.sample_token(x, **kw), (k, roll)
+
+
 def test_without_top_k(sampler):
     rng = np.random.default_rng(6)
     n = 128256
