@@ -270,15 +270,30 @@ __global__ void __launch_bounds__(256) moe_combine_kernel(MoePlan p, float* __re
   const int i = blockIdx.x * blockDim.x + threadIdx.x;
   const int H = p.hidden, K = p.top_k;
   if (i >= H) return;
+  // the ranks' outputs (just written by another launch, on other XCDs) are
+  // loaded 8 ranks at a time before the sums, which run in rank order
+  const float dsh = has_shared ? p.down_out[(int64_t)(tokens * K + t) * H + i] : 0.f;
   float acc = 0.f;
-  for (int r = 0; r < K; ++r) {
-    const int q = t * K + r;
-    if (p.top_idx[q] < 0) continue;
-    const float prod = p.top_w[q] * p.down_out[(int64_t)q * H + i];
-    acc = acc + prod;
+  constexpr int kBatch = 8;
+  for (int r0 = 0; r0 < K; r0 += kBatch) {
+    float d[kBatch], wv[kBatch];
+    int ix[kBatch];
+#pragma unroll
+    for (int b = 0; b < kBatch; ++b) {
+      const int q = t * K + min(r0 + b, K - 1);
+      ix[b] = p.top_idx[q];
+      wv[b] = p.top_w[q];
+      d[b] = p.down_out[(int64_t)q * H + i];
+    }
+#pragma unroll
+    for (int b = 0; b < kBatch; ++b) {
+      if (r0 + b >= K || ix[b] < 0) continue;
+      const float prod = wv[b] * d[b];
+      acc = acc + prod;
+    }
   }
   if (has_shared) {
-    const float d = p.down_out[(int64_t)(tokens * K + t) * H + i];
+    const float d = dsh;
     if (p.variant == kQwen3Next) {
       const float prod = p.shared_w[t] * d;
       acc = acc + prod;
