@@ -500,8 +500,13 @@ __device__ __forceinline__ void gemv_mfma_body(uint8_t* lds, int wg, int nwg, co
   // bytes the whole workgroup loads at once.
   constexpr int kGroups = kMfmaWaves / S;
   const int grp = wave / S, sw = wave - grp * S;
-  const int wg_first = (int)(((int64_t)wg * tiles) / nwg);
-  const int wg_end = (int)(((int64_t)(wg + 1) * tiles) / nwg);
+  // Workgroups b and b + nwg / 2 (dispatched to the same CU when the grid
+  // is two per CU) take the adjacent ranges 2 b and 2 b + 1 (measured: the
+  // Llama decode token -1.2%, the head unchanged).
+  const int half = (nwg + 1) >> 1;
+  const int rix = wg < half ? 2 * wg : 2 * (wg - half) + 1;
+  const int wg_first = (int)(((int64_t)rix * tiles) / nwg);
+  const int wg_end = (int)(((int64_t)(rix + 1) * tiles) / nwg);
   const int rounds = (wg_end - wg_first + kGroups - 1) / kGroups;  // same for every group
   const int first_tile = wg_first + grp;
   const int tile_step = kGroups;
