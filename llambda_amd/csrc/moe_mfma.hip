@@ -165,6 +165,20 @@ hipError_t router_mfma_launch(const float* x, int T, const float* R, int Er, int
 // `row` is the dword-aligned LDS image of one row's chunk; the chunk's first
 // byte is at row + sh (sh < 4; 0 for Q4_K).  codes(): lane g's codes of
 // scale group j as bf16 128 + q.  scale(): that group's delta and c.
+// kPieces 16-byte pieces hold a chunk and its shift; rows sit kPitch bytes
+// apart in LDS, an odd number of pieces, so that the 16 rows one read
+// instruction touches start in 16 different bank quads (an even pitch of
+// 12 or 14 pieces puts them in 2 or 4 and serialises the reads 8- or
+// 4-fold).  The pad piece of each row is a second copy of its last piece.
+#ifndef LLHIP_MOE_ODD_PITCH
+#define LLHIP_MOE_ODD_PITCH 1
+#endif
+#ifndef LLHIP_MOE_Q5_SPREAD
+#define LLHIP_MOE_Q5_SPREAD 1
+#endif
+__host__ __device__ constexpr int odd_pitch(int pieces) {
+  return 16 * (LLHIP_MOE_ODD_PITCH ? (pieces | 1) : pieces);
+}
 
 __device__ __forceinline__ uint32_t lds_dword(const uint8_t* row, uint32_t i) {
   return reinterpret_cast<const uint32_t*>(row)[i];
@@ -189,7 +203,8 @@ struct GemmB;
 // low nibbles for even j, high for odd (llambda.lisp:4145-4201, 6815-6859).
 template <>
 struct GemmB<kQ4_K> {
-  static constexpr int kSpan = 144, kPitch = 144, kSteps = 8, kStepK = 32;
+  static constexpr int kSpan = 144, kPieces = 9, kPitch = odd_pitch(kPieces), kSteps = 8,
+                       kStepK = 32;
   static constexpr bool kWide = true;
   typedef bf16x8 Frag;
   static __device__ __forceinline__ Frag codes(const uint8_t* row, uint32_t, int j, int g,
@@ -226,7 +241,8 @@ struct GemmB<kQ4_K> {
 // 6919-6978); lane g takes l = 16s + 4g .. +3 of group u = 8h + 2k + s.
 template <>
 struct GemmB<kQ6_K> {
-  static constexpr int kSpan = 210, kPitch = 224, kSteps = 16, kStepK = 16;
+  static constexpr int kSpan = 210, kPieces = 14, kPitch = odd_pitch(kPieces), kSteps = 16,
+                       kStepK = 16;
   static constexpr bool kWide = false;
   typedef shortx4 Frag;
   static __device__ __forceinline__ Frag codes(const uint8_t* row, uint32_t sh, int u, int g,
@@ -250,11 +266,15 @@ struct GemmB<kQ6_K> {
 
 // Q5_0: chunk = 8 blocks of 22 B (llambda.lisp:3965-3990, 4037-4066).
 // Lane g takes elements 8g .. 8g+7: qs bytes 8 (g & 1) .. +7, low nibbles
-// for g < 2, high for g >= 2, fifth bits from qh bits 8g .. 8g+7.  `hbits`
-// maps a qh byte to its eight bits at bit 4 of eight bytes.
+// for g < 2, high for g >= 2, fifth bits from qh bits 8g .. 8g+7, each
+// moved to bit 4 of its code byte: for a nibble v, v * 0x204081 puts bit i
+// of v at bit 8i (the copies shifted by 0, 7, 14 and 21 occupy disjoint
+// bits, so nothing carries), and the mask keeps bits 0, 8, 16 and 24.
+// (`hbits`, a 256-entry table in LDS, is the alternative.)
 template <>
 struct GemmB<kQ5_0> {
-  static constexpr int kSpan = 176, kPitch = 192, kSteps = 8, kStepK = 32;
+  static constexpr int kSpan = 176, kPieces = 12, kPitch = odd_pitch(kPieces), kSteps = 8,
+                       kStepK = 32;
   static constexpr bool kWide = true;
   typedef bf16x8 Frag;
   static __device__ __forceinline__ Frag codes(const uint8_t* row, uint32_t sh, int j, int g,
@@ -263,8 +283,16 @@ struct GemmB<kQ5_0> {
     const uint32_t os = o + 6u + 8u * (uint32_t)(g & 1);
     const uint32_t shift = 4u * (uint32_t)(g >> 1);
     const uint32_t q0 = lds_dword_even(row, os) >> shift, q1 = lds_dword_even(row, os + 4u) >> shift;
+#if LLHIP_MOE_Q5_SPREAD
+    const uint32_t ob = o + 2u + (uint32_t)g;
+    const uint32_t w = lds_dword(row, ob >> 2), bit = 8u * (ob & 3u);
+    const uint32_t h0 = (__builtin_amdgcn_ubfe(w, bit, 4u) * 0x204081u) & 0x01010101u;
+    const uint32_t h1 = (__builtin_amdgcn_ubfe(w, bit + 4u, 4u) * 0x204081u) & 0x01010101u;
+    return codes_to_b((q0 & 0x0F0F0F0Fu) | (h0 << 4), (q1 & 0x0F0F0F0Fu) | (h1 << 4));
+#else
     const uint2 hb = hbits[lds_u8(row, o + 2u + (uint32_t)g)];
     return codes_to_b((q0 & 0x0F0F0F0Fu) | hb.x, (q1 & 0x0F0F0F0Fu) | hb.y);
+#endif
   }
   static __device__ __forceinline__ void scale(const uint8_t* row, uint32_t sh, int j, float& delta,
                                                float& c) {
@@ -277,7 +305,8 @@ struct GemmB<kQ5_0> {
 // code u = q ^ 0x80 = q + 128 (0..255) is exact in bf16 (8 significant bits).
 template <>
 struct GemmB<kQ8_0> {
-  static constexpr int kSpan = 272, kPitch = 288, kSteps = 8, kStepK = 32;
+  static constexpr int kSpan = 272, kPieces = 18, kPitch = odd_pitch(kPieces), kSteps = 8,
+                       kStepK = 32;
   static constexpr bool kWide = true;
   typedef bf16x8 Frag;
   static __device__ __forceinline__ uint32_t pack2(uint32_t u, int k) {
@@ -359,7 +388,7 @@ struct GemmShape {
   static constexpr int S_OFF = ROWBUF + 1024;                       // decode: its 16 group sums
   static constexpr int STAGE = PIPE == kPipeDecode ? ROWBUF + 1024 + 256 : ROWBUF;
   static constexpr int DEPTH = PIPE == kPipeWide ? 1 : PIPE == kPipeDouble ? 2 : 8;
-  static constexpr int LUT = TYPE == kQ5_0 ? 256 * 8 : 0;          // Q5_0 fifth-bit table
+  static constexpr int LUT = TYPE == kQ5_0 && !LLHIP_MOE_Q5_SPREAD ? 256 * 8 : 0;  // fifth bits
   static constexpr int DMA = NB * LOADS + (PIPE == kPipeDecode ? 2 : 0);  // loads per stage
   // decode: the waves' partial sums, added in wave order
   static constexpr int RED = PIPE == kPipeDecode ? kWaves * NS * NB * 64 * 16 : 0;
@@ -419,7 +448,7 @@ moe_gemm_kernel(MoeGemmArgs args) {
 
   // Q5_0: qh byte -> its bits at bit 4 of eight bytes
   const uint2* hbits = reinterpret_cast<const uint2*>(lds);
-  if constexpr (TYPE == kQ5_0) {
+  if constexpr (Sh::LUT > 0) {
     uint2* lut = reinterpret_cast<uint2*>(lds);
     for (int b = threadIdx.x; b < 256; b += 64 * Sh::kWaves) {
       uint2 v = {0u, 0u};
@@ -463,7 +492,7 @@ moe_gemm_kernel(MoeGemmArgs args) {
     const int idx = min(64 * i + lane, Sh::PIECES - 1);
     const int r = idx / Sh::PPR;
     prow[i] = (uint32_t)min(n0 + r, a.N - 1) * rb;
-    ppc[i] = 16u * (uint32_t)(idx - r * Sh::PPR);
+    ppc[i] = 16u * (uint32_t)min(idx - r * Sh::PPR, B::kPieces - 1);
   }
   uint32_t brow[NS];
 #pragma unroll
@@ -744,7 +773,11 @@ static hipError_t launch_gemm_t(const MoeGemmArgs& a_in, int max_chunks, hipStre
   MoeGemmArgs a = a_in;
   const int nchunk = (std::max(a.K, a.joint ? a.s_K : 0) + 255) / 256;
   const int per_wave = (nchunk + Sh::kWaves - 1) / Sh::kWaves;
-  a.depth = PIPE == kPipeDecode ? std::max(1, std::min(Sh::DEPTH, per_wave)) : Sh::DEPTH;
+  // the decode ring: at most DEPTH stages, no more than a wave's chunks, and
+  // no more than fit the 160 KB of LDS a workgroup may hold
+  constexpr int kLdsMax = 160 * 1024;
+  const int fit = (kLdsMax - gemm_lds_bytes<TYPE, EPI, PIPE>(0)) / (Sh::kWaves * Sh::STAGE);
+  a.depth = PIPE == kPipeDecode ? std::max(1, std::min({Sh::DEPTH, per_wave, fit})) : Sh::DEPTH;
   const int lds = gemm_lds_bytes<TYPE, EPI, PIPE>(a.depth);
   const auto kernel = moe_gemm_kernel<TYPE, EPI, MT, PIPE, ALIGNED>;
   if (lds > 65536) {
