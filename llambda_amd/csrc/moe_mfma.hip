@@ -163,8 +163,10 @@ hipError_t router_mfma_launch(const float* x, int T, const float* R, int Er, int
 
 // ------------------------------------------------------ B operand per type
 // `row` is the dword-aligned LDS image of one row's chunk; the chunk's first
-// byte is at row + sh (sh < 4; 0 for Q4_K).  codes(): lane g's codes of
-// scale group j as bf16 128 + q.  scale(): that group's delta and c.
+// byte is at row + sh (sh < 4; 0 for Q4_K).  fetch(): the LDS words holding
+// lane g's codes of scale group j; decode(): those codes as bf16 128 + q
+// (split so that the next group's reads are in flight while this group
+// decodes and multiplies).  scale(): the group's delta and c.
 // kPieces 16-byte pieces hold a chunk and its shift; rows sit kPitch bytes
 // apart in LDS, an odd number of pieces, so that the 16 rows one read
 // instruction touches start in 16 different bank quads (an even pitch of
@@ -173,9 +175,6 @@ hipError_t router_mfma_launch(const float* x, int T, const float* R, int Er, int
 #ifndef LLHIP_MOE_ODD_PITCH
 #define LLHIP_MOE_ODD_PITCH 1
 #endif
-#ifndef LLHIP_MOE_Q5_SPREAD
-#define LLHIP_MOE_Q5_SPREAD 1
-#endif
 __host__ __device__ constexpr int odd_pitch(int pieces) {
   return 16 * (LLHIP_MOE_ODD_PITCH ? (pieces | 1) : pieces);
 }
@@ -183,16 +182,20 @@ __host__ __device__ constexpr int odd_pitch(int pieces) {
 __device__ __forceinline__ uint32_t lds_dword(const uint8_t* row, uint32_t i) {
   return reinterpret_cast<const uint32_t*>(row)[i];
 }
-// Four bytes at byte offset o (o even) of the dword-aligned image.
-__device__ __forceinline__ uint32_t lds_dword_even(const uint8_t* row, uint32_t o) {
-  const uint32_t* q = reinterpret_cast<const uint32_t*>(row) + (o >> 2);
-  return (o & 3u) ? __builtin_amdgcn_alignbyte(q[1], q[0], o & 3u) : q[0];
-}
 __device__ __forceinline__ uint32_t lds_u16_even(const uint8_t* row, uint32_t o) {
   return (lds_dword(row, o >> 2) >> (8 * (o & 3u))) & 0xFFFFu;
 }
 __device__ __forceinline__ uint32_t lds_u8(const uint8_t* row, uint32_t o) {
   return (lds_dword(row, o >> 2) >> (8 * (o & 3u))) & 0xFFu;
+}
+
+// Bit i of a nibble v at bit 8i: v * 0x204081 masked to bits 0, 8, 16, 24.
+// Written as the 24-bit multiply (full rate) because the compiler, once it
+// keeps the constant in a scalar register, emits the quarter-rate 32-bit one.
+__device__ __forceinline__ uint32_t spread_nibble(uint32_t v) {
+  uint32_t r;
+  asm("v_mul_u32_u24 %0, 0x204081, %1" : "=v"(r) : "v"(v));
+  return r & 0x01010101u;
 }
 
 template <int TYPE>
@@ -207,9 +210,11 @@ struct GemmB<kQ4_K> {
                        kStepK = 32;
   static constexpr bool kWide = true;
   typedef bf16x8 Frag;
-  static __device__ __forceinline__ Frag codes(const uint8_t* row, uint32_t, int j, int g,
-                                               const uint2*) {
-    const uint2 q = *reinterpret_cast<const uint2*>(row + 16 + 32 * (j >> 1) + 8 * g);
+  typedef uint2 Raw;
+  static __device__ __forceinline__ Raw fetch(const uint8_t* row, uint32_t, int j, int g) {
+    return *reinterpret_cast<const uint2*>(row + 16 + 32 * (j >> 1) + 8 * g);
+  }
+  static __device__ __forceinline__ Frag decode(const Raw& q, uint32_t, int j, int) {
     const uint32_t c0 = (j & 1) ? (q.x >> 4) & 0x0F0F0F0Fu : q.x & 0x0F0F0F0Fu;
     const uint32_t c1 = (j & 1) ? (q.y >> 4) & 0x0F0F0F0Fu : q.y & 0x0F0F0F0Fu;
     return codes_to_b(c0, c1);
@@ -245,12 +250,17 @@ struct GemmB<kQ6_K> {
                        kStepK = 16;
   static constexpr bool kWide = false;
   typedef shortx4 Frag;
-  static __device__ __forceinline__ Frag codes(const uint8_t* row, uint32_t sh, int u, int g,
-                                               const uint2*) {
+  typedef u32x4 Raw;
+  static __device__ __forceinline__ Raw fetch(const uint8_t* row, uint32_t, int u, int g) {
     const int h = u >> 3, k = (u >> 1) & 3, s = u & 1;
     const uint32_t ol = 64 * h + 32 * (k & 1) + 16 * s + 4 * g, oh = 128 + 32 * h + 16 * s + 4 * g;
-    const uint32_t ql = __builtin_amdgcn_alignbyte(lds_dword(row, (ol >> 2) + 1), lds_dword(row, ol >> 2), sh);
-    const uint32_t qh = __builtin_amdgcn_alignbyte(lds_dword(row, (oh >> 2) + 1), lds_dword(row, oh >> 2), sh);
+    return u32x4{lds_dword(row, ol >> 2), lds_dword(row, (ol >> 2) + 1), lds_dword(row, oh >> 2),
+                 lds_dword(row, (oh >> 2) + 1)};
+  }
+  static __device__ __forceinline__ Frag decode(const Raw& w, uint32_t sh, int u, int) {
+    const int k = (u >> 1) & 3;
+    const uint32_t ql = __builtin_amdgcn_alignbyte(w[1], w[0], sh);
+    const uint32_t qh = __builtin_amdgcn_alignbyte(w[3], w[2], sh);
     const uint32_t nib = (ql >> (4 * (k >> 1))) & 0x0F0F0F0Fu;
     const uint32_t hb = ((qh >> (2 * k)) & 0x03030303u) << 4;
     return codes4_to_b(nib | hb);
@@ -270,29 +280,29 @@ struct GemmB<kQ6_K> {
 // moved to bit 4 of its code byte: for a nibble v, v * 0x204081 puts bit i
 // of v at bit 8i (the copies shifted by 0, 7, 14 and 21 occupy disjoint
 // bits, so nothing carries), and the mask keeps bits 0, 8, 16 and 24.
-// (`hbits`, a 256-entry table in LDS, is the alternative.)
 template <>
 struct GemmB<kQ5_0> {
   static constexpr int kSpan = 176, kPieces = 12, kPitch = odd_pitch(kPieces), kSteps = 8,
                        kStepK = 32;
   static constexpr bool kWide = true;
   typedef bf16x8 Frag;
-  static __device__ __forceinline__ Frag codes(const uint8_t* row, uint32_t sh, int j, int g,
-                                               const uint2* hbits) {
+  typedef u32x4 Raw;  // three words from the qs bytes' dword, the qh byte's word
+  static __device__ __forceinline__ Raw fetch(const uint8_t* row, uint32_t sh, int j, int g) {
     const uint32_t o = sh + 22u * (uint32_t)j;
-    const uint32_t os = o + 6u + 8u * (uint32_t)(g & 1);
+    const uint32_t os = (o + 6u + 8u * (uint32_t)(g & 1)) >> 2, ob = (o + 2u + (uint32_t)g) >> 2;
+    return u32x4{lds_dword(row, os), lds_dword(row, os + 1u), lds_dword(row, os + 2u),
+                 lds_dword(row, ob)};
+  }
+  static __device__ __forceinline__ Frag decode(const Raw& w, uint32_t sh, int j, int g) {
+    const uint32_t o = sh + 22u * (uint32_t)j;
+    const uint32_t a = (o + 6u + 8u * (uint32_t)(g & 1)) & 3u;  // 0 or 2
     const uint32_t shift = 4u * (uint32_t)(g >> 1);
-    const uint32_t q0 = lds_dword_even(row, os) >> shift, q1 = lds_dword_even(row, os + 4u) >> shift;
-#if LLHIP_MOE_Q5_SPREAD
-    const uint32_t ob = o + 2u + (uint32_t)g;
-    const uint32_t w = lds_dword(row, ob >> 2), bit = 8u * (ob & 3u);
-    const uint32_t h0 = (__builtin_amdgcn_ubfe(w, bit, 4u) * 0x204081u) & 0x01010101u;
-    const uint32_t h1 = (__builtin_amdgcn_ubfe(w, bit + 4u, 4u) * 0x204081u) & 0x01010101u;
+    const uint32_t q0 = __builtin_amdgcn_alignbyte(w[1], w[0], a) >> shift;
+    const uint32_t q1 = __builtin_amdgcn_alignbyte(w[2], w[1], a) >> shift;
+    const uint32_t bit = 8u * ((o + 2u + (uint32_t)g) & 3u);
+    const uint32_t h0 = spread_nibble(__builtin_amdgcn_ubfe(w[3], bit, 4u));
+    const uint32_t h1 = spread_nibble(__builtin_amdgcn_ubfe(w[3], bit + 4u, 4u));
     return codes_to_b((q0 & 0x0F0F0F0Fu) | (h0 << 4), (q1 & 0x0F0F0F0Fu) | (h1 << 4));
-#else
-    const uint2 hb = hbits[lds_u8(row, o + 2u + (uint32_t)g)];
-    return codes_to_b((q0 & 0x0F0F0F0Fu) | hb.x, (q1 & 0x0F0F0F0Fu) | hb.y);
-#endif
   }
   static __device__ __forceinline__ void scale(const uint8_t* row, uint32_t sh, int j, float& delta,
                                                float& c) {
@@ -314,11 +324,15 @@ struct GemmB<kQ8_0> {
     return __builtin_amdgcn_perm(__builtin_bit_cast(uint32_t, f1), __builtin_bit_cast(uint32_t, f0),
                                  0x07060302u);
   }
-  static __device__ __forceinline__ Frag codes(const uint8_t* row, uint32_t sh, int j, int g,
-                                               const uint2*) {
-    const uint32_t os = sh + 34u * (uint32_t)j + 2u + 8u * (uint32_t)g;
-    const uint32_t u0 = lds_dword_even(row, os) ^ 0x80808080u;
-    const uint32_t u1 = lds_dword_even(row, os + 4u) ^ 0x80808080u;
+  typedef u32x4 Raw;  // three words from the codes' dword
+  static __device__ __forceinline__ Raw fetch(const uint8_t* row, uint32_t sh, int j, int g) {
+    const uint32_t os = (sh + 34u * (uint32_t)j + 2u + 8u * (uint32_t)g) >> 2;
+    return u32x4{lds_dword(row, os), lds_dword(row, os + 1u), lds_dword(row, os + 2u), 0u};
+  }
+  static __device__ __forceinline__ Frag decode(const Raw& w, uint32_t sh, int j, int g) {
+    const uint32_t a = (sh + 34u * (uint32_t)j + 2u + 8u * (uint32_t)g) & 3u;
+    const uint32_t u0 = __builtin_amdgcn_alignbyte(w[1], w[0], a) ^ 0x80808080u;
+    const uint32_t u1 = __builtin_amdgcn_alignbyte(w[2], w[1], a) ^ 0x80808080u;
     u32x4 v = {pack2(u0, 0), pack2(u0, 2), pack2(u1, 0), pack2(u1, 2)};
     return __builtin_bit_cast(bf16x8, v);
   }
@@ -382,13 +396,13 @@ struct GemmShape {
   static constexpr int PPR = B::kPitch / 16;                        // 16-byte pieces per row
   static constexpr int PIECES = ROWS * PPR;
   static constexpr int LOADS = (PIECES + 63) / 64;                  // per matrix
-  static constexpr int ROWBUF = 1024 * LOADS * NB;                  // rows of one chunk
+  static constexpr int MATBUF = 1024 * LOADS;                       // one matrix's rows
+  static constexpr int ROWBUF = MATBUF * NB;                        // rows of one chunk
   static constexpr int TABLE = NS * NB * B::kSteps * 16 * 8;        // (delta, -c) per group and row
   static constexpr int A_OFF = ROWBUF;                              // decode: the token's chunk
   static constexpr int S_OFF = ROWBUF + 1024;                       // decode: its 16 group sums
   static constexpr int STAGE = PIPE == kPipeDecode ? ROWBUF + 1024 + 256 : ROWBUF;
-  static constexpr int DEPTH = PIPE == kPipeWide ? 1 : PIPE == kPipeDouble ? 2 : 8;
-  static constexpr int LUT = TYPE == kQ5_0 && !LLHIP_MOE_Q5_SPREAD ? 256 * 8 : 0;  // fifth bits
+  static constexpr int DEPTH = PIPE == kPipeWide ? 1 : PIPE == kPipeDecode ? 8 : 2;
   static constexpr int DMA = NB * LOADS + (PIPE == kPipeDecode ? 2 : 0);  // loads per stage
   // decode: the waves' partial sums, added in wave order
   static constexpr int RED = PIPE == kPipeDecode ? kWaves * NS * NB * 64 * 16 : 0;
@@ -399,7 +413,7 @@ struct GemmShape {
 template <int TYPE, int EPI, int PIPE>
 constexpr int gemm_lds_bytes(int depth) {
   using Sh = GemmShape<TYPE, EPI, PIPE>;
-  return Sh::LUT + Sh::RED + Sh::kWaves * (depth * Sh::STAGE + Sh::TABLE);
+  return Sh::RED + Sh::kWaves * (depth * Sh::STAGE + Sh::TABLE);
 }
 
 // ------------------------------------------------------------ the kernel
@@ -446,26 +460,10 @@ moe_gemm_kernel(MoeGemmArgs args) {
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int n = lane & 15, g = lane >> 4;
 
-  // Q5_0: qh byte -> its bits at bit 4 of eight bytes
-  const uint2* hbits = reinterpret_cast<const uint2*>(lds);
-  if constexpr (Sh::LUT > 0) {
-    uint2* lut = reinterpret_cast<uint2*>(lds);
-    for (int b = threadIdx.x; b < 256; b += 64 * Sh::kWaves) {
-      uint2 v = {0u, 0u};
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        v.x |= ((uint32_t)(b >> i) & 1u) << (8 * i + 4);
-        v.y |= ((uint32_t)(b >> (i + 4)) & 1u) << (8 * i + 4);
-      }
-      lut[b] = v;
-    }
-    if constexpr (Sh::kWaves > 1) __syncthreads();
-  }
-
   const int n0 = PIPE == kPipeDecode ? by * Sh::ROWS : (by * Sh::kWaves + wave) * Sh::ROWS;
   if (n0 >= a.N) return;  // uniform over the workgroup for the decode pipeline
   const int depth = PIPE == kPipeDecode ? a.depth : Sh::DEPTH;
-  uint8_t* wlds = lds + Sh::LUT + Sh::RED + wave * (depth * Sh::STAGE + Sh::TABLE);
+  uint8_t* wlds = lds + Sh::RED + wave * (depth * Sh::STAGE + Sh::TABLE);
   float2* table = reinterpret_cast<float2*>(wlds + depth * Sh::STAGE);
   const uint32_t wlds_addr = lds_address(wlds);
 
@@ -511,7 +509,7 @@ moe_gemm_kernel(MoeGemmArgs args) {
 #pragma unroll
       for (int i = 0; i < Sh::LOADS; ++i)
         load_lds16(base[nb], ((prow[i] + koff) & ~3u) + ppc[i],
-                   st + (uint32_t)(nb * Sh::LOADS * 1024 + 1024 * i));
+                   st + (uint32_t)(nb * Sh::MATBUF + 1024 * i));
     if constexpr (PIPE == kPipeDecode) {
       // lane l: 16 bytes [16 l, 16 l + 16) of the token's chunk; the sums
       // (16 floats; lanes past them re-read the last one into slack)
@@ -549,7 +547,7 @@ moe_gemm_kernel(MoeGemmArgs args) {
     for (int m = 0; m < NS; ++m)
 #pragma unroll
       for (int nb = 0; nb < NB; ++nb) {
-        const uint8_t* row = stage + nb * Sh::LOADS * 1024 + (16 * m + n) * B::kPitch;
+        const uint8_t* row = stage + nb * Sh::MATBUF + (16 * m + n) * B::kPitch;
 #pragma unroll
         for (int e = 0; e < KS / 4; ++e) {
           const int j = g * (KS / 4) + e;
@@ -559,23 +557,48 @@ moe_gemm_kernel(MoeGemmArgs args) {
           table[((m * NB + nb) * KS + j) * 16 + n] = float2{ok ? delta : 0.f, ok ? -c : 0.f};
         }
       }
+    // Software pipeline over the groups: the LDS words (codes and delta) of
+    // group j + 1 and, in the wide pipeline, whose activations come from
+    // memory, those of group j + 2 are requested before group j decodes and
+    // multiplies, so that neither latency stalls the group's MFMAs.
+    constexpr int kAhead = PIPE == kPipeWide ? 2 : 0;
+    typename B::Raw raw[2][NS][NB];
+    float dl[2][NS][NB];
+    AF af[kAhead + 1][MT];
+    auto fetch = [&](int j, typename B::Raw (&r)[NS][NB], float (&d)[NS][NB]) {
+#pragma unroll
+      for (int m = 0; m < NS; ++m)
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb) {
+          const uint8_t* row = stage + nb * Sh::MATBUF + (16 * m + n) * B::kPitch;
+          r[m][nb] = B::fetch(row, sh[m], j, g);
+          d[m][nb] = table[((m * NB + nb) * KS + j) * 16 + n].x;
+        }
+    };
+#pragma unroll
+    for (int j = 0; j < kAhead; ++j)
+      if (FULL || j < valid)
+#pragma unroll
+        for (int i = 0; i < MT; ++i) get_a(i, j, af[j][i]);
+    fetch(0, raw[0], dl[0]);
 #pragma unroll
     for (int j = 0; j < KS; ++j) {
       if (FULL || j < valid) {
-        AF af[MT];
+        if (j + kAhead < KS && (FULL || j + kAhead < valid))
 #pragma unroll
-        for (int i = 0; i < MT; ++i) get_a(i, j, af[i]);
+          for (int i = 0; i < MT; ++i) get_a(i, j + kAhead, af[(j + kAhead) % (kAhead + 1)][i]);
+        if (j + 1 < KS && (FULL || j + 1 < valid)) fetch(j + 1, raw[(j + 1) & 1], dl[(j + 1) & 1]);
 #pragma unroll
         for (int m = 0; m < NS; ++m)
 #pragma unroll
           for (int nb = 0; nb < NB; ++nb) {
-            const uint8_t* row = stage + nb * Sh::LOADS * 1024 + (16 * m + n) * B::kPitch;
-            const typename B::Frag bf = B::codes(row, sh[m], j, g, hbits);
-            const float delta = table[((m * NB + nb) * KS + j) * 16 + n].x;
+            const typename B::Frag bf = B::decode(raw[j & 1][m][nb], sh[m], j, g);
+            const float delta = dl[j & 1][m][nb];
 #pragma unroll
             for (int i = 0; i < MT; ++i) {
-              floatx4 d = mfma_b(af[i].hi, bf, floatx4{0.f, 0.f, 0.f, 0.f});
-              d = mfma_b(af[i].lo, bf, d);
+              const AF& a_ = af[j % (kAhead + 1)][i];
+              floatx4 d = mfma_b(a_.hi, bf, floatx4{0.f, 0.f, 0.f, 0.f});
+              d = mfma_b(a_.lo, bf, d);
               floatx4& t = tot[i][m][nb];
               t[0] = fmaf(delta, d[0], t[0]);
               t[1] = fmaf(delta, d[1], t[1]);
@@ -616,6 +639,18 @@ moe_gemm_kernel(MoeGemmArgs args) {
     else return s[gi];
   };
 
+  // activations and group sums of chunk kc of the lane's token into registers
+  auto load_regs = [&](int kc, AF (&ar)[KS], float (&sr)[NQ]) {
+    const int valid = min(KS, groups - kc * KS);
+#pragma unroll
+    for (int j = 0; j < KS; ++j) {
+      if (j < valid) ar[j].load(arow[0] + 512 * kc + AF::offset(j, g));
+      else ar[j].zero();
+    }
+#pragma unroll
+    for (int q = 0; q < NQ; ++q) sr[q] = row_sum(srow[0], min(kc * KS + 4 * q + g, groups - 1));
+  };
+
   if constexpr (PIPE == kPipeWide) {
     for (int kc = 0; kc < nchunk; ++kc) {
       issue(kc, 0);
@@ -631,16 +666,6 @@ moe_gemm_kernel(MoeGemmArgs args) {
     // chunk activations and sums in registers, one chunk ahead
     AF acur[KS], anext[KS];
     float scur[NQ], snext[NQ];
-    auto load_regs = [&](int kc, AF (&ar)[KS], float (&sr)[NQ]) {
-      const int valid = min(KS, groups - kc * KS);
-#pragma unroll
-      for (int j = 0; j < KS; ++j) {
-        if (j < valid) ar[j].load(arow[0] + 512 * kc + AF::offset(j, g));
-        else ar[j].zero();
-      }
-#pragma unroll
-      for (int q = 0; q < NQ; ++q) sr[q] = row_sum(srow[0], min(kc * KS + 4 * q + g, groups - 1));
-    };
     issue(0, 0);
     load_regs(0, acur, scur);
     __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
@@ -701,7 +726,7 @@ moe_gemm_kernel(MoeGemmArgs args) {
       if (it + depth < mine) issue(kc + Sh::kWaves * depth, slot);
     }
     // partial sums of the four K slices, added in wave order by wave 0
-    floatx4* red = reinterpret_cast<floatx4*>(lds + Sh::LUT);
+    floatx4* red = reinterpret_cast<floatx4*>(lds);
 #pragma unroll
     for (int m = 0; m < NS; ++m)
 #pragma unroll

@@ -185,6 +185,34 @@ def test_small_qwen_shapes(hip):
     check_layer(layer, x, "qwen small")
 
 
+# Batches whose average load per expert (tokens * k / E) is above 16 pairs:
+# chunks of two token tiles (the wide pipeline) against the oracle.  Every
+# weight type, relu^2 (one matrix) and silu-gate (two side by side) products.
+@pytest.mark.parametrize("variant,types,tokens", [
+    ("nemotron", (ggml.Q5_0, ggml.Q5_0), 64), ("nemotron", (ggml.Q5_0, ggml.Q5_0), 96),
+    ("nemotron", (ggml.Q4_K, ggml.Q6_K), 96), ("nemotron", (ggml.Q8_0, ggml.Q8_0), 96),
+    ("qwen", (ggml.Q4_K, ggml.Q6_K), 64), ("qwen", (ggml.Q4_K, ggml.Q6_K), 96),
+    ("qwen", (ggml.Q8_0, ggml.Q5_0), 96)])
+def test_long_chunks(hip, variant, types, tokens):
+    rng = np.random.default_rng(12 + tokens)
+    if variant == "nemotron":
+        layer = synthetic_nemotron_h(rng, hidden=512, experts=8, top_k=3, ffn=256, shared_ffn=256,
+                                     expert_type=types[0], down_type=types[1])
+    else:
+        layer = synthetic_qwen3next(rng, hidden=512, experts=8, top_k=3, ffn=256, shared_ffn=256,
+                                    gate_type=types[0], down_type=types[1])
+    avg = tokens * layer.top_k / layer.expert_count
+    assert 16 < avg
+    x = synthetic.activations(rng, tokens, layer.hidden)
+    y, _ = check_layer(layer, x, f"{variant} {types} long chunks")
+    # the same tokens in a batch of 5 (one-tile chunks) give the same bits
+    session = HipMoeSession(layer)
+    try:
+        np.testing.assert_array_equal(session.run(x[3:8]), y[3:8])
+    finally:
+        session.close()
+
+
 def test_nemotron_unnormalised_scaled(hip):
     rng = np.random.default_rng(10)
     layer = synthetic_nemotron_h(rng, hidden=512, experts=64, top_k=4, ffn=256, shared_ffn=0,
