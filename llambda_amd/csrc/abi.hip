@@ -426,7 +426,10 @@ struct llambda_hip_moe_session {
     shared_w.alloc(T * sizeof(float), "shared weights");
     perm.alloc(pairs * sizeof(int), "permutation");
     p.capacity = tokens;
-    chunks.alloc((size_t)moe_max_chunks(p, tokens, 1) * sizeof(MoeChunk), "chunk table");
+    // (+ 8: the batch products read the entry of every workgroup of their
+    // grid, which is padded to a multiple of 8, before they compare its
+    // index with the count)
+    chunks.alloc((size_t)(moe_max_chunks(p, tokens, 1) + 8) * sizeof(MoeChunk), "chunk table");
     down_out.alloc(pairs * (size_t)p.hidden * sizeof(float), "expert outputs");
     const size_t H = (size_t)p.hidden;
     // the decode pipeline stages whole 256-element chunks (1 KB of split

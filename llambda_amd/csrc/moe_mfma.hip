@@ -441,12 +441,14 @@ moe_gemm_kernel(MoeGemmArgs args) {
     by = (L >> 3) % T;
   }
   const int* cc = args.chunk_counts;
+  // joint launches: routed chunks, then the shared expert's (their entries
+  // follow the routed ones in the table).  Except for a separate shared
+  // launch, the entry's index does not depend on the counts, and it is read
+  // together with them (the table has room for every workgroup of the grid).
+  const MoeChunk ch = args.chunks[(!args.joint && args.group ? cc[0] : 0) + bx];
   const int all_chunks = cc[0] + cc[1];
   const int nchunks = args.joint ? all_chunks : cc[args.group];
   if (bx >= nchunks) return;
-  // joint launches: routed chunks, then the shared expert's (their entries
-  // follow the routed ones in the table)
-  const MoeChunk ch = args.chunks[args.joint ? bx : (args.group ? cc[0] : 0) + bx];
   MoeGemmArgs a = args;
   if (args.joint && bx >= cc[0]) {
     a.w0 = args.s_w0;
@@ -478,6 +480,16 @@ moe_gemm_kernel(MoeGemmArgs args) {
     arow[i] = a.aq + r * a.aq_stride;
     srow[i] = a.as + r * a.as_stride;
   }
+  // the pairs whose outputs this lane writes (tokens 16 i + 4 g + r of each
+  // tile), read now rather than after the products
+  int qout[MT][4];
+#pragma unroll
+  for (int i = 0; i < MT; ++i)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int tk = 16 * i + 4 * g + r;
+      qout[i][r] = tk < ch.count ? a.perm[ch.start + tk] : 0;
+    }
   const uint8_t* base[NB];
   base[0] = uniform_ptr(a.w0 + (int64_t)ch.expert * a.expert_stride);
   if constexpr (NB == 2) base[NB - 1] = uniform_ptr(a.w1 + (int64_t)ch.expert * a.expert_stride);
@@ -752,7 +764,7 @@ moe_gemm_kernel(MoeGemmArgs args) {
     for (int r = 0; r < 4; ++r) {
       const int tk = 16 * i + 4 * g + r;
       const bool ok_t = tk < ch.count;
-      const int q = ok_t ? a.perm[ch.start + tk] : 0;
+      const int q = qout[i][r];
       if constexpr (EPI == kEpiDown) {
 #pragma unroll
         for (int m = 0; m < NS; ++m) {
