@@ -495,15 +495,6 @@ moe_gemm_kernel(MoeGemmArgs args) {
   if constexpr (NB == 2) base[NB - 1] = uniform_ptr(a.w1 + (int64_t)ch.expert * a.expert_stride);
   const uint32_t rb = (uint32_t)a.row_bytes;
 
-  // this lane's DMA pieces: (row, piece) per load instruction
-  uint32_t prow[Sh::LOADS], ppc[Sh::LOADS];
-#pragma unroll
-  for (int i = 0; i < Sh::LOADS; ++i) {
-    const int idx = min(64 * i + lane, Sh::PIECES - 1);
-    const int r = idx / Sh::PPR;
-    prow[i] = (uint32_t)min(n0 + r, a.N - 1) * rb;
-    ppc[i] = 16u * (uint32_t)min(idx - r * Sh::PPR, B::kPieces - 1);
-  }
   uint32_t brow[NS];
 #pragma unroll
   for (int m = 0; m < NS; ++m) brow[m] = (uint32_t)min(n0 + 16 * m + n, a.N - 1) * rb;
@@ -513,15 +504,26 @@ moe_gemm_kernel(MoeGemmArgs args) {
 
   // Issue chunk kc's loads into stage `slot`: the rows; for the decode
   // pipeline also the token's 256 split elements (1 KB) and 16 group sums.
+  // Lane l of load instruction i carries piece 64 i + l of the stage: row
+  // r = piece / PPR, its 16-byte piece p = piece % PPR (the pad piece p =
+  // PPR - 1 repeats the last one).  The offsets are formed anew at every
+  // issue (the empty asm keeps the compiler from holding them in registers
+  // across the products, where the wide pipeline has none to spare).
   auto issue = [&](int kc, int slot) {
     const uint32_t koff = (uint32_t)kc * (uint32_t)B::kSpan;
     const uint32_t st = wlds_addr + (uint32_t)(slot * Sh::STAGE);
+    int lane_v = lane;
+    asm volatile("" : "+v"(lane_v));
 #pragma unroll
-    for (int nb = 0; nb < NB; ++nb)
+    for (int i = 0; i < Sh::LOADS; ++i) {
+      const int idx = min(64 * i + lane_v, Sh::PIECES - 1);
+      const int r = idx / Sh::PPR;
+      const uint32_t off = (((uint32_t)min(n0 + r, a.N - 1) * rb + koff) & ~3u) +
+                           16u * (uint32_t)min(idx - r * Sh::PPR, B::kPieces - 1);
 #pragma unroll
-      for (int i = 0; i < Sh::LOADS; ++i)
-        load_lds16(base[nb], ((prow[i] + koff) & ~3u) + ppc[i],
-                   st + (uint32_t)(nb * Sh::MATBUF + 1024 * i));
+      for (int nb = 0; nb < NB; ++nb)
+        load_lds16(base[nb], off, st + (uint32_t)(nb * Sh::MATBUF + 1024 * i));
+    }
     if constexpr (PIPE == kPipeDecode) {
       // lane l: 16 bytes [16 l, 16 l + 16) of the token's chunk; the sums
       // (16 floats; lanes past them re-read the last one into slack)
@@ -665,13 +667,34 @@ moe_gemm_kernel(MoeGemmArgs args) {
 
   if constexpr (PIPE == kPipeWide) {
     for (int kc = 0; kc < nchunk; ++kc) {
+      const int gbase = kc * KS;
+      // The chunk's group sums and its first group's activations are
+      // requested with its rows, under the one wait; the later groups'
+      // activations load two groups ahead of use (two groups here would not
+      // fit the registers).  Lanes of padding tokens read the chunk's first
+      // token (their outputs are dropped).
+      AF a_first[1][MT];
+      float sv[MT][NQ];
+#pragma unroll
+      for (int j = 0; j < 1; ++j)
+#pragma unroll
+        for (int i = 0; i < MT; ++i) {
+          if (gbase + j < groups) a_first[j][i].load(arow[i] + 512 * kc + AF::offset(j, g));
+          else a_first[j][i].zero();
+        }
+#pragma unroll
+      for (int i = 0; i < MT; ++i)
+#pragma unroll
+        for (int q = 0; q < NQ; ++q) sv[i][q] = row_sum(srow[i], min(gbase + 4 * q + g, groups - 1));
       issue(kc, 0);
       __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
-      const int gbase = kc * KS;
-      // lanes of padding tokens read the chunk's first token (outputs dropped)
       run_chunk(
-          kc, wlds, [&](int i, int j, AF& af) { af.load(arow[i] + 512 * kc + AF::offset(j, g)); },
-          [&](int i, int q) { return row_sum(srow[i], min(gbase + 4 * q + g, groups - 1)); });
+          kc, wlds,
+          [&](int i, int j, AF& af) {
+            if (j < 1) af = a_first[j][i];
+            else af.load(arow[i] + 512 * kc + AF::offset(j, g));
+          },
+          [&](int i, int q) { return sv[i][q]; });
       __builtin_amdgcn_s_waitcnt(kWaitLgkm0);
     }
   } else if constexpr (PIPE == kPipeDouble) {
