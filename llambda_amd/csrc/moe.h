@@ -103,7 +103,8 @@ struct MoeGemmArgs {
   float* out;
   int64_t out_stride;
   int depth;      // LDS stages per wave (set by the launcher)
-  int row_tiles;  // row tiles of the grid (set by the launcher)
+  int row_tiles;  // row-tile groups of the grid (set by the launcher)
+  int tiles_per_wg;  // consecutive row tiles per workgroup (set by the launcher)
   // routed and shared chunks in one launch (same weight type): the shared
   // expert's tensors, rows and K
   int joint;

@@ -462,7 +462,10 @@ moe_gemm_kernel(MoeGemmArgs args) {
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int n = lane & 15, g = lane >> 4;
 
-  const int n0 = PIPE == kPipeDecode ? by * Sh::ROWS : (by * Sh::kWaves + wave) * Sh::ROWS;
+  // first rows of this wave (the double pipeline's workgroups take
+  // tiles_per_wg consecutive row tiles of the chunk, one after the other)
+  const int n0 = PIPE == kPipeDecode ? by * Sh::ROWS
+                                     : by * a.tiles_per_wg * Sh::WG_ROWS + wave * Sh::ROWS;
   if (n0 >= a.N) return;  // uniform over the workgroup for the decode pipeline
   const int depth = PIPE == kPipeDecode ? a.depth : Sh::DEPTH;
   uint8_t* wlds = lds + Sh::RED + wave * (depth * Sh::STAGE + Sh::TABLE);
@@ -495,9 +498,14 @@ moe_gemm_kernel(MoeGemmArgs args) {
   if constexpr (NB == 2) base[NB - 1] = uniform_ptr(a.w1 + (int64_t)ch.expert * a.expert_stride);
   const uint32_t rb = (uint32_t)a.row_bytes;
 
+  // byte offsets of this lane's rows (their chunks' shift when rows are not
+  // dword multiples)
   uint32_t brow[NS];
+  auto set_rows = [&](int n0t) {
 #pragma unroll
-  for (int m = 0; m < NS; ++m) brow[m] = (uint32_t)min(n0 + 16 * m + n, a.N - 1) * rb;
+    for (int m = 0; m < NS; ++m) brow[m] = (uint32_t)min(n0t + 16 * m + n, a.N - 1) * rb;
+  };
+  set_rows(n0);
 
   const int groups = a.K / B::kStepK;
   const int nchunk = (a.K + 255) >> 8;
@@ -509,7 +517,7 @@ moe_gemm_kernel(MoeGemmArgs args) {
   // PPR - 1 repeats the last one).  The offsets are formed anew at every
   // issue (the empty asm keeps the compiler from holding them in registers
   // across the products, where the wide pipeline has none to spare).
-  auto issue = [&](int kc, int slot) {
+  auto issue = [&](int kc, int slot, int n0t) {
     const uint32_t koff = (uint32_t)kc * (uint32_t)B::kSpan;
     const uint32_t st = wlds_addr + (uint32_t)(slot * Sh::STAGE);
     int lane_v = lane;
@@ -518,7 +526,7 @@ moe_gemm_kernel(MoeGemmArgs args) {
     for (int i = 0; i < Sh::LOADS; ++i) {
       const int idx = min(64 * i + lane_v, Sh::PIECES - 1);
       const int r = idx / Sh::PPR;
-      const uint32_t off = (((uint32_t)min(n0 + r, a.N - 1) * rb + koff) & ~3u) +
+      const uint32_t off = (((uint32_t)min(n0t + r, a.N - 1) * rb + koff) & ~3u) +
                            16u * (uint32_t)min(idx - r * Sh::PPR, B::kPieces - 1);
 #pragma unroll
       for (int nb = 0; nb < NB; ++nb)
@@ -665,6 +673,53 @@ moe_gemm_kernel(MoeGemmArgs args) {
     for (int q = 0; q < NQ; ++q) sr[q] = row_sum(srow[0], min(kc * KS + 4 * q + g, groups - 1));
   };
 
+  // ---------------------------------------------------------- epilogue
+  // lane (n, G) holds tokens 16 i + 4 G + r of rows n0t + 16 m + n
+  auto finish = [&](int n0t) {
+#pragma unroll
+    for (int i = 0; i < MT; ++i) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int tk = 16 * i + 4 * g + r;
+        const bool ok_t = tk < ch.count;
+        const int q = qout[i][r];
+        if constexpr (EPI == kEpiDown) {
+#pragma unroll
+          for (int m = 0; m < NS; ++m) {
+            const int row = n0t + 16 * m + n;
+            if (ok_t && row < a.N) a.out[(int64_t)q * a.out_stride + row] = tot[i][m][0][r];
+          }
+        } else {
+          uint16_t* oq = a.oq + (int64_t)q * a.oq_stride;
+          float* os = a.os + (int64_t)q * a.os_stride;
+#pragma unroll
+          for (int m = 0; m < NS; ++m) {
+            const int row = n0t + 16 * m + n;
+            float act;
+            if constexpr (EPI == kEpiSwiglu) {
+#pragma clang fp contract(off)
+              act = silu_ref(tot[i][m][0][r]) * tot[i][m][1][r];  // llambda.lisp:5386-5401
+            } else {
+              act = relu2_ref(tot[i][m][0][r]);  // llambda.lisp:5921-5926
+            }
+            uint32_t hb, lb;
+            float sum;
+            split_bf16(act, hb, lb, sum);
+            const bool ok = ok_t && row < a.N;
+            if (ok) {
+              uint16_t* p = oq + 64 * (row >> 5) + (row & 31);
+              p[0] = (uint16_t)hb;
+              p[32] = (uint16_t)lb;
+            }
+            // the 16 rows of the subtile are one 16-group of the activation row
+            const float s16 = group_sum(ok ? sum : 0.f, 4);
+            if (n == 0 && ok) os[row >> 4] = s16;
+          }
+        }
+      }
+    }
+  };
+
   if constexpr (PIPE == kPipeWide) {
     for (int kc = 0; kc < nchunk; ++kc) {
       const int gbase = kc * KS;
@@ -686,7 +741,7 @@ moe_gemm_kernel(MoeGemmArgs args) {
       for (int i = 0; i < MT; ++i)
 #pragma unroll
         for (int q = 0; q < NQ; ++q) sv[i][q] = row_sum(srow[i], min(gbase + 4 * q + g, groups - 1));
-      issue(kc, 0);
+      issue(kc, 0, n0);
       __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
       run_chunk(
           kc, wlds,
@@ -698,36 +753,56 @@ moe_gemm_kernel(MoeGemmArgs args) {
       __builtin_amdgcn_s_waitcnt(kWaitLgkm0);
     }
   } else if constexpr (PIPE == kPipeDouble) {
-    // chunk activations and sums in registers, one chunk ahead
+    // Steps (tile, chunk) over the workgroup's row tiles that hold rows of
+    // this wave, tile by tile; the rows (by DMA) and the activations and
+    // sums (into registers) of the next step load while a step computes, so
+    // the chain of dependent loads before the first step is paid once for
+    // tiles_per_wg tiles.
+    const int ntile = min(a.tiles_per_wg, (a.N - n0 + Sh::WG_ROWS - 1) / Sh::WG_ROWS);
+    const int steps = ntile * nchunk;
     AF acur[KS], anext[KS];
     float scur[NQ], snext[NQ];
-    issue(0, 0);
+    issue(0, 0, n0);
     load_regs(0, acur, scur);
     __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
-    for (int kc = 0; kc < nchunk; ++kc) {
-      const bool more = kc + 1 < nchunk;
+    for (int st = 0, tt = 0, kc = 0; st < steps; ++st) {
+      const bool more = st + 1 < steps;
+      const int kc1 = kc + 1 < nchunk ? kc + 1 : 0;
+      const int tt1 = kc + 1 < nchunk ? tt : tt + 1;
       if (more) {
-        issue(kc + 1, (kc + 1) & 1);
-        load_regs(kc + 1, anext, snext);
+        issue(kc1, (st + 1) & 1, n0 + tt1 * Sh::WG_ROWS);
+        load_regs(kc1, anext, snext);
       }
       run_chunk(
-          kc, wlds + (kc & 1) * Sh::STAGE, [&](int, int j, AF& af) { af = acur[j]; },
+          kc, wlds + (st & 1) * Sh::STAGE, [&](int, int j, AF& af) { af = acur[j]; },
           [&](int, int q) { return scur[q]; });
       __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
       __builtin_amdgcn_s_waitcnt(kWaitLgkm0);
+      if (kc + 1 == nchunk) {
+        finish(n0 + tt * Sh::WG_ROWS);
+#pragma unroll
+        for (int i = 0; i < MT; ++i)
+#pragma unroll
+          for (int m = 0; m < NS; ++m)
+#pragma unroll
+            for (int nb = 0; nb < NB; ++nb) tot[i][m][nb] = floatx4{0.f, 0.f, 0.f, 0.f};
+        if (more && !ALIGNED) set_rows(n0 + tt1 * Sh::WG_ROWS);
+      }
       if (more) {
 #pragma unroll
         for (int j = 0; j < KS; ++j) acur[j] = anext[j];
 #pragma unroll
         for (int q = 0; q < NQ; ++q) scur[q] = snext[q];
       }
+      kc = kc1;
+      tt = tt1;
     }
   } else {
     // decode: one token; wave w takes chunks w, w + 4, ... through a ring of
     // `depth` stages filled ahead of use
     const int mine = (nchunk - wave + Sh::kWaves - 1) / Sh::kWaves;
     const int first = min(depth, mine);
-    for (int s = 0; s < first; ++s) issue(wave + Sh::kWaves * s, s);
+    for (int s = 0; s < first; ++s) issue(wave + Sh::kWaves * s, s, n0);
     for (int it = 0; it < mine; ++it) {
       const int kc = wave + Sh::kWaves * it;
       const int ahead = min(mine, it + depth) - it - 1;  // stages issued after this one
@@ -758,7 +833,7 @@ moe_gemm_kernel(MoeGemmArgs args) {
             else return ssum[gi];
           });
       __builtin_amdgcn_s_waitcnt(kWaitLgkm0);
-      if (it + depth < mine) issue(kc + Sh::kWaves * depth, slot);
+      if (it + depth < mine) issue(kc + Sh::kWaves * depth, slot, n0);
     }
     // partial sums of the four K slices, added in wave order by wave 0
     floatx4* red = reinterpret_cast<floatx4*>(lds);
@@ -779,50 +854,7 @@ moe_gemm_kernel(MoeGemmArgs args) {
       }
   }
 
-  // ---------------------------------------------------------- epilogue
-  // lane (n, G) holds tokens 16 i + 4 G + r of row n0 + 16 m + n
-#pragma unroll
-  for (int i = 0; i < MT; ++i) {
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int tk = 16 * i + 4 * g + r;
-      const bool ok_t = tk < ch.count;
-      const int q = qout[i][r];
-      if constexpr (EPI == kEpiDown) {
-#pragma unroll
-        for (int m = 0; m < NS; ++m) {
-          const int row = n0 + 16 * m + n;
-          if (ok_t && row < a.N) a.out[(int64_t)q * a.out_stride + row] = tot[i][m][0][r];
-        }
-      } else {
-        uint16_t* oq = a.oq + (int64_t)q * a.oq_stride;
-        float* os = a.os + (int64_t)q * a.os_stride;
-#pragma unroll
-        for (int m = 0; m < NS; ++m) {
-          const int row = n0 + 16 * m + n;
-          float act;
-          if constexpr (EPI == kEpiSwiglu) {
-#pragma clang fp contract(off)
-            act = silu_ref(tot[i][m][0][r]) * tot[i][m][1][r];  // llambda.lisp:5386-5401
-          } else {
-            act = relu2_ref(tot[i][m][0][r]);  // llambda.lisp:5921-5926
-          }
-          uint32_t hb, lb;
-          float sum;
-          split_bf16(act, hb, lb, sum);
-          const bool ok = ok_t && row < a.N;
-          if (ok) {
-            uint16_t* p = oq + 64 * (row >> 5) + (row & 31);
-            p[0] = (uint16_t)hb;
-            p[32] = (uint16_t)lb;
-          }
-          // the 16 rows of the subtile are one 16-group of the activation row
-          const float s16 = group_sum(ok ? sum : 0.f, 4);
-          if (n == 0 && ok) os[row >> 4] = s16;
-        }
-      }
-    }
-  }
+  if constexpr (PIPE != kPipeDouble) finish(n0);
 }
 
 // ------------------------------------------------------------------ host
@@ -847,10 +879,15 @@ static hipError_t launch_gemm_t(const MoeGemmArgs& a_in, int max_chunks, hipStre
   }
   const int rows = a.joint ? std::max(a.N, a.s_N) : a.N;
   const int tiles = (rows + Sh::WG_ROWS - 1) / Sh::WG_ROWS;
-  a.row_tiles = tiles;
+  // the double pipeline's workgroups take two row tiles when K is short (at
+  // most 4 chunks), so that their prologue is paid once for both (measured
+  // on Qwen3Next B=256: one, two and four tiles within 2% of each other,
+  // two ahead)
+  a.tiles_per_wg = PIPE == kPipeDouble && nchunk <= 4 ? 2 : 1;
+  a.row_tiles = (tiles + a.tiles_per_wg - 1) / a.tiles_per_wg;
   // batch pipelines: the XCD-grouped 1-D grid (chunks padded to a multiple of 8)
   const dim3 grid = PIPE == kPipeDecode ? dim3(max_chunks, tiles)
-                                        : dim3(((max_chunks + 7) / 8) * 8 * tiles);
+                                        : dim3(((max_chunks + 7) / 8) * 8 * a.row_tiles);
   hipLaunchKernelGGL(kernel, grid, dim3(64 * Sh::kWaves), lds, stream, a);
   return hipGetLastError();
 }
