@@ -1114,12 +1114,13 @@ struct llambda_hip_sampler {
   int device = 0;
   hipStream_t stream = nullptr;
   int64_t vocab = 0;
-  DevBuf work, logits, history, result;
+  DevBuf work, logits, history;
   size_t history_cap = 0;
-  // pinned host staging of the history and the result (small synchronous
-  // copies without a pageable bounce)
+  // pinned host staging of long histories (a small copy without a pageable
+  // bounce) and the mapped result the kernel writes
   int* host_history = nullptr;
   int* host_result = nullptr;
+  int* dev_result = nullptr;  // host_result as the device addresses it
   ~llambda_hip_sampler() {
     if (host_history) (void)hipHostFree(host_history);
     if (host_result) (void)hipHostFree(host_result);
@@ -1175,7 +1176,8 @@ int64_t run_sampler(llambda_hip_sampler* s, const float* dev_logits, int64_t n,
   if (!topk && a->top_p < 1.0f)
     failf("sample: top-p without top-k is not supported on the device (it needs a sort of the "
           "whole row)");
-  if (distinct.size() > s->history_cap) {
+  const bool inline_history = distinct.size() <= (size_t)kSampleInlineHistory;
+  if (!inline_history && distinct.size() > s->history_cap) {
     const size_t cap = std::max<size_t>(distinct.size(), 2 * s->history_cap);
     s->history.alloc(cap * sizeof(int), "sampling history");
     if (s->host_history) HIPC(hipHostFree(s->host_history));
@@ -1183,23 +1185,27 @@ int64_t run_sampler(llambda_hip_sampler* s, const float* dev_logits, int64_t n,
     HIPC(hipHostMalloc((void**)&s->host_history, cap * sizeof(int), hipHostMallocDefault));
     s->history_cap = cap;
   }
-  if (!distinct.empty()) {
+  SampleParams p;
+  p.n = (int)n;
+  p.nh = (int)distinct.size();
+  if (inline_history) {
+    p.history = nullptr;
+    std::copy(distinct.begin(), distinct.end(), p.hist_inline);
+  } else {
     std::copy(distinct.begin(), distinct.end(), s->host_history);
     HIPC(hipMemcpyAsync(s->history.ptr, s->host_history, distinct.size() * sizeof(int),
                         hipMemcpyHostToDevice, s->stream));
+    p.history = s->history.as<int>();
   }
-  SampleParams p;
-  p.n = (int)n;
-  p.history = s->history.as<int>();
-  p.nh = (int)distinct.size();
   p.penalty = a->repetition_penalty;
   p.top_k = (int)std::min<int64_t>(a->top_k, n);
   p.top_p = a->top_p;
   p.temperature = a->temperature;
   p.roll = a->random_value;
-  HIPC(sample_launch(dev_logits, s->work.as<float>(), p, s->result.as<int>(), s->stream));
   int* res = s->host_result;
-  HIPC(hipMemcpyAsync(res, s->result.ptr, 2 * sizeof(int), hipMemcpyDeviceToHost, s->stream));
+  res[0] = -1;
+  res[1] = -1;
+  HIPC(sample_launch(dev_logits, s->work.as<float>(), p, s->dev_result, s->stream));
   HIPC(hipStreamSynchronize(s->stream));
   if (res[1] == kSampleErrNaN) failf("sample: NaN logit");
   if (res[1] == kSampleErrTies)
@@ -1224,8 +1230,11 @@ int llambda_hip_sampler_create(size_t vocab, llambda_hip_sampler** result) {
     HIPC(hipStreamCreateWithFlags(&s->stream, hipStreamNonBlocking));
     s->work.alloc(sample_work_floats((int)vocab) * sizeof(float), "sampling row");
     s->logits.alloc(vocab * sizeof(float), "sampling input");
-    s->result.alloc(2 * sizeof(int), "sampling result");
-    HIPC(hipHostMalloc((void**)&s->host_result, 2 * sizeof(int), hipHostMallocDefault));
+    // the result lands in mapped, coherent pinned memory: the kernel writes
+    // it there and no copy follows the launches
+    HIPC(hipHostMalloc((void**)&s->host_result, 2 * sizeof(int),
+                       hipHostMallocMapped | hipHostMallocCoherent));
+    HIPC(hipHostGetDevicePointer((void**)&s->dev_result, s->host_result, 0));
     *result = s.release();
   });
 }

@@ -96,6 +96,7 @@ __global__ void __launch_bounds__(256) topk_gate_kernel(MoePlan p, int tokens, i
   float acc[JPL + 1];
   int col[JPL + 1];
   bool use[JPL + 1];
+  float bias[JPL];
 #pragma unroll
   for (int j = 0; j <= JPL; ++j) {
     const int e = j < JPL ? lane + kWave * j : E;
@@ -104,13 +105,36 @@ __global__ void __launch_bounds__(256) topk_gate_kernel(MoePlan p, int tokens, i
     const float v = p.router_part[(int64_t)t * ld + col[j]];
     acc[j] = use[j] ? v : 0.f;
   }
-  for (int ks = 1; ks < p.router_ks; ++ks) {
-    const float* part = p.router_part + ((int64_t)ks * tokens + t) * ld;
-    float v[JPL + 1];
 #pragma unroll
-    for (int j = 0; j <= JPL; ++j) v[j] = part[col[j]];
+  for (int j = 0; j < JPL; ++j)
+    bias[j] = p.variant == kNemotronH ? p.bias[min(lane + kWave * j, E - 1)] : 0.f;
+  // The slices were just written by the router launch, on other XCDs: up to
+  // kMaxSlices of them are requested in one round (rather than one round
+  // per slice), then added in slice order.
+  constexpr int kMaxSlices = 8;
+  if (p.router_ks <= kMaxSlices) {
+    float v[kMaxSlices - 1][JPL + 1];
 #pragma unroll
-    for (int j = 0; j <= JPL; ++j) acc[j] = use[j] ? acc[j] + v[j] : 0.f;
+    for (int ks = 1; ks < kMaxSlices; ++ks)
+      if (ks < p.router_ks) {
+        const float* part = p.router_part + ((int64_t)ks * tokens + t) * ld;
+#pragma unroll
+        for (int j = 0; j <= JPL; ++j) v[ks - 1][j] = part[col[j]];
+      }
+#pragma unroll
+    for (int ks = 1; ks < kMaxSlices; ++ks)
+      if (ks < p.router_ks)
+#pragma unroll
+        for (int j = 0; j <= JPL; ++j) acc[j] = use[j] ? acc[j] + v[ks - 1][j] : 0.f;
+  } else {
+    for (int ks = 1; ks < p.router_ks; ++ks) {
+      const float* part = p.router_part + ((int64_t)ks * tokens + t) * ld;
+      float v[JPL + 1];
+#pragma unroll
+      for (int j = 0; j <= JPL; ++j) v[j] = part[col[j]];
+#pragma unroll
+      for (int j = 0; j <= JPL; ++j) acc[j] = use[j] ? acc[j] + v[j] : 0.f;
+    }
   }
   float vals[JPL];
 #pragma unroll
@@ -119,7 +143,7 @@ __global__ void __launch_bounds__(256) topk_gate_kernel(MoePlan p, int tokens, i
     float v = -INFINITY;
     if (e < E) {
       float raw = acc[j];
-      if (p.variant == kNemotronH) raw = __fadd_rn(raw, p.bias[e]);
+      if (p.variant == kNemotronH) raw = __fadd_rn(raw, bias[j]);
       lg[e] = raw;
       v = selectable(raw);
     }

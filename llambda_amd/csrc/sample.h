@@ -16,9 +16,14 @@ enum SampleError : int {
   kSampleErrTies = 2,  // more than kSampleMaxSurvivors logits tie at or above the cutoff
 };
 
+// Histories of up to this many distinct tokens travel in the launch's
+// arguments (no copy to the device before the launch).
+constexpr int kSampleInlineHistory = 128;
+
 struct SampleParams {
   int n;               // logits
-  const int* history;  // device, distinct token ids < n (host-validated)
+  const int* history;  // device, distinct token ids < n (host-validated), or
+                       // null: the ids are hist_inline[0 .. nh)
   int nh;
   float penalty;       // repetition penalty (> 0)
   int top_k;           // 0 or >= n: no top-k (top_p must then be 1); at most
@@ -26,6 +31,7 @@ struct SampleParams {
   float top_p;         // (0, 1]
   float temperature;   // > 0
   float roll;          // random value in [0, 1)
+  int hist_inline[kSampleInlineHistory];
 };
 
 // Scratch floats sample_launch needs for n logits: the penalised row, the

@@ -194,7 +194,7 @@ sample_prep_kernel(const float* __restrict__ logits, float* __restrict__ work, S
   }
   __syncthreads();
   for (int i = tid; i < p.nh; i += kPrepThreads) {
-    const int t = p.history[i] - lo;
+    const int t = (p.history ? p.history[i] : p.hist_inline[i]) - lo;
     if (t >= 0 && t < m) atomicOr(&bitmap[t >> 5], 1u << (t & 31));
   }
   __syncthreads();

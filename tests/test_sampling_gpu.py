@@ -63,6 +63,25 @@ def test_full_vocab_matches_oracle(sampler, top_k, top_p, temperature):
         assert got == want, (trial, got, want)
 
 
+def test_long_histories(sampler):
+    # up to 128 distinct history tokens travel in the launch's arguments,
+    # longer histories through a device buffer: both sides of the threshold,
+    # with the penalised tokens among the top candidates
+    rng = np.random.default_rng(77)
+    n = 128256
+    for distinct in (127, 128, 129, 1000):
+        x = _head_like(rng, n)
+        top = np.argsort(-x)[:200]
+        hist = rng.choice(n, size=distinct, replace=False)
+        hist[:50] = top[:50]
+        hist = rng.permutation(hist).tolist()
+        hist += hist[:5]  # repeats do not count
+        for roll in (0.05, 0.5, 0.95):
+            kw = dict(history=hist, repetition_penalty=1.3, top_k=40, top_p=0.9,
+                      temperature=1.0, random_value=roll)
+            assert sampler.sample(x, **kw) == oracle.sample_token(x, **kw), (distinct, roll)
+
+
 def test_ties_at_the_cutoff(sampler):
     rng = np.random.default_rng(5)
     n = 50000
