@@ -172,12 +172,7 @@ hipError_t router_mfma_launch(const float* x, int T, const float* R, int Er, int
 // instruction touches start in 16 different bank quads (an even pitch of
 // 12 or 14 pieces puts them in 2 or 4 and serialises the reads 8- or
 // 4-fold).  The pad piece of each row is a second copy of its last piece.
-#ifndef LLHIP_MOE_ODD_PITCH
-#define LLHIP_MOE_ODD_PITCH 1
-#endif
-__host__ __device__ constexpr int odd_pitch(int pieces) {
-  return 16 * (LLHIP_MOE_ODD_PITCH ? (pieces | 1) : pieces);
-}
+__host__ __device__ constexpr int odd_pitch(int pieces) { return 16 * (pieces | 1); }
 
 __device__ __forceinline__ uint32_t lds_dword(const uint8_t* row, uint32_t i) {
   return reinterpret_cast<const uint32_t*>(row)[i];
