@@ -361,6 +361,11 @@ def main():
                  "ms_per_step": round(ms, 3), "tokens_per_s": round(1024 / (ms * 1e-3), 1),
                  "distinct_experts": distinct, "algorithmic_bytes": nbytes,
                  "GB/s": round(nbytes / (ms * 1e-3) / 1e9, 1)}
+        if args.cpu_seconds > 0:
+            tps, n = cpu_moe_baseline(nem, 8, args.cpu_seconds / 2)
+            entry["cpu_baseline"] = {"tokens_per_s": round(tps, 2), "cores": CPU_THREADS,
+                                     "kind": "port", "sample": f"{n} tokens, one at a time"}
+            entry["speedup_vs_cpu"] = round(entry["tokens_per_s"] / tps, 1)
         workloads.append(entry)
         log(f"nemotron B=1024: {ms:.3f} ms, {entry['tokens_per_s']} tok/s")
 
