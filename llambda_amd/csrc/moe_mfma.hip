@@ -35,9 +35,15 @@
 //   kPipeWide    2 token tiles (chunks of up to 32 pairs): 4 waves x 64
 //                rows, one LDS stage per wave; latency is hidden by the
 //                other waves of the SIMD, the MFMA work per chunk is long.
+//                The chunk's group sums and first group's activations load
+//                with its rows, later groups' activations two groups ahead.
 //   kPipeDouble  1 token tile: 4 waves x 32 rows, two LDS stages per wave;
 //                chunk kc + 1 (rows by DMA, activations and group sums into
-//                registers) loads while chunk kc computes.
+//                registers) loads while chunk kc computes; with at most four
+//                chunks in K a workgroup takes two row tiles in a row.
+// In every pipeline the LDS words of group j + 1 are read while group j
+// decodes and multiplies, and rows sit an odd number of 16-byte pieces apart
+// in LDS so that the 16 rows of one read fall in different bank quads.
 //   kPipeDecode  one token: 4 waves share 32 rows and split K (wave w takes
 //                chunks w, w + 4, ...), each through a ring of up to 8 LDS
 //                stages of rows, the token's activations and group sums,
