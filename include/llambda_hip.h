@@ -311,10 +311,11 @@ void llambda_hip_sampler_destroy(llambda_hip_sampler* sampler);
 /* The token sample-token-id-from-logits draws from logits[count] (host
  * memory, or device memory when logits_on_device = 1); the logits are not
  * modified.  With top-k (1 <= top_k < count) the token is the reference's bit
- * for bit; without top-k, top_p must be 1 and the token matches wherever the
- * random value is not within rounding of a cumulative boundary.  Errors: the
- * reference's argument errors, NaN logits, more than 4096 logits tied at or
- * above the top-k cutoff, top-p without top-k.  Synchronous. */
+ * for bit; without top-k the token matches wherever the random value, and with
+ * top_p < 1 the running sum at the top-p cut, is not within rounding of a
+ * cumulative boundary (the whole row is ranked and summed in a fixed tree
+ * order).  Errors: the reference's argument errors, NaN logits, more than 4096
+ * logits tied at or above the top-k cutoff.  Synchronous. */
 int llambda_hip_sampler_sample(llambda_hip_sampler* sampler, const float* logits, size_t count,
                                int logits_on_device, const llambda_hip_sampling* params,
                                int64_t* token);

@@ -1173,9 +1173,6 @@ int64_t run_sampler(llambda_hip_sampler* s, const float* dev_logits, int64_t n,
   if (topk && a->top_k > kSampleMaxSurvivors)
     failf("sample: top-k %lld above %d is not supported on the device", (long long)a->top_k,
           kSampleMaxSurvivors);
-  if (!topk && a->top_p < 1.0f)
-    failf("sample: top-p without top-k is not supported on the device (it needs a sort of the "
-          "whole row)");
   const bool inline_history = distinct.size() <= (size_t)kSampleInlineHistory;
   if (!inline_history && distinct.size() > s->history_cap) {
     const size_t cap = std::max<size_t>(distinct.size(), 2 * s->history_cap);

@@ -171,9 +171,27 @@ __device__ __host__ inline PrepScratch prep_scratch(float* work, int n) {
   return ps;
 }
 
-size_t sample_work_floats(int n) {
+// Top-p without top-k: the row's sort keys and token ids, twice (the radix
+// passes alternate between the two copies), after the prep scratch.
+struct ToppScratch {
+  uint32_t* key[2];
+  int* idx[2];
+};
+__device__ __host__ inline size_t prep_work_floats(int n) {
   return (size_t)((n + 3) & ~3) + 2 * kPrepGroups * kPrepCap + 3 * kPrepGroups;
 }
+__device__ __host__ inline ToppScratch topp_scratch(float* work, int n) {
+  const size_t n4 = (size_t)((n + 3) & ~3);
+  uint32_t* base = reinterpret_cast<uint32_t*>(work + prep_work_floats(n));
+  ToppScratch t;
+  t.key[0] = base;
+  t.idx[0] = reinterpret_cast<int*>(base + n4);
+  t.key[1] = base + 2 * n4;
+  t.idx[1] = reinterpret_cast<int*>(base + 3 * n4);
+  return t;
+}
+
+size_t sample_work_floats(int n) { return prep_work_floats(n) + 4 * (size_t)((n + 3) & ~3); }
 
 __global__ void __launch_bounds__(kPrepThreads)
 sample_prep_kernel(const float* __restrict__ logits, float* __restrict__ work, SampleParams p) {
@@ -574,11 +592,197 @@ sample_kernel(float* __restrict__ work, SampleParams p, int* __restrict__ result
   }
 }
 
+// Exclusive prefix sum of one int per thread over the block, in thread order.
+__device__ int block_exclusive_scan_int(int v, int* red) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  int inc = v;
+  for (int o = 1; o < 64; o <<= 1) {
+    const int t = __shfl_up(inc, o, 64);
+    if (lane >= o) inc += t;
+  }
+  if (lane == 63) red[wave] = inc;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    int acc = 0;
+    for (int w = 0; w < kSampleThreads / 64; ++w) {
+      const int t = red[w];
+      red[w] = acc;
+      acc += t;
+    }
+  }
+  __syncthreads();
+  const int r = red[wave] + inc - v;
+  __syncthreads();
+  return r;
+}
+
+// Top-p without top-k (apply-top-p-with-workspace, llambda.lisp:1163-1240,
+// after apply-top-k with k = 0 or k >= n): the logits above the mask value
+// ranked by value, descending, equal values in index order (the reference's
+// stable insertion sort; -0 and +0 compare equal), exp(x / T - max / T) per
+// rank, the first rank at which the running sum of exp / sum reaches p gives
+// the cut value, and every logit below it is masked in the row.  The ranking
+// is a stable LSD radix sort in eight 4-bit passes over the row; thread t
+// owns a contiguous range of positions, so counts laid out digit-major and
+// scanned in order give each (digit, thread) its output range.  The sums run
+// in a fixed tree order (the reference adds serially): the cut can move by a
+// rank where the running sum meets p within its rounding.  The draw itself
+// is sample_kernel's path for rows without top-k, over the masked row.
+__global__ void __launch_bounds__(kSampleThreads)
+sample_topp_kernel(float* __restrict__ work, SampleParams p) {
+#pragma clang fp contract(off)
+  __shared__ int cnt[16 * kSampleThreads];
+  __shared__ int ired[kSampleThreads / 64];
+  __shared__ float fred[kSampleThreads / 64 + 1];
+  __shared__ int s_nan, s_active, s_first;
+  const int n = p.n, tid = threadIdx.x;
+  const PrepScratch ps = prep_scratch(work, n);
+  if (tid == 0) {
+    int any = 0;
+    for (int g = 0; g < kPrepGroups; ++g) any |= ps.nan[g];
+    s_nan = any;  // reported by the draw's launch
+    s_active = 0;
+    s_first = INT_MAX;
+  }
+  __syncthreads();
+  if (s_nan) return;
+  const ToppScratch t = topp_scratch(work, n);
+  const int per = (n + kSampleThreads - 1) / kSampleThreads;
+  const int lo = min(n, tid * per), hi = min(n, lo + per);
+  // Every loop over a thread's range loads kB elements in one round before
+  // using them (the row was just written by another launch, and each
+  // dependent round of loads costs a full memory round trip).
+  constexpr int kB = 16;
+  int act = 0;
+  for (int i0 = lo; i0 < hi; i0 += kB) {
+    float xb[kB];
+#pragma unroll
+    for (int b = 0; b < kB; ++b) xb[b] = i0 + b < hi ? work[i0 + b] : 0.f;
+#pragma unroll
+    for (int b = 0; b < kB; ++b) {
+      if (i0 + b >= hi) break;
+      float x = xb[b];
+      act += x > kMaskedLogit;
+      if (x == 0.0f) x = 0.0f;  // -0 ranks with +0
+      t.key[0][i0 + b] = ~float_key(x);  // ascending key order = descending value
+      t.idx[0][i0 + b] = i0 + b;
+    }
+  }
+  atomicAdd(&s_active, act);
+  __syncthreads();
+  for (int pass = 0; pass < 8; ++pass) {
+    const uint32_t* kin = t.key[pass & 1];
+    const int* iin = t.idx[pass & 1];
+    uint32_t* kout = t.key[(pass + 1) & 1];
+    int* iout = t.idx[(pass + 1) & 1];
+    const int sh = 4 * pass;
+#pragma unroll
+    for (int d = 0; d < 16; ++d) cnt[d * kSampleThreads + tid] = 0;
+    for (int i0 = lo; i0 < hi; i0 += kB) {
+      uint32_t kb[kB];
+#pragma unroll
+      for (int b = 0; b < kB; ++b) kb[b] = i0 + b < hi ? kin[i0 + b] : 0u;
+#pragma unroll
+      for (int b = 0; b < kB; ++b)
+        if (i0 + b < hi) ++cnt[((kb[b] >> sh) & 15u) * kSampleThreads + tid];
+    }
+    __syncthreads();
+    int v[16], local = 0;
+#pragma unroll
+    for (int e = 0; e < 16; ++e) {
+      v[e] = cnt[16 * tid + e];
+      local += v[e];
+    }
+    int base = block_exclusive_scan_int(local, ired);
+#pragma unroll
+    for (int e = 0; e < 16; ++e) {
+      cnt[16 * tid + e] = base;
+      base += v[e];
+    }
+    __syncthreads();
+    for (int i0 = lo; i0 < hi; i0 += kB) {
+      uint32_t kb[kB];
+      int ib[kB];
+#pragma unroll
+      for (int b = 0; b < kB; ++b) {
+        kb[b] = i0 + b < hi ? kin[i0 + b] : 0u;
+        ib[b] = i0 + b < hi ? iin[i0 + b] : 0;
+      }
+#pragma unroll
+      for (int b = 0; b < kB; ++b) {
+        if (i0 + b >= hi) break;
+        const int pos = cnt[((kb[b] >> sh) & 15u) * kSampleThreads + tid]++;
+        kout[pos] = kb[b];
+        iout[pos] = ib[b];
+      }
+    }
+    __syncthreads();
+  }
+  // eight passes: the ranking is in copy 0; rank r < active holds the r-th
+  // largest logit above the mask value
+  const int active = s_active;
+  if (active <= 1) return;
+  const int* rank = t.idx[0];
+  const float max_scaled = work[rank[0]] / p.temperature;
+  const int rper = (active + kSampleThreads - 1) / kSampleThreads;
+  const int rlo = min(active, tid * rper), rhi = min(active, rlo + rper);
+  // this thread's ranks' exponentials, kept in the rank order in copy 1's
+  // key array (no longer needed) for the three passes over them
+  float* ex = reinterpret_cast<float*>(t.key[1]);
+  float local = 0.f;
+  for (int r0 = rlo; r0 < rhi; r0 += kB) {
+    int rb[kB];
+#pragma unroll
+    for (int b = 0; b < kB; ++b) rb[b] = r0 + b < rhi ? rank[r0 + b] : 0;
+    float vb[kB];
+#pragma unroll
+    for (int b = 0; b < kB; ++b) vb[b] = work[rb[b]];
+#pragma unroll
+    for (int b = 0; b < kB; ++b) {
+      if (r0 + b >= rhi) break;
+      const float e = (float)exp((double)(vb[b] / p.temperature - max_scaled));
+      ex[r0 + b] = e;
+      local += e;
+    }
+  }
+  const float sum = block_sum(local, fred);
+  float mine = 0.f;
+  for (int r = rlo; r < rhi; ++r) mine += ex[r] / sum;
+  float run = block_exclusive_scan(mine, fred);
+  for (int r = rlo; r < rhi; ++r) {
+    run += ex[r] / sum;
+    if (run >= p.top_p) {
+      atomicMin(&s_first, r);
+      break;
+    }
+  }
+  __syncthreads();
+  const float cut = work[rank[s_first == INT_MAX ? active - 1 : s_first]];
+  __syncthreads();
+  for (int i0 = lo; i0 < hi; i0 += kB) {
+    float xb[kB];
+#pragma unroll
+    for (int b = 0; b < kB; ++b) xb[b] = i0 + b < hi ? work[i0 + b] : 0.f;
+#pragma unroll
+    for (int b = 0; b < kB; ++b)
+      if (i0 + b < hi && xb[b] < cut) work[i0 + b] = kMaskedLogit;
+  }
+}
+
 hipError_t sample_launch(const float* logits, float* work, const SampleParams& p, int* result,
                          hipStream_t stream) {
   if (p.n <= 0 || p.n > kSampleMaxVocab) return hipErrorInvalidValue;
   hipLaunchKernelGGL(sample_prep_kernel, dim3(kPrepGroups), dim3(kPrepThreads), 0, stream, logits,
                      work, p);
+  const bool topk = p.top_k > 0 && p.top_k < p.n;
+  if (!topk && p.top_p < 1.0f) {
+    // top-p alone: cut the row, then draw from it as without top-p
+    hipLaunchKernelGGL(sample_topp_kernel, dim3(1), dim3(kSampleThreads), 0, stream, work, p);
+    SampleParams q = p;
+    q.top_p = 1.0f;
+    hipLaunchKernelGGL(sample_kernel, dim3(1), dim3(kSampleThreads), 0, stream, work, q, result);
+    return hipGetLastError();
+  }
   hipLaunchKernelGGL(sample_kernel, dim3(1), dim3(kSampleThreads), 0, stream, work, p, result);
   return hipGetLastError();
 }

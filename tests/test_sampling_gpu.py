@@ -1,8 +1,9 @@
 """Device sampling (llambda_hip_sampler_*) against the oracle's restatement of
 sample-token-id-from-logits (llambda.lisp:1272-1317): the token is identical
 for every case with top-k (the reference's serial sums over the survivors
-are reproduced in order); without top-k, wherever the random value is not
-within the rounding of the reference's serial cumulative sum (n * 2^-24)."""
+are reproduced in order); without top-k, wherever the random value (and, with
+top-p, the cut's running sum) is not within the rounding of the reference's
+serial cumulative sums (n * 2^-24)."""
 import numpy as np
 import pytest
 
@@ -22,16 +23,8 @@ def sampler(hip):
 def test_reference_sampling_kats_on_device(sampler, kats):
     k = kats["sampling"]
     for logits, kw, roll, want in k["tokens"]:
-        kw = dict(kw)
-        if kw.get("top_k", 40) == 0 and kw.get("top_p", 0.95) < 1.0:
-            # top-p without top-k runs on the host only
-            with pytest.raises(SamplingError, match="top-p without top-k"):
-                sampler.sample(logits, random_value=roll, **kw)
-            continue
-        assert sampler.sample(logits, random_value=roll, **kw) == want, (logits, kw)
+        assert sampler.sample(logits, random_value=roll, **dict(kw)) == want, (logits, kw)
     for logits, kw1, kw2, roll in k["same"]:
-        if (kw1.get("top_k") == 0) and (kw1.get("top_p") is None or kw1.get("top_p", 1.0) < 1):
-            continue
         assert sampler.sample(logits, random_value=roll, **kw1) == \
             sampler.sample(logits, random_value=roll, **kw2)
 
@@ -139,6 +132,51 @@ def test_without_top_k(sampler):
             a, b = min(got, want), max(got, want)
             # every cumulative between the two draws lies within the window
             assert c[a] >= roll - tol and c[b - 1] <= roll + tol, (trial, got, want)
+
+
+def _near(c, level, tol):
+    return np.any(np.abs(c - level) <= tol)
+
+
+@pytest.mark.parametrize("n", [1000, 20000])
+def test_top_p_without_top_k(sampler, n):
+    # the device ranks the whole row (stable radix sort) and sums in a fixed
+    # tree order; it matches the oracle except where the reference's serial
+    # running sums meet p, or the roll, within their rounding
+    rng = np.random.default_rng(n)
+    tol = n * 2.0 ** -24
+    checked = 0
+    for trial in range(12):
+        x = _head_like(rng, n)
+        if trial % 3 == 0:
+            x[rng.integers(0, n, size=50)] = x.max()  # ties at the top
+        top_p = (0.5, 0.9, 0.99)[trial % 3]
+        temperature = (1.0, 0.7, 1.6)[(trial // 3) % 3]
+        hist = rng.integers(0, n, size=20).tolist()
+        roll = float(np.float32(rng.random()))
+        kw = dict(history=hist, repetition_penalty=1.15, top_k=0, top_p=top_p,
+                  temperature=temperature, random_value=roll)
+        got = sampler.sample(x, **kw)
+        want = oracle.sample_token(x, **kw)
+        if got == want:
+            checked += 1
+            continue
+        # rank order and running sum of the penalised row, in float64
+        y = x.astype(np.float64).copy()
+        for t in set(hist):
+            y[t] = y[t] / 1.15 if y[t] > 0 else y[t] * 1.15
+        order = np.argsort(-y, kind="stable")
+        e = np.exp(y[order] / temperature - y[order[0]] / temperature)
+        c = np.cumsum(e / e.sum())
+        cut = np.searchsorted(c, top_p)  # first rank whose running sum reaches p
+        if _near(c[max(0, cut - 1):cut + 1], top_p, tol):
+            continue  # the cut itself is within rounding
+        keep = y >= y[order[cut]]
+        q = np.where(keep, np.exp(y / temperature - y.max() / temperature), 0.0)
+        cq = np.cumsum(q / q.sum())
+        a, b = min(got, want), max(got, want)
+        assert cq[a] >= roll - tol and cq[b - 1] <= roll + tol, (trial, got, want)
+    assert checked >= 6
 
 
 def test_errors(sampler):
