@@ -171,27 +171,29 @@ __device__ __host__ inline PrepScratch prep_scratch(float* work, int n) {
   return ps;
 }
 
-// Top-p without top-k: the row's sort keys and token ids, twice (the radix
-// passes alternate between the two copies), after the prep scratch.
+// Top-p without top-k: the row's (sort key << 32 | token id) words, twice
+// (the radix passes alternate between the two copies), after the prep
+// scratch.
 struct ToppScratch {
-  uint32_t* key[2];
-  int* idx[2];
+  uint64_t* item[2];
 };
 __device__ __host__ inline size_t prep_work_floats(int n) {
   return (size_t)((n + 3) & ~3) + 2 * kPrepGroups * kPrepCap + 3 * kPrepGroups;
 }
 __device__ __host__ inline ToppScratch topp_scratch(float* work, int n) {
   const size_t n4 = (size_t)((n + 3) & ~3);
-  uint32_t* base = reinterpret_cast<uint32_t*>(work + prep_work_floats(n));
+  // prep_work_floats(n) is even (n4 + 2 * 64 * 64 + 3 * 64), so the words
+  // are 8-byte aligned
+  uint64_t* base = reinterpret_cast<uint64_t*>(work + prep_work_floats(n));
   ToppScratch t;
-  t.key[0] = base;
-  t.idx[0] = reinterpret_cast<int*>(base + n4);
-  t.key[1] = base + 2 * n4;
-  t.idx[1] = reinterpret_cast<int*>(base + 3 * n4);
+  t.item[0] = base;
+  t.item[1] = base + n4;
   return t;
 }
 
 size_t sample_work_floats(int n) { return prep_work_floats(n) + 4 * (size_t)((n + 3) & ~3); }
+static_assert(2 * kPrepGroups * kPrepCap % 2 == 0 && 3 * kPrepGroups % 2 == 0,
+              "the top-p words must stay 8-byte aligned");
 
 __global__ void __launch_bounds__(kPrepThreads)
 sample_prep_kernel(const float* __restrict__ logits, float* __restrict__ work, SampleParams p) {
@@ -664,27 +666,25 @@ sample_topp_kernel(float* __restrict__ work, SampleParams p) {
       float x = xb[b];
       act += x > kMaskedLogit;
       if (x == 0.0f) x = 0.0f;  // -0 ranks with +0
-      t.key[0][i0 + b] = ~float_key(x);  // ascending key order = descending value
-      t.idx[0][i0 + b] = i0 + b;
+      // ascending key order = descending value; equal keys keep index order
+      t.item[0][i0 + b] = ((uint64_t)~float_key(x) << 32) | (uint32_t)(i0 + b);
     }
   }
   atomicAdd(&s_active, act);
   __syncthreads();
   for (int pass = 0; pass < 8; ++pass) {
-    const uint32_t* kin = t.key[pass & 1];
-    const int* iin = t.idx[pass & 1];
-    uint32_t* kout = t.key[(pass + 1) & 1];
-    int* iout = t.idx[(pass + 1) & 1];
-    const int sh = 4 * pass;
+    const uint64_t* in = t.item[pass & 1];
+    uint64_t* out = t.item[(pass + 1) & 1];
+    const int sh = 32 + 4 * pass;
 #pragma unroll
     for (int d = 0; d < 16; ++d) cnt[d * kSampleThreads + tid] = 0;
     for (int i0 = lo; i0 < hi; i0 += kB) {
-      uint32_t kb[kB];
+      uint64_t kb[kB];
 #pragma unroll
-      for (int b = 0; b < kB; ++b) kb[b] = i0 + b < hi ? kin[i0 + b] : 0u;
+      for (int b = 0; b < kB; ++b) kb[b] = i0 + b < hi ? in[i0 + b] : 0ull;
 #pragma unroll
       for (int b = 0; b < kB; ++b)
-        if (i0 + b < hi) ++cnt[((kb[b] >> sh) & 15u) * kSampleThreads + tid];
+        if (i0 + b < hi) ++cnt[(int)((kb[b] >> sh) & 15u) * kSampleThreads + tid];
     }
     __syncthreads();
     int v[16], local = 0;
@@ -701,19 +701,14 @@ sample_topp_kernel(float* __restrict__ work, SampleParams p) {
     }
     __syncthreads();
     for (int i0 = lo; i0 < hi; i0 += kB) {
-      uint32_t kb[kB];
-      int ib[kB];
+      uint64_t kb[kB];
 #pragma unroll
-      for (int b = 0; b < kB; ++b) {
-        kb[b] = i0 + b < hi ? kin[i0 + b] : 0u;
-        ib[b] = i0 + b < hi ? iin[i0 + b] : 0;
-      }
+      for (int b = 0; b < kB; ++b) kb[b] = i0 + b < hi ? in[i0 + b] : 0ull;
 #pragma unroll
       for (int b = 0; b < kB; ++b) {
         if (i0 + b >= hi) break;
-        const int pos = cnt[((kb[b] >> sh) & 15u) * kSampleThreads + tid]++;
-        kout[pos] = kb[b];
-        iout[pos] = ib[b];
+        const int pos = cnt[(int)((kb[b] >> sh) & 15u) * kSampleThreads + tid]++;
+        out[pos] = kb[b];
       }
     }
     __syncthreads();
@@ -722,18 +717,19 @@ sample_topp_kernel(float* __restrict__ work, SampleParams p) {
   // largest logit above the mask value
   const int active = s_active;
   if (active <= 1) return;
-  const int* rank = t.idx[0];
-  const float max_scaled = work[rank[0]] / p.temperature;
+  const uint64_t* ranked = t.item[0];
+  auto rank = [&](int r) { return (int)(uint32_t)ranked[r]; };
+  const float max_scaled = work[rank(0)] / p.temperature;
   const int rper = (active + kSampleThreads - 1) / kSampleThreads;
   const int rlo = min(active, tid * rper), rhi = min(active, rlo + rper);
-  // this thread's ranks' exponentials, kept in the rank order in copy 1's
-  // key array (no longer needed) for the three passes over them
-  float* ex = reinterpret_cast<float*>(t.key[1]);
+  // this thread's ranks' exponentials, kept in rank order in copy 1 (no
+  // longer needed) for the three passes over them
+  float* ex = reinterpret_cast<float*>(t.item[1]);
   float local = 0.f;
   for (int r0 = rlo; r0 < rhi; r0 += kB) {
     int rb[kB];
 #pragma unroll
-    for (int b = 0; b < kB; ++b) rb[b] = r0 + b < rhi ? rank[r0 + b] : 0;
+    for (int b = 0; b < kB; ++b) rb[b] = r0 + b < rhi ? rank(r0 + b) : 0;
     float vb[kB];
 #pragma unroll
     for (int b = 0; b < kB; ++b) vb[b] = work[rb[b]];
@@ -757,7 +753,7 @@ sample_topp_kernel(float* __restrict__ work, SampleParams p) {
     }
   }
   __syncthreads();
-  const float cut = work[rank[s_first == INT_MAX ? active - 1 : s_first]];
+  const float cut = work[rank(s_first == INT_MAX ? active - 1 : s_first)];
   __syncthreads();
   for (int i0 = lo; i0 < hi; i0 += kB) {
     float xb[kB];
