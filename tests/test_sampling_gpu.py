@@ -138,13 +138,34 @@ def _near(c, level, tol):
     return np.any(np.abs(c - level) <= tol)
 
 
+def _top_p_rounding_only(x, hist, penalty, top_p, temperature, roll, got, want):
+    """True when two top-p-only draws may differ by the sums' order alone: the
+    reference's running sum meets p at the cut, or the roll at the draw, within
+    the rounding of a serial fp32 sum (n * 2^-24), computed in float64."""
+    n = x.size
+    tol = n * 2.0 ** -24
+    y = x.astype(np.float64).copy()
+    for t in set(hist):
+        y[t] = y[t] / penalty if y[t] > 0 else y[t] * penalty
+    order = np.argsort(-y, kind="stable")
+    e = np.exp(y[order] / temperature - y[order[0]] / temperature)
+    c = np.cumsum(e / e.sum())
+    cut = np.searchsorted(c, top_p)  # first rank whose running sum reaches p
+    if _near(c[max(0, cut - 1):cut + 1], top_p, tol):
+        return True
+    keep = y >= y[order[cut]]
+    q = np.where(keep, np.exp(y / temperature - y.max() / temperature), 0.0)
+    cq = np.cumsum(q / q.sum())
+    a, b = min(got, want), max(got, want)
+    return bool(cq[a] >= roll - tol and cq[b - 1] <= roll + tol)
+
+
 @pytest.mark.parametrize("n", [1000, 20000])
 def test_top_p_without_top_k(sampler, n):
     # the device ranks the whole row (stable radix sort) and sums in a fixed
     # tree order; it matches the oracle except where the reference's serial
     # running sums meet p, or the roll, within their rounding
     rng = np.random.default_rng(n)
-    tol = n * 2.0 ** -24
     checked = 0
     for trial in range(12):
         x = _head_like(rng, n)
@@ -160,23 +181,31 @@ def test_top_p_without_top_k(sampler, n):
         want = oracle.sample_token(x, **kw)
         if got == want:
             checked += 1
-            continue
-        # rank order and running sum of the penalised row, in float64
-        y = x.astype(np.float64).copy()
-        for t in set(hist):
-            y[t] = y[t] / 1.15 if y[t] > 0 else y[t] * 1.15
-        order = np.argsort(-y, kind="stable")
-        e = np.exp(y[order] / temperature - y[order[0]] / temperature)
-        c = np.cumsum(e / e.sum())
-        cut = np.searchsorted(c, top_p)  # first rank whose running sum reaches p
-        if _near(c[max(0, cut - 1):cut + 1], top_p, tol):
-            continue  # the cut itself is within rounding
-        keep = y >= y[order[cut]]
-        q = np.where(keep, np.exp(y / temperature - y.max() / temperature), 0.0)
-        cq = np.cumsum(q / q.sum())
-        a, b = min(got, want), max(got, want)
-        assert cq[a] >= roll - tol and cq[b - 1] <= roll + tol, (trial, got, want)
+        else:
+            assert _top_p_rounding_only(x, hist, 1.15, top_p, temperature, roll, got, want), \
+                (trial, got, want)
     assert checked >= 6
+
+
+def test_top_p_without_top_k_largest_row(hip):
+    # the longest row the device sampler takes, nearly in descending order so
+    # that the reference's insertion sort (the oracle's) stays linear; a few
+    # swapped neighbours and equal values exercise the stable ranking
+    n = 262144
+    rng = np.random.default_rng(21)
+    x = np.sort(rng.normal(size=n).astype(np.float32) * 4)[::-1].copy()
+    x[100:140] = x[100]  # equal values
+    for i in rng.integers(0, 5000, size=30):
+        x[i], x[i + 1] = x[i + 1], x[i]
+    s = HipSampler(n)
+    try:
+        for top_p, roll in ((0.5, 0.3), (0.9, 0.8), (0.97, 0.01)):
+            kw = dict(top_k=0, top_p=top_p, temperature=1.0, random_value=roll)
+            got, want = s.sample(x, **kw), oracle.sample_token(x, **kw)
+            assert got == want or _top_p_rounding_only(x, [], 1.15, top_p, 1.0, roll, got, want), \
+                (top_p, got, want)
+    finally:
+        s.close()
 
 
 def test_errors(sampler):
