@@ -29,7 +29,47 @@ from llambda_amd.moe import HipMoeSession, synthetic_nemotron_h, synthetic_qwen3
 
 METRIC = "Dequant-GEMV GB/s (% HBM peak) + MoE layer tokens/s, 1 MI355X"
 HBM_PEAK_GBS = 8000.0
-CPU_THREADS = min(16, os.cpu_count() or 1)
+MFMA_BF16_PEAK_TFLOPS = 2500.0  # dense bf16 MFMA, MI355X
+DTYPE = "f32 via bf16 hi+lo MFMA"  # x split into two bf16, exact bf16 codes, fp32 accumulation
+
+
+def _cpu_facts():
+    """Host cores, the CPU model, and the cores this process may use: its
+    affinity set, capped by a cgroup CPU quota when one is set."""
+    host = os.cpu_count() or 1
+    usable = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else host
+    quota = None
+    try:
+        with open("/sys/fs/cgroup/cpu.max") as fh:
+            q, period = fh.read().split()[:2]
+            if q != "max":
+                quota = max(1, int(int(q) / int(period)))
+    except (OSError, ValueError):
+        pass
+    model = "unknown"
+    try:
+        with open("/proc/cpuinfo") as fh:
+            for line in fh:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    threads = min(usable, quota) if quota else usable
+    return {"host_cores": host, "usable_cores": usable, "cgroup_cpus": quota,
+            "cpu_model": model, "threads": threads}
+
+
+CPU = _cpu_facts()
+CPU_THREADS = CPU["threads"]
+
+
+def cpu_entry(value, unit, sample, kind="port"):
+    """A cpu_baseline object: the oracle (a C restatement of the reference's
+    CPU loops) on every core this process may use."""
+    return {"value": value, "unit": unit, "cores": CPU_THREADS, "kind": kind, "sample": sample,
+            "host_cores": CPU["host_cores"], "usable_cores": CPU["usable_cores"],
+            "cgroup_cpus": CPU["cgroup_cpus"], "cpu_model": CPU["cpu_model"]}
 
 
 def log(msg: str) -> None:
@@ -140,6 +180,41 @@ def bench_head_sampling(torch, timer, rows, columns, steps, warmup):
                         "token returned to the host every step",
             "us_per_token": round(res[True], 1), "us_sampling": round(res[False], 1),
             "tokens_per_s": round(1e6 / res[True], 1)}
+
+
+def _per_call_us(fn, calls, warmup=5):
+    for _ in range(warmup):
+        fn()
+    t0 = time.perf_counter()
+    for _ in range(calls):
+        fn()
+    return (time.perf_counter() - t0) / calls * 1e6
+
+
+def bench_boundary_gemv(rows, columns, calls):
+    """The synchronous host-pointer entry point as the Lisp adapter calls it
+    (run-hip-session-into: x copied in, the GEMV, y copied out, stream
+    synchronised), Q4_K rows x columns."""
+    rng = np.random.default_rng(5)
+    sess = make_hip_session_packed(synthetic.packed(ggml.Q4_K, rng, rows, columns), ggml.Q4_K,
+                                   rows, columns)
+    x = synthetic.activations(rng, 1, columns)[0]
+    y = np.empty(rows, dtype=np.float32)
+    us = _per_call_us(lambda: sess.run_into(y, x), calls)
+    sess.close()
+    return us
+
+
+def bench_boundary_moe(layer, calls):
+    """llambda_hip_moe_session_run for one token from host memory, as the
+    MoE hook calls it (synchronous)."""
+    rng = np.random.default_rng(6)
+    sess = HipMoeSession(layer)
+    x = synthetic.activations(rng, 1, layer.hidden)[0]
+    y = np.empty(layer.hidden, dtype=np.float32)
+    us = _per_call_us(lambda: sess.run_into(y, x), calls)
+    sess.close()
+    return us
 
 
 def cpu_gemv_baseline(type_tag, rows, columns, seconds):
@@ -298,10 +373,10 @@ def main():
         cpu = None
         if args.cpu_seconds > 0:
             cpu_gbs, n = cpu_gemv_baseline(ggml.Q6_K, rows, cols, args.cpu_seconds)
-            cpu = {"value": round(cpu_gbs, 3), "unit": "GB/s", "cores": CPU_THREADS, "kind": "port",
-                   "sample": f"{n} full Q6_K 128256x4096 GEMVs, C restatement of the reference "
-                             f"CPU loop (8-lane fma accumulator, row partition over "
-                             f"{CPU_THREADS} threads); not the Lisp reference itself"}
+            cpu = cpu_entry(round(cpu_gbs, 3), "GB/s",
+                            f"{n} full Q6_K 128256x4096 GEMVs, C restatement of the reference "
+                            f"CPU loop (8-lane fma accumulator, row partition over "
+                            f"{CPU_THREADS} threads); not the Lisp reference itself")
             log(f"CPU baseline: {cpu_gbs:.2f} GB/s over {n} runs")
         samp = bench_head_sampling(torch, timer, rows, cols, max(20, steps // 4), min(warmup, 5))
         workloads.append(samp)
@@ -311,7 +386,7 @@ def main():
         line = {
             "metric": METRIC, "value": round(gbs, 1), "unit": "GB/s", "n_gpus": 1,
             "steps": steps, "warmup": warmup, "ms_per_step": round(ms, 5),
-            "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "f32",
+            "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": DTYPE,
             "data": "synthetic (seeded random Q6_K blocks, x ~ N(0,1))",
             "config": {"workload": "Q6_K output-head GEMV, W 128256x4096, batch 1",
                        "rows": rows, "columns": cols, "algorithmic_bytes": nbytes},
@@ -331,6 +406,13 @@ def main():
                               "us_per_launch": round(ms * 1e3, 2), "GB/s": round(gbs, 1),
                               "frac_hbm": round(gbs / HBM_PEAK_GBS, 4)})
             log(f"Q4_K 4096^2 {label}: {ms * 1e3:.2f} us, {gbs:.0f} GB/s")
+        us = bench_boundary_gemv(4096, 4096, max(50, steps))
+        workloads.append({"workload": "boundary: llambda_hip_session_run, Q4_K 4096x4096, host x "
+                                      "and y (copy in, GEMV, copy out, synchronise), as "
+                                      "run-hip-session-into calls it",
+                          "us_per_call": round(us, 2),
+                          "GB/s_incl_pcie": round(nbytes / (us * 1e-6) / 1e9, 1)})
+        log(f"boundary session_run Q4_K 4096^2: {us:.1f} us per call")
 
     if args.only in (None, "moe"):
         rng = np.random.default_rng(2024)
@@ -346,11 +428,17 @@ def main():
                      "GB/s": round(nbytes / (ms * 1e-3) / 1e9, 1)}
             if args.cpu_seconds > 0:
                 tps, n = cpu_moe_baseline(qwen, 8, args.cpu_seconds / 2)
-                entry["cpu_baseline"] = {"tokens_per_s": round(tps, 2), "cores": CPU_THREADS,
-                                         "kind": "port", "sample": f"{n} tokens, one at a time"}
+                entry["cpu_baseline"] = cpu_entry(round(tps, 2), "tokens/s",
+                                                  f"{n} tokens, one at a time")
                 entry["speedup_vs_cpu"] = round(entry["tokens_per_s"] / tps, 1)
             workloads.append(entry)
             log(f"qwen3next B={tokens}: {ms:.3f} ms, {entry['tokens_per_s']} tok/s")
+        us = bench_boundary_moe(qwen, max(50, steps // 2))
+        workloads.append({"workload": "boundary: llambda_hip_moe_session_run, Qwen3Next layer, "
+                                      "one token from host memory (synchronous), as the MoE "
+                                      "hook calls it",
+                          "us_per_call": round(us, 2), "tokens_per_s": round(1e6 / us, 1)})
+        log(f"boundary moe_session_run B=1: {us:.1f} us per call")
         del qwen
         rng = np.random.default_rng(2025)
         nem = synthetic_nemotron_h(rng)
@@ -361,10 +449,15 @@ def main():
                  "ms_per_step": round(ms, 3), "tokens_per_s": round(1024 / (ms * 1e-3), 1),
                  "distinct_experts": distinct, "algorithmic_bytes": nbytes,
                  "GB/s": round(nbytes / (ms * 1e-3) / 1e9, 1)}
+        flops = 1024 * nem.flops_per_token()
+        entry["algorithmic_flops"] = flops
+        entry["TFLOP/s"] = round(flops / (ms * 1e-3) / 1e12, 1)
+        entry["frac_mfma_bf16"] = round(flops / (ms * 1e-3) / 1e12 / MFMA_BF16_PEAK_TFLOPS, 4)
+        entry["frac_hbm"] = round(nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)
         if args.cpu_seconds > 0:
             tps, n = cpu_moe_baseline(nem, 8, args.cpu_seconds / 2)
-            entry["cpu_baseline"] = {"tokens_per_s": round(tps, 2), "cores": CPU_THREADS,
-                                     "kind": "port", "sample": f"{n} tokens, one at a time"}
+            entry["cpu_baseline"] = cpu_entry(round(tps, 2), "tokens/s",
+                                              f"{n} tokens, one at a time")
             entry["speedup_vs_cpu"] = round(entry["tokens_per_s"] / tps, 1)
         workloads.append(entry)
         log(f"nemotron B=1024: {ms:.3f} ms, {entry['tokens_per_s']} tok/s")
@@ -382,10 +475,9 @@ def main():
                  "frac_hbm": round(total / (ms_g * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
         if args.cpu_seconds > 0:
             tps, n = cpu_llama_baseline(args.cpu_seconds)
-            entry["cpu_baseline"] = {"tokens_per_s": round(tps, 3), "cores": CPU_THREADS,
-                                     "kind": "port",
-                                     "sample": f"{n} oracle steps of one 8B-shaped layer at "
-                                               f"position 4096, x32, plus one Q6_K head GEMV"}
+            entry["cpu_baseline"] = cpu_entry(round(tps, 3), "tokens/s",
+                                              f"{n} oracle steps of one 8B-shaped layer at "
+                                              f"position 4096, x32, plus one Q6_K head GEMV")
             entry["speedup_vs_cpu"] = round(entry["tokens_per_s"] / tps, 1)
         workloads.append(entry)
         log(f"llama 8B token: {ms_g:.3f} ms (graph), {ms_e:.3f} ms (eager), "
@@ -407,7 +499,7 @@ def main():
     if line is None:
         line = {"metric": METRIC, "value": None, "unit": "GB/s", "n_gpus": 1, "steps": steps,
                 "warmup": warmup, "higher_is_better": True, "scaling": "weak",
-                "vs_baseline": None, "dtype": "f32", "data": "synthetic",
+                "vs_baseline": None, "dtype": DTYPE, "data": "synthetic",
                 "config": {"workload": f"partial run ({args.only})"}}
     line["workloads"] = workloads
     print(json.dumps(line), flush=True)

@@ -152,18 +152,32 @@ typedef struct llambda_hip_moe_desc {
   const void* shared_up;
   int shared_down_type;       /* ffn_down_shexp [H][Fs] */
   const void* shared_down;
+  /* ffn_latent_down [Lt][H] and ffn_latent_up [H][Lt] (nemotron, optional,
+   * llambda.lisp:5845-5864, 5883-5887, 5933-5938): the routed experts' input
+   * and output pass through them.  Not supported: a layer that has them is
+   * refused at creation, and the host runs its CPU body. */
+  int latent_down_type;
+  const void* latent_down;
+  int latent_up_type;
+  const void* latent_up;
 } llambda_hip_moe_desc;
 
 /* Upload one layer.  No counterpart in the reference's bridge (its routed
  * experts bypass the accelerator store, llambda.lisp:4951-4971); this is the
- * per-layer hook registered under blk.N.ffn_gate_inp.weight. */
+ * per-layer hook, bound per layer index in a table of its own beside the
+ * tensor-indexed projection store (never under a tensor name, so the 2-D
+ * router projection blk.N.ffn_gate_inp.weight stays a 2-D binding). */
 int llambda_hip_moe_session_create(const llambda_hip_moe_desc* desc,
                                    llambda_hip_moe_session** result);
 
 void llambda_hip_moe_session_destroy(llambda_hip_moe_session* session);
 
-/* H; 0 for null. */
+/* H; 0 for null.  Registration checks it against the columns of the layer's
+ * ffn_gate_inp (the MoE counterpart of the N x K check, llambda.lisp:2686-2703). */
 size_t llambda_hip_moe_session_hidden_size(const llambda_hip_moe_session* session);
+
+/* E (rows of ffn_gate_inp); 0 for null. */
+size_t llambda_hip_moe_session_expert_count(const llambda_hip_moe_session* session);
 
 /* output[batch][H] = the layer's FFN output (before the residual add) for
  * input[batch][H], token by token as the reference computes it.  Synchronous.
@@ -267,7 +281,11 @@ int llambda_hip_llama_session_step(llambda_hip_llama_session* session, int64_t t
 /* Device-resident form: logits is device memory [vocab] (null = the
  * session's own logits buffer, read back with llambda_hip_llama_session_logits);
  * enqueued on `stream` (null = the session's stream).  use_graph = 1 replays
- * a HIP graph of the step captured on the first call for these logits. */
+ * a HIP graph of the step captured on the first call for these logits.
+ * Steps of one session are ordered whatever streams they are given: each
+ * waits on the device for the previous one (they share the position word,
+ * the cache and the logits), and _logits, _sample, _read_kv, _write_kv and
+ * _sync wait for the last one. */
 int llambda_hip_llama_session_step_device(llambda_hip_llama_session* session, int64_t token,
                                           int64_t position, float* logits, void* stream,
                                           int use_graph);

@@ -504,6 +504,9 @@ int llambda_hip_moe_session_create(const llambda_hip_moe_desc* d,
     if (qwen && d->gate_type != d->up_type)
       failf("moe_session_create: ffn_gate_exps and ffn_up_exps must share a type");
     if (!qwen && !d->router_bias) failf("moe_session_create: missing exp_probs_b.bias");
+    if (d->latent_down || d->latent_up)
+      failf("moe_session_create: layers with ffn_latent_down / ffn_latent_up are not supported "
+            "(the host runs the layer's CPU body)");
     if (Fs > 0) {
       if (!d->shared_up || !d->shared_down) failf("moe_session_create: missing shared expert tensors");
       if (qwen && (!d->shared_gate || !d->shared_gate_inp))
@@ -607,6 +610,10 @@ void llambda_hip_moe_session_destroy(llambda_hip_moe_session* session) { delete 
 
 size_t llambda_hip_moe_session_hidden_size(const llambda_hip_moe_session* session) {
   return session ? (size_t)session->plan.hidden : 0;
+}
+
+size_t llambda_hip_moe_session_expert_count(const llambda_hip_moe_session* session) {
+  return session ? (size_t)session->plan.experts : 0;
 }
 
 int llambda_hip_moe_session_run(llambda_hip_moe_session* s, const float* input, size_t n_in,
@@ -722,7 +729,12 @@ struct llambda_hip_llama_session {
   hipGraph_t graph = nullptr;
   hipGraphExec_t exec = nullptr;
   float* graph_logits = nullptr;
+  // recorded after every step on the stream it ran on: the next step (on
+  // any stream), logits and sample wait for it, so steps that share the
+  // session's state word, cache and logits never overlap
+  hipEvent_t done = nullptr;
   ~llambda_hip_llama_session() {
+    if (done) (void)hipEventDestroy(done);
     if (exec) (void)hipGraphExecDestroy(exec);
     if (graph) (void)hipGraphDestroy(graph);
     if (stream) (void)hipStreamDestroy(stream);
@@ -842,6 +854,8 @@ int llambda_hip_llama_session_create(const llambda_hip_llama_desc* d,
     std::unique_ptr<llambda_hip_llama_session> s(new llambda_hip_llama_session());
     s->device = current_device_checked();
     HIPC(hipStreamCreateWithFlags(&s->stream, hipStreamNonBlocking));
+    HIPC(hipEventCreateWithFlags(&s->done, hipEventDisableTiming));
+    HIPC(hipEventRecord(s->done, s->stream));
     DecoderPlan& p = s->plan;
     p.hidden = (int)H;
     p.heads = (int)NH;
@@ -999,10 +1013,12 @@ int llambda_hip_llama_session_step(llambda_hip_llama_session* s, int64_t token, 
     check_token(s, token, position);
     std::lock_guard<std::mutex> lock(s->run_mutex);
     HIPC(hipSetDevice(s->device));
+    HIPC(hipStreamWaitEvent(s->stream, s->done, 0));
     HIPC(decoder_state_launch(s->plan.state, (int)token, (int)position, s->stream));
     HIPC(decoder_step_launch(s->plan, s->logits.as<float>(), s->stream));
     HIPC(hipMemcpyAsync(logits, s->logits.ptr, logits_count * sizeof(float), hipMemcpyDeviceToHost,
                         s->stream));
+    HIPC(hipEventRecord(s->done, s->stream));
     HIPC(hipStreamSynchronize(s->stream));
   });
 }
@@ -1022,8 +1038,10 @@ int llambda_hip_llama_session_step_device(llambda_hip_llama_session* s, int64_t 
       if (s->graph) HIPC(hipGraphDestroy(s->graph));
       s->exec = nullptr;
       s->graph = nullptr;
-      // capture on the session's own stream, after whatever `st` holds
+      // capture on the session's own stream, after whatever `st` holds and
+      // the previous step
       HIPC(hipStreamSynchronize(st));
+      HIPC(hipEventSynchronize(s->done));
       HIPC(hipStreamBeginCapture(s->stream, hipStreamCaptureModeRelaxed));
       const hipError_t e = decoder_step_launch(s->plan, logits, s->stream);
       hipGraph_t g = nullptr;
@@ -1034,9 +1052,11 @@ int llambda_hip_llama_session_step_device(llambda_hip_llama_session* s, int64_t 
       HIPC(hipGraphInstantiate(&s->exec, s->graph, nullptr, nullptr, 0));
       s->graph_logits = logits;
     }
+    HIPC(hipStreamWaitEvent(st, s->done, 0));
     HIPC(decoder_state_launch(s->plan.state, (int)token, (int)position, st));
     if (use_graph) HIPC(hipGraphLaunch(s->exec, st));
     else HIPC(decoder_step_launch(s->plan, logits, st));
+    HIPC(hipEventRecord(s->done, st));
   });
 }
 
@@ -1048,6 +1068,8 @@ int llambda_hip_llama_session_logits(llambda_hip_llama_session* s, float* logits
       failf("llama logits: count %zu does not match vocab %d", logits_count, s->plan.vocab);
     std::lock_guard<std::mutex> lock(s->run_mutex);
     HIPC(hipSetDevice(s->device));
+    // the last step may have run on a caller's stream
+    HIPC(hipStreamWaitEvent(s->stream, s->done, 0));
     HIPC(hipMemcpyAsync(logits, s->logits.ptr, logits_count * sizeof(float), hipMemcpyDeviceToHost,
                         s->stream));
     HIPC(hipStreamSynchronize(s->stream));
@@ -1066,6 +1088,7 @@ int llambda_hip_llama_session_write_kv(llambda_hip_llama_session* s, int64_t lay
     if (count == 0) return;
     std::lock_guard<std::mutex> lock(s->run_mutex);
     HIPC(hipSetDevice(s->device));
+    HIPC(hipStreamWaitEvent(s->stream, s->done, 0));
     const size_t D = (size_t)s->plan.head_dim, C = (size_t)s->plan.context;
     const hipMemcpyKind kind = on_device ? hipMemcpyDeviceToDevice : hipMemcpyHostToDevice;
     const size_t w = (size_t)count * D * sizeof(float);
@@ -1088,6 +1111,7 @@ int llambda_hip_llama_session_read_kv(llambda_hip_llama_session* s, int64_t laye
     if (count == 0) return;
     std::lock_guard<std::mutex> lock(s->run_mutex);
     HIPC(hipSetDevice(s->device));
+    HIPC(hipStreamWaitEvent(s->stream, s->done, 0));
     const size_t D = (size_t)s->plan.head_dim, C = (size_t)s->plan.context;
     const size_t w = (size_t)count * D * sizeof(float);
     HIPC(hipMemcpy2DAsync(keys, w, s->kcache(layer) + first * D, C * D * sizeof(float), w,
@@ -1102,6 +1126,7 @@ int llambda_hip_llama_session_sync(llambda_hip_llama_session* s, void* stream) {
   return guarded([&] {
     if (!s) failf("llama sync: null session");
     HIPC(hipStreamSynchronize(stream ? static_cast<hipStream_t>(stream) : s->stream));
+    HIPC(hipEventSynchronize(s->done));
   });
 }
 
@@ -1266,8 +1291,11 @@ int llambda_hip_llama_session_sample(llambda_hip_llama_session* session,
     if (!session || !s || !token) failf("sample: null argument");
     std::lock_guard<std::mutex> lock(s->run_mutex);
     HIPC(hipSetDevice(s->device));
-    // the session's stream holds the step that wrote the logits
-    HIPC(hipStreamSynchronize(session->stream));
+    // the last step wrote the logits, on whichever stream it was given
+    {
+      std::lock_guard<std::mutex> slock(session->run_mutex);
+      HIPC(hipEventSynchronize(session->done));
+    }
     *token = run_sampler(s, session->logits.as<float>(), session->plan.vocab, params);
   });
 }

@@ -247,10 +247,13 @@ sample_prep_kernel(const float* __restrict__ logits, float* __restrict__ work, S
   const bool topk = p.top_k > 0 && p.top_k < n;
   uint32_t ck = 0u;
   if (topk && p.top_k <= kPrepCap && !nan_flag) {
-    // every logit >= the slice's k-th largest (all of them when m <= k)
+    // every logit >= the slice's k-th largest (all of them when m <= k),
+    // compared as floats as the reference compares, so that -0 and +0 tie
+    // at a cutoff of zero (their keys differ)
     ck = m > p.top_k ? radix_select<kPrepThreads>(vals, m, p.top_k, hist, sel) : 0u;
+    const float cut = key_float(ck);
     for (int i = tid; i < m; i += kPrepThreads) {
-      if (float_key(vals[i]) >= ck) {
+      if (ck == 0u || !(vals[i] < cut)) {
         const int slot = atomicAdd(&count, 1);
         if (slot < kPrepCap) {
           ps.val[g * kPrepCap + slot] = vals[i];

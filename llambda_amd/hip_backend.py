@@ -163,6 +163,10 @@ def close_hip_session(session: Optional[HipSession]) -> None:
 
 
 def run_hip_session_into(dest, session: HipSession, vector):
+    """run-session-function: 2-D projection sessions only (a MoE layer session
+    is bound in the MoE-layer table and run by the MoE hook)."""
+    if not isinstance(session, HipSession):
+        raise HipBackendError(f"{type(session).__name__} is not a 2-D projection session.")
     return session.run_into(dest, vector)
 
 

@@ -5,8 +5,10 @@ A ``MoeLayer`` holds the tensors one layer of qwen3next-moe-into
 reads; ``HipMoeSession`` uploads them once and runs the whole feed-forward
 (router, top-k, gating, experts, combine) on the device for a batch of
 tokens.  In the reference the routed experts bypass the accelerator store
-(llambda.lisp:4951-4971); this session is the per-layer hook registered under
-the layer's router tensor name, blk.N.ffn_gate_inp.weight.
+(llambda.lisp:4951-4971); this session is the per-layer hook, bound by layer
+index in the model's MoE-layer table (projection.register_model_accelerator_
+moe_layer), apart from the tensor-indexed 2-D projections, so the router
+tensor blk.N.ffn_gate_inp.weight keeps its own 2-D binding.
 """
 from __future__ import annotations
 
@@ -44,6 +46,8 @@ class MoeLayer:
     shared_gate: Optional[Packed] = None      # [Fs][H]       ffn_gate_shexp (qwen3next)
     shared_up: Optional[Packed] = None        # [Fs][H]       ffn_up_shexp
     shared_down: Optional[Packed] = None      # [H][Fs]       ffn_down_shexp
+    latent_down: Optional[Packed] = None      # [Lt][H]       ffn_latent_down (nemotron)
+    latent_up: Optional[Packed] = None        # [H][Lt]       ffn_latent_up (nemotron)
 
     def weight_bytes(self) -> int:
         """Packed bytes of every tensor the layer can read."""
@@ -63,6 +67,15 @@ class MoeLayer:
             per += ggml.row_bytes(self.gate[0], self.hidden) * self.expert_ffn
         per += ggml.row_bytes(self.down[0], self.expert_ffn) * self.hidden
         return per
+
+    def flops_per_token(self) -> int:
+        """2 x the multiply-adds of one token: the router (and the shared-expert
+        gate row), k routed experts (gate, up and down rows), the shared expert."""
+        H, F, Fs = self.hidden, self.expert_ffn, self.shared_ffn
+        per_expert = (3 if self.gate is not None else 2) * F * H
+        shared = ((3 if self.shared_gate is not None else 2) * Fs * H) if Fs else 0
+        router = self.expert_count * H + (H if self.shared_gate_inp is not None else 0)
+        return 2 * (self.top_k * per_expert + shared + router)
 
     def shared_bytes(self) -> int:
         if not self.shared_ffn:
@@ -102,7 +115,8 @@ class HipMoeSession:
         d.expert_weights_norm = int(bool(layer.expert_weights_norm))
         for name, field in (("gate", "gate_exps"), ("up", "up_exps"), ("down", "down_exps"),
                             ("shared_gate", "shared_gate"), ("shared_up", "shared_up"),
-                            ("shared_down", "shared_down")):
+                            ("shared_down", "shared_down"), ("latent_down", "latent_down"),
+                            ("latent_up", "latent_up")):
             pair = getattr(layer, name)
             if pair is not None:
                 setattr(d, name + "_type", pair[0])
@@ -127,6 +141,25 @@ class HipMoeSession:
         if not self.pointer:
             raise HipBackendError("HIP MoE session is closed.")
         return self.pointer
+
+    @property
+    def hidden_size(self) -> int:
+        return native.lib().llambda_hip_moe_session_hidden_size(self.pointer)
+
+    @property
+    def expert_count(self) -> int:
+        return native.lib().llambda_hip_moe_session_expert_count(self.pointer)
+
+    def run_into(self, dest: np.ndarray, vector: np.ndarray) -> np.ndarray:
+        """One token, the shape of the reference's MoE functions: dest[H] =
+        the layer's FFN output for vector[H] (before the residual add)."""
+        for a, what in ((dest, "destination"), (vector, "input")):
+            if not (isinstance(a, np.ndarray) and a.dtype == np.float32 and a.flags.c_contiguous):
+                raise HipBackendError(f"HIP MoE {what} must be a contiguous float32 array.")
+        _check(native.lib().llambda_hip_moe_session_run(
+            self._live(), vector.ctypes.data, vector.size, dest.ctypes.data, dest.size, 1,
+            None, None, None), "HIP MoE run")
+        return dest
 
     def run(self, x: np.ndarray, with_routing: bool = False):
         """FFN output (before the residual) for x [tokens][H]; with_routing also
@@ -155,6 +188,50 @@ class HipMoeSession:
     def sync(self, stream: int = 0) -> None:
         _check(native.lib().llambda_hip_moe_session_sync(self._live(), stream or None),
                "HIP MoE sync")
+
+
+def moe_layer_from_model(model, layer_index: int, variant: int, *, expert_used_count: int,
+                         expert_weights_scale: float = 1.0,
+                         expert_weights_norm: bool = False) -> MoeLayer:
+    """The tensors of layer `layer_index` as the reference's MoE functions look
+    them up (blk.N.<name>.weight, llambda.lisp:5321-5426, 5827-5949), from a
+    projection.ProjectionModel; k = min(E, expert_used_count)."""
+    def info(name, required=False):
+        suffix = ".bias" if name == "exp_probs_b" else ".weight"
+        return model.tensor_info(f"blk.{layer_index}.{name}{suffix}", required=required)
+
+    def packed(name, required=False):
+        t = info(name, required)
+        return (t.type_tag, t.data) if t is not None else None
+
+    def vector(name, required=False):
+        t = info(name, required)
+        if t is None:
+            return None
+        if t.type_tag != ggml.F32:
+            raise HipBackendError(f"blk.{layer_index}.{name} must be F32")
+        return np.ascontiguousarray(t.data).view(np.float32)
+
+    router = info("ffn_gate_inp", required=True)
+    if router.type_tag != ggml.F32:
+        raise HipBackendError(f"blk.{layer_index}.ffn_gate_inp must be F32")
+    up = info("ffn_up_exps", required=True)
+    shared_up = info("ffn_up_shexp")
+    E, H = router.rows, router.columns
+    return MoeLayer(
+        variant=variant, hidden=H, expert_count=E, top_k=min(E, expert_used_count),
+        expert_ffn=up.rows, shared_ffn=shared_up.rows if shared_up is not None else 0,
+        router=np.ascontiguousarray(router.data).view(np.float32).reshape(E, H),
+        up=(up.type_tag, up.data), down=packed("ffn_down_exps", True),
+        gate=packed("ffn_gate_exps", variant == QWEN3NEXT),
+        shared_gate_inp=vector("ffn_gate_inp_shexp") if variant == QWEN3NEXT else None,
+        router_bias=vector("exp_probs_b", True) if variant == NEMOTRON_H else None,
+        expert_weights_scale=expert_weights_scale if variant == NEMOTRON_H else 1.0,
+        expert_weights_norm=expert_weights_norm if variant == NEMOTRON_H else True,
+        shared_gate=packed("ffn_gate_shexp"), shared_up=packed("ffn_up_shexp"),
+        shared_down=packed("ffn_down_shexp"),
+        latent_down=packed("ffn_latent_down") if variant == NEMOTRON_H else None,
+        latent_up=packed("ffn_latent_up") if variant == NEMOTRON_H else None)
 
 
 def select_top_k(logits: np.ndarray, k: int):

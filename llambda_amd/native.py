@@ -45,6 +45,8 @@ class MoeDesc(ctypes.Structure):
         ("shared_gate_type", c_int), ("shared_gate", c_void_p),
         ("shared_up_type", c_int), ("shared_up", c_void_p),
         ("shared_down_type", c_int), ("shared_down", c_void_p),
+        ("latent_down_type", c_int), ("latent_down", c_void_p),
+        ("latent_up_type", c_int), ("latent_up", c_void_p),
     ]
 
 
@@ -124,6 +126,7 @@ SIGNATURES = {
     "llambda_hip_moe_session_create": (c_int, [ctypes.POINTER(MoeDesc), ctypes.POINTER(c_void_p)]),
     "llambda_hip_moe_session_destroy": (None, [c_void_p]),
     "llambda_hip_moe_session_hidden_size": (c_size, [c_void_p]),
+    "llambda_hip_moe_session_expert_count": (c_size, [c_void_p]),
     "llambda_hip_moe_session_run": (c_int, [c_void_p, c_void_p, c_size, c_void_p, c_size, c_size,
                                             c_void_p, c_void_p, c_void_p]),
     "llambda_hip_moe_session_run_device": (c_int, [c_void_p, c_void_p, c_void_p, c_size, c_void_p]),

@@ -9,6 +9,12 @@ Mirrors the reference's binding store and its protocol (llambda.lisp):
   setup fallback / try-enable       3144-3208
   layer-role projection names       3256-3295
   run with runtime fallback         4660-4741
+plus the one addition this backend needs: routed-MoE layer sessions, bound
+per layer index in a table of their own (``accelerator_moe_layers``) and
+tried first by the MoE functions (qwen3next-moe-into, llambda.lisp:5321;
+nemotron-h-moe-ffn-into, 5827), falling back to their CPU body.  The
+reference's routed experts never reach its store (4951-4971), and the
+layer's router tensor, blk.N.ffn_gate_inp.weight, keeps its own 2-D binding.
 The bottom of every fallback chain is the host's own CPU kernel
 (%gguf-model-matrix-vector-multiply-into in the reference), which the host
 supplies as ``ProjectionModel.cpu_matrix_vector``; this package has none.
@@ -75,6 +81,7 @@ class ProjectionModel:
         self.architecture = architecture
         self.cpu_matrix_vector = cpu_matrix_vector
         self.accelerator_projections: Dict[str, Tuple[AcceleratorProjection, ...]] = {}
+        self.accelerator_moe_layers: Dict[int, Tuple[AcceleratorProjection, ...]] = {}
         self.retired: List[AcceleratorProjection] = []
         self.active_inference_count = 0
         self.runtime_mutex = threading.Lock()
@@ -174,13 +181,16 @@ def clear_model_accelerator_projections(model: ProjectionModel, backend=None):
     """clear-model-accelerator-projections (llambda.lisp:2791-2824)."""
     b = resolve_accelerator_backend(backend) if backend is not None else None
     with model.runtime_mutex:
-        table, removed = {}, []
-        for name, projections in model.accelerator_projections.items():
-            remaining = tuple(p for p in projections if b is not None and p.backend.name != b.name)
-            removed.extend(p for p in projections if p not in remaining)
-            if remaining:
-                table[name] = remaining
-        model.accelerator_projections = table
+        removed = []
+        for attr in ("accelerator_projections", "accelerator_moe_layers"):
+            table = {}
+            for key, projections in getattr(model, attr).items():
+                remaining = tuple(p for p in projections
+                                  if b is not None and p.backend.name != b.name)
+                removed.extend(p for p in projections if p not in remaining)
+                if remaining:
+                    table[key] = remaining
+            setattr(model, attr, table)
         to_close = _defer_or_collect(model, removed)
     _close_projections(to_close)
     return model
@@ -401,3 +411,136 @@ def matrix_vector_multiply(model: ProjectionModel, tensor_name: str, vector: np.
     info = model.tensor_info(tensor_name, required=True)
     return matrix_vector_multiply_into(np.empty(info.rows, dtype=np.float32), model, tensor_name,
                                        vector)
+
+
+# ------------------------------------------------------- MoE layer hook
+
+def model_accelerator_moe_layer(model: ProjectionModel, backend, layer_index: int):
+    b = resolve_accelerator_backend(backend)
+    for p in model.accelerator_moe_layers.get(layer_index, ()):
+        if p.backend.name == b.name:
+            return p
+    return None
+
+
+def register_model_accelerator_moe_layer(model: ProjectionModel, backend, layer_index: int,
+                                         session):
+    """Bind a routed-MoE layer session (an object with ``hidden_size``,
+    ``expert_count``, ``run_into(dest, x)`` and ``close()``) to layer
+    `layer_index`.  The check mirrors register-model-accelerator-projection's
+    N x K check (llambda.lisp:2686-2703) for a layer: the session's hidden size
+    must be the columns and its expert count the rows of the layer's router
+    tensor blk.N.ffn_gate_inp.weight.  The table is copy-on-write like the
+    projection table; the session is closed when registration fails.  No
+    counterpart in the reference store (its routed experts bypass it,
+    llambda.lisp:4951-4971)."""
+    b = resolve_accelerator_backend(backend)
+    try:
+        if not (isinstance(layer_index, int) and 0 <= layer_index < max(model.layer_count, 1)):
+            raise ValueError(f"Layer index {layer_index!r} is invalid for a "
+                             f"{model.layer_count}-layer model.")
+        router_name = f"blk.{layer_index}.ffn_gate_inp.weight"
+        router = model.tensor_info(router_name, required=True)
+        if session.hidden_size != router.columns:
+            raise ValueError(f"{b.display_name} MoE session hidden size {session.hidden_size} does "
+                             f"not match tensor {router_name!r} ({router.columns} columns).")
+        if session.expert_count != router.rows:
+            raise ValueError(f"{b.display_name} MoE session expert count {session.expert_count} "
+                             f"does not match tensor {router_name!r} ({router.rows} rows).")
+        with model.runtime_mutex:
+            if model.closed:
+                raise RuntimeError("REGISTER-MODEL-ACCELERATOR-MOE-LAYER on a closed model.")
+            existing = model.accelerator_moe_layers.get(layer_index, ())
+            if any(p.backend.name == b.name for p in existing):
+                raise ValueError(f"Layer {layer_index} already has a {b.display_name} MoE session.")
+            table = dict(model.accelerator_moe_layers)
+            table[layer_index] = tuple(sorted(existing + (AcceleratorProjection(b, session),),
+                                              key=lambda p: p.backend.priority))
+            model.accelerator_moe_layers = table
+        session = None
+    finally:
+        if session is not None:
+            b.close_session_function(session)
+    return model
+
+
+def unregister_model_accelerator_moe_layer(model: ProjectionModel, backend, layer_index: int):
+    """Remove the backend's MoE session of a layer; closed now, or when the
+    model's active inferences end (as unregister-model-accelerator-projection,
+    llambda.lisp:2743-2789)."""
+    b = resolve_accelerator_backend(backend)
+    to_close: List[AcceleratorProjection] = []
+    with model.runtime_mutex:
+        existing = model.accelerator_moe_layers.get(layer_index, ())
+        victim = next((p for p in existing if p.backend.name == b.name), None)
+        if victim is not None:
+            remaining = tuple(p for p in existing if p is not victim)
+            table = dict(model.accelerator_moe_layers)
+            if remaining:
+                table[layer_index] = remaining
+            else:
+                table.pop(layer_index, None)
+            model.accelerator_moe_layers = table
+            to_close = _defer_or_collect(model, [victim])
+    _close_projections(to_close)
+    return model
+
+
+def try_enable_model_accelerator_moe_layers(model: ProjectionModel, backend, layer_indices,
+                                            make_session):
+    """Setup for the hook: load and probe the backend, then for each layer
+    make_session(model, layer_index) and register it -- all or nothing, under
+    the setup fallback (a failure warns, and the layers keep their CPU body),
+    as try-enable-model-accelerator-projections (llambda.lisp:3160-3208)."""
+    b = resolve_accelerator_backend(backend)
+
+    def setup():
+        layers = list(layer_indices)
+        if not layers:
+            signal_accelerator_backend_error(
+                b, "%s MoE acceleration was requested without any layers.", b.display_name)
+        b.load_function()
+        if not b.available_p_function():
+            signal_accelerator_backend_error(b, "%s acceleration is unavailable.", b.display_name)
+        added, completed = [], False
+        try:
+            for layer in layers:
+                if model_accelerator_moe_layer(model, b, layer) is None:
+                    register_model_accelerator_moe_layer(model, b, layer, make_session(model, layer))
+                    added.append(layer)
+            completed = True
+        finally:
+            if not completed:
+                for layer in added:
+                    unregister_model_accelerator_moe_layer(model, b, layer)
+        return True
+
+    return call_with_accelerator_setup_fallback(b, setup)
+
+
+def moe_layer_into(dest: np.ndarray, model: ProjectionModel, layer_index: int,
+                   vector: np.ndarray, cpu_body: Callable[[], np.ndarray]) -> np.ndarray:
+    """The hook at the top of qwen3next-moe-into / nemotron-h-moe-ffn-into:
+    the layer's MoE sessions in priority order, each falling through to the
+    next on its backend's error (and unregistered), then ``cpu_body`` -- the
+    reference function's own body -- exactly as the projection path falls
+    back (llambda.lisp:4660-4741)."""
+    projections = model.accelerator_moe_layers.get(layer_index)
+    if not projections:
+        return cpu_body()
+    name = f"blk.{layer_index} MoE layer"
+
+    def run_or_next(index: int):
+        if index >= len(projections):
+            return cpu_body()
+        p = projections[index]
+
+        def run():
+            with p.run_mutex:
+                return p.session.run_into(dest, vector)
+
+        return call_with_accelerator_runtime_fallback(
+            p.backend, run, lambda: run_or_next(index + 1),
+            lambda: unregister_model_accelerator_moe_layer(model, p.backend, layer_index), name)
+
+    return run_or_next(0)

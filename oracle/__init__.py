@@ -124,6 +124,9 @@ def lib():
         L.oracle_llama_step.argtypes = [ctypes.POINTER(LlamaDesc), ctypes.c_void_p,
                                         ctypes.c_int64, ctypes.c_int64, ctypes.c_int64,
                                         ctypes.c_void_p, ctypes.c_int]
+        L.oracle_llama_step_hidden.argtypes = [ctypes.POINTER(LlamaDesc), ctypes.c_void_p,
+                                               ctypes.c_int64, ctypes.c_int64, ctypes.c_int64,
+                                               ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int]
         i64p = ctypes.c_void_p
         L.oracle_repetition_penalty.argtypes = [ctypes.c_void_p, ctypes.c_int64, i64p,
                                                 ctypes.c_int64, ctypes.c_float]
@@ -320,10 +323,12 @@ def attention(q, kcache, vcache, n: int) -> np.ndarray:
     return out
 
 
-def llama_step(weights, kv: np.ndarray, token: int, position: int, threads: int = 1) -> np.ndarray:
+def llama_step(weights, kv: np.ndarray, token: int, position: int, threads: int = 1,
+               return_hidden: bool = False):
     """One step of the Llama step function on host weights (an object with the
     attributes of llambda_amd.llama.LlamaWeights).  kv: float32
-    [layers][2][kv_heads][cap][head_dim], updated in place (slot `position`)."""
+    [layers][2][kv_heads][cap][head_dim], updated in place (slot `position`).
+    With return_hidden, (logits, the output rows' input rms-norm(x) * output_norm)."""
     c = weights.config
     assert kv.dtype == np.float32 and kv.flags["C_CONTIGUOUS"]
     cap = kv.shape[3]
@@ -360,9 +365,10 @@ def llama_step(weights, kv: np.ndarray, token: int, position: int, threads: int 
     d.output_norm = vec(weights.output_norm)
     d.layers = layers
     logits = np.empty(c.vocab, dtype=np.float32)
-    _check(lib().oracle_llama_step(ctypes.byref(d), kv.ctypes.data, cap, token, position,
-                                   logits.ctypes.data, threads))
-    return logits
+    hidden = np.empty(c.hidden, dtype=np.float32)
+    _check(lib().oracle_llama_step_hidden(ctypes.byref(d), kv.ctypes.data, cap, token, position,
+                                          logits.ctypes.data, hidden.ctypes.data, threads))
+    return (logits, hidden) if return_hidden else logits
 
 
 def repetition_penalty(logits, history, penalty: float) -> np.ndarray:

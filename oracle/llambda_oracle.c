@@ -804,6 +804,13 @@ int oracle_attention(const float* q, const float* kc, const float* vc, int64_t c
  * kv: [layers][2][kv_heads][cap][head_dim]. */
 int oracle_llama_step(const oracle_llama_desc* m, float* kv, int64_t cap, int64_t token,
                       int64_t position, float* logits, int threads) {
+  return oracle_llama_step_hidden(m, kv, cap, token, position, logits, NULL, threads);
+}
+
+/* The same step; `hidden` (optional, [hidden]) receives the output rows'
+ * input, rms-norm(x) * output_norm, for per-row bounds of the logits. */
+int oracle_llama_step_hidden(const oracle_llama_desc* m, float* kv, int64_t cap, int64_t token,
+                             int64_t position, float* logits, float* hidden, int threads) {
   if (!m || !kv || !logits) return fail("llama step: null argument");
   const int64_t H = m->hidden, NH = m->heads, NKV = m->kv_heads, F = m->ffn;
   if (H <= 0 || NH <= 0 || NKV <= 0 || H % NH || NH % NKV) return fail("llama step: bad dims");
@@ -867,6 +874,7 @@ int oracle_llama_step(const oracle_llama_desc* m, float* kv, int64_t cap, int64_
   }
   if (status == 0) {
     oracle_rms_norm(x, m->output_norm, H, m->norm_eps, xin);
+    if (hidden) memcpy(hidden, xin, (size_t)H * sizeof(float));
     if (oracle_gemv(m->output.type, m->output.data, m->vocab, H, xin, logits, threads)) status = -1;
   }
   free(buf);

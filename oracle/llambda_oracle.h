@@ -170,6 +170,8 @@ typedef struct oracle_llama_desc {
 /* llambda.lisp:6315-6441; kv: [layers][2][kv_heads][cap][head_dim] */
 int oracle_llama_step(const oracle_llama_desc* m, float* kv, int64_t cap, int64_t token,
                       int64_t position, float* logits, int threads);
+int oracle_llama_step_hidden(const oracle_llama_desc* m, float* kv, int64_t cap, int64_t token,
+                             int64_t position, float* logits, float* hidden, int threads);
 
 /* ---- sampling (llambda.lisp:1036-1317) ------------------------------ */
 int oracle_repetition_penalty(float* logits, int64_t n, const int64_t* history, int64_t nh,

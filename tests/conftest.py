@@ -11,6 +11,18 @@ if ROOT not in sys.path:
 
 def pytest_configure(config):
     config.addinivalue_line("markers", "gpu: needs an MI355X (runs through the HIP C ABI)")
+    # torch ships its own HIP runtime (libamdhip64.so, no soname) beside
+    # /opt/rocm's (libamdhip64.so.7, which libllambda_hip.so names).  When
+    # torch's is initialised first -- as bench.py does -- the library's HIP
+    # calls resolve to that same runtime, so torch streams and device memory
+    # can be handed to it; if the library initialised the device first,
+    # torch would find none.  GPU tests that use torch need this order.
+    try:
+        import torch
+    except ImportError:
+        return
+    if torch.cuda.is_available():
+        torch.cuda.init()
 
 
 @pytest.fixture(scope="session")

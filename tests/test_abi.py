@@ -96,3 +96,31 @@ def test_packed_create_validates_geometry():
     assert L.llambda_hip_session_create_packed(buf.ctypes.data, buf.size, 99, 3, 256,
                                                ctypes.byref(handle)) == -1
     assert "unsupported GGML tensor type" in native.last_error()
+
+
+def test_moe_session_refuses_latent_projections():
+    """nemotron-h-moe-ffn-into's optional ffn_latent_down / ffn_latent_up
+    (llambda.lisp:5845-5864, 5883-5887, 5933-5938) are refused at creation --
+    before any device work -- so the host keeps the layer's CPU body."""
+    from llambda_amd import ggml, projection, synthetic
+    from llambda_amd.hip_backend import HipBackendError
+    from llambda_amd.moe import NEMOTRON_H, HipMoeSession, moe_layer_from_model
+
+    rng = np.random.default_rng(3)
+    H, E, F, Lt = 256, 8, 64, 128
+    t = projection.TensorInfo
+    names = {
+        "ffn_gate_inp.weight": (ggml.F32, (H, E), synthetic.f32(rng, E, H)),
+        "exp_probs_b.bias": (ggml.F32, (E,), synthetic.f32(rng, 1, E)),
+        "ffn_up_exps.weight": (ggml.Q8_0, (Lt, F, E), synthetic.q8_0(rng, E * F, Lt)),
+        "ffn_down_exps.weight": (ggml.Q8_0, (F, Lt, E), synthetic.q8_0(rng, E * Lt, F)),
+        "ffn_latent_down.weight": (ggml.Q8_0, (H, Lt), synthetic.q8_0(rng, Lt, H)),
+        "ffn_latent_up.weight": (ggml.Q8_0, (Lt, H), synthetic.q8_0(rng, H, Lt)),
+    }
+    model = projection.ProjectionModel([t(f"blk.0.{n}", ty, dims, data)
+                                        for n, (ty, dims, data) in names.items()], layer_count=1)
+    layer = moe_layer_from_model(model, 0, NEMOTRON_H, expert_used_count=2)
+    assert layer.latent_down is not None and layer.latent_up is not None
+    assert (layer.hidden, layer.expert_count, layer.top_k, layer.expert_ffn) == (H, E, 2, F)
+    with pytest.raises(HipBackendError, match="ffn_latent_down / ffn_latent_up are not supported"):
+        HipMoeSession(layer)

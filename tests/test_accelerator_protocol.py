@@ -261,3 +261,163 @@ def test_cache_key_has_reference_fields():
         assert path == f"/tmp/cache/{key}/projection.onnx" and root == "/tmp/cache"
     finally:
         acc.unregister_accelerator_backend("hip")
+
+
+# ------------------------------------------------------------ MoE layer hook
+# The routed-MoE layer sessions live in a table of their own, keyed by layer
+# index; the reference's fallback rules apply to them as to projections
+# (tests.lisp:543-715 for the projection case).
+
+class FakeMoeSession:
+    def __init__(self, name, hidden, experts, run):
+        self.name, self.hidden_size, self.expert_count, self._run = name, hidden, experts, run
+        self.closed = False
+
+    def run_into(self, dest, vector):
+        return self._run(self, dest, vector)
+
+    def close(self):
+        self.closed = True
+
+
+def moe_model(hidden=4, experts=3, layers=2):
+    """Router tensors blk.N.ffn_gate_inp.weight (F32 [experts][hidden])."""
+    tensors = []
+    for layer in range(layers):
+        data = np.arange(experts * hidden, dtype=np.float32).view(np.uint8)
+        tensors.append(projection.TensorInfo(f"blk.{layer}.ffn_gate_inp.weight", ggml.F32,
+                                             (hidden, experts), data))
+
+    def cpu(dest, tensor, vector):  # the router GEMV on the CPU
+        w = tensor.data.view(np.float32).reshape(tensor.rows, tensor.columns)
+        dest[:] = w @ vector
+        return dest
+
+    return projection.ProjectionModel(tensors, layer_count=layers, cpu_matrix_vector=cpu)
+
+
+def test_moe_hook_priority_fallback_and_its_own_table():
+    closed = []
+    state = {"gpu_fails": False, "npu_fails": False}
+
+    def runner(value, key):
+        def run(session, dest, vector):
+            if state[key]:
+                raise FakeAcceleratorError(f"simulated {session.name} failure")
+            dest[:] = value
+            return dest
+        return run
+
+    gpu = make_fake_backend("fake-mgpu", 1, lambda d, s, v: d, lambda s: closed.append(s.name))
+    npu = make_fake_backend("fake-mnpu", 2, lambda d, s, v: d, lambda s: closed.append(s.name))
+    acc.register_accelerator_backend(gpu)
+    acc.register_accelerator_backend(npu)
+    try:
+        model = moe_model()
+        x = np.ones(4, dtype=np.float32)
+        out = np.zeros(4, dtype=np.float32)
+        cpu_calls = []
+
+        def cpu_body():
+            cpu_calls.append(1)
+            out[:] = -1.0
+            return out
+
+        # no session bound: the CPU body
+        projection.moe_layer_into(out, model, 0, x, cpu_body)
+        assert out[0] == -1.0 and len(cpu_calls) == 1
+        projection.register_model_accelerator_moe_layer(
+            model, npu, 0, FakeMoeSession("npu0", 4, 3, runner(20.0, "npu_fails")))
+        projection.register_model_accelerator_moe_layer(
+            model, gpu, 0, FakeMoeSession("gpu0", 4, 3, runner(10.0, "gpu_fails")))
+        assert [p.backend for p in model.accelerator_moe_layers[0]] == [gpu, npu]
+        # the router keeps its own 2-D path: the MoE table is never consulted
+        # for the tensor name, so its GEMV runs on the CPU kernel here
+        assert not model.accelerator_projections
+        logits = projection.matrix_vector_multiply(model, "blk.0.ffn_gate_inp.weight", x)
+        assert np.array_equal(logits, np.array([6.0, 22.0, 38.0], dtype=np.float32))
+        projection.moe_layer_into(out, model, 0, x, cpu_body)
+        assert out[0] == 10.0 and len(cpu_calls) == 1
+        # layer 1 has no session
+        projection.moe_layer_into(out, model, 1, x, cpu_body)
+        assert out[0] == -1.0 and len(cpu_calls) == 2
+        # the first backend fails: warned, unregistered and closed; the next runs
+        state["gpu_fails"] = True
+        with pytest.warns(UserWarning, match="failed and was disabled"):
+            projection.moe_layer_into(out, model, 0, x, cpu_body)
+        assert out[0] == 20.0 and closed == ["gpu0"]
+        assert projection.model_accelerator_moe_layer(model, gpu, 0) is None
+        # all fail: the CPU body
+        state["npu_fails"] = True
+        with pytest.warns(UserWarning):
+            projection.moe_layer_into(out, model, 0, x, cpu_body)
+        assert out[0] == -1.0 and closed == ["gpu0", "npu0"] and not model.accelerator_moe_layers
+        # retirement is deferred while inference is active; clear covers the table
+        state["gpu_fails"] = False
+        s = FakeMoeSession("gpu1", 4, 3, runner(10.0, "gpu_fails"))
+        projection.register_model_accelerator_moe_layer(model, gpu, 1, s)
+        projection.acquire_model_inference_use(model)
+        projection.clear_model_accelerator_projections(model)
+        assert not model.accelerator_moe_layers and closed == ["gpu0", "npu0"]
+        projection.release_model_inference_use(model)
+        assert closed == ["gpu0", "npu0", "gpu1"]
+    finally:
+        acc.unregister_accelerator_backend("fake-mgpu")
+        acc.unregister_accelerator_backend("fake-mnpu")
+
+
+def test_moe_hook_registration_checks_the_router_shape():
+    closed = []
+    b = make_fake_backend("fake-mreg", 1, lambda d, s, v: d, lambda s: closed.append(s.name))
+    acc.register_accelerator_backend(b, replace=True)
+    try:
+        model = moe_model(hidden=4, experts=3)
+        ok = lambda s, d, v: d  # noqa: E731
+        with pytest.raises(ValueError, match="hidden size 5"):
+            projection.register_model_accelerator_moe_layer(model, b, 0,
+                                                            FakeMoeSession("h", 5, 3, ok))
+        with pytest.raises(ValueError, match="expert count 4"):
+            projection.register_model_accelerator_moe_layer(model, b, 0,
+                                                            FakeMoeSession("e", 4, 4, ok))
+        with pytest.raises(ValueError, match="invalid"):
+            projection.register_model_accelerator_moe_layer(model, b, 7,
+                                                            FakeMoeSession("l", 4, 3, ok))
+        assert closed == ["h", "e", "l"]  # a refused session is closed
+        projection.register_model_accelerator_moe_layer(model, b, 0, FakeMoeSession("a", 4, 3, ok))
+        with pytest.raises(ValueError, match="already has"):
+            projection.register_model_accelerator_moe_layer(model, b, 0,
+                                                            FakeMoeSession("b", 4, 3, ok))
+        assert closed == ["h", "e", "l", "b"] and not model.accelerator_projections
+    finally:
+        acc.unregister_accelerator_backend("fake-mreg")
+
+
+def test_moe_hook_enable_rolls_back_and_falls_back():
+    closed = []
+    b = make_fake_backend("fake-men", 1, lambda d, s, v: d, lambda s: closed.append(s.name))
+    acc.register_accelerator_backend(b, replace=True)
+    try:
+        model = moe_model(layers=3)
+        made = []
+
+        def make(model, layer):
+            made.append(layer)
+            if layer == 2:
+                raise FakeAcceleratorError("layer 2 cannot be uploaded")
+            return FakeMoeSession(f"s{layer}", 4, 3, lambda s, d, v: d)
+
+        with pytest.warns(UserWarning, match="setup failed"):
+            assert projection.try_enable_model_accelerator_moe_layers(model, b, [0, 1, 2],
+                                                                      make) is None
+        assert made == [0, 1, 2] and closed == ["s0", "s1"] and not model.accelerator_moe_layers
+        assert projection.try_enable_model_accelerator_moe_layers(model, b, [0, 1], make) is True
+        assert sorted(model.accelerator_moe_layers) == [0, 1]
+    finally:
+        acc.unregister_accelerator_backend("fake-men")
+
+
+def test_hip_projection_runner_refuses_a_moe_session():
+    from llambda_amd.hip_backend import HipBackendError, run_hip_session_into
+    with pytest.raises(HipBackendError, match="not a 2-D projection session"):
+        run_hip_session_into(np.zeros(4, np.float32), FakeMoeSession("m", 4, 3, None),
+                             np.zeros(4, np.float32))

@@ -6,7 +6,8 @@ Bounds: every cache slot the step writes (rotated keys, values) within
 rotation; logits within 1e-3 of the largest |logit| -- the fp32 orders of
 the fused GEMV, the chunked attention softmax and the norms differ from the
 reference's serial loops, and a wrong head mapping, rotation or cache slot
-moves logits by O(1)."""
+moves logits by O(1); the full-size token, in addition, every logit within
+1e-4 * sum_i |w_ri h_i| of its row (h the oracle's input to the output rows)."""
 import numpy as np
 import pytest
 
@@ -171,6 +172,36 @@ def test_llama_step_then_sample_on_device(hip):
         sess.close()
 
 
+def test_steps_on_caller_streams_are_ordered(hip):
+    """Steps enqueued on two different caller streams, each followed at once
+    by a device-side sample of the session's logits: every step waits for the
+    previous one and the sampler for the last, so the tokens and logits are
+    those of the same steps run synchronously on a second session."""
+    import torch
+
+    from llambda_amd.sampling import HipSampler
+    c, _ = CONFIGS["g4d128"]
+    w = synthetic_llama(np.random.default_rng(17), c)
+    a, b = HipLlamaSession(w), HipLlamaSession(w)
+    sampler = HipSampler(c.vocab)
+    streams = [torch.cuda.Stream(), torch.cuda.Stream()]
+    try:
+        token = 3
+        for pos in range(8):
+            st = streams[pos % 2].cuda_stream
+            a.step_device(token, pos, stream=st, graph=bool(pos % 3))
+            kw = dict(top_k=40, top_p=0.9, temperature=1.0, random_value=0.37)
+            got = sampler.sample_session(a, **kw)
+            ref = b.step(token, pos)
+            assert np.array_equal(a.logits(), ref), pos
+            assert got == oracle.sample_token(ref, **kw), pos
+            token = got
+    finally:
+        sampler.close()
+        a.close()
+        b.close()
+
+
 def test_llama_from_gguf_file(hip, tmp_path):
     """A model written to a GGUF file, mapped, parsed and uploaded straight
     from the mapping (the file is closed before the steps run)."""
@@ -210,6 +241,75 @@ def test_llama_8b_layer_shapes_at_4096(hip):
         _check_logits(got, ref, "8B layers at 4096")
         _check_slot(sess, w, kv, 0, 4096, 123)
         _check_slot(sess, w, kv, 1, 4096)
+    finally:
+        sess.close()
+
+
+def _host_copy(w_dev):
+    """Host LlamaWeights with the bytes of device-drawn weights."""
+    from llambda_amd.llama import LlamaLayerWeights, LlamaWeights
+
+    def h(t):
+        return (t.type, t.owner.reshape(-1).cpu().numpy())
+
+    layers = [LlamaLayerWeights(attn_norm=L.attn_norm, attn_q=h(L.attn_q), attn_k=h(L.attn_k),
+                                attn_v=h(L.attn_v), attn_output=h(L.attn_output),
+                                ffn_norm=L.ffn_norm, ffn_gate=h(L.ffn_gate), ffn_up=h(L.ffn_up),
+                                ffn_down=h(L.ffn_down)) for L in w_dev.layers]
+    return LlamaWeights(config=w_dev.config, token_embd=h(w_dev.token_embd),
+                        output=h(w_dev.output), output_norm=w_dev.output_norm,
+                        rope_factors=w_dev.rope_factors, layers=layers)
+
+
+def test_llama31_8b_full_token_at_4096(hip):
+    """The whole Llama-3.1-8B-layout token the benchmark times: 32 layers,
+    the 128256-row Q6_K output head with output_norm fused, the fp32 cache
+    prefilled to 4096 slots ~ N(0, 1), the step at 4096 -- against the
+    oracle's step on the same bytes.  Every logit within 1e-4 of
+    sum_i |w_ri h_i| of its row (h the oracle's input to the output rows: the
+    north-star bound, with the 32 layers' own rounding inside it), plus the
+    per-row bound of the layer-0 cache slot and the largest-logit check."""
+    import os
+
+    import torch
+
+    from llambda_amd.llama import LLAMA31_8B, synthetic_llama_device
+
+    from helpers import abs_dot_bound
+
+    c = LLAMA31_8B
+    context, pos, token = 4224, 4096, 4242
+    print("full 8B token: drawing weights on the device", flush=True)
+    w_dev = synthetic_llama_device(41, c, np.random.default_rng(41))
+    sess = HipLlamaSession(w_dev, context=context)
+    try:
+        w = _host_copy(w_dev)
+        del w_dev
+        torch.cuda.empty_cache()
+        kv = np.zeros((c.layer_count, 2, c.kv_head_count, context, c.head_dim), dtype=np.float32)
+        gen = torch.Generator(device="cuda")
+        gen.manual_seed(42)
+        for layer in range(c.layer_count):
+            k = torch.randn((c.kv_head_count, pos, c.head_dim), device="cuda", generator=gen)
+            v = torch.randn((c.kv_head_count, pos, c.head_dim), device="cuda", generator=gen)
+            torch.cuda.synchronize()
+            sess.write_kv_device(layer, 0, pos, k.data_ptr(), v.data_ptr())
+            kv[layer, 0, :, :pos] = k.cpu().numpy()
+            kv[layer, 1, :, :pos] = v.cpu().numpy()
+        del k, v
+        print("full 8B token: device step", flush=True)
+        got = sess.step(token, pos)
+        print("full 8B token: oracle step", flush=True)
+        threads = min(16, os.cpu_count() or 1)
+        ref, hidden = oracle.llama_step(w, kv, token, pos, threads=threads, return_hidden=True)
+        _check_logits(got, ref, "full 8B token at 4096")
+        bound = abs_dot_bound(w.output[0], w.output[1], c.vocab, c.hidden, hidden)
+        err = np.abs(got.astype(np.float64) - ref.astype(np.float64))
+        ratio = float(np.max(err / bound))
+        print(f"full 8B token: max |dlogit| / sum|w h| = {ratio:.2e}", flush=True)
+        assert ratio <= 1e-4, ratio
+        _check_slot(sess, w, kv, 0, pos, token)
+        _check_slot(sess, w, kv, c.layer_count - 1, pos)
     finally:
         sess.close()
 
