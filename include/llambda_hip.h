@@ -202,6 +202,23 @@ int llambda_hip_moe_session_run_device(llambda_hip_moe_session* session, const f
  * raised by the kernels since the last check. */
 int llambda_hip_moe_session_sync(llambda_hip_moe_session* session, void* stream);
 
+/* The device-resident run above with no allocation of any kind (no hipMalloc,
+ * hipFree or allocating library call), for callers that cannot allocate:
+ * code under HIP graph capture, tight serving loops, harnesses that forbid
+ * it.  No counterpart in the reference.  The forward's scratch (router
+ * logits and slice sums, top-k, histogram, permutation, chunk table, split
+ * activations, per-pair expert outputs) lives in one file-scope device array
+ * of 32 MiB per GPU, held until the process ends; a call whose batch needs
+ * more (the layer's per-token scratch times `batch`; e.g. Qwen3Next-shaped
+ * layers up to 251 tokens, Nemotron-H-shaped ones up to 166) is
+ * refused with an error, before anything is enqueued.  Every call on a GPU
+ * shares that GPU's array: calls that overlap on one GPU (on different
+ * streams, or from different sessions) race.  Errors raised by the kernels
+ * reach the session's flag and are reported by llambda_hip_moe_session_sync. */
+int llambda_hip_moe_session_run_device_noalloc(llambda_hip_moe_session* session,
+                                               const float* input, float* output, size_t batch,
+                                               void* stream);
+
 /* ---- routing primitive ---------------------------------------------- */
 
 /* For each of `batch` rows of n logits, the k selected by

@@ -397,6 +397,38 @@ int llambda_hip_session_dequantize(llambda_hip_session* s, float* output, size_t
 
 // ------------------------------------------------------------- MoE sessions
 
+// Bytes of each per-run scratch buffer of one MoE forward over T tokens, as
+// the kernels index them.
+struct MoeScratchBytes {
+  size_t logits, router_part, top_idx, top_w, shared_w, perm, chunks, down_out, xq, xsum, aq,
+      asum;
+};
+
+static MoeScratchBytes moe_scratch_bytes(const MoePlan& p, size_t T) {
+  const size_t K = (size_t)p.top_k, E = (size_t)p.experts, H = (size_t)p.hidden;
+  const size_t pairs = T * (K + 1);
+  const size_t act_w = (size_t)std::max(p.ffn, p.shared_ffn);
+  MoeScratchBytes b;
+  b.logits = T * (E + 1) * sizeof(float);
+  b.router_part = (size_t)router_slices(p.hidden) * T * (E + 1) * sizeof(float);
+  b.top_idx = T * K * sizeof(int);
+  b.top_w = T * K * sizeof(float);
+  b.shared_w = T * sizeof(float);
+  b.perm = pairs * sizeof(int);
+  // (+ 8: the batch products read the entry of every workgroup of their
+  // grid, which is padded to a multiple of 8, before they compare its index
+  // with the count)
+  b.chunks = (size_t)(moe_max_chunks(p, (int64_t)T, 1) + 8) * sizeof(MoeChunk);
+  b.down_out = pairs * H * sizeof(float);
+  // the decode pipeline stages whole 256-element chunks (1 KB of split row)
+  // of a row's last, partial chunk: 1 KB of readable slack
+  b.xq = T * 2 * H * sizeof(uint16_t) + 1024;
+  b.xsum = T * (H / 16) * sizeof(float);
+  b.aq = pairs * 2 * act_w * sizeof(uint16_t) + 1024;
+  b.asum = pairs * (act_w / 16) * sizeof(float);
+  return b;
+}
+
 struct llambda_hip_moe_session {
   std::mutex run_mutex;
   int device = 0;
@@ -414,30 +446,22 @@ struct llambda_hip_moe_session {
   void ensure_capacity(int tokens) {
     if (tokens <= plan.capacity) return;
     MoePlan& p = plan;
-    const size_t T = (size_t)tokens, K = (size_t)p.top_k, E = (size_t)p.experts;
-    const size_t pairs = T * (K + 1);
-    const size_t act_w = (size_t)std::max(p.ffn, p.shared_ffn);
-    logits.alloc(T * (E + 1) * sizeof(float), "router logits");
+    const MoeScratchBytes b = moe_scratch_bytes(p, (size_t)tokens);
     p.router_ks = router_slices(p.hidden);
-    router_part.alloc((size_t)p.router_ks * T * (E + 1) * sizeof(float), "router slice sums");
-    p.router_part = router_part.as<float>();
-    top_idx.alloc(T * K * sizeof(int), "top-k indices");
-    top_w.alloc(T * K * sizeof(float), "top-k weights");
-    shared_w.alloc(T * sizeof(float), "shared weights");
-    perm.alloc(pairs * sizeof(int), "permutation");
+    logits.alloc(b.logits, "router logits");
+    router_part.alloc(b.router_part, "router slice sums");
+    top_idx.alloc(b.top_idx, "top-k indices");
+    top_w.alloc(b.top_w, "top-k weights");
+    shared_w.alloc(b.shared_w, "shared weights");
+    perm.alloc(b.perm, "permutation");
+    chunks.alloc(b.chunks, "chunk table");
+    down_out.alloc(b.down_out, "expert outputs");
+    xq.alloc(b.xq, "split input");
+    xsum.alloc(b.xsum, "input group sums");
+    aq.alloc(b.aq, "split activations");
+    asum.alloc(b.asum, "activation group sums");
     p.capacity = tokens;
-    // (+ 8: the batch products read the entry of every workgroup of their
-    // grid, which is padded to a multiple of 8, before they compare its
-    // index with the count)
-    chunks.alloc((size_t)(moe_max_chunks(p, tokens, 1) + 8) * sizeof(MoeChunk), "chunk table");
-    down_out.alloc(pairs * (size_t)p.hidden * sizeof(float), "expert outputs");
-    const size_t H = (size_t)p.hidden;
-    // the decode pipeline stages whole 256-element chunks (1 KB of split
-    // row) of a row's last, partial chunk: 1 KB of readable slack
-    xq.alloc(T * 2 * H * sizeof(uint16_t) + 1024, "split input");
-    xsum.alloc(T * (H / 16) * sizeof(float), "input group sums");
-    aq.alloc(pairs * 2 * act_w * sizeof(uint16_t) + 1024, "split activations");
-    asum.alloc(pairs * (act_w / 16) * sizeof(float), "activation group sums");
+    p.router_part = router_part.as<float>();
     p.xq = xq.as<uint16_t>();
     p.xsum = xsum.as<float>();
     p.aq = aq.as<uint16_t>();
@@ -682,6 +706,108 @@ int llambda_hip_moe_session_sync(llambda_hip_moe_session* s, void* stream) {
     HIPC(hipSetDevice(s->device));
     const int flag = s->take_error(stream ? static_cast<hipStream_t>(stream) : s->stream);
     if (flag) raise_moe_error(flag, s->plan.variant);
+  });
+}
+
+}  // extern "C"
+
+// ----------------------------------------------- no-allocation MoE runs
+// One MoE forward's scratch for llambda_hip_moe_session_run_device_noalloc:
+// a file-scope device array, one per GPU, held until the process ends.  Its
+// name is a host-side stand-in: host code uses only the device address that
+// hipGetSymbolAddress returns for the current device (kept per device).
+constexpr size_t kMoeNoallocScratchBytes = (size_t)32 << 20;
+static __device__ __align__(256) uint8_t scratch[kMoeNoallocScratchBytes];
+
+namespace {
+
+constexpr int kMaxScratchDevices = 64;
+std::mutex g_scratch_mutex;
+uint8_t* g_scratch[kMaxScratchDevices];
+
+// The device address of `scratch` on `device`, which must be current.
+uint8_t* noalloc_scratch(int device) {
+  std::lock_guard<std::mutex> lock(g_scratch_mutex);
+  if (device < 0 || device >= kMaxScratchDevices)
+    failf("moe_session_run_device_noalloc: device %d beyond the %d tracked", device,
+          kMaxScratchDevices);
+  if (!g_scratch[device]) {
+    void* ptr = nullptr;
+    HIPC(hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)));
+    if (!ptr) failf("moe_session_run_device_noalloc: no device address for the scratch array");
+    g_scratch[device] = static_cast<uint8_t*>(ptr);
+  }
+  return g_scratch[device];
+}
+
+// Point p's per-run buffers into [base, base + limit) for T tokens; returns
+// the bytes the layout needs (nothing is assigned when that exceeds limit).
+size_t carve_moe_scratch(MoePlan& p, int T, uint8_t* base, size_t limit) {
+  const MoeScratchBytes b = moe_scratch_bytes(p, (size_t)T);
+  const size_t E = (size_t)p.experts;
+  const size_t sizes[] = {b.logits, b.router_part, b.top_idx, b.top_w, b.shared_w, b.perm,
+                          b.chunks, b.down_out, b.xq, b.xsum, b.aq, b.asum,
+                          E * sizeof(int), 2 * sizeof(int), sizeof(int)};
+  constexpr int kBuffers = sizeof(sizes) / sizeof(sizes[0]);
+  size_t off[kBuffers], total = 0;
+  for (int i = 0; i < kBuffers; ++i) {
+    off[i] = total;
+    total += (sizes[i] + 255) & ~(size_t)255;
+  }
+  if (total > limit) return total;
+  p.logits = reinterpret_cast<float*>(base + off[0]);
+  p.router_part = reinterpret_cast<float*>(base + off[1]);
+  p.top_idx = reinterpret_cast<int*>(base + off[2]);
+  p.top_w = reinterpret_cast<float*>(base + off[3]);
+  p.shared_w = reinterpret_cast<float*>(base + off[4]);
+  p.perm = reinterpret_cast<int*>(base + off[5]);
+  p.chunks = reinterpret_cast<MoeChunk*>(base + off[6]);
+  p.down_out = reinterpret_cast<float*>(base + off[7]);
+  p.xq = reinterpret_cast<uint16_t*>(base + off[8]);
+  p.xsum = reinterpret_cast<float*>(base + off[9]);
+  p.aq = reinterpret_cast<uint16_t*>(base + off[10]);
+  p.asum = reinterpret_cast<float*>(base + off[11]);
+  p.counts = reinterpret_cast<int*>(base + off[12]);
+  p.chunk_counts = reinterpret_cast<int*>(base + off[13]);
+  p.error = reinterpret_cast<int*>(base + off[14]);
+  p.router_ks = router_slices(p.hidden);
+  p.capacity = T;
+  return total;
+}
+
+}  // namespace
+
+extern "C" {
+
+int llambda_hip_moe_session_run_device_noalloc(llambda_hip_moe_session* s, const float* input,
+                                               float* output, size_t batch, void* stream) {
+  return guarded([&] {
+    if (!s) failf("moe_session_run_device_noalloc: null session");
+    if (!input || !output) failf("moe_session_run_device_noalloc: null input or output");
+    if (batch == 0 || batch > (1u << 20))
+      failf("moe_session_run_device_noalloc: bad batch %zu", batch);
+    if (reinterpret_cast<uintptr_t>(input) & 15u)
+      failf("moe_session_run_device_noalloc: input must be 16-byte aligned");
+    std::lock_guard<std::mutex> lock(s->run_mutex);
+    HIPC(hipSetDevice(s->device));
+    const int T = (int)batch;
+    MoePlan p = s->plan;  // the session's weights and knobs; the scratch is replaced
+    const size_t need = carve_moe_scratch(p, T, nullptr, 0);
+    if (need > kMoeNoallocScratchBytes)
+      failf("moe_session_run_device_noalloc: %zu tokens of this layer need %zu bytes of scratch; "
+            "the no-allocation entry point holds %zu (run fewer tokens per call, or use "
+            "llambda_hip_moe_session_run_device)",
+            batch, need, kMoeNoallocScratchBytes);
+    uint8_t* base = noalloc_scratch(s->device);
+    carve_moe_scratch(p, T, base, kMoeNoallocScratchBytes);
+    const hipStream_t st = stream ? static_cast<hipStream_t>(stream) : s->stream;
+    // the histogram and the error flag must start at zero (the array keeps
+    // the last call's contents); a fill kernel, not a memset, so that a
+    // captured graph replays it faithfully
+    HIPC(moe_reset_launch(p, st));
+    HIPC(moe_forward_launch(p, input, output, T, st));
+    // errors reach the session's own flag, reported by moe_session_sync
+    HIPC(moe_error_merge_launch(p.error, s->plan.error, st));
   });
 }
 

@@ -138,6 +138,9 @@ hipError_t moe_forward_launch(const MoePlan& p, const float* x, float* y, int to
 // the histogram zeroed again).
 hipError_t moe_reset_launch(const MoePlan& p, hipStream_t stream);
 
+// OR the flags at src into dst (one thread; no host round trip).
+hipError_t moe_error_merge_launch(const int* src, int* dst, hipStream_t stream);
+
 // Batched device top-k with the reference's selection rule (test hook).
 hipError_t topk_launch(const float* logits, int n, int k, int batch, int* idx, float* val,
                        hipStream_t stream);

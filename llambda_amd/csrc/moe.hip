@@ -334,6 +334,14 @@ __global__ void moe_reset_kernel(int* counts, int n, int* error) {
   if (blockIdx.x == 0 && threadIdx.x == 0) *error = 0;
 }
 
+// OR a run's error flags into another flag word (one thread).
+__global__ void moe_error_merge_kernel(const int* __restrict__ src, int* __restrict__ dst) {
+  if (threadIdx.x == 0) {
+    const int f = *src;
+    if (f) atomicOr(dst, f);
+  }
+}
+
 // ------------------------------------------------------------------ host
 
 
@@ -507,6 +515,10 @@ hipError_t moe_forward_launch(const MoePlan& p, const float* x, float* y, int to
 
 hipError_t moe_reset_launch(const MoePlan& p, hipStream_t s) {
   return launch(moe_reset_kernel, dim3(4), dim3(256), 0, s, p.counts, p.experts, p.error);
+}
+
+hipError_t moe_error_merge_launch(const int* src, int* dst, hipStream_t s) {
+  return launch(moe_error_merge_kernel, dim3(1), dim3(64), 0, s, src, dst);
 }
 
 hipError_t topk_launch(const float* logits, int n, int k, int batch, int* idx, float* val,

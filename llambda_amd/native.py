@@ -131,6 +131,8 @@ SIGNATURES = {
                                             c_void_p, c_void_p, c_void_p]),
     "llambda_hip_moe_session_run_device": (c_int, [c_void_p, c_void_p, c_void_p, c_size, c_void_p]),
     "llambda_hip_moe_session_sync": (c_int, [c_void_p, c_void_p]),
+    "llambda_hip_moe_session_run_device_noalloc": (c_int, [c_void_p, c_void_p, c_void_p, c_size,
+                                                           c_void_p]),
     "llambda_hip_select_top_k": (c_int, [c_void_p, c_size, c_size, c_size, c_void_p, c_void_p]),
     "llambda_hip_llama_session_create": (c_int, [ctypes.POINTER(LlamaDesc),
                                                  ctypes.POINTER(c_void_p)]),
