@@ -423,9 +423,11 @@ static MoeScratchBytes moe_scratch_bytes(const MoePlan& p, size_t T) {
   // the decode pipeline stages whole 256-element chunks (1 KB of split row)
   // of a row's last, partial chunk: 1 KB of readable slack
   b.xq = T * 2 * H * sizeof(uint16_t) + 1024;
-  b.xsum = T * (H / 16) * sizeof(float);
+  // (+ 256: the group pipeline stages the sums of two 32-groups at a time
+  // and reads past a row whose group count is odd)
+  b.xsum = T * (H / 16) * sizeof(float) + 256;
   b.aq = pairs * 2 * act_w * sizeof(uint16_t) + 1024;
-  b.asum = pairs * (act_w / 16) * sizeof(float);
+  b.asum = pairs * (act_w / 16) * sizeof(float) + 256;
   return b;
 }
 

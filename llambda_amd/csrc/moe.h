@@ -121,9 +121,12 @@ hipError_t router_mfma_launch(const float* x, int T, const float* R, int Er, int
                               int ld, uint16_t* q, int64_t q_stride, float* s, int64_t s_stride,
                               hipStream_t stream);
 // mt: 0 = one token (K split over four wavefronts), 1 = chunks of up to 16
-// pairs (double-buffered), 2 = chunks of up to 32 pairs.
+// pairs (double-buffered), 2 = chunks of up to 32 pairs, 4 = chunks of up to
+// 64 pairs, activations shared by the workgroup (32-weight block types only:
+// moe_group_pipeline_types).
 hipError_t moe_gemm_launch(int type, int epi, const MoeGemmArgs& a, int mt, int max_chunks,
                            hipStream_t stream);
+bool moe_group_pipeline_types(int type);
 
 // Upper bound of the chunk table for `tokens` tokens with chunk size nt.
 int64_t moe_max_chunks(const MoePlan& p, int64_t tokens, int nt);

@@ -377,7 +377,16 @@ static int64_t row_bytes_of(int type, int64_t columns) {
 static int moe_mfma_tiles(const MoePlan& p, int tokens) {
   if (tokens == 1) return 0;
   const int64_t avg = ((int64_t)tokens * p.top_k + p.experts - 1) / p.experts;
-  return avg <= 16 ? 1 : 2;
+  if (avg <= 16) return 1;
+  // the group pipeline (64-pair chunks) for 32-weight block types, while its
+  // 32-bit byte offsets into the split rows and their sums fit
+  const bool types = moe_group_pipeline_types(p.up_type) && moe_group_pipeline_types(p.down_type) &&
+                     (p.shared_ffn == 0 || (moe_group_pipeline_types(p.sh_up_type) &&
+                                            moe_group_pipeline_types(p.sh_down_type)));
+  const int64_t act_w = std::max(p.ffn, p.shared_ffn);
+  const int64_t split_bytes = std::max((int64_t)tokens * (p.top_k + 1) * 4 * act_w,
+                                       (int64_t)tokens * 4 * p.hidden);
+  return types && split_bytes < ((int64_t)1 << 31) ? 4 : 2;
 }
 static int moe_chunk_tokens(int mt) { return mt == 0 ? 1 : 16 * mt; }
 

@@ -44,6 +44,9 @@
 // In every pipeline the LDS words of group j + 1 are read while group j
 // decodes and multiplies, and rows sit an odd number of 16-byte pieces apart
 // in LDS so that the 16 rows of one read fall in different bank quads.
+//   moe_group_kernel  4 token tiles (chunks of up to 64 pairs), 32-weight
+//                block types only: the chunk's activations staged once per
+//                workgroup by DMA and shared by its four waves (see below).
 //   kPipeDecode  one token: 4 waves share 32 rows and split K (wave w takes
 //                chunks w, w + 4, ...), each through a ring of up to 8 LDS
 //                stages of rows, the token's activations and group sums,
@@ -858,6 +861,351 @@ moe_gemm_kernel(MoeGemmArgs args) {
   if constexpr (PIPE != kPipeDouble) finish(n0);
 }
 
+// ------------------------------------------------------ group pipeline
+// Batches whose experts average more than 16 pairs, with 32-weight block
+// types (Q5_0, Q8_0): chunks of up to 64 (token, rank) pairs of one expert,
+// four 16-token tiles.  A workgroup of four waves takes 64 rows per wave (32
+// of gate and 32 of up for silu-gate products) and streams K in stages of two
+// 32-groups through a double-buffered LDS ring, both operands by DMA:
+//   the chunk's split activations and group sums, once per workgroup and
+//   shared by its waves -- stored piece-major, [piece][token][16 bytes], so
+//   that the 16 tokens of one MFMA fragment read 256 contiguous bytes;
+//   each wave's weight rows, piece-major as well, [piece][row][16 bytes].
+// One barrier per stage: after it, every wave's DMA of the stage has landed
+// and every wave is done with the other buffer, which then takes the next
+// stage's DMA while this one computes.  The per-output arithmetic is the
+// other batch pipelines' instruction for instruction (exact bf16 codes, hi
+// then lo MFMA, per-group delta fma in group order, the -c * sum offsets of
+// each 256-element chunk after its eight groups), so a token's output does
+// not depend on the pipeline, and hence on the batch, it runs in.
+constexpr int kGroupWaves = 4;
+constexpr int kGroupTiles = 4;    // 16-token tiles per chunk
+constexpr int kGroupAPieces = 17; // 16 pieces of split activations + 1 of group sums
+
+template <int TYPE>
+struct GroupB;
+template <>
+struct GroupB<kQ5_0> {
+  static constexpr int kBlock = 22, kPieces = 3;  // two blocks + a 0..3-byte shift
+};
+template <>
+struct GroupB<kQ8_0> {
+  static constexpr int kBlock = 34, kPieces = 5;
+};
+
+template <int TYPE, int EPI>
+struct GroupShape {
+  static constexpr int NB = EPI == kEpiSwiglu ? 2 : 1;
+  static constexpr int ROWS = 64 / NB;  // rows per matrix and wave
+  static constexpr int NS = ROWS / 16;
+  static constexpr int WG_ROWS = kGroupWaves * ROWS;
+  static constexpr int PIECES = GroupB<TYPE>::kPieces;
+  static constexpr int A_BYTES = kGroupAPieces * 1024;
+  static constexpr int B_BYTES = PIECES * NB * 1024;  // per wave
+  static constexpr int STAGE = A_BYTES + kGroupWaves * B_BYTES;
+  static constexpr int LDS = 2 * STAGE;
+};
+
+// Dword i of row r of a piece-major weight stage (matrix nb).
+template <int NB>
+__device__ __forceinline__ uint32_t pm_dword(const uint8_t* wbuf, int nb, int r, uint32_t i) {
+  return *reinterpret_cast<const uint32_t*>(wbuf + (((i >> 2) * NB + nb) * 64 + r) * 16 + 4 * (i & 3));
+}
+
+// The words GemmB<TYPE>::fetch reads and the scale of group j, from the
+// piece-major stage (byte o of the row image: dword o >> 2).
+template <int TYPE, int NB>
+__device__ __forceinline__ typename GemmB<TYPE>::Raw group_fetch(const uint8_t* wbuf, int nb, int r,
+                                                                 uint32_t sh, int j, int g) {
+  if constexpr (TYPE == kQ5_0) {
+    const uint32_t o = sh + 22u * (uint32_t)j;
+    const uint32_t os = (o + 6u + 8u * (uint32_t)(g & 1)) >> 2, ob = (o + 2u + (uint32_t)g) >> 2;
+    return u32x4{pm_dword<NB>(wbuf, nb, r, os), pm_dword<NB>(wbuf, nb, r, os + 1u),
+                 pm_dword<NB>(wbuf, nb, r, os + 2u), pm_dword<NB>(wbuf, nb, r, ob)};
+  } else {
+    const uint32_t os = (sh + 34u * (uint32_t)j + 2u + 8u * (uint32_t)g) >> 2;
+    return u32x4{pm_dword<NB>(wbuf, nb, r, os), pm_dword<NB>(wbuf, nb, r, os + 1u),
+                 pm_dword<NB>(wbuf, nb, r, os + 2u), 0u};
+  }
+}
+template <int TYPE, int NB>
+__device__ __forceinline__ void group_scale(const uint8_t* wbuf, int nb, int r, uint32_t sh, int j,
+                                            float& delta, float& c) {
+  const uint32_t o = sh + (uint32_t)GroupB<TYPE>::kBlock * (uint32_t)j;  // even
+  const uint32_t bits = (pm_dword<NB>(wbuf, nb, r, o >> 2) >> (8 * (o & 3u))) & 0xFFFFu;
+  delta = half_bits_to_float(bits);
+  if constexpr (TYPE == kQ5_0) c = 144.f * delta;
+  else c = 128.f * delta;
+}
+
+template <int TYPE, int EPI>
+__global__ void __launch_bounds__(64 * kGroupWaves, 2) moe_group_kernel(MoeGemmArgs args) {
+  using B = GemmB<TYPE>;
+  using Sh = GroupShape<TYPE, EPI>;
+  constexpr int NB = Sh::NB, NS = Sh::NS, MT = kGroupTiles;
+  constexpr int BB = GroupB<TYPE>::kBlock;
+  extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+
+  // (chunk, row tile) from the XCD-grouped 1-D grid of the batch pipelines
+  const int T = args.row_tiles, L = blockIdx.x;
+  const int bx = (L / (8 * T)) * 8 + (L & 7);
+  const int by = (L >> 3) % T;
+  const int* cc = args.chunk_counts;
+  const MoeChunk ch = args.chunks[(!args.joint && args.group ? cc[0] : 0) + bx];
+  const int nchunks = args.joint ? cc[0] + cc[1] : cc[args.group];
+  if (bx >= nchunks) return;  // the whole workgroup, before any barrier
+  MoeGemmArgs a = args;
+  if (args.joint && bx >= cc[0]) {
+    a.w0 = args.s_w0;
+    a.w1 = args.s_w1;
+    a.row_bytes = args.s_row_bytes;
+    a.expert_stride = 0;
+    a.N = args.s_N;
+    a.K = args.s_K;
+  }
+  const int wg_row0 = by * Sh::WG_ROWS;
+  if (wg_row0 >= a.N) return;  // the whole workgroup
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int n = lane & 15, g = lane >> 4;
+  // rows of this wave (a wave past the last row still takes part in every
+  // barrier: its rows clamp to the last one and its outputs are dropped)
+  const int n0 = wg_row0 + wave * Sh::ROWS;
+  const int count = __builtin_amdgcn_readfirstlane(ch.count);
+  const int start = __builtin_amdgcn_readfirstlane(ch.start);
+  const int expert = __builtin_amdgcn_readfirstlane(ch.expert);
+  const int nt = (count + 15) >> 4;  // token tiles holding pairs
+
+  // lane l = token l of the chunk: its split row and group sums (tokens past
+  // the count read the first token's)
+  const int q_l = a.perm[start + (lane < count ? lane : 0)];
+  const int64_t r_l = a.a_by_token ? (q_l < a.pairs ? q_l / a.top_k : q_l - a.pairs) : q_l;
+  const uint32_t a_off = (uint32_t)(r_l * a.aq_stride * 2);
+  const uint32_t s_off = (uint32_t)(r_l * a.as_stride * 4);
+  const uint8_t* aq_base = uniform_ptr(reinterpret_cast<const uint8_t*>(a.aq));
+  const uint8_t* as_base = uniform_ptr(reinterpret_cast<const uint8_t*>(a.as));
+  const uint8_t* base[NB];
+  base[0] = uniform_ptr(a.w0 + (int64_t)expert * a.expert_stride);
+  if constexpr (NB == 2) base[1] = uniform_ptr(a.w1 + (int64_t)expert * a.expert_stride);
+  const uint32_t rb = (uint32_t)a.row_bytes;
+  // DMA lane l: row (l mod ROWS) of each matrix
+  const uint32_t brow = (uint32_t)min(n0 + (lane & (Sh::ROWS - 1)), a.N - 1) * rb;
+  // fetch rows 16 m + n: their byte shift within a dword is the same at
+  // every stage (2 blocks span a multiple of 4 bytes) and for every m (rows
+  // 16 apart: row_bytes * 16 is a multiple of 4), so the subtiles' LDS words
+  // sit at constant offsets from one address.  (A row past the last one
+  // reads the clamped row's bytes at this shift; its outputs are dropped.)
+  const uint32_t sh0 = ((uint32_t)(n0 + n) * rb) & 3u;
+  uint32_t sh[NS];
+#pragma unroll
+  for (int m = 0; m < NS; ++m) sh[m] = sh0;
+
+  const int groups = a.K >> 5;
+  const int nstage = (groups + 1) >> 1;
+  const uint32_t lds0 = lds_address(lds);
+
+  auto issue = [&](int st, int buf) {
+    const uint32_t stg = lds0 + (uint32_t)(buf * Sh::STAGE);
+    for (int p = wave; p < kGroupAPieces; p += kGroupWaves) {
+      if (p < 16) load_lds16(aq_base, a_off + 256u * (uint32_t)st + 16u * (uint32_t)p, stg + 1024u * p);
+      else load_lds16(as_base, s_off + 16u * (uint32_t)st, stg + 1024u * 16u);
+    }
+    const uint32_t wst = stg + Sh::A_BYTES + (uint32_t)wave * Sh::B_BYTES;
+    const uint32_t off = (brow + (uint32_t)st * (uint32_t)(2 * BB)) & ~3u;
+#pragma unroll
+    for (int k = 0; k < Sh::PIECES; ++k)
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb)
+        load_lds16(base[nb], off + 16u * (uint32_t)k, wst + (uint32_t)((k * NB + nb) * 1024));
+  };
+
+  floatx4 tot[MT][NS][NB];
+#pragma unroll
+  for (int i = 0; i < MT; ++i)
+#pragma unroll
+    for (int m = 0; m < NS; ++m)
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb) tot[i][m][nb] = floatx4{0.f, 0.f, 0.f, 0.f};
+  // offsets of the current 256-element chunk: -c of group 4 q + g of the
+  // lane's rows, and the lane token's sum of that group
+  float cneg[NS][NB][2];
+  float sv[MT][2];
+  auto clear_offsets = [&]() {
+#pragma unroll
+    for (int m = 0; m < NS; ++m)
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb) cneg[m][nb][0] = cneg[m][nb][1] = 0.f;
+#pragma unroll
+    for (int i = 0; i < MT; ++i) sv[i][0] = sv[i][1] = 0.f;
+  };
+  clear_offsets();
+
+  // The token-tile count is a compile-time parameter of the stage loop (four
+  // copies, one chosen per workgroup): no branch may separate an MFMA from
+  // the VALU instruction that reads its result, or the wait states the
+  // result needs can be lost on the branch path.
+  auto apply_offsets = [&](auto ntc) {
+    constexpr int NT = decltype(ntc)::value;
+#pragma unroll
+    for (int q = 0; q < 2; ++q)
+#pragma unroll
+      for (int i = 0; i < NT; ++i)
+#pragma unroll
+        for (int m = 0; m < NS; ++m)
+#pragma unroll
+          for (int nb = 0; nb < NB; ++nb)
+            tot[i][m][nb] = mfma4f32(sv[i][q], cneg[m][nb][q], tot[i][m][nb]);
+    clear_offsets();
+  };
+
+  auto compute = [&](auto ntc, int st, auto bufc) {
+    constexpr int NT = decltype(ntc)::value;
+    const uint8_t* stg = lds + decltype(bufc)::value * Sh::STAGE;
+    const uint8_t* wbuf = stg + Sh::A_BYTES + wave * Sh::B_BYTES;
+    const int ls = st & 3;  // stage within the 256-element chunk
+#pragma unroll
+    for (int jj = 0; jj < 2; ++jj) {
+      if (2 * st + jj < groups) {
+        const int j8 = 2 * ls + jj;  // group within the chunk
+        typename B::Raw raw[NS][NB];
+        float dl[NS][NB];
+#pragma unroll
+        for (int m = 0; m < NS; ++m)
+#pragma unroll
+          for (int nb = 0; nb < NB; ++nb) {
+            raw[m][nb] = group_fetch<TYPE, NB>(wbuf, nb, 16 * m + n, sh[m], jj, g);
+            float c;
+            group_scale<TYPE, NB>(wbuf, nb, 16 * m + n, sh[m], jj, dl[m][nb], c);
+            // (q = j8 >> 2 is uniform: a select per lane, not an indexed write)
+            const bool mine = (j8 & 3) == g;
+            cneg[m][nb][0] = (mine && j8 < 4) ? -c : cneg[m][nb][0];
+            cneg[m][nb][1] = (mine && j8 >= 4) ? -c : cneg[m][nb][1];
+          }
+        bf16x8 hi[NT], lo[NT];
+#pragma unroll
+        for (int i = 0; i < NT; ++i) {
+          const uint8_t* ap = stg + ((jj * 8 + g) * 64 + 16 * i + n) * 16;
+          hi[i] = *reinterpret_cast<const bf16x8*>(ap);
+          lo[i] = *reinterpret_cast<const bf16x8*>(ap + 4 * 1024);
+        }
+#pragma unroll
+        for (int m = 0; m < NS; ++m)
+#pragma unroll
+          for (int nb = 0; nb < NB; ++nb) {
+            const typename B::Frag bf = B::decode(raw[m][nb], sh[m], jj, g);
+            const float delta = dl[m][nb];
+#pragma unroll
+            for (int i = 0; i < NT; ++i) {
+              floatx4 d = mfma_b(hi[i], bf, floatx4{0.f, 0.f, 0.f, 0.f});
+              d = mfma_b(lo[i], bf, d);
+              floatx4& t = tot[i][m][nb];
+              t[0] = fmaf(delta, d[0], t[0]);
+              t[1] = fmaf(delta, d[1], t[1]);
+              t[2] = fmaf(delta, d[2], t[2]);
+              t[3] = fmaf(delta, d[3], t[3]);
+            }
+          }
+      }
+    }
+    // this stage holds groups 2 st and 2 st + 1: lanes whose offset group
+    // 4 q + g is one of them take the lane token's sum of it (the sum of
+    // its two 16-halves, as the other pipelines form it)
+    {
+      const bool mine = (g >> 1) == (ls & 1);
+      const bool ok = 2 * st + (g & 1) < groups;
+#pragma unroll
+      for (int i = 0; i < NT; ++i) {
+        const float* sp = reinterpret_cast<const float*>(stg + 16 * 1024 + (16 * i + n) * 16);
+        const float v = sp[2 * (g & 1)] + sp[2 * (g & 1) + 1];
+        const float val = ok ? v : 0.f;
+        sv[i][0] = (mine && ls < 2) ? val : sv[i][0];
+        sv[i][1] = (mine && ls >= 2) ? val : sv[i][1];
+      }
+    }
+  };
+
+  // epilogue: lane (n, g) holds tokens 16 i + 4 g + r of rows n0 + 16 m + n
+  // (the pairs they belong to are read here, not held through the products)
+  auto finish = [&](auto ntc) {
+    constexpr int NT = decltype(ntc)::value;
+#pragma unroll
+    for (int i = 0; i < NT; ++i) {
+      int qout[4];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int tk = 16 * i + 4 * g + r;
+        qout[r] = tk < count ? a.perm[start + tk] : 0;
+      }
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int tk = 16 * i + 4 * g + r;
+        const bool ok_t = tk < count;
+        const int q = qout[r];
+        if constexpr (EPI == kEpiDown) {
+#pragma unroll
+          for (int m = 0; m < NS; ++m) {
+            const int row = n0 + 16 * m + n;
+            if (ok_t && row < a.N) a.out[(int64_t)q * a.out_stride + row] = tot[i][m][0][r];
+          }
+        } else {
+          uint16_t* oq = a.oq + (int64_t)q * a.oq_stride;
+          float* os = a.os + (int64_t)q * a.os_stride;
+#pragma unroll
+          for (int m = 0; m < NS; ++m) {
+            const int row = n0 + 16 * m + n;
+            float act;
+            if constexpr (EPI == kEpiSwiglu) {
+#pragma clang fp contract(off)
+              act = silu_ref(tot[i][m][0][r]) * tot[i][m][1][r];  // llambda.lisp:5386-5401
+            } else {
+              act = relu2_ref(tot[i][m][0][r]);  // llambda.lisp:5921-5926
+            }
+            uint32_t hb, lb;
+            float sum;
+            split_bf16(act, hb, lb, sum);
+            const bool ok = ok_t && row < a.N;
+            if (ok) {
+              uint16_t* p = oq + 64 * (row >> 5) + (row & 31);
+              p[0] = (uint16_t)hb;
+              p[32] = (uint16_t)lb;
+            }
+            const float s16 = group_sum(ok ? sum : 0.f, 4);
+            if (n == 0 && ok) os[row >> 4] = s16;
+          }
+        }
+      }
+    }
+  };
+
+  // the stages; each 256-element chunk's offsets follow its last stage (the
+  // final chunk's after the loop, in line with the epilogue)
+  // (two stages per iteration: the buffer of each is a compile-time
+  // constant, folded into the LDS instructions' offsets)
+  auto stage = [&](auto ntc, int st, auto bufc) {
+    __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
+    __syncthreads();
+    if (st + 1 < nstage) issue(st + 1, 1 - decltype(bufc)::value);
+    compute(ntc, st, bufc);
+    if ((st & 3) == 3 && st + 1 < nstage) apply_offsets(ntc);
+  };
+  auto run = [&](auto ntc) {
+    issue(0, 0);
+    for (int st = 0; st < nstage; st += 2) {
+      stage(ntc, st, std::integral_constant<int, 0>{});
+      if (st + 1 < nstage) stage(ntc, st + 1, std::integral_constant<int, 1>{});
+    }
+    apply_offsets(ntc);
+    finish(ntc);
+  };
+  switch (nt) {
+    case 1: run(std::integral_constant<int, 1>{}); break;
+    case 2: run(std::integral_constant<int, 2>{}); break;
+    case 3: run(std::integral_constant<int, 3>{}); break;
+    default: run(std::integral_constant<int, 4>{}); break;
+  }
+
+}
+
 // ------------------------------------------------------------------ host
 
 template <int TYPE, int EPI, int MT, int PIPE, bool ALIGNED>
@@ -925,9 +1273,50 @@ static hipError_t launch_gemm_epi(int type, const MoeGemmArgs& a, int mt, int ma
   }
 }
 
+template <int TYPE, int EPI>
+static hipError_t launch_group_t(const MoeGemmArgs& a_in, int max_chunks, hipStream_t stream) {
+  using Sh = GroupShape<TYPE, EPI>;
+  MoeGemmArgs a = a_in;
+  const auto kernel = moe_group_kernel<TYPE, EPI>;
+  if (Sh::LDS > 65536) {
+    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kernel),
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, Sh::LDS);
+    if (e != hipSuccess) return e;
+  }
+  const int rows = a.joint ? std::max(a.N, a.s_N) : a.N;
+  a.row_tiles = (rows + Sh::WG_ROWS - 1) / Sh::WG_ROWS;
+  a.tiles_per_wg = 1;
+  a.depth = 2;
+  const dim3 grid(((max_chunks + 7) / 8) * 8 * a.row_tiles);
+  hipLaunchKernelGGL(kernel, grid, dim3(64 * kGroupWaves), Sh::LDS, stream, a);
+  return hipGetLastError();
+}
+
+template <int EPI>
+static hipError_t launch_group_epi(int type, const MoeGemmArgs& a, int max_chunks, hipStream_t s) {
+  // the stage offsets (256 bytes of split row, 16 of sums per stage) are
+  // 32-bit: the launcher only chooses this pipeline when they fit
+  if (a.K % 32 || (a.joint && a.s_K % 32)) return hipErrorInvalidValue;
+  switch (type) {
+    case kQ5_0: return launch_group_t<kQ5_0, EPI>(a, max_chunks, s);
+    case kQ8_0: return launch_group_t<kQ8_0, EPI>(a, max_chunks, s);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+bool moe_group_pipeline_types(int type) { return type == kQ5_0 || type == kQ8_0; }
+
 hipError_t moe_gemm_launch(int type, int epi, const MoeGemmArgs& a, int mt, int max_chunks,
                            hipStream_t stream) {
   if (max_chunks <= 0 || a.N <= 0) return hipSuccess;
+  if (mt == 4) {
+    switch (epi) {
+      case kEpiSwiglu: return launch_group_epi<kEpiSwiglu>(type, a, max_chunks, stream);
+      case kEpiRelu2: return launch_group_epi<kEpiRelu2>(type, a, max_chunks, stream);
+      case kEpiDown: return launch_group_epi<kEpiDown>(type, a, max_chunks, stream);
+      default: return hipErrorInvalidValue;
+    }
+  }
   switch (epi) {
     case kEpiSwiglu: return launch_gemm_epi<kEpiSwiglu>(type, a, mt, max_chunks, stream);
     case kEpiRelu2: return launch_gemm_epi<kEpiRelu2>(type, a, mt, max_chunks, stream);
