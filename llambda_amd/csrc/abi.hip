@@ -437,7 +437,7 @@ struct llambda_hip_moe_session {
   hipStream_t stream = nullptr;
   MoePlan plan{};
   DevBuf router, bias, gate, up, down, sh_gate, sh_up, sh_down;
-  DevBuf logits, router_part, top_idx, top_w, shared_w, counts, perm, chunks, chunk_counts,
+  DevBuf logits, router_part, top_idx, top_w, shared_w, perm, chunks, chunk_counts,
       down_out, error, xq, xsum, aq, asum;
   DevBuf x, y;
   int staged = 0;
@@ -614,10 +614,8 @@ int llambda_hip_moe_session_create(const llambda_hip_moe_desc* d,
         p.sh_up = s->sh_up.as<uint8_t>();
         p.sh_down = s->sh_down.as<uint8_t>();
       }
-      s->counts.alloc((size_t)E * sizeof(int), "expert histogram");
       s->chunk_counts.alloc(2 * sizeof(int), "chunk counts");
       s->error.alloc(sizeof(int), "error flag");
-      p.counts = s->counts.as<int>();
       p.chunk_counts = s->chunk_counts.as<int>();
       p.error = s->error.as<int>();
       p.capacity = 0;
@@ -746,10 +744,9 @@ uint8_t* noalloc_scratch(int device) {
 // the bytes the layout needs (nothing is assigned when that exceeds limit).
 size_t carve_moe_scratch(MoePlan& p, int T, uint8_t* base, size_t limit) {
   const MoeScratchBytes b = moe_scratch_bytes(p, (size_t)T);
-  const size_t E = (size_t)p.experts;
   const size_t sizes[] = {b.logits, b.router_part, b.top_idx, b.top_w, b.shared_w, b.perm,
-                          b.chunks, b.down_out, b.xq, b.xsum, b.aq, b.asum,
-                          E * sizeof(int), 2 * sizeof(int), sizeof(int)};
+                          b.chunks, b.down_out, b.xq, b.xsum, b.aq, b.asum, 2 * sizeof(int),
+                          sizeof(int)};
   constexpr int kBuffers = sizeof(sizes) / sizeof(sizes[0]);
   size_t off[kBuffers], total = 0;
   for (int i = 0; i < kBuffers; ++i) {
@@ -769,9 +766,8 @@ size_t carve_moe_scratch(MoePlan& p, int T, uint8_t* base, size_t limit) {
   p.xsum = reinterpret_cast<float*>(base + off[9]);
   p.aq = reinterpret_cast<uint16_t*>(base + off[10]);
   p.asum = reinterpret_cast<float*>(base + off[11]);
-  p.counts = reinterpret_cast<int*>(base + off[12]);
-  p.chunk_counts = reinterpret_cast<int*>(base + off[13]);
-  p.error = reinterpret_cast<int*>(base + off[14]);
+  p.chunk_counts = reinterpret_cast<int*>(base + off[12]);
+  p.error = reinterpret_cast<int*>(base + off[13]);
   p.router_ks = router_slices(p.hidden);
   p.capacity = T;
   return total;
@@ -803,9 +799,9 @@ int llambda_hip_moe_session_run_device_noalloc(llambda_hip_moe_session* s, const
     uint8_t* base = noalloc_scratch(s->device);
     carve_moe_scratch(p, T, base, kMoeNoallocScratchBytes);
     const hipStream_t st = stream ? static_cast<hipStream_t>(stream) : s->stream;
-    // the histogram and the error flag must start at zero (the array keeps
-    // the last call's contents); a fill kernel, not a memset, so that a
-    // captured graph replays it faithfully
+    // the error flag must start at zero (the array keeps the last call's
+    // contents); a fill kernel, not a memset, so that a captured graph
+    // replays it faithfully
     HIPC(moe_reset_launch(p, st));
     HIPC(moe_forward_launch(p, input, output, T, st));
     // errors reach the session's own flag, reported by moe_session_sync

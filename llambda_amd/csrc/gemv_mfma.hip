@@ -287,12 +287,52 @@ __device__ float rms_scale(const float* __restrict__ x, int K, float eps, float*
   return 1.f / sqrtf(mean + eps);
 }
 
+// One batch of the activation table: the thread's items base + threadIdx.x
+// + j * T (j < kMaxI) with their elements v (and, with a fused rms-norm-into,
+// norm weights wv) loaded.  A table of one batch takes the rms scale from
+// the loaded elements (sum of squares over the workgroup); then x (or
+// (x * w) * scale, rounded as the reference rounds) is split into the table.
+template <typename IT, int WAVES>
+__device__ __forceinline__ void table_batch(float (&v)[16 / IT::kEl][IT::kEl],
+                                            const float (&wv)[16 / IT::kEl][IT::kEl], int base,
+                                            int items, bool one_batch, float& nscale,
+                                            const float* __restrict__ nw, int nblk, float eps,
+                                            float* red, uint8_t* table, float* gsum) {
+  constexpr int T = 64 * WAVES, EL = IT::kEl, kMaxI = 16 / EL;
+  if (nw && one_batch) {
+    float acc = 0.f;
+#pragma unroll
+    for (int j = 0; j < kMaxI; ++j)
+      if (base + threadIdx.x + j * T < items)
+#pragma unroll
+        for (int e = 0; e < EL; ++e) acc += v[j][e] * v[j][e];
+    for (int o = 32; o > 0; o >>= 1) acc += __shfl_xor(acc, o, 64);
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = acc;
+    __syncthreads();
+    float sum = red[0];
+#pragma unroll
+    for (int w = 1; w < WAVES; ++w) sum += red[w];
+    __syncthreads();
+    nscale = 1.f / sqrtf(sum / (float)(nblk * 256) + eps);
+  }
+#pragma unroll
+  for (int j = 0; j < kMaxI; ++j) {
+    const int i = base + threadIdx.x + j * T;
+    if (i < items) {
+      if (nw) {
+#pragma unroll
+        for (int e = 0; e < EL; ++e) v[j][e] = (v[j][e] * wv[j][e]) * nscale;
+      }
+      IT::emit(table, gsum, i, v[j]);
+    }
+  }
+}
+
 // The activation table of one workgroup: every thread loads the elements of
 // its items (up to kMaxI items, 16 floats, at once: one memory latency),
 // with a fused rms-norm-into (llambda.lisp:859-879) also their norm weights
-// and the sum of squares; then splits x (or (x * w) * scale, rounded as the
-// reference rounds) into the table.  x is 16-byte aligned.  red: kMfmaWaves
-// floats of LDS.
+// and the sum of squares; then splits x into the table.  x is 16-byte
+// aligned.  red: kMfmaWaves floats of LDS.
 template <typename IT, int WAVES>
 __device__ void build_table(uint8_t* table, float* gsum, const float* __restrict__ x, int nblk,
                             const float* __restrict__ nw, float eps, float* red) {
@@ -317,34 +357,101 @@ __device__ void build_table(uint8_t* table, float* gsum, const float* __restrict
         }
       }
     }
-    if (nw && one_batch) {
-      float acc = 0.f;
-#pragma unroll
-      for (int j = 0; j < kMaxI; ++j)
-        if (base + threadIdx.x + j * T < items)
-#pragma unroll
-          for (int e = 0; e < EL; ++e) acc += v[j][e] * v[j][e];
-      for (int o = 32; o > 0; o >>= 1) acc += __shfl_xor(acc, o, 64);
-      if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = acc;
-      __syncthreads();
-      float sum = red[0];
-#pragma unroll
-      for (int w = 1; w < WAVES; ++w) sum += red[w];
-      __syncthreads();
-      nscale = 1.f / sqrtf(sum / (float)(nblk * 256) + eps);
-    }
-#pragma unroll
-    for (int j = 0; j < kMaxI; ++j) {
-      const int i = base + threadIdx.x + j * T;
-      if (i < items) {
-        if (nw) {
-#pragma unroll
-          for (int e = 0; e < EL; ++e) v[j][e] = (v[j][e] * wv[j][e]) * nscale;
-        }
-        IT::emit(table, gsum, i, v[j]);
-      }
-    }
+    table_batch<IT, WAVES>(v, wv, base, items, one_batch, nscale, nw, nblk, eps, red, table, gsum);
   }
+}
+
+// true when the table of nblk blocks is one batch of per-thread items
+template <typename IT, int WAVES>
+__host__ __device__ constexpr bool table_one_batch(int nblk) {
+  return nblk * IT::kPerBlock <= 64 * WAVES * (16 / IT::kEl);
+}
+
+// The loads of a one-batch table and of a wave's first stage in one asm
+// statement: the thread's four 16-byte x loads and four norm-weight loads
+// (x again without a norm), then the stage's NL DMAs (lane i of load k:
+// 16 bytes from wb + wo[k] to LDS dst + 1024 k + 16 i), then a wait until
+// only the DMAs are in flight (vector loads complete in issue order).  The
+// x registers are outputs of the statement, defined only after its wait, so
+// no instruction can read them while their loads are in flight; the table
+// is then built while the stage streams in.
+#define LLHIP_PRO_DMA(k, imm) \
+  "s_add_u32 m0, %[dst], " #imm "\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %[w" #k "], %[wb]\n\t"
+#define LLHIP_PRO_DMA1 LLHIP_PRO_DMA(0, 0)
+#define LLHIP_PRO_DMA2 LLHIP_PRO_DMA1 LLHIP_PRO_DMA(1, 0x400)
+#define LLHIP_PRO_DMA3 LLHIP_PRO_DMA2 LLHIP_PRO_DMA(2, 0x800)
+#define LLHIP_PRO_DMA4 LLHIP_PRO_DMA3 LLHIP_PRO_DMA(3, 0xc00)
+#define LLHIP_PRO_DMA5 LLHIP_PRO_DMA4 LLHIP_PRO_DMA(4, 0x1000)
+#define LLHIP_PRO_DMA6 LLHIP_PRO_DMA5 LLHIP_PRO_DMA(5, 0x1400)
+#define LLHIP_PRO_DMA7 LLHIP_PRO_DMA6 LLHIP_PRO_DMA(6, 0x1800)
+#define LLHIP_PRO_ASM(NL)                                                                   \
+  asm volatile("global_load_dwordx4 %[v0], %[o0], %[xb]\n\t"                                \
+               "global_load_dwordx4 %[v1], %[o1], %[xb]\n\t"                                \
+               "global_load_dwordx4 %[v2], %[o2], %[xb]\n\t"                                \
+               "global_load_dwordx4 %[v3], %[o3], %[xb]\n\t"                                \
+               "global_load_dwordx4 %[v4], %[o0], %[nb]\n\t"                                \
+               "global_load_dwordx4 %[v5], %[o1], %[nb]\n\t"                                \
+               "global_load_dwordx4 %[v6], %[o2], %[nb]\n\t"                                \
+               "global_load_dwordx4 %[v7], %[o3], %[nb]\n\t" LLHIP_PRO_DMA##NL            \
+               "s_waitcnt vmcnt(" #NL ")"                                                   \
+               : [m0o] "=&{m0}"(m0_out), [v0] "=&v"(r[0]), [v1] "=&v"(r[1]),               \
+                 [v2] "=&v"(r[2]), [v3] "=&v"(r[3]), [v4] "=&v"(r[4]), [v5] "=&v"(r[5]),   \
+                 [v6] "=&v"(r[6]), [v7] "=&v"(r[7])                                         \
+               : [o0] "v"(xo[0]), [o1] "v"(xo[1]), [o2] "v"(xo[2]), [o3] "v"(xo[3]),        \
+                 [xb] "s"(xb), [nb] "s"(nb), [wb] "s"(wb), [dst] "s"(dst), [w0] "v"(o[0]),  \
+                 [w1] "v"(o[1]), [w2] "v"(o[2]), [w3] "v"(o[3]), [w4] "v"(o[4]),            \
+                 [w5] "v"(o[5]), [w6] "v"(o[6])                                             \
+               : "memory", "scc")
+
+template <int NL>
+__device__ __forceinline__ void prologue_loads(floatx4 (&r)[8], const float* xb, const float* nb,
+                                               const uint32_t (&xo)[4], const uint8_t* wb,
+                                               const uint32_t* wo, uint32_t dst) {
+  static_assert(NL >= 1 && NL <= 7, "stage loads per wave");
+  uint32_t o[7] = {0u, 0u, 0u, 0u, 0u, 0u, 0u};
+#pragma unroll
+  for (int k = 0; k < NL; ++k) o[k] = wo[k];
+  uint32_t m0_out;
+  if constexpr (NL == 1) LLHIP_PRO_ASM(1);
+  else if constexpr (NL == 2) LLHIP_PRO_ASM(2);
+  else if constexpr (NL == 3) LLHIP_PRO_ASM(3);
+  else if constexpr (NL == 4) LLHIP_PRO_ASM(4);
+  else if constexpr (NL == 5) LLHIP_PRO_ASM(5);
+  else if constexpr (NL == 6) LLHIP_PRO_ASM(6);
+  else LLHIP_PRO_ASM(7);
+  (void)m0_out;
+}
+
+// A one-batch table built while stage 0 (NL loads from wb + wo to LDS dst)
+// streams in: the same items, values and arithmetic as build_table.
+template <typename IT, int WAVES, int NL>
+__device__ __forceinline__ void build_table_overlapped(uint8_t* table, float* gsum,
+                                                       const float* __restrict__ x, int nblk,
+                                                       const float* __restrict__ nw, float eps,
+                                                       float* red, const uint8_t* wb,
+                                                       const uint32_t* wo, uint32_t dst) {
+  constexpr int T = 64 * WAVES, EL = IT::kEl, kMaxI = 16 / EL;
+  static_assert(kMaxI * EL == 16, "four 16-byte loads of x per thread");
+  const int items = nblk * IT::kPerBlock;
+  uint32_t xo[4];
+#pragma unroll
+  for (int j = 0; j < kMaxI; ++j) {
+    const int x0 = IT::first(min((int)threadIdx.x + j * T, items - 1));
+#pragma unroll
+    for (int e = 0; e < EL; e += 4) xo[(j * EL + e) / 4] = (uint32_t)(x0 + e) * 4u;
+  }
+  floatx4 r[8];
+  prologue_loads<NL>(r, x, nw ? nw : x, xo, wb, wo, dst);
+  float v[kMaxI][EL], wv[kMaxI][EL];
+#pragma unroll
+  for (int j = 0; j < kMaxI; ++j)
+#pragma unroll
+    for (int e = 0; e < EL; ++e) {
+      v[j][e] = r[(j * EL + e) / 4][e & 3];
+      wv[j][e] = r[4 + (j * EL + e) / 4][e & 3];
+    }
+  float nscale = 1.f;
+  table_batch<IT, WAVES>(v, wv, 0, items, true, nscale, nw, nblk, eps, red, table, gsum);
 }
 
 // Store the value v of row `row` (every lane of the wavefront calls this with
@@ -533,18 +640,16 @@ __device__ __forceinline__ void gemv_mfma_body(uint8_t* lds, int wg, int nwg, co
   // Row r of the tile starts at base + r * rb; its range is read from the
   // dword at or below that, i.e. from base_al + ((bsh + r * rb) & ~3) with
   // base_al = base & ~3 and bsh = base & 3 (offsets stay non-negative).
-  auto issue = [&](int s) {
+  auto stage_src = [&](int s, uint32_t (&o)[Ch::kLoads]) {
     const int tile = tile_of(s);
     const int chunk = chunk_of(s);
     const uint8_t* base =
         uniform_ptr(w + (int64_t)tile * 16 * row_bytes + (int64_t)chunk * Ch::kSpan);
     const uint32_t bsh = ALIGNED ? 0u : (uint32_t)(reinterpret_cast<uintptr_t>(base) & 3u);
-    const uint8_t* base_al = base - bsh;
-    const uint32_t dst = stage_lds + (uint32_t)((s % nbuf) * Ch::kBuffer);
     const int rmax = rows - 1 - tile * 16;
     if (ALIGNED && rmax >= 15) {
 #pragma unroll
-      for (int i = 0; i < Ch::kLoads; ++i) load_lds16(base_al, voff[i], dst + 1024u * i);
+      for (int i = 0; i < Ch::kLoads; ++i) o[i] = voff[i];
     } else {
       // unaligned rows, or the last, partial tile (rows past the end re-read
       // the last row)
@@ -553,24 +658,39 @@ __device__ __forceinline__ void gemv_mfma_body(uint8_t* lds, int wg, int nwg, co
         const int idx = min(64 * i + lane, 16 * Ch::kPieces - 1);
         const int r = idx / Ch::kPieces;
         const uint32_t rr = (uint32_t)min(r, rmax);
-        const uint32_t o = ((bsh + rr * rb) & ~3u) + 16u * (uint32_t)(idx - r * Ch::kPieces);
-        load_lds16(base_al, o, dst + 1024u * i);
+        o[i] = ((bsh + rr * rb) & ~3u) + 16u * (uint32_t)(idx - r * Ch::kPieces);
       }
     }
+    return base - bsh;
+  };
+  auto issue = [&](int s) {
+    uint32_t o[Ch::kLoads];
+    const uint8_t* base_al = stage_src(s, o);
+    const uint32_t dst = stage_lds + (uint32_t)((s % nbuf) * Ch::kBuffer);
+#pragma unroll
+    for (int i = 0; i < Ch::kLoads; ++i) load_lds16(base_al, o[i], dst + 1024u * i);
   };
 
-  // activation table first: its loads would otherwise queue behind the
-  // weight stages' and hold every wave's first step back (measured: the
-  // 4096 x 4096 Q4_K GEMV 7.5 -> 6.2 us, the Llama decode token -5%)
   for (int i = threadIdx.x; i < T::kZero / 16; i += blockDim.x)
     reinterpret_cast<u32x4*>(lds)[i] = u32x4{0u, 0u, 0u, 0u};
-  if constexpr (TYPE == kQ4_K)
-    build_table<Q4Items, kMfmaWaves>(table, gsum, x, nblk, f.norm_w, f.norm_eps, partial);
-  else
-    build_table<Q6Items, kMfmaWaves>(table, gsum, x, nblk, f.norm_w, f.norm_eps, partial);
-  // then every stage is filled
+  using IT = std::conditional_t<TYPE == kQ4_K, Q4Items, Q6Items>;
   const int first = min(nbuf, steps);
-  for (int s = 0; s < first; ++s) issue(s);
+  if (table_one_batch<IT, kMfmaWaves>(nblk) && first == 1) {
+    // one stage per wave: its DMA is issued right behind the table's loads
+    // and streams in while the table is built
+    uint32_t o[Ch::kLoads];
+    const uint8_t* base_al = stage_src(0, o);
+    build_table_overlapped<IT, kMfmaWaves, Ch::kLoads>(table, gsum, x, nblk, f.norm_w,
+                                                        f.norm_eps, partial, base_al, o,
+                                                        stage_lds);
+  } else {
+    // activation table first: its loads would otherwise queue behind the
+    // weight stages' and hold every wave's first step back (measured: the
+    // 4096 x 4096 Q4_K GEMV 7.5 -> 6.2 us, the Llama decode token -5%)
+    build_table<IT, kMfmaWaves>(table, gsum, x, nblk, f.norm_w, f.norm_eps, partial);
+    // then every stage is filled
+    for (int s = 0; s < first; ++s) issue(s);
+  }
   __syncthreads();
 
   float acc = 0.f;

@@ -4,9 +4,9 @@
 // nemotron-h-moe-ffn-into (llambda.lisp:5827-5949) for a batch of tokens,
 // as a fixed sequence of launches on one stream:
 //   1 router GEMV (F32)              logits[t][e]  (+ shared-gate dot, qwen3next)
-//   2 top-k + gating, one wavefront per token; expert histogram
-//   3 scan + scatter (one workgroup): token-to-expert permutation and the
-//     chunk table of (expert, first pair, pair count) work items
+//   2 top-k + gating, one wavefront per token
+//   3 histogram, scan + scatter (one workgroup): token-to-expert permutation
+//     and the chunk table of (expert, first pair, pair count) work items
 //   4 grouped up: gate/up rows of each expert against its chunk of tokens,
 //     activation fused (silu(g)*u, or relu(u)^2)
 //   5 grouped down: down rows against the chunk's activations, per pair
@@ -54,7 +54,6 @@ struct MoePlan {
   int* top_idx;        // [capacity][top_k]
   float* top_w;        // [capacity][top_k]
   float* shared_w;     // [capacity]
-  int* counts;         // [experts]          zero between runs
   int* perm;           // [capacity * (top_k + 1)]
   MoeChunk* chunks;    // [max_chunks(capacity)]
   int* chunk_counts;   // [2]: routed chunks, shared chunks
@@ -137,8 +136,7 @@ int64_t moe_max_chunks(const MoePlan& p, int64_t tokens, int nt);
 hipError_t moe_forward_launch(const MoePlan& p, const float* x, float* y, int tokens,
                               hipStream_t stream);
 
-// Zero the histogram and the error flag (session set-up; every run leaves
-// the histogram zeroed again).
+// Zero the error flag (a fill kernel, so that a captured graph replays it).
 hipError_t moe_reset_launch(const MoePlan& p, hipStream_t stream);
 
 // OR the flags at src into dst (one thread; no host round trip).

@@ -74,9 +74,8 @@ __global__ void __launch_bounds__(256) topk_kernel(const float* __restrict__ log
 // sigmoid, renormalise, error when the sum is not positive) or 5894-5913
 // (nemotron: bias before selection, sigmoid, optional renormalise, scale).
 // The weight sum runs over the ranks in order, as the reference's loop does.
-// Then either the expert histogram (batches) or, for a single token, the
-// chunk table itself: one chunk per selected expert in rank order, then the
-// shared expert.
+// For a single token it also writes the chunk table: one chunk per selected
+// expert in rank order, then the shared expert.
 template <int JPL>
 __global__ void __launch_bounds__(256) topk_gate_kernel(MoePlan p, int tokens, int single) {
 #pragma clang fp contract(off)
@@ -171,10 +170,7 @@ __global__ void __launch_bounds__(256) topk_gate_kernel(MoePlan p, int tokens, i
   if (lane == 0) p.shared_w[t] = has_shared_row ? sigmoid_ref(shared_logit) : 1.f;
   if (err) atomicOr(p.error, err);
   const bool valid = has && mi >= 0 && mi < E;
-  if (!single) {
-    if (valid) atomicAdd(&p.counts[mi], 1);
-    return;
-  }
+  if (!single) return;  // the scan kernel counts the experts' pairs
   // single token: pair id of rank r is r; the shared pair is K
   const uint64_t mask = __ballot(valid);
   const int pos = __popcll(mask & ((1ull << lane) - 1ull));
@@ -195,10 +191,10 @@ __global__ void __launch_bounds__(256) topk_gate_kernel(MoePlan p, int tokens, i
 }
 
 // ------------------------------------------------------------ scan/scatter
-// One workgroup: exclusive scans of the expert histogram (pairs and chunks),
-// the chunk table, and the permutation that groups (token, rank) pairs by
-// expert.  Pair id p = token * k + rank; the shared expert's pairs are
-// tokens * k + token.  Leaves the histogram zeroed for the next run.
+// One workgroup: the expert histogram of the top-k indices (in LDS), its
+// exclusive scans (pairs and chunks), the chunk table, and the permutation
+// that groups (token, rank) pairs by expert.  Pair id p = token * k + rank;
+// the shared expert's pairs are tokens * k + token.
 constexpr int kScanThreads = 1024;
 
 __global__ void __launch_bounds__(kScanThreads) moe_scan_kernel(MoePlan p, int tokens, int nt,
@@ -210,10 +206,17 @@ __global__ void __launch_bounds__(kScanThreads) moe_scan_kernel(MoePlan p, int t
   __shared__ int s_part[kScanThreads];
   __shared__ int s_cpart[kScanThreads];
   const int E = p.experts, K = p.top_k, tid = threadIdx.x;
+  const int P = tokens * K;
   for (int e = tid; e < E; e += kScanThreads) {
-    s_cnt[e] = p.counts[e];
+    s_cnt[e] = 0;
     s_cur[e] = 0;
-    p.counts[e] = 0;
+  }
+  __syncthreads();
+  // the histogram of the selected experts, in LDS (global atomics on a hot
+  // expert's counter serialise hundreds of increments)
+  for (int q = tid; q < P; q += kScanThreads) {
+    const int e = p.top_idx[q];
+    if (e >= 0 && e < E) atomicAdd(&s_cnt[e], 1);
   }
   __syncthreads();
   const int per = (E + kScanThreads - 1) / kScanThreads;
@@ -257,7 +260,6 @@ __global__ void __launch_bounds__(kScanThreads) moe_scan_kernel(MoePlan p, int t
       p.chunks[s_coff[e] + j] = ch;
     }
   }
-  const int P = tokens * K;
   int shared_chunks = 0;
   if (has_shared) {
     shared_chunks = (tokens + nt - 1) / nt;
@@ -328,10 +330,8 @@ __global__ void __launch_bounds__(256) moe_combine_kernel(MoePlan p, float* __re
   y[(int64_t)t * H + i] = acc;
 }
 
-__global__ void moe_reset_kernel(int* counts, int n, int* error) {
-  for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x)
-    counts[i] = 0;
-  if (blockIdx.x == 0 && threadIdx.x == 0) *error = 0;
+__global__ void moe_reset_kernel(int* error) {
+  if (threadIdx.x == 0) *error = 0;
 }
 
 // OR a run's error flags into another flag word (one thread).
@@ -523,7 +523,7 @@ hipError_t moe_forward_launch(const MoePlan& p, const float* x, float* y, int to
 }
 
 hipError_t moe_reset_launch(const MoePlan& p, hipStream_t s) {
-  return launch(moe_reset_kernel, dim3(4), dim3(256), 0, s, p.counts, p.experts, p.error);
+  return launch(moe_reset_kernel, dim3(1), dim3(64), 0, s, p.error);
 }
 
 hipError_t moe_error_merge_launch(const int* src, int* dst, hipStream_t s) {
