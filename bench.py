@@ -113,9 +113,12 @@ def gemv_bytes(type_tag, rows, columns, tokens=1):
     return rows * ggml.row_bytes(type_tag, columns) + 4 * columns * tokens + 4 * rows * tokens
 
 
-def bench_gemv(torch, timer, type_tag, rows, columns, steps, warmup, seed=1, copies=1):
+def bench_gemv(torch, timer, type_tag, rows, columns, steps, warmup, seed=1, copies=1,
+               sustained=None):
     """One GEMV; with copies > 1 each launch reads a different weight copy
-    (rotation), so the 256 MB MALL cannot serve them."""
+    (rotation), so the 256 MB MALL cannot serve them.  sustained = (settle,
+    launches): after the timed steps, `settle` more launches untimed, then
+    `launches` timed ones (ms per launch in state["sustained_ms"])."""
     rng = np.random.default_rng(seed)
     log(f"generating {copies} x {ggml.NAMES[type_tag]} {rows}x{columns}")
     sessions = []
@@ -134,9 +137,14 @@ def bench_gemv(torch, timer, type_tag, rows, columns, steps, warmup, seed=1, cop
         s.run_device(x.data_ptr(), y.data_ptr(), 1, timer.handle)
 
     ms = timer.time(step, steps, warmup)
+    if sustained:
+        settle, launches = sustained
+        state["sustained_ms"] = timer.time(step, launches, settle)
     for s in sessions:
         s.close()
     nbytes = gemv_bytes(type_tag, rows, columns)
+    if sustained:
+        return ms, nbytes, state["sustained_ms"]
     return ms, nbytes
 
 
@@ -367,9 +375,15 @@ def main():
 
     if args.only in (None, "head"):
         rows, cols = 128256, 4096
-        ms, nbytes = bench_gemv(torch, timer, ggml.Q6_K, rows, cols, steps, warmup)
+        # the timed steps, then a sustained figure: a fresh process's first
+        # ~100 ms of launches carry a power-management transient (launches
+        # 26-75 run ~15% slower), so 800 launches are timed after 300 more
+        ms, nbytes, ms_sus = bench_gemv(torch, timer, ggml.Q6_K, rows, cols, steps, warmup,
+                                        sustained=(300, 800))
         gbs = nbytes / (ms * 1e-3) / 1e9
-        log(f"Q6_K head: {ms * 1e3:.1f} us/launch, {gbs:.0f} GB/s")
+        gbs_sus = nbytes / (ms_sus * 1e-3) / 1e9
+        log(f"Q6_K head: {ms * 1e3:.1f} us/launch, {gbs:.0f} GB/s; sustained "
+            f"{ms_sus * 1e3:.1f} us/launch, {gbs_sus:.0f} GB/s")
         cpu = None
         if args.cpu_seconds > 0:
             cpu_gbs, n = cpu_gemv_baseline(ggml.Q6_K, rows, cols, args.cpu_seconds)
@@ -393,6 +407,9 @@ def main():
             "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS,
                          "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4),
                          "traffic": traffic},
+            "sustained": {"launches": 800, "after_launches": steps + warmup + 300,
+                          "us_per_launch": round(ms_sus * 1e3, 2), "GB/s": round(gbs_sus, 1),
+                          "frac": round(gbs_sus / HBM_PEAK_GBS, 4)},
             "cpu_baseline": cpu,
         }
 

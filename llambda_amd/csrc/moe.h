@@ -127,6 +127,21 @@ hipError_t moe_gemm_launch(int type, int epi, const MoeGemmArgs& a, int mt, int 
                            hipStream_t stream);
 bool moe_group_pipeline_types(int type);
 
+// One token's down products and their combine in one launch (moe_mfma.hip):
+// a.chunks / a.chunk_counts / a.perm as topk_gate_kernel writes them for a
+// single token; routed and shared down rows of one weight type (a.joint, or
+// no shared expert).  y = sum over valid ranks r (in order) of top_w[r] *
+// down_r, then + shared_w * down_shared (shared_scaled) or + down_shared.
+struct MoeCombineArgs {
+  float* y;               // [hidden]
+  const float* top_w;     // [top_k] gating weights by rank
+  const float* shared_w;  // [1] shared-expert gate
+  int shared_scaled;      // 1: Qwen3Next's sigmoid-gated shared expert; 0: Nemotron-H's
+};
+bool moe_down_combine_supported(int type, const MoeGemmArgs& a);
+hipError_t moe_down_combine_launch(int type, const MoeGemmArgs& a, const MoeCombineArgs& c,
+                                   hipStream_t stream);
+
 // Upper bound of the chunk table for `tokens` tokens with chunk size nt.
 int64_t moe_max_chunks(const MoePlan& p, int64_t tokens, int nt);
 

@@ -503,6 +503,15 @@ hipError_t moe_forward_launch(const MoePlan& p, const float* x, float* y, int to
     a.s_N = H;
     a.s_K = p.shared_ffn;
   }
+  // one token: the down products and the combine in one launch
+  if (single && (!has_shared || joint_down) && moe_down_combine_supported(p.down_type, a)) {
+    MoeCombineArgs c{};
+    c.y = y;
+    c.top_w = p.top_w;
+    c.shared_w = p.shared_w;
+    c.shared_scaled = p.variant == kQwen3Next;
+    return moe_down_combine_launch(p.down_type, a, c, s);
+  }
   e = moe_gemm_launch(p.down_type, kEpiDown, a, mt, routed_chunks + (joint_down ? shared_chunks : 0), s);
   if (e != hipSuccess) return e;
   if (has_shared && !joint_down) {

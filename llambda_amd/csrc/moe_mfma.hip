@@ -861,6 +861,233 @@ moe_gemm_kernel(MoeGemmArgs args) {
   if constexpr (PIPE != kPipeDouble) finish(n0);
 }
 
+// ------------------------------------------------ one token: down + combine
+// The down products of one token's chunks (its valid ranks' experts in rank
+// order, then the shared expert) and their weighted combine, in one launch.
+// Workgroup r takes rows 16 r .. 16 r + 15 of every chunk.  The work units
+// are the chunks' 256-element K steps (chunk by chunk, steps in order); wave
+// w of 8 takes units w, w + 8, ..., streaming each unit's rows by DMA with
+// the pair's 256 split activations and their 16 group sums through a ring of
+// LDS stages filled ahead of use.  A unit leaves the partial sums of its 16
+// rows in LDS; after one barrier lanes 0..15 of wave 0 add each chunk's
+// partials in K order (the single-token pipeline's split-K sum) and combine
+// the chunks as moe_combine_kernel does: rank order, every product and sum
+// rounded separately (llambda.lisp:3465-3489; 5359, 5409, 5426, 5914, 5932,
+// 5949).  At batch 1 the chunk table has chunk c = {expert, start c, one
+// pair} and perm[c] = its rank (the shared chunk: perm[c] = top_k), as
+// topk_gate_kernel writes them.
+constexpr int kCombineSlots = 64;   // chunks of one token: top_k + 1 (read back by readlane)
+constexpr int kCombineUnits = 128;  // (chunk, K step) units of one token
+
+template <int TYPE>
+struct CombineShape {
+  using B = GemmB<TYPE>;
+  static constexpr int kWaves = 8;
+  static constexpr int PPR = B::kPitch / 16;       // 16-byte pieces per row
+  static constexpr int PIECES = 16 * PPR;          // 16 rows
+  static constexpr int LOADS = (PIECES + 63) / 64;
+  static constexpr int ROWBUF = 1024 * LOADS;
+  static constexpr int A_OFF = ROWBUF;             // the pair's 256 split elements (1 KB)
+  static constexpr int S_OFF = ROWBUF + 1024;      // their 16 group sums
+  static constexpr int STAGE = ROWBUF + 1024 + 256;
+  static constexpr int DEPTH = 4;
+  static constexpr int DMA = LOADS + 2;            // loads per stage
+  static constexpr int TABLE = B::kSteps * 16 * 8;  // (delta, -c) per group and row
+  static constexpr int OUT = kCombineUnits * 16 * 4;
+};
+
+template <int TYPE>
+constexpr int combine_lds_bytes(int depth) {
+  using Sh = CombineShape<TYPE>;
+  return Sh::OUT + Sh::kWaves * (depth * Sh::STAGE + Sh::TABLE);
+}
+
+// One 256-element K step of a wave's 16 rows for the one token: the body of
+// moe_gemm_kernel's per-chunk computation with one subtile, one matrix and
+// one token tile (scale table, groups with the next group's LDS words
+// fetched ahead, then the chunk's offsets).
+template <int TYPE, bool ALIGNED, bool FULL>
+__device__ __forceinline__ void combine_step(int kc, const uint8_t* stage, uint32_t brow,
+                                             int groups, float2* table, int n, int g,
+                                             floatx4& tot) {
+  using B = GemmB<TYPE>;
+  using Sh = CombineShape<TYPE>;
+  constexpr int NQ = B::kSteps / 4, KS = B::kSteps;
+  typedef AFrag<B::kWide> AF;
+  const uint32_t koff = (uint32_t)kc * (uint32_t)B::kSpan;
+  const int valid = FULL ? KS : min(KS, groups - kc * KS);
+  const uint32_t sh = ALIGNED ? (koff & 3u) : ((brow + koff) & 3u);
+  const uint8_t* row = stage + n * B::kPitch;
+  // scale table: lane (n, g) decodes groups g*KS/4 .. +KS/4-1 of row n
+#pragma unroll
+  for (int e = 0; e < KS / 4; ++e) {
+    const int j = g * (KS / 4) + e;
+    float delta, c;
+    B::scale(row, sh, j, delta, c);
+    const bool ok = j < valid;
+    table[j * 16 + n] = float2{ok ? delta : 0.f, ok ? -c : 0.f};
+  }
+  typename B::Raw raw[2];
+  float dl[2];
+  auto fetch = [&](int j, typename B::Raw& r, float& d) {
+    r = B::fetch(row, sh, j, g);
+    d = table[j * 16 + n].x;
+  };
+  fetch(0, raw[0], dl[0]);
+#pragma unroll
+  for (int j = 0; j < KS; ++j) {
+    if (FULL || j < valid) {
+      AF af;
+      af.load(reinterpret_cast<const uint16_t*>(stage + Sh::A_OFF) + AF::offset(j, g));
+      if (j + 1 < KS && (FULL || j + 1 < valid)) fetch(j + 1, raw[(j + 1) & 1], dl[(j + 1) & 1]);
+      const typename B::Frag bf = B::decode(raw[j & 1], sh, j, g);
+      const float delta = dl[j & 1];
+      floatx4 d = mfma_b(af.hi, bf, floatx4{0.f, 0.f, 0.f, 0.f});
+      d = mfma_b(af.lo, bf, d);
+      tot[0] = fmaf(delta, d[0], tot[0]);
+      tot[1] = fmaf(delta, d[1], tot[1]);
+      tot[2] = fmaf(delta, d[2], tot[2]);
+      tot[3] = fmaf(delta, d[3], tot[3]);
+    }
+  }
+  // offsets: group 4q + g of the chunk in K slice g of MFMA q
+  const float* ssum = reinterpret_cast<const float*>(stage + Sh::S_OFF);
+#pragma unroll
+  for (int q = 0; q < NQ; ++q) {
+    const float cb = table[(4 * q + g) * 16 + n].y;
+    const int gi = min(kc * KS + 4 * q + g, groups - 1) - kc * KS;
+    float sv;
+    if constexpr (B::kStepK == 32) sv = ssum[2 * gi] + ssum[2 * gi + 1];
+    else sv = ssum[gi];
+    tot = mfma4f32(sv, cb, tot);
+  }
+}
+
+template <int TYPE, bool ALIGNED>
+__global__ void __launch_bounds__(64 * CombineShape<TYPE>::kWaves)
+moe_down_combine_kernel(MoeGemmArgs a, MoeCombineArgs cb) {
+  using B = GemmB<TYPE>;
+  using Sh = CombineShape<TYPE>;
+  constexpr int KS = B::kSteps, W = Sh::kWaves;
+  extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int n = lane & 15, g = lane >> 4;
+  const int n0 = blockIdx.x * 16;
+  const int K = a.top_k;
+  float* parts = reinterpret_cast<float*>(lds);  // [kCombineUnits][16]
+  const int depth = a.depth;
+  uint8_t* wlds = lds + Sh::OUT + wave * (depth * Sh::STAGE + Sh::TABLE);
+  float2* table = reinterpret_cast<float2*>(wlds + depth * Sh::STAGE);
+  const uint32_t wlds_addr = lds_address(wlds);
+
+  // lane i: the entry and the pair of chunk i, read with the counts (chunk
+  // c's pair is perm[c] at batch 1), and its K, K steps and row bytes, read
+  // back by readlane
+  const int ci = min(lane, K);
+  const int ex = a.chunks[ci].expert;
+  const int pq = a.perm[ci];
+  // wave 0: the gating weight of routed chunk `lane` (its rank perm[lane];
+  // lanes past the token's chunks read a clamped, unused entry)
+  float wl = 0.f;
+  if (wave == 0) wl = cb.top_w[max(0, min(a.perm[ci], K - 1))];
+  const float shw = cb.shared_scaled ? cb.shared_w[0] : 0.f;
+  const int nv = a.chunk_counts[0], ns = a.chunk_counts[1];
+  const bool lane_shared = lane >= nv;
+  const int kv = lane_shared ? a.s_K : a.K;
+  const int rbv = (int)(lane_shared ? a.s_row_bytes : a.row_bytes);
+  const int nk_r = (a.K + 255) >> 8, nk_s = ns ? (a.s_K + 255) >> 8 : 0;
+  const int routed_units = nv * nk_r;
+  const int units = routed_units + nk_s;
+  const int mine = units > wave ? (units - wave + W - 1) / W : 0;  // units of this wave
+  // unit u: chunk u / nk_r, step u % nk_r (routed), or the shared chunk nv
+  auto chunk_of = [=](int u) { return u < routed_units ? u / nk_r : nv; };
+  auto step_of = [=](int u) { return u < routed_units ? u - (u / nk_r) * nk_r : u - routed_units; };
+
+  auto issue = [&](int i, int slot) __attribute__((always_inline)) {
+    const int u = wave + W * i;
+    const int c = chunk_of(u), kc = step_of(u);
+    const int e = __builtin_amdgcn_readlane(ex, c);
+    const int q = __builtin_amdgcn_readlane(pq, c);
+    const uint8_t* base =
+        uniform_ptr(c >= nv ? a.s_w0 : a.w0 + (int64_t)e * a.expert_stride);
+    const uint32_t rb = (uint32_t)__builtin_amdgcn_readlane(rbv, c);
+    const int Kc = __builtin_amdgcn_readlane(kv, c);
+    const uint32_t koff = (uint32_t)kc * (uint32_t)B::kSpan;
+    const uint32_t st = wlds_addr + (uint32_t)(slot * Sh::STAGE);
+#pragma unroll
+    for (int l = 0; l < Sh::LOADS; ++l) {
+      const int idx = min(64 * l + lane, Sh::PIECES - 1);
+      const int r = idx / Sh::PPR;
+      const uint32_t off = (((uint32_t)min(n0 + r, a.N - 1) * rb + koff) & ~3u) +
+                           16u * (uint32_t)min(idx - r * Sh::PPR, B::kPieces - 1);
+      load_lds16(base, off, st + (uint32_t)(1024 * l));
+    }
+    const uint8_t* abase = uniform_ptr(
+        reinterpret_cast<const uint8_t*>(a.aq + (int64_t)q * a.aq_stride + 512 * kc));
+    load_lds16(abase, 16u * (uint32_t)lane, st + Sh::A_OFF);
+    const uint8_t* sbase =
+        uniform_ptr(reinterpret_cast<const uint8_t*>(a.as + (int64_t)q * a.as_stride + 16 * kc));
+    const int smax = min(16, (Kc >> 4) - 16 * kc) - 1;
+    load_lds4(sbase, 4u * (uint32_t)min(lane, smax), st + Sh::S_OFF);
+  };
+
+  const int first = min(depth, mine);
+  for (int i = 0; i < first; ++i) issue(i, i);
+  for (int i = 0; i < mine; ++i) {
+    const int ahead = min(mine, i + depth) - i - 1;  // stages issued after this one
+    switch (ahead) {
+      case 0: __builtin_amdgcn_s_waitcnt(waitcnt_vm(0)); break;
+      case 1: __builtin_amdgcn_s_waitcnt(waitcnt_vm(std::min(63, 1 * Sh::DMA))); break;
+      case 2: __builtin_amdgcn_s_waitcnt(waitcnt_vm(std::min(63, 2 * Sh::DMA))); break;
+      default: __builtin_amdgcn_s_waitcnt(waitcnt_vm(std::min(63, 3 * Sh::DMA))); break;
+    }
+    const int slot = i % depth;
+    const uint8_t* stage = wlds + slot * Sh::STAGE;
+    const int u = wave + W * i;
+    const int c = chunk_of(u), kc = step_of(u);
+    const int groups = __builtin_amdgcn_readlane(kv, c) / B::kStepK;
+    const uint32_t rb = (uint32_t)__builtin_amdgcn_readlane(rbv, c);
+    const uint32_t brow = (uint32_t)min(n0 + n, a.N - 1) * rb;
+    floatx4 tot = floatx4{0.f, 0.f, 0.f, 0.f};
+    if (kc * KS + KS <= groups)
+      combine_step<TYPE, ALIGNED, true>(kc, stage, brow, groups, table, n, g, tot);
+    else
+      combine_step<TYPE, ALIGNED, false>(kc, stage, brow, groups, table, n, g, tot);
+    __builtin_amdgcn_s_waitcnt(kWaitLgkm0);
+    if (i + depth < mine) issue(i + depth, slot);
+    // lane (n, 0) holds row n0 + n of the unit's one token
+    if (g == 0) parts[u * 16 + n] = tot[0];
+  }
+  __syncthreads();
+  if (wave != 0 || g != 0) return;
+  {
+#pragma clang fp contract(off)
+    auto chunk_sum = [&](int u0, int nk) {
+      float d = parts[u0 * 16 + n];
+      for (int k = 1; k < nk; ++k) d = d + parts[(u0 + k) * 16 + n];
+      return d;
+    };
+    float acc = 0.f;
+    for (int c = 0; c < nv; ++c) {
+      const float w = __builtin_bit_cast(
+          float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, wl), c));
+      const float prod = w * chunk_sum(c * nk_r, nk_r);
+      acc = acc + prod;
+    }
+    if (ns) {
+      const float d = chunk_sum(routed_units, nk_s);
+      if (cb.shared_scaled) {
+        const float prod = shw * d;
+        acc = acc + prod;
+      } else {
+        acc = acc + d;
+      }
+    }
+    if (n0 + n < a.N) cb.y[n0 + n] = acc;
+  }
+}
+
 // ------------------------------------------------------ group pipeline
 // Batches whose experts average more than 16 pairs, with 32-weight block
 // types (Q5_0, Q8_0): chunks of up to 64 (token, rank) pairs of one expert,
@@ -1305,6 +1532,51 @@ static hipError_t launch_group_epi(int type, const MoeGemmArgs& a, int max_chunk
 }
 
 bool moe_group_pipeline_types(int type) { return type == kQ5_0 || type == kQ8_0; }
+
+template <int TYPE, bool ALIGNED>
+static hipError_t launch_combine_t(const MoeGemmArgs& a_in, const MoeCombineArgs& c,
+                                   hipStream_t stream) {
+  using Sh = CombineShape<TYPE>;
+  MoeGemmArgs a = a_in;
+  constexpr int kLdsMax = 160 * 1024;
+  const int fit = (kLdsMax - combine_lds_bytes<TYPE>(0)) / (Sh::kWaves * Sh::STAGE);
+  a.depth = std::max(1, std::min(Sh::DEPTH, fit));
+  const int lds = combine_lds_bytes<TYPE>(a.depth);
+  const auto kernel = moe_down_combine_kernel<TYPE, ALIGNED>;
+  if (lds > 65536) {
+    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kernel),
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, lds);
+    if (e != hipSuccess) return e;
+  }
+  hipLaunchKernelGGL(kernel, dim3((a.N + 15) / 16), dim3(64 * Sh::kWaves), lds, stream, a, c);
+  return hipGetLastError();
+}
+
+bool moe_down_combine_supported(int type, const MoeGemmArgs& a) {
+  if (a.top_k < 1 || a.top_k + 1 > kCombineSlots || a.N <= 0) return false;
+  const int64_t units = (int64_t)a.top_k * ((a.K + 255) / 256) + (a.joint ? (a.s_K + 255) / 256 : 0);
+  if (units > kCombineUnits) return false;
+  return type == kQ4_K || type == kQ6_K || type == kQ5_0 || type == kQ8_0;
+}
+
+hipError_t moe_down_combine_launch(int type, const MoeGemmArgs& a, const MoeCombineArgs& c,
+                                   hipStream_t stream) {
+  if (!moe_down_combine_supported(type, a)) return hipErrorInvalidValue;
+  const bool aligned = a.row_bytes % 4 == 0 && (!a.joint || a.s_row_bytes % 4 == 0);
+  switch (type) {
+    case kQ4_K: return launch_combine_t<kQ4_K, true>(a, c, stream);
+    case kQ6_K:
+      return aligned ? launch_combine_t<kQ6_K, true>(a, c, stream)
+                     : launch_combine_t<kQ6_K, false>(a, c, stream);
+    case kQ5_0:
+      return aligned ? launch_combine_t<kQ5_0, true>(a, c, stream)
+                     : launch_combine_t<kQ5_0, false>(a, c, stream);
+    case kQ8_0:
+      return aligned ? launch_combine_t<kQ8_0, true>(a, c, stream)
+                     : launch_combine_t<kQ8_0, false>(a, c, stream);
+    default: return hipErrorInvalidValue;
+  }
+}
 
 hipError_t moe_gemm_launch(int type, int epi, const MoeGemmArgs& a, int mt, int max_chunks,
                            hipStream_t stream) {
