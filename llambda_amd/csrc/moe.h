@@ -111,6 +111,12 @@ struct MoeGemmArgs {
   const uint8_t* s_w1;
   int64_t s_row_bytes;
   int s_N, s_K;
+  // one token, up products: the launch selects and gates the token itself
+  // (top-k over router_part, gate_jpl = logits per lane); x index 0 is the
+  // shared expert (joint), then the valid ranks in rank order
+  int fused_gate;
+  int gate_jpl;
+  MoePlan plan;
 };
 
 // Router logits of T tokens (fp32 MFMA) as router_slices(H) partial sums

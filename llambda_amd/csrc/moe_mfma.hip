@@ -56,6 +56,7 @@
 #include "activations.h"
 #include "mfma.h"
 #include "moe.h"
+#include "moe_gate.h"
 
 #include <algorithm>
 #include <type_traits>
@@ -423,7 +424,9 @@ constexpr int gemm_lds_bytes(int depth) {
 // ------------------------------------------------------------ the kernel
 // ALIGNED: row_bytes % 4 == 0, so every row's chunk starts at the same offset
 // from a dword (Q4_K, Q5_0, Q8_0: 0; Q6_K: 2 in odd chunks).
-template <int TYPE, int EPI, int MT, int PIPE, bool ALIGNED>
+// GATE (single-token pipeline, one token): the launch also selects and
+// gates the token (gate_token) instead of reading a chunk table.
+template <int TYPE, int EPI, int MT, int PIPE, bool ALIGNED, bool GATE = false>
 __global__ void __launch_bounds__((64 * GemmShape<TYPE, EPI, PIPE>::kWaves),
                                   (PIPE == kPipeWide ? 2 : 1))
 moe_gemm_kernel(MoeGemmArgs args) {
@@ -449,12 +452,59 @@ moe_gemm_kernel(MoeGemmArgs args) {
   // follow the routed ones in the table).  Except for a separate shared
   // launch, the entry's index does not depend on the counts, and it is read
   // together with them (the table has room for every workgroup of the grid).
-  const MoeChunk ch = args.chunks[(!args.joint && args.group ? cc[0] : 0) + bx];
-  const int all_chunks = cc[0] + cc[1];
-  const int nchunks = args.joint ? all_chunks : cc[args.group];
-  if (bx >= nchunks) return;
+  MoeChunk ch;
+  bool shared_chunk;
+  int gate_pair = 0;  // GATE: the pair id of this workgroup's chunk
+  if constexpr (GATE) {
+    static_assert(PIPE == kPipeDecode && MT == 1, "the gate runs with the single-token pipeline");
+    // x index 0: the shared expert (when the launch carries it), which does
+    // not wait for the gate; then the token's valid ranks in rank order.
+    // Wave 0 selects and gates the token; the workgroup of the first rank's
+    // row tile 0 also stores the gate's outputs and the chunk table, which
+    // the later launches read.
+    __shared__ int gate_lds[2 * kMoeMaxTopK + 1];
+    const int has_sh = args.joint;
+    if (has_sh && bx == 0) {
+      ch = MoeChunk{0, args.top_k, 1};
+      shared_chunk = true;
+      gate_pair = args.top_k;
+    } else {
+      const int pos = bx - has_sh;
+      if (threadIdx.x < 64) {
+        const bool write = pos == 0 && by == 0;
+        GateRank r{};
+        switch (args.gate_jpl) {
+          case 1: r = gate_token<1>(args.plan, 0, 1, write); break;
+          case 2: r = gate_token<2>(args.plan, 0, 1, write); break;
+          case 4: r = gate_token<4>(args.plan, 0, 1, write); break;
+          case 8: r = gate_token<8>(args.plan, 0, 1, write); break;
+          default: r = gate_token<16>(args.plan, 0, 1, write); break;
+        }
+        const int l = threadIdx.x;
+        const uint64_t mask = __ballot(r.valid);
+        if (r.valid) {
+          const int pp = __popcll(mask & ((1ull << l) - 1ull));
+          gate_lds[pp] = r.idx;
+          gate_lds[kMoeMaxTopK + pp] = l;
+        }
+        if (l == 0) gate_lds[2 * kMoeMaxTopK] = __popcll(mask);
+        if (write) gate_chunk_table(args.plan, r.valid, r.idx);
+      }
+      __syncthreads();
+      if (pos >= gate_lds[2 * kMoeMaxTopK]) return;
+      ch = MoeChunk{gate_lds[pos], pos, 1};
+      gate_pair = gate_lds[kMoeMaxTopK + pos];
+      shared_chunk = false;
+    }
+  } else {
+    ch = args.chunks[(!args.joint && args.group ? cc[0] : 0) + bx];
+    const int all_chunks = cc[0] + cc[1];
+    const int nchunks = args.joint ? all_chunks : cc[args.group];
+    if (bx >= nchunks) return;
+    shared_chunk = args.joint && bx >= cc[0];
+  }
   MoeGemmArgs a = args;
-  if (args.joint && bx >= cc[0]) {
+  if (shared_chunk) {
     a.w0 = args.s_w0;
     a.w1 = args.s_w1;
     a.row_bytes = args.s_row_bytes;
@@ -482,7 +532,7 @@ moe_gemm_kernel(MoeGemmArgs args) {
 #pragma unroll
   for (int i = 0; i < MT; ++i) {
     const int tk = 16 * i + n;
-    const int q = a.perm[ch.start + (tk < ch.count ? tk : 0)];
+    const int q = GATE ? gate_pair : a.perm[ch.start + (tk < ch.count ? tk : 0)];
     const int64_t r = a.a_by_token ? (q < a.pairs ? q / a.top_k : q - a.pairs) : q;
     arow[i] = a.aq + r * a.aq_stride;
     srow[i] = a.as + r * a.as_stride;
@@ -495,7 +545,7 @@ moe_gemm_kernel(MoeGemmArgs args) {
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       const int tk = 16 * i + 4 * g + r;
-      qout[i][r] = tk < ch.count ? a.perm[ch.start + tk] : 0;
+      qout[i][r] = tk < ch.count ? (GATE ? gate_pair : a.perm[ch.start + tk]) : 0;
     }
   const uint8_t* base[NB];
   base[0] = uniform_ptr(a.w0 + (int64_t)ch.expert * a.expert_stride);
@@ -1435,7 +1485,7 @@ __global__ void __launch_bounds__(64 * kGroupWaves, 2) moe_group_kernel(MoeGemmA
 
 // ------------------------------------------------------------------ host
 
-template <int TYPE, int EPI, int MT, int PIPE, bool ALIGNED>
+template <int TYPE, int EPI, int MT, int PIPE, bool ALIGNED, bool GATE = false>
 static hipError_t launch_gemm_t(const MoeGemmArgs& a_in, int max_chunks, hipStream_t stream) {
   using Sh = GemmShape<TYPE, EPI, PIPE>;
   MoeGemmArgs a = a_in;
@@ -1447,7 +1497,7 @@ static hipError_t launch_gemm_t(const MoeGemmArgs& a_in, int max_chunks, hipStre
   const int fit = (kLdsMax - gemm_lds_bytes<TYPE, EPI, PIPE>(0)) / (Sh::kWaves * Sh::STAGE);
   a.depth = PIPE == kPipeDecode ? std::max(1, std::min({Sh::DEPTH, per_wave, fit})) : Sh::DEPTH;
   const int lds = gemm_lds_bytes<TYPE, EPI, PIPE>(a.depth);
-  const auto kernel = moe_gemm_kernel<TYPE, EPI, MT, PIPE, ALIGNED>;
+  const auto kernel = moe_gemm_kernel<TYPE, EPI, MT, PIPE, ALIGNED, GATE>;
   if (lds > 65536) {
     hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kernel),
                                        hipFuncAttributeMaxDynamicSharedMemorySize, lds);
@@ -1471,7 +1521,10 @@ static hipError_t launch_gemm_t(const MoeGemmArgs& a_in, int max_chunks, hipStre
 template <int TYPE, int EPI, bool ALIGNED>
 static hipError_t launch_gemm_mt(const MoeGemmArgs& a, int mt, int max_chunks, hipStream_t s) {
   switch (mt) {
-    case 0: return launch_gemm_t<TYPE, EPI, 1, kPipeDecode, ALIGNED>(a, max_chunks, s);
+    case 0:
+      if constexpr (EPI != kEpiDown)
+        if (a.fused_gate) return launch_gemm_t<TYPE, EPI, 1, kPipeDecode, ALIGNED, true>(a, max_chunks, s);
+      return launch_gemm_t<TYPE, EPI, 1, kPipeDecode, ALIGNED>(a, max_chunks, s);
     case 1: return launch_gemm_t<TYPE, EPI, 1, kPipeDouble, ALIGNED>(a, max_chunks, s);
     case 2: return launch_gemm_t<TYPE, EPI, 2, kPipeWide, ALIGNED>(a, max_chunks, s);
     default: return hipErrorInvalidValue;
