@@ -93,6 +93,7 @@ constexpr int kDppXor1 = 0xB1;         // quad_perm [1,0,3,2]
 constexpr int kDppXor2 = 0x4E;         // quad_perm [2,3,0,1]
 constexpr int kDppHalfMirror = 0x141;  // lane i <- 7-i within 8
 constexpr int kDppMirror = 0x140;      // lane i <- 15-i within 16
+constexpr int kDppRowRor8 = 0x128;     // lane i <- (i+8) mod 16 within 16, i.e. i ^ 8
 
 template <int CTRL>
 __device__ __forceinline__ int dpp_i(int v) {
@@ -135,6 +136,17 @@ __device__ __forceinline__ float group_sum(float v, int log2w) {
   }
   if (log2w >= 6) v += __shfl_xor(v, 32, 64);
   return v;
+}
+
+// Sum over the wavefront, every lane receiving it: rows of 16 lanes by DPP
+// (group_sum), then the four row sums as (r0 + r1) + (r2 + r3).
+__device__ __forceinline__ float wave_total(float v) {
+  const int b = __builtin_bit_cast(int, group_sum(v, 4));
+  const float r0 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 0));
+  const float r1 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 16));
+  const float r2 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 32));
+  const float r3 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 48));
+  return (r0 + r1) + (r2 + r3);
 }
 
 // Sum across `width` consecutive lanes (width a power of two <= 64).

@@ -96,9 +96,7 @@ struct Q4Items {
     *reinterpret_cast<u32x4*>(base + (2 * s) * 16) = vh;
     *reinterpret_cast<u32x4*>(base + (2 * s + 1) * 16) = vl;
     // group sum over the sub-block's 32 elements: 8 threads m = 0..7 share it
-    part += __shfl_xor(part, 1, 64);
-    part += __shfl_xor(part, 2, 64);
-    part += __shfl_xor(part, 4, 64);
+    part = group_sum(part, 3);
     if (m == 0) gsum[b * 8 + s] = part;
   }
 };
@@ -182,7 +180,7 @@ struct Q6Items {
     *reinterpret_cast<u32x4*>(base + (ahi * 2 + (g & 1)) * 16) = vh;
     *reinterpret_cast<u32x4*>(base + ((ahi + 1) * 2 + (g & 1)) * 16) = vl;
     // group (h, k, half = g >> 1) sums 16 elements: threads g, g ^ 1
-    part += __shfl_xor(part, 1, 64);
+    part = group_sum(part, 1);
     if ((g & 1) == 0) gsum[b * 16 + h * 8 + 2 * k + (g >> 1)] = part;
   }
 };
@@ -276,7 +274,7 @@ template <int WAVES>
 __device__ float rms_scale(const float* __restrict__ x, int K, float eps, float* red) {
   float acc = 0.f;
   for (int i = threadIdx.x; i < K; i += 64 * WAVES) acc += x[i] * x[i];
-  for (int o = 32; o > 0; o >>= 1) acc += __shfl_xor(acc, o, 64);
+  acc = wave_total(acc);
   if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = acc;
   __syncthreads();
   float sum = red[0];
@@ -306,7 +304,7 @@ __device__ __forceinline__ void table_batch(float (&v)[16 / IT::kEl][IT::kEl],
       if (base + threadIdx.x + j * T < items)
 #pragma unroll
         for (int e = 0; e < EL; ++e) acc += v[j][e] * v[j][e];
-    for (int o = 32; o > 0; o >>= 1) acc += __shfl_xor(acc, o, 64);
+    acc = wave_total(acc);
     if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = acc;
     __syncthreads();
     float sum = red[0];
@@ -467,7 +465,7 @@ __device__ __forceinline__ void store_row(const GemvFuse& f, float* __restrict__
     case kGemvSwiglu8: {
       // apply-silu-into then vector-elementwise-multiply-into
       // (llambda.lisp:6433-6441)
-      const float u = __shfl_xor(v, 8, 64);
+      const float u = dpp<kDppRowRor8>(v);  // lane n ^ 8
       if (writer && (row & 8) == 0 && row < rows) y[((row >> 4) << 3) | (row & 7)] = silu_ref(v) * u;
       return;
     }
@@ -478,7 +476,7 @@ __device__ __forceinline__ void store_row(const GemvFuse& f, float* __restrict__
       if (f.epi == kGemvRope) {
         // apply-rope-head-in-place (llambda.lisp:3760-3795): the pair
         // (x0, x1) rotated in double, each result rounded to single
-        const float other = __shfl_xor(v, 1, 64);
+        const float other = dpp<kDppXor1>(v);  // lane n ^ 1
         const int local = (row < f.split ? row : row - f.split) % hd;
         const int pair = local >> 1;
         if (pair < f.rope_pairs) {
