@@ -50,11 +50,6 @@ __global__ void rope_table_kernel(const int* __restrict__ state, const double* _
 // does).
 constexpr int kAttnWaves = 8;
 
-__device__ __forceinline__ float wave_sum(float v) {
-  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
-  return v;
-}
-
 __device__ __forceinline__ float4 operator+(float4 a, float4 b) {
   return make_float4(a.x + b.x, a.y + b.y, a.z + b.z, a.w + b.w);
 }
@@ -124,10 +119,7 @@ attention_kernel(const float* __restrict__ q, const float* __restrict__ kc,
         float s = 0.f;
 #pragma unroll
         for (int j = 0; j < DL; ++j) s += qr[h][j] * kr[st][j];
-        s += __shfl_xor(s, 1, 64);
-        s += __shfl_xor(s, 2, 64);
-        s += __shfl_xor(s, 4, 64);
-        s += __shfl_xor(s, 8, 64);
+        s = group_sum(s, 4);  // the 16 lanes of the slot
         if (sub == 0) sc[h][pl] = p0 + pl < n ? s : -INFINITY;
       }
     }
@@ -152,7 +144,7 @@ attention_kernel(const float* __restrict__ q, const float* __restrict__ kc,
       sc[h][lane + 64 * e] = ev;
       t += ev;
     }
-    t = wave_sum(t);
+    t = wave_total(t);
     if (lane == 0) {
       pmax[((int64_t)kvh * max_chunks + chunk) * G + h] = m;
       psum[((int64_t)kvh * max_chunks + chunk) * G + h] = t;
