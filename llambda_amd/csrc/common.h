@@ -123,6 +123,25 @@ __device__ __forceinline__ int wave_min(int v) {
              min(__builtin_amdgcn_readlane(v, 32), __builtin_amdgcn_readlane(v, 48)));
 }
 
+// v + v of lane i ^ 16 (rows 0/1 and 2/3 of 16 lanes) and v + v of lane
+// i ^ 32 (the two halves), by gfx950's row swaps: with v in both operands,
+// v_permlane16_swap leaves (rows 0,0,2,2) in the first and (rows 1,1,3,3) in
+// the second, v_permlane32_swap (lanes 0-31 twice) and (lanes 32-63 twice);
+// their sum is each lane's own value plus its partner's (the sum commutes).
+// Written as assembly with both registers as in/out operands (the compiler's
+// builtin returned the first register twice), with two wait states on each
+// side of the swap.  Every lane must be active.
+__device__ __forceinline__ float row_pair_sum(float v) {
+  float a = v, b = v;
+  asm volatile("s_nop 1\n\tv_permlane16_swap_b32 %0, %1\n\ts_nop 1" : "+v"(a), "+v"(b));
+  return a + b;
+}
+__device__ __forceinline__ float half_pair_sum(float v) {
+  float a = v, b = v;
+  asm volatile("s_nop 1\n\tv_permlane32_swap_b32 %0, %1\n\ts_nop 1" : "+v"(a), "+v"(b));
+  return a + b;
+}
+
 // Sum over aligned groups of 2^log2w lanes; every lane of a group receives
 // its group's sum.
 __device__ __forceinline__ float group_sum(float v, int log2w) {
@@ -130,11 +149,8 @@ __device__ __forceinline__ float group_sum(float v, int log2w) {
   if (log2w >= 2) v += dpp<kDppXor2>(v);
   if (log2w >= 3) v += dpp<kDppHalfMirror>(v);
   if (log2w >= 4) v += dpp<kDppMirror>(v);
-  if (log2w >= 5) {
-    // xor 16 within groups of 32 lanes (ds_swizzle bit mode: and 0x1F, xor 0x10)
-    v += __builtin_bit_cast(float, __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, v), 0x401F));
-  }
-  if (log2w >= 6) v += __shfl_xor(v, 32, 64);
+  if (log2w >= 5) v = row_pair_sum(v);
+  if (log2w >= 6) v = half_pair_sum(v);
   return v;
 }
 

@@ -36,9 +36,7 @@ namespace llhip {
 
 // Sum over the four lanes n, n+16, n+32, n+48.
 __device__ __forceinline__ float sum_lane_groups(float v) {
-  v += __shfl_xor(v, 16, 64);
-  v += __shfl_xor(v, 32, 64);
-  return v;
+  return half_pair_sum(row_pair_sum(v));
 }
 
 // ------------------------------------------------------------ row staging

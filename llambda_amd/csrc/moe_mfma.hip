@@ -95,7 +95,7 @@ __device__ __forceinline__ void split_octet(const float* __restrict__ xrow, int 
                                          hi[4] | (hi[5] << 16), hi[6] | (hi[7] << 16)};
   *reinterpret_cast<u32x4*>(dst + 32) = u32x4{lo[0] | (lo[1] << 16), lo[2] | (lo[3] << 16),
                                               lo[4] | (lo[5] << 16), lo[6] | (lo[7] << 16)};
-  const float s16 = sum + __shfl_xor(sum, 1, 64);
+  const float s16 = sum + dpp<kDppXor1>(sum);
   if ((o & 1) == 0) srow[o >> 1] = s16;
 }
 
