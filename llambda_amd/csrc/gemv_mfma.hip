@@ -75,21 +75,20 @@ struct Q4Items {
   }
   __device__ static void emit(uint8_t* table, float* gsum, int i, const float* v) {
     const int b = i >> 6, s = (i >> 3) & 7, m = i & 7;
-    uint32_t hi[4], lo[4];
+    uint32_t hi[2], lo[2];
+    float sum[4];
+    split_bf16_pair(v[0], v[1], hi[0], lo[0], sum[0], sum[1]);
+    split_bf16_pair(v[2], v[3], hi[1], lo[1], sum[2], sum[3]);
     float part = 0.f;
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      float sum;
-      split_bf16(v[e], hi[e], lo[e], sum);
-      part += sum;
-    }
+    for (int e = 0; e < 4; ++e) part += sum[e];
     // rows a = 2s (hi) and 2s+1 (lo); the data sits in half (s & 1) of the 8 slots
     const int half = s & 1;
     u32x4 vh = {0u, 0u, 0u, 0u}, vl = {0u, 0u, 0u, 0u};
-    vh[2 * half] = hi[0] | (hi[1] << 16);
-    vh[2 * half + 1] = hi[2] | (hi[3] << 16);
-    vl[2 * half] = lo[0] | (lo[1] << 16);
-    vl[2 * half + 1] = lo[2] | (lo[3] << 16);
+    vh[2 * half] = hi[0];
+    vh[2 * half + 1] = hi[1];
+    vl[2 * half] = lo[0];
+    vl[2 * half + 1] = lo[1];
     uint8_t* base = table + b * kQ4Table + m * 256;
     *reinterpret_cast<u32x4*>(base + (2 * s) * 16) = vh;
     *reinterpret_cast<u32x4*>(base + (2 * s + 1) * 16) = vl;
@@ -160,21 +159,19 @@ struct Q6Items {
   }
   __device__ static void emit(uint8_t* table, float* gsum, int i, const float* v) {
     const int b = i >> 5, h = (i >> 4) & 1, k = (i >> 2) & 3, g = i & 3;
-    uint32_t hi[8], lo[8];
+    uint32_t hi[4], lo[4];
+    float sum[8];
+#pragma unroll
+    for (int e = 0; e < 8; e += 2)
+      split_bf16_pair(v[e], v[e + 1], hi[e / 2], lo[e / 2], sum[e], sum[e + 1]);
     float part = 0.f;
 #pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      float sum;
-      split_bf16(v[e], hi[e], lo[e], sum);
-      part += sum;
-    }
+    for (int e = 0; e < 8; ++e) part += sum[e];
     // slot = 2k + (g >> 1): A rows 4k + 2(g >> 1) (hi) and +1 (lo)
     const int ahi = 2 * (g >> 1);
     uint8_t* base = table + b * kQ6Table + (h * 4 + k) * 128;
-    const u32x4 vh = {hi[0] | (hi[1] << 16), hi[2] | (hi[3] << 16), hi[4] | (hi[5] << 16),
-                      hi[6] | (hi[7] << 16)};
-    const u32x4 vl = {lo[0] | (lo[1] << 16), lo[2] | (lo[3] << 16), lo[4] | (lo[5] << 16),
-                      lo[6] | (lo[7] << 16)};
+    const u32x4 vh = {hi[0], hi[1], hi[2], hi[3]};
+    const u32x4 vl = {lo[0], lo[1], lo[2], lo[3]};
     *reinterpret_cast<u32x4*>(base + (ahi * 2 + (g & 1)) * 16) = vh;
     *reinterpret_cast<u32x4*>(base + ((ahi + 1) * 2 + (g & 1)) * 16) = vl;
     // group (h, k, half = g >> 1) sums 16 elements: threads g, g ^ 1

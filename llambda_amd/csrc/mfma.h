@@ -33,6 +33,22 @@ __device__ __forceinline__ void split_bf16(float x, uint32_t& hi, uint32_t& lo, 
   sum = fh + __builtin_bit_cast(float, lo << 16);
 }
 
+// Two elements split at once: (x0, x1) = (hi0 + lo0, hi1 + lo1), the bf16
+// pairs packed with x0 in the low half (split_bf16's hi0 | hi1 << 16), by
+// v_cvt_pk_bf16_f32, whose round-to-nearest-even equals bf16_bits_rne on
+// every finite value and infinity; the fp32 sums hi + lo in s0, s1.
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef float floatx2 __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ void split_bf16_pair(float x0, float x1, uint32_t& hi, uint32_t& lo,
+                                                float& s0, float& s1) {
+  hi = __builtin_bit_cast(uint32_t, __builtin_convertvector(floatx2{x0, x1}, bf16x2));
+  const float h0 = __builtin_bit_cast(float, hi << 16);
+  const float h1 = __builtin_bit_cast(float, hi & 0xFFFF0000u);
+  lo = __builtin_bit_cast(uint32_t, __builtin_convertvector(floatx2{x0 - h0, x1 - h1}, bf16x2));
+  s0 = h0 + __builtin_bit_cast(float, lo << 16);
+  s1 = h1 + __builtin_bit_cast(float, lo & 0xFFFF0000u);
+}
+
 // 8 codes (two dwords of code bytes, each < 128) -> 8 bf16 of 128 + q.
 __device__ __forceinline__ bf16x8 codes_to_b(uint32_t c0, uint32_t c1) {
   u32x4 v;

@@ -82,19 +82,16 @@ __device__ __forceinline__ void split_octet(const float* __restrict__ xrow, int 
   const float4* xp = reinterpret_cast<const float4*>(xrow + 8 * o);
   const float4 a = xp[0], b = xp[1];
   const float v[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
-  uint32_t hi[8], lo[8];
+  uint32_t hi[4], lo[4];
+  float t[8];
+#pragma unroll
+  for (int e = 0; e < 8; e += 2) split_bf16_pair(v[e], v[e + 1], hi[e / 2], lo[e / 2], t[e], t[e + 1]);
   float sum = 0.f;
 #pragma unroll
-  for (int e = 0; e < 8; ++e) {
-    float t;
-    split_bf16(v[e], hi[e], lo[e], t);
-    sum += t;
-  }
+  for (int e = 0; e < 8; ++e) sum += t[e];
   uint16_t* dst = qrow + 64 * (o >> 2) + 8 * (o & 3);
-  *reinterpret_cast<u32x4*>(dst) = u32x4{hi[0] | (hi[1] << 16), hi[2] | (hi[3] << 16),
-                                         hi[4] | (hi[5] << 16), hi[6] | (hi[7] << 16)};
-  *reinterpret_cast<u32x4*>(dst + 32) = u32x4{lo[0] | (lo[1] << 16), lo[2] | (lo[3] << 16),
-                                              lo[4] | (lo[5] << 16), lo[6] | (lo[7] << 16)};
+  *reinterpret_cast<u32x4*>(dst) = u32x4{hi[0], hi[1], hi[2], hi[3]};
+  *reinterpret_cast<u32x4*>(dst + 32) = u32x4{lo[0], lo[1], lo[2], lo[3]};
   const float s16 = sum + dpp<kDppXor1>(sum);
   if ((o & 1) == 0) srow[o >> 1] = s16;
 }
