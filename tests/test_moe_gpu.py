@@ -9,6 +9,7 @@ absolute-value sum of the final contraction,
   S_i = sum_r |w_r| sum_f |Wd_r[i,f] h_r[f]| + |s| sum_f |Wsd[i,f] hs[f]|,
 evaluated in float64 from the oracle's exact dequantised weights.
 """
+import dataclasses
 import os
 
 import numpy as np
@@ -208,6 +209,44 @@ def test_nemotron_h_1024_batch_invariance(hip):
     err = np.abs(y[sub].astype(np.float64) - ref.y.astype(np.float64))
     bad = (err > REL * S) & same_set[:, None]
     assert not bad.any(), f"B=1024: {int(bad.sum())} outputs of the sampled tokens exceed 1e-4*S"
+
+
+# One token through each single-token launch sequence: the up launch that
+# selects and gates the token itself and the down launch that combines
+# (no shared expert; K not a multiple of 256; top-k of 1 and of 12 over 600
+# experts, 16 logits per lane), and the sequence with a separate top-k
+# launch and combine (a shared expert of another weight type).
+def _single_token_layer(case, rng):
+    if case == "qwen no shared":
+        return synthetic_qwen3next(rng, hidden=512, experts=32, top_k=4, ffn=256, shared_ffn=0)
+    if case == "nemotron no shared, partial K":
+        return synthetic_nemotron_h(rng, hidden=512, experts=32, top_k=4, ffn=96, shared_ffn=0,
+                                    expert_type=ggml.Q5_0, down_type=ggml.Q5_0)
+    if case == "nemotron shared, partial K":
+        return synthetic_nemotron_h(rng, hidden=512, experts=32, top_k=3, ffn=224,
+                                    shared_ffn=160, expert_type=ggml.Q8_0, down_type=ggml.Q8_0)
+    if case == "qwen top-1":
+        return synthetic_qwen3next(rng, hidden=512, experts=16, top_k=1, ffn=256, shared_ffn=256)
+    if case == "qwen top-12 of 600":
+        return synthetic_qwen3next(rng, hidden=256, experts=600, top_k=12, ffn=64, shared_ffn=64,
+                                   gate_type=ggml.Q8_0, down_type=ggml.Q8_0)
+    assert case == "qwen shared of another type"
+    layer = synthetic_qwen3next(rng, hidden=512, experts=32, top_k=4, ffn=256, shared_ffn=256)
+    gen = synthetic.packed
+    return dataclasses.replace(
+        layer, shared_gate=(ggml.Q8_0, gen(ggml.Q8_0, rng, 256, 512)),
+        shared_up=(ggml.Q8_0, gen(ggml.Q8_0, rng, 256, 512)),
+        shared_down=(ggml.Q5_0, gen(ggml.Q5_0, rng, 512, 256)))
+
+
+@pytest.mark.parametrize("case", ["qwen no shared", "nemotron no shared, partial K",
+                                  "nemotron shared, partial K", "qwen top-1",
+                                  "qwen top-12 of 600", "qwen shared of another type"])
+def test_single_token_sequences(hip, case):
+    rng = np.random.default_rng(sum(map(ord, case)))
+    layer = _single_token_layer(case, rng)
+    for t in range(3):
+        check_layer(layer, synthetic.activations(rng, 1, layer.hidden), f"{case} token {t}")
 
 
 def test_small_qwen_shapes(hip):
