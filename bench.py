@@ -425,8 +425,8 @@ def main():
             log(f"Q4_K 4096^2 {label}: {ms * 1e3:.2f} us, {gbs:.0f} GB/s")
         us = bench_boundary_gemv(4096, 4096, max(50, steps))
         workloads.append({"workload": "boundary: llambda_hip_session_run, Q4_K 4096x4096, host x "
-                                      "and y (copy in, GEMV, copy out, synchronise), as "
-                                      "run-hip-session-into calls it",
+                                      "and y (pinned copy in, GEMV storing into mapped host "
+                                      "memory, synchronise), as run-hip-session-into calls it",
                           "us_per_call": round(us, 2),
                           "GB/s_incl_pcie": round(nbytes / (us * 1e-6) / 1e9, 1)})
         log(f"boundary session_run Q4_K 4096^2: {us:.1f} us per call")

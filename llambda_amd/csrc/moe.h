@@ -143,6 +143,8 @@ struct MoeCombineArgs {
   const float* top_w;     // [top_k] gating weights by rank
   const float* shared_w;  // [1] shared-expert gate
   int shared_scaled;      // 1: Qwen3Next's sigmoid-gated shared expert; 0: Nemotron-H's
+  const int* error;       // [1] the run's error word
+  int* error_out;         // [1] optional copy of it (see moe_forward_launch)
 };
 bool moe_down_combine_supported(int type, const MoeGemmArgs& a);
 hipError_t moe_down_combine_launch(int type, const MoeGemmArgs& a, const MoeCombineArgs& c,
@@ -151,11 +153,13 @@ hipError_t moe_down_combine_launch(int type, const MoeGemmArgs& a, const MoeComb
 // Upper bound of the chunk table for `tokens` tokens with chunk size nt.
 int64_t moe_max_chunks(const MoePlan& p, int64_t tokens, int nt);
 
-// Enqueue one forward for `tokens` tokens: x, y are [tokens][hidden] on the
-// device.  `error` codes (bit flags): 1 = fewer than k finite router logits,
-// 2 = non-positive weight sum, 4 = expert index out of range.
+// Enqueue one forward for `tokens` tokens: x, y are [tokens][hidden] in
+// memory the device can address.  `error` codes (bit flags): 1 = fewer than
+// k finite router logits, 2 = non-positive weight sum, 4 = expert index out
+// of range.  With `error_out`, the final launch also stores the run's error
+// word there (host-mapped memory, read after the stream is synchronised).
 hipError_t moe_forward_launch(const MoePlan& p, const float* x, float* y, int tokens,
-                              hipStream_t stream);
+                              hipStream_t stream, int* error_out = nullptr);
 
 // Zero the error flag (a fill kernel, so that a captured graph replays it).
 hipError_t moe_reset_launch(const MoePlan& p, hipStream_t stream);

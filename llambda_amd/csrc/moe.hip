@@ -144,11 +144,13 @@ __global__ void __launch_bounds__(kScanThreads) moe_scan_kernel(MoePlan p, int t
 // vector-add-bias-in-place (llambda.lisp:3465-3489; 5359, 5409, 5426, 5914,
 // 5932, 5949).
 __global__ void __launch_bounds__(256) moe_combine_kernel(MoePlan p, float* __restrict__ y,
-                                                          int tokens, int has_shared) {
+                                                          int tokens, int has_shared,
+                                                          int* __restrict__ error_out) {
 #pragma clang fp contract(off)
   const int t = blockIdx.y;
   const int i = blockIdx.x * blockDim.x + threadIdx.x;
   const int H = p.hidden, K = p.top_k;
+  if (error_out && i == 0 && t == 0) *error_out = *p.error;
   if (i >= H) return;
   // the ranks' outputs (just written by another launch, on other XCDs) are
   // loaded 8 ranks at a time before the sums, which run in rank order
@@ -247,7 +249,7 @@ static int moe_chunk_tokens(int mt) { return mt == 0 ? 1 : 16 * mt; }
 // One forward: router GEMM (+ split x), top-k and gating, scan (batches),
 // grouped gate/up and down products, combine.
 hipError_t moe_forward_launch(const MoePlan& p, const float* x, float* y, int tokens,
-                              hipStream_t s) {
+                              hipStream_t s, int* error_out) {
   if (tokens <= 0) return hipSuccess;
   if (tokens > p.capacity) return hipErrorInvalidValue;
   // the router and the split read x with 16-byte loads
@@ -378,6 +380,8 @@ hipError_t moe_forward_launch(const MoePlan& p, const float* x, float* y, int to
     c.top_w = p.top_w;
     c.shared_w = p.shared_w;
     c.shared_scaled = p.variant == kQwen3Next;
+    c.error = p.error;
+    c.error_out = error_out;
     return moe_down_combine_launch(p.down_type, a, c, s);
   }
   e = moe_gemm_launch(p.down_type, kEpiDown, a, mt, routed_chunks + (joint_down ? shared_chunks : 0), s);
@@ -396,7 +400,7 @@ hipError_t moe_forward_launch(const MoePlan& p, const float* x, float* y, int to
   // behind a device-scope fence and an atomic per workgroup, measured 10 us
   // slower for one Qwen3Next token)
   return launch(moe_combine_kernel, dim3((H + 255) / 256, tokens), dim3(256), 0, s, p, y, tokens,
-                has_shared);
+                has_shared, error_out);
 }
 
 hipError_t moe_reset_launch(const MoePlan& p, hipStream_t s) {

@@ -1132,6 +1132,7 @@ moe_down_combine_kernel(MoeGemmArgs a, MoeCombineArgs cb) {
       }
     }
     if (n0 + n < a.N) cb.y[n0 + n] = acc;
+    if (cb.error_out && blockIdx.x == 0 && n == 0) *cb.error_out = *cb.error;
   }
 }
 
