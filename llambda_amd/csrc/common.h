@@ -114,6 +114,14 @@ __device__ __forceinline__ float wave_max(float v) {
   const float r3 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 48));
   return fmaxf(fmaxf(r0, r1), fmaxf(r2, r3));
 }
+__device__ __forceinline__ int wave_max_i(int v) {
+  v = max(v, dpp_i<kDppXor1>(v));
+  v = max(v, dpp_i<kDppXor2>(v));
+  v = max(v, dpp_i<kDppHalfMirror>(v));
+  v = max(v, dpp_i<kDppMirror>(v));
+  return max(max(__builtin_amdgcn_readlane(v, 0), __builtin_amdgcn_readlane(v, 16)),
+             max(__builtin_amdgcn_readlane(v, 32), __builtin_amdgcn_readlane(v, 48)));
+}
 __device__ __forceinline__ int wave_min(int v) {
   v = min(v, dpp_i<kDppXor1>(v));
   v = min(v, dpp_i<kDppXor2>(v));

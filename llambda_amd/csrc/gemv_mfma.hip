@@ -900,7 +900,14 @@ static hipError_t launch_mfma(const GemvProblem& p, const GemvFuse& f, hipStream
       per_cu < 1)
     per_cu = 1;
   const int needed = (tiles + kMfmaWaves / S - 1) / (kMfmaWaves / S);
-  const int grid = std::max(1, std::min(needed, device_cu_count() * per_cu));
+  const int cap = device_cu_count() * per_cu;
+  // Long launches take the smallest grid with the same number of rounds, so
+  // that every workgroup has as many (the Q6_K head: 501 workgroups of 16
+  // tiles instead of 512 of 15 or 16, 77.1 -> 76.7 us sustained); for a few
+  // rounds that changed nothing or lost (the decode token's gate|up: 448 of
+  // 4 instead of 512 of 3 or 4, +0.2%).
+  const int nrounds = (needed + cap - 1) / cap;
+  const int grid = std::max(1, nrounds >= 8 ? (needed + nrounds - 1) / nrounds : std::min(needed, cap));
   const MfmaArgs args{p.weights, p.row_bytes, (int)p.rows, nblk, p.x, p.y, f, nbuf};
   hipLaunchKernelGGL(kernel, dim3(grid), dim3(64 * kMfmaWaves), lds, stream, args);
   return hipGetLastError();

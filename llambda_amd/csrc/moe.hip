@@ -23,9 +23,10 @@ __global__ void __launch_bounds__(256) topk_kernel(const float* __restrict__ log
     const int e = lane + kWave * j;
     vals[j] = e < n ? selectable(logits[(int64_t)t * n + e]) : -INFINITY;
   }
+  __shared__ int64_t sel[4][kSelectScratch];
   int mi;
   float mv;
-  wave_select<JPL>(vals, k, lane, mi, mv);
+  wave_select<JPL>(vals, k, lane, sel[threadIdx.x >> 6], mi, mv);
   if (lane < k) {
     idx[(int64_t)t * k + lane] = mi;
     val[(int64_t)t * k + lane] = mv;
@@ -37,9 +38,10 @@ __global__ void __launch_bounds__(256) topk_kernel(const float* __restrict__ log
 // the shared expert.
 template <int JPL>
 __global__ void __launch_bounds__(256) topk_gate_kernel(MoePlan p, int tokens, int single) {
+  __shared__ int64_t sel[4][kSelectScratch];
   const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
   if (t >= tokens) return;
-  const GateRank r = gate_token<JPL>(p, t, tokens, true);
+  const GateRank r = gate_token<JPL>(p, t, tokens, true, sel[threadIdx.x >> 6]);
   if (!single) return;  // the scan kernel counts the experts' pairs
   gate_chunk_table(p, r.valid, r.idx);
 }

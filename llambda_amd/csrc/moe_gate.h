@@ -8,6 +8,7 @@
 
 #include <cfloat>
 #include <climits>
+#include <utility>
 
 namespace llhip {
 
@@ -15,36 +16,178 @@ namespace llhip {
 // select-top-k-logits-into (llambda.lisp:5265-5292) keeps, in descending
 // order, the k largest logits strictly above most-negative-single-float,
 // lower index first among equal values, never NaN; unfilled slots stay
-// (-1, -FLT_MAX).  Here one wavefront holds JPL logits per lane and takes k
-// rounds of a wave-wide (value desc, index asc) arg-max; lane r keeps rank
-// r.  `bias` (optional) is added first and the biased logits are written
-// back.
-template <int JPL>
-__device__ __forceinline__ void wave_select(float (&vals)[JPL], int K, int lane, int& my_idx,
-                                            float& my_val) {
-  my_idx = -1;
-  my_val = -FLT_MAX;
-  for (int r = 0; r < K; ++r) {
-    // the lane's best (lowest index among equals), then the wave's
-    float lv = -INFINITY;
-    int li = INT_MAX;
-#pragma unroll
-    for (int j = 0; j < JPL; ++j) {
-      if (vals[j] > lv) {
-        lv = vals[j];
-        li = lane + kWave * j;
-      }
+// (-1, -FLT_MAX).  Here one wavefront holds JPL logits per lane (-inf where
+// not selectable) and takes k rounds of a wave-wide (value desc, index asc)
+// arg-max; lane r keeps rank r.
+//
+// A candidate is the entry (key << 32) | (~index << 1) | (value is -0), a
+// signed 64-bit integer: a larger entry is a larger value, or an equal value
+// at a lower index.  Values map to integers that order as the floats do, -0
+// to the key of +0, which it equals (NaN never occurs: `selectable` turns it
+// into -inf); the entry's lowest bit keeps the sign of a zero, so the
+// selected value is returned bit for bit.
+//
+// Selection by threshold (a fixed number of steps, not k dependent rounds):
+// the k-th largest of the 64 lanes' maxima, t, is found by counting ranks;
+// every entry of the top k is at least t (the k largest maxima are k entries
+// >= t), and only the k lanes whose maximum is >= t hold such entries, so
+// at most k * JPL candidates remain.  They are compacted into LDS by ballot
+// prefix counts and ranked by counting; more than 64 (possible only when
+// k * JPL > 64) take the round-by-round selection instead.
+__device__ __forceinline__ int order_key(float v) {
+  const int b = __builtin_bit_cast(int, v == 0.f ? 0.f : v);
+  return b >= 0 ? b : b ^ 0x7FFFFFFF;
+}
+__device__ __forceinline__ float order_value(int k) {
+  return __builtin_bit_cast(float, k >= 0 ? k : k ^ 0x7FFFFFFF);
+}
+
+// The list operations below index the candidates with compile-time
+// constants only (template recursion, fold expressions), so the array lives
+// in registers from the start: written as loops, a select between two of its
+// entries can become an access at a computed index, lowered to a chain of
+// compares and selects per entry.
+constexpr int kSelectNone = (int)0x807FFFFF;  // order_key(-inf): nothing selectable
+// LDS a wavefront's selection uses (int64 entries)
+constexpr int kSelectScratch = 2 * kWave + 1;
+
+__device__ __forceinline__ int64_t select_entry(float v, int index) {
+  const uint32_t neg0 = __builtin_bit_cast(uint32_t, v) == 0x80000000u ? 1u : 0u;
+  return (int64_t)((uint64_t)(uint32_t)order_key(v) << 32 |
+                   ((uint32_t)~(uint32_t)index << 1 | neg0));
+}
+__device__ __forceinline__ void select_decode(int64_t e, int& idx, float& val) {
+  const int k = (int)(e >> 32);
+  idx = (int)(~(uint32_t)e >> 1);
+  val = (k == 0 && (e & 1)) ? -0.f : order_value(k);
+}
+
+// descending bitonic sort: stage (KB, J), comparator I
+template <int JPL, int KB, int J, int I>
+__device__ __forceinline__ void select_sort(int64_t (&c)[JPL]) {
+  if constexpr (I < JPL) {
+    constexpr int L = I ^ J;
+    if constexpr (L > I) {
+      constexpr bool kDesc = (I & KB) == 0;
+      const bool sw = kDesc ? c[L] > c[I] : c[I] > c[L];
+      const int64_t a = sw ? c[L] : c[I], b = sw ? c[I] : c[L];
+      c[I] = a;
+      c[L] = b;
     }
-    const float bv = wave_max(lv);
-    const int bi = wave_min(lv == bv ? li : INT_MAX);
-    const bool own = bi != INT_MAX && (bi & (kWave - 1)) == lane;
-#pragma unroll
-    for (int j = 0; j < JPL; ++j) vals[j] = (own && j == (bi >> 6)) ? -INFINITY : vals[j];
-    if (lane == r && bi != INT_MAX) {
+    select_sort<JPL, KB, J, I + 1>(c);
+  } else if constexpr (J > 1) {
+    select_sort<JPL, KB, J / 2, 0>(c);
+  } else if constexpr (KB < JPL) {
+    select_sort<JPL, KB * 2, KB, 0>(c);
+  }
+}
+
+template <int JPL, int... J>
+__device__ __forceinline__ void select_fill(int64_t (&c)[JPL], const float (&vals)[JPL], int lane,
+                                            std::integer_sequence<int, J...>) {
+  ((c[J] = select_entry(vals[J], lane + kWave * J)), ...);
+}
+
+// drop the head of the list where `own`
+template <int JPL, int... J>
+__device__ __forceinline__ void select_pop(int64_t (&c)[JPL], bool own,
+                                           std::integer_sequence<int, J...>) {
+  ((c[J] = own ? c[J + 1] : c[J]), ...);
+  c[JPL - 1] = own ? (int64_t)((uint64_t)(uint32_t)kSelectNone << 32) : c[JPL - 1];
+}
+
+__device__ __forceinline__ int64_t readlane64(int64_t v, int l) {
+  const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)v, l);
+  const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)((uint64_t)v >> 32), l);
+  return (int64_t)((uint64_t)hi << 32 | lo);
+}
+
+// Round by round: each lane's list sorted, then per round the wave's largest
+// head (an integer max, then an index min over the lanes holding it) and a
+// shift of the winning lane's list.
+template <int JPL>
+__device__ __forceinline__ void wave_select_rounds(int64_t (&c)[JPL], int K, int lane, int& my_idx,
+                                                float& my_val) {
+  if constexpr (JPL > 1) select_sort<JPL, 2, 1, 0>(c);
+  for (int r = 0; r < K; ++r) {
+    const int hk = (int)(c[0] >> 32);
+    const int m = wave_max_i(hk);
+    if (m == kSelectNone) break;  // uniform: the remaining slots stay unfilled
+    const int hi = (int)(~(uint32_t)c[0] >> 1);
+    const int bi = wave_min(hk == m ? hi : INT_MAX);
+    const bool own = (bi & (kWave - 1)) == lane;
+    float v = order_value(m);
+    if (m == 0 && (__builtin_amdgcn_readlane((int)(uint32_t)c[0], bi & (kWave - 1)) & 1)) v = -0.f;
+    select_pop<JPL>(c, own, std::make_integer_sequence<int, JPL - 1>{});
+    if (lane == r) {
       my_idx = bi;
-      my_val = bv;
+      my_val = v;
     }
   }
+}
+
+// `s`: kSelectScratch int64 entries of LDS owned by this wavefront.
+template <int JPL>
+__device__ __forceinline__ void wave_select(const float (&vals)[JPL], int K, int lane, int64_t* s,
+                                            int& my_idx, float& my_val) {
+  int64_t c[JPL];
+  select_fill<JPL>(c, vals, lane, std::make_integer_sequence<int, JPL>{});
+  my_idx = -1;
+  my_val = -FLT_MAX;
+  // the threshold: the lane maximum of rank K - 1 (ranks are distinct, the
+  // indices being distinct, and K <= 64)
+  int64_t h = c[0];
+#pragma unroll
+  for (int j = 1; j < JPL; ++j) h = c[j] > h ? c[j] : h;
+  s[lane] = h;
+  int rank = 0;
+#pragma unroll
+  for (int i = 0; i < kWave; ++i) rank += s[i] > h ? 1 : 0;
+  const int tl = (int)__builtin_ctzll(__ballot(rank == K - 1));
+  const int64_t t = readlane64(h, tl);
+  // the candidates: selectable entries >= t, and their exclusive prefix
+  // count over the lanes (at most 16 per lane: 5 bits)
+  bool take[JPL];
+  int cnt = 0;
+#pragma unroll
+  for (int j = 0; j < JPL; ++j) {
+    take[j] = c[j] >= t && (int)(c[j] >> 32) != kSelectNone;
+    cnt += take[j] ? 1 : 0;
+  }
+  int pre = 0, total = 0;
+#pragma unroll
+  for (int b = 0; b < 5; ++b) {
+    const uint64_t m = __ballot((cnt >> b) & 1);
+    pre += (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32),
+                                          __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u)) << b;
+    total += __popcll(m) << b;
+  }
+  if (total > kWave) {
+    wave_select_rounds<JPL>(c, K, lane, my_idx, my_val);
+    return;
+  }
+  // compact into s[64 .. 64 + total) (non-candidates write the spare entry
+  // s[128]); the wavefront's LDS accesses execute in order, so the reads of
+  // the maxima above are done before these writes
+  int64_t* cs = s + kWave;
+  int at = pre;
+#pragma unroll
+  for (int j = 0; j < JPL; ++j) {
+    cs[take[j] ? at : kWave] = c[j];
+    at += take[j] ? 1 : 0;
+  }
+  // entries past the candidates read as the smallest entry, so the ranks
+  // are counted eight at a time
+  if (lane >= total) cs[lane] = INT64_MIN;
+  const int64_t mine = cs[lane];
+  int r2 = 0;
+  for (int i0 = 0; i0 < total; i0 += 8)
+#pragma unroll
+    for (int i = i0; i < i0 + 8; ++i) r2 += cs[i] > mine ? 1 : 0;
+  // rank r2 of the first min(K, total) to lane r2, through s[0 .. K)
+  const int filled = min(K, total);
+  if (lane < total && r2 < filled) s[r2] = mine;
+  if (lane < filled) select_decode(s[lane], my_idx, my_val);
 }
 
 // The selectable logits of one token: NaN, -inf and -FLT_MAX never qualify.
@@ -54,7 +197,8 @@ __device__ __forceinline__ float selectable(float raw) { return raw > -FLT_MAX ?
 // sigmoid, renormalise, error when the sum is not positive) or 5894-5913
 // (nemotron: bias before selection, sigmoid, optional renormalise, scale).
 // The weight sum runs over the ranks in order, as the reference's loop does.
-// Run by one wavefront for token t; with `write` it stores the token's
+// Run by one wavefront for token t (`sel`: its kSelectScratch entries of
+// LDS); with `write` it stores the token's
 // logits, top-k indices and weights, shared weight and error flags.  Lane r
 // < k returns rank r: its expert (-1 where fewer than k logits qualify), its
 // weight and whether the expert is valid.
@@ -65,7 +209,8 @@ struct GateRank {
 };
 
 template <int JPL>
-__device__ __forceinline__ GateRank gate_token(const MoePlan& p, int t, int tokens, bool write) {
+__device__ __forceinline__ GateRank gate_token(const MoePlan& p, int t, int tokens, bool write,
+                                               int64_t* sel) {
 #pragma clang fp contract(off)
   const int lane = threadIdx.x & 63;
   const int E = p.experts, K = p.top_k;
@@ -138,7 +283,7 @@ __device__ __forceinline__ GateRank gate_token(const MoePlan& p, int t, int toke
   if (write && lane == 0 && has_shared_row) lg[E] = shared_logit;
   int mi;
   float mv;
-  wave_select<JPL>(vals, K, lane, mi, mv);
+  wave_select<JPL>(vals, K, lane, sel, mi, mv);
   const bool has = lane < K;
   float w = has ? sigmoid_ref(mv) : 0.f;
   float sum = 0.f;

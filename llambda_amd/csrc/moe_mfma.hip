@@ -469,13 +469,17 @@ moe_gemm_kernel(MoeGemmArgs args) {
       const int pos = bx - has_sh;
       if (threadIdx.x < 64) {
         const bool write = pos == 0 && by == 0;
+        // the selection's scratch: the start of the dynamic LDS, whose
+        // stages and sums are first written after the barrier below
+        static_assert(Sh::RED >= kSelectScratch * (int)sizeof(int64_t), "selection scratch");
+        int64_t* sel = reinterpret_cast<int64_t*>(lds);
         GateRank r{};
         switch (args.gate_jpl) {
-          case 1: r = gate_token<1>(args.plan, 0, 1, write); break;
-          case 2: r = gate_token<2>(args.plan, 0, 1, write); break;
-          case 4: r = gate_token<4>(args.plan, 0, 1, write); break;
-          case 8: r = gate_token<8>(args.plan, 0, 1, write); break;
-          default: r = gate_token<16>(args.plan, 0, 1, write); break;
+          case 1: r = gate_token<1>(args.plan, 0, 1, write, sel); break;
+          case 2: r = gate_token<2>(args.plan, 0, 1, write, sel); break;
+          case 4: r = gate_token<4>(args.plan, 0, 1, write, sel); break;
+          case 8: r = gate_token<8>(args.plan, 0, 1, write, sel); break;
+          default: r = gate_token<16>(args.plan, 0, 1, write, sel); break;
         }
         const int l = threadIdx.x;
         const uint64_t mask = __ballot(r.valid);
