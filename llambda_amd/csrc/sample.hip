@@ -301,6 +301,7 @@ sample_kernel(float* __restrict__ work, SampleParams p, int* __restrict__ result
   __syncthreads();
   if (tid == 0) {
     int any = 0;
+#pragma unroll 16
     for (int g = 0; g < kPrepGroups; ++g) any |= s_nan[g];
     flag = any;
     ncand = 0;
@@ -361,6 +362,7 @@ sample_kernel(float* __restrict__ work, SampleParams p, int* __restrict__ result
   if (tid == 0) {
     int ok = p.top_k <= kPrepCap;
     uint32_t cmax = 0u;
+#pragma unroll 16
     for (int g = 0; g < kPrepGroups; ++g) {
       ok &= s_cnt[g] <= kPrepCap;
       cmax = max(cmax, s_cut[g]);
@@ -393,6 +395,7 @@ sample_kernel(float* __restrict__ work, SampleParams p, int* __restrict__ result
     // counting: the g with #{> key_g} < k <= #{>= key_g}
     if (tid < kPrepGroups) {
       uint32_t mx = 0u;
+#pragma unroll 8
       for (int slot = 0; slot < s_cnt[tid]; ++slot)
         mx = max(mx, float_key(s_val[tid * kPrepCap + slot]));
       s_cut[tid] = mx;
@@ -401,6 +404,7 @@ sample_kernel(float* __restrict__ work, SampleParams p, int* __restrict__ result
     if (tid < kPrepGroups) {
       const uint32_t v = s_cut[tid];
       int gt = 0, ge = 0;
+#pragma unroll 16
       for (int h = 0; h < kPrepGroups; ++h) {
         gt += s_cut[h] > v;
         ge += s_cut[h] >= v;
@@ -493,9 +497,11 @@ sample_kernel(float* __restrict__ work, SampleParams p, int* __restrict__ result
     if (tid < cand) {
       const float v = c_val[tid];
       int gt = 0, ge = 0;
+#pragma unroll 8
       for (int d = 0; d < cand; ++d) {
-        gt += c_val[d] > v;
-        ge += c_val[d] >= v;
+        const float cv = c_val[d];
+        gt += (int)(cv > v);
+        ge += (int)(cv >= v);
       }
       if (gt < p.top_k && p.top_k <= ge) fred[0] = v;  // equal values write equal values
     }
@@ -513,7 +519,8 @@ sample_kernel(float* __restrict__ work, SampleParams p, int* __restrict__ result
     if (c_val[c] < cutoff) continue;
     const int idx = c_idx[c];
     int pos = 0;
-    for (int d = 0; d < cand; ++d) pos += !(c_val[d] < cutoff) && c_idx[d] < idx;
+#pragma unroll 8
+    for (int d = 0; d < cand; ++d) pos += (int)!(c_val[d] < cutoff) & (int)(c_idx[d] < idx);
     s_idx[pos] = idx;
     s_val[pos] = c_val[c];
     atomicAdd(&flag, 1);
@@ -528,9 +535,10 @@ sample_kernel(float* __restrict__ work, SampleParams p, int* __restrict__ result
       const float v = s_val[a];
       int rank = 0;
       if (v > kMaskedLogit) {
+#pragma unroll 8
         for (int b = 0; b < total; ++b) {
           const float w = s_val[b];
-          rank += (w > kMaskedLogit) && (w > v || (w == v && b < a));
+          rank += (int)(w > kMaskedLogit) & ((int)(w > v) | ((int)(w == v) & (int)(b < a)));
         }
         s_order[rank] = a;
       }
@@ -538,6 +546,7 @@ sample_kernel(float* __restrict__ work, SampleParams p, int* __restrict__ result
     __syncthreads();
     if (tid == 0) {
       int active = 0;
+#pragma unroll 8
       for (int a = 0; a < total; ++a) active += s_val[a] > kMaskedLogit;
       red[0] = active;
     }
@@ -548,50 +557,86 @@ sample_kernel(float* __restrict__ work, SampleParams p, int* __restrict__ result
       for (int j = tid; j < active; j += kSampleThreads)
         s_e[j] = (float)exp((double)(s_val[s_order[j]] / p.temperature - max_scaled));
       __syncthreads();
-      if (tid == 0) {
+      // the reference's serial single-precision sums, run by every lane of
+      // wavefront 0 (the same loads in the same order: equal results), each
+      // lane dividing its own terms by the sum in between
+      if (tid < kWave) {
         float sum = 0.0f;
+#pragma unroll 8
         for (int j = 0; j < active; ++j) sum += s_e[j];
-        float cumulative = 0.0f, cut = s_val[s_order[active - 1]];
-        for (int j = 0; j < active; ++j) {
-          cumulative += s_e[j] / sum;
-          if (cumulative >= p.top_p) {
-            cut = s_val[s_order[j]];
+        for (int j = tid; j < active; j += kWave) s_e[j] = s_e[j] / sum;
+        float cumulative = 0.0f;
+        int at = active - 1;
+        for (int j0 = 0; j0 < active; j0 += 8) {
+          float q[8];
+#pragma unroll
+          for (int u = 0; u < 8; ++u) q[u] = j0 + u < active ? s_e[j0 + u] : 0.f;
+          int hit = -1;
+#pragma unroll
+          for (int u = 0; u < 8; ++u) {
+            if (hit < 0 && j0 + u < active) {
+              cumulative += q[u];
+              if (cumulative >= p.top_p) hit = j0 + u;
+            }
+          }
+          if (hit >= 0) {
+            at = hit;
             break;
           }
         }
-        for (int a = 0; a < total; ++a)
+        if (tid == 0) fred[0] = s_val[s_order[at]];
+      }
+      __syncthreads();
+      {
+        const float cut = fred[0];
+        for (int a = tid; a < total; a += kSampleThreads)
           if (s_val[a] < cut) s_val[a] = kMaskedLogit;
       }
       __syncthreads();
     }
   }
 
-  // 5. temperature, softmax, draw (masked logits contribute exactly 0)
+  // 5. temperature, softmax, draw (masked logits contribute exactly 0).
+  // Wavefront 0: the maximum (order-free) and each exp (rounded to single as
+  // the reference rounds it) across its lanes; the reference's serial sums
+  // in index order by every lane (the same loads in the same order: equal
+  // results), each lane dividing its own terms by the sum in between.  The
+  // wavefront's LDS accesses execute in order, so no barrier is needed.
   for (int a = tid; a < total; a += kSampleThreads) s_e[a] = s_val[a] / p.temperature;
   __syncthreads();
-  if (tid == 0) {
-    float mx = s_e[0];
-    for (int a = 1; a < total; ++a)
-      if (s_e[a] > mx) mx = s_e[a];
-    float sum = 0.0f;
-    for (int a = 0; a < total; ++a) {
-      const float e = (float)exp((double)(s_e[a] - mx));
-      s_e[a] = e;
-      sum += e;
-    }
-    int token = n - 1;
+  if (tid >= kWave) return;
+  float mx = -INFINITY;
+  for (int a = tid; a < total; a += kWave) mx = fmaxf(mx, s_e[a]);
+  mx = wave_max(mx);
+  for (int a = tid; a < total; a += kWave) s_e[a] = (float)exp((double)(s_e[a] - mx));
+  float sum = 0.0f;
+#pragma unroll 8
+  for (int a = 0; a < total; ++a) sum += s_e[a];
+  for (int a = tid; a < total; a += kWave) s_e[a] = s_e[a] / sum;
+  int token = n - 1;
+  if (p.roll <= 0.0f) {
+    token = 0;
+  } else {
     float running = 0.0f;
-    if (p.roll <= 0.0f) {
-      token = 0;
-    } else {
-      for (int a = 0; a < total; ++a) {
-        running += s_e[a] / sum;
-        if (p.roll <= running) {
-          token = s_idx[a];
-          break;
+    for (int a0 = 0; a0 < total; a0 += 8) {
+      float q[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) q[u] = a0 + u < total ? s_e[a0 + u] : 0.f;
+      int hit = -1;
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        if (hit < 0 && a0 + u < total) {
+          running += q[u];
+          if (p.roll <= running) hit = a0 + u;
         }
       }
+      if (hit >= 0) {
+        token = s_idx[hit];
+        break;
+      }
     }
+  }
+  if (tid == 0) {
     result[0] = token;
     result[1] = 0;
   }
