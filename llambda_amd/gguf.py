@@ -62,7 +62,11 @@ class GgufFile:
             native.lib().llambda_hip_gguf_close(self._h)
             self._h = None
 
-    __del__ = close
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:  # noqa: BLE001 - interpreter shutdown
+            pass
 
     def __enter__(self):
         return self

@@ -277,7 +277,11 @@ class HipLlamaSession:
             native.lib().llambda_hip_llama_session_destroy(self._h)
             self._h = None
 
-    __del__ = close
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:  # noqa: BLE001 - interpreter shutdown
+            pass
 
     def step(self, token: int, position: int) -> np.ndarray:
         """logits[vocab] of one decode step (synchronous)."""

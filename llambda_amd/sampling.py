@@ -51,7 +51,11 @@ class HipSampler:
             native.lib().llambda_hip_sampler_destroy(self._h)
             self._h = None
 
-    __del__ = close
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:  # noqa: BLE001 - interpreter shutdown
+            pass
 
     def sample(self, logits, *, random_value: float, history: Optional[Sequence[int]] = None,
                repetition_penalty: float = 1.15, top_k: Optional[int] = DEFAULT_TOP_K,
