@@ -117,6 +117,17 @@ router_mfma_kernel(const float* __restrict__ x, int T, const float* __restrict__
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int i = lane & 15, kg = lane >> 4;
   const int t0 = blockIdx.y * 16, e0 = blockIdx.x * 16, k0 = blockIdx.z * kRouterSlice;
+  // the products' operands are requested first, so that the split below
+  // (expert-tile 0) overlaps their round trip instead of preceding it
+  const float* xr = x + (int64_t)min(t0 + i, T - 1) * H + 4 * kg;
+  const float* rr = R + (int64_t)min(e0 + i, Er - 1) * H + 4 * kg;
+  float4 xa[4], rb[4];
+#pragma unroll
+  for (int c = 0; c < 4; ++c) {
+    const int k = k0 + 64 * wave + 16 * c;
+    xa[c] = k < H ? *reinterpret_cast<const float4*>(xr + k) : float4{0.f, 0.f, 0.f, 0.f};
+    rb[c] = k < H ? *reinterpret_cast<const float4*>(rr + k) : float4{0.f, 0.f, 0.f, 0.f};
+  }
   if (blockIdx.x == 0) {
     const int octets = min(kRouterSlice, H - k0) >> 3, ofirst = k0 >> 3;
     for (int idx = threadIdx.x; idx < 16 * octets; idx += 64 * kRouterWaves) {
@@ -126,20 +137,15 @@ router_mfma_kernel(const float* __restrict__ x, int T, const float* __restrict__
                     s + (int64_t)(t0 + tt) * s_stride);
     }
   }
-  const float* xr = x + (int64_t)min(t0 + i, T - 1) * H + 4 * kg;
-  const float* rr = R + (int64_t)min(e0 + i, Er - 1) * H + 4 * kg;
   floatx4 acc[4];
 #pragma unroll
   for (int c = 0; c < 4; ++c) {
     acc[c] = floatx4{0.f, 0.f, 0.f, 0.f};
-    const int k = k0 + 64 * wave + 16 * c;
-    if (k < H) {
-      const float4 xa = *reinterpret_cast<const float4*>(xr + k);
-      const float4 rb = *reinterpret_cast<const float4*>(rr + k);
-      acc[c] = mfma4f32(xa.x, rb.x, acc[c]);
-      acc[c] = mfma4f32(xa.y, rb.y, acc[c]);
-      acc[c] = mfma4f32(xa.z, rb.z, acc[c]);
-      acc[c] = mfma4f32(xa.w, rb.w, acc[c]);
+    if (k0 + 64 * wave + 16 * c < H) {
+      acc[c] = mfma4f32(xa[c].x, rb[c].x, acc[c]);
+      acc[c] = mfma4f32(xa[c].y, rb[c].y, acc[c]);
+      acc[c] = mfma4f32(xa[c].z, rb[c].z, acc[c]);
+      acc[c] = mfma4f32(xa[c].w, rb[c].w, acc[c]);
     }
   }
   red[wave][lane] = (acc[0] + acc[1]) + (acc[2] + acc[3]);
@@ -424,8 +430,11 @@ constexpr int gemm_lds_bytes(int depth) {
 // GATE (single-token pipeline, one token): the launch also selects and
 // gates the token (gate_token) instead of reading a chunk table.
 template <int TYPE, int EPI, int MT, int PIPE, bool ALIGNED, bool GATE = false>
+// (the wide pipeline asks for two workgroups per CU, except for the
+// 32-weight block types, whose decode state does not fit the registers that
+// leaves: they ran with 52-500 bytes of scratch per lane)
 __global__ void __launch_bounds__((64 * GemmShape<TYPE, EPI, PIPE>::kWaves),
-                                  (PIPE == kPipeWide ? 2 : 1))
+                                  (PIPE == kPipeWide && TYPE != kQ5_0 && TYPE != kQ8_0 ? 2 : 1))
 moe_gemm_kernel(MoeGemmArgs args) {
   using B = GemmB<TYPE>;
   using Sh = GemmShape<TYPE, EPI, PIPE>;

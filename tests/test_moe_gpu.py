@@ -285,6 +285,33 @@ def test_long_chunks(hip, variant, types, tokens):
         session.close()
 
 
+# The same long chunks for 32-weight block experts beside a K-quant shared
+# expert: the group pipeline needs every tensor in a 32-weight type, so these
+# run on the wide pipeline; ffn 224 makes the down rows 154 (Q5_0) or 238
+# (Q8_0) bytes, not dword multiples.
+@pytest.mark.parametrize("variant,types", [
+    ("nemotron", (ggml.Q5_0, ggml.Q5_0)), ("nemotron", (ggml.Q8_0, ggml.Q8_0)),
+    ("qwen", (ggml.Q8_0, ggml.Q5_0))])
+def test_long_chunks_wide_pipeline_32_weight_types(hip, variant, types):
+    rng = np.random.default_rng(40)
+    gen = synthetic.packed
+    if variant == "nemotron":
+        layer = synthetic_nemotron_h(rng, hidden=512, experts=8, top_k=3, ffn=224, shared_ffn=256,
+                                     expert_type=types[0], down_type=types[1])
+        layer = dataclasses.replace(layer, shared_up=(ggml.Q4_K, gen(ggml.Q4_K, rng, 256, 512)),
+                                    shared_down=(ggml.Q6_K, gen(ggml.Q6_K, rng, 512, 256)))
+    else:
+        layer = synthetic_qwen3next(rng, hidden=512, experts=8, top_k=3, ffn=224, shared_ffn=256,
+                                    gate_type=types[0], down_type=types[1])
+        layer = dataclasses.replace(layer, shared_gate=(ggml.Q4_K, gen(ggml.Q4_K, rng, 256, 512)),
+                                    shared_up=(ggml.Q4_K, gen(ggml.Q4_K, rng, 256, 512)),
+                                    shared_down=(ggml.Q6_K, gen(ggml.Q6_K, rng, 512, 256)))
+    tokens = 96
+    assert tokens * layer.top_k / layer.expert_count > 16
+    x = synthetic.activations(rng, tokens, layer.hidden)
+    check_layer(layer, x, f"{variant} {types} wide pipeline")
+
+
 def test_nemotron_unnormalised_scaled(hip):
     rng = np.random.default_rng(10)
     layer = synthetic_nemotron_h(rng, hidden=512, experts=64, top_k=4, ffn=256, shared_ffn=0,
