@@ -721,8 +721,10 @@ sample_topp_kernel(float* __restrict__ work, SampleParams p) {
   atomicAdd(&s_active, act);
   __syncthreads();
   for (int pass = 0; pass < 8; ++pass) {
-    const uint64_t* in = t.item[pass & 1];
-    uint64_t* out = t.item[(pass + 1) & 1];
+    // (selected, not indexed: an index into the pointer pair put it in
+    // scratch memory)
+    const uint64_t* in = (pass & 1) ? t.item[1] : t.item[0];
+    uint64_t* out = (pass & 1) ? t.item[0] : t.item[1];
     const int sh = 32 + 4 * pass;
 #pragma unroll
     for (int d = 0; d < 16; ++d) cnt[d * kSampleThreads + tid] = 0;
