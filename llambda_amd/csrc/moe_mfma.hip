@@ -363,6 +363,11 @@ struct AFrag<true> {
     hi = *reinterpret_cast<const bf16x8*>(p);
     lo = *reinterpret_cast<const bf16x8*>(p + 32);
   }
+  // one token: the hi part in the even rows of the A operand, the lo part in
+  // the odd ones (into `hi`), so one product yields both sums (rows 0, 1)
+  __device__ __forceinline__ void load_pair(const uint16_t* p, int n) {
+    hi = *reinterpret_cast<const bf16x8*>(p + 32 * (n & 1));
+  }
   __device__ __forceinline__ void zero() {
     hi = __builtin_bit_cast(bf16x8, u32x4{0u, 0u, 0u, 0u});
     lo = hi;
@@ -377,6 +382,9 @@ struct AFrag<false> {
   __device__ __forceinline__ void load(const uint16_t* p) {
     hi = *reinterpret_cast<const shortx4*>(p);
     lo = *reinterpret_cast<const shortx4*>(p + 32);
+  }
+  __device__ __forceinline__ void load_pair(const uint16_t* p, int n) {
+    hi = *reinterpret_cast<const shortx4*>(p + 32 * (n & 1));
   }
   __device__ __forceinline__ void zero() {
     hi = shortx4{0, 0, 0, 0};
@@ -683,13 +691,20 @@ moe_gemm_kernel(MoeGemmArgs args) {
 #pragma unroll
             for (int i = 0; i < MT; ++i) {
               const AF& a_ = af[j % (kAhead + 1)][i];
-              floatx4 d = mfma_b(a_.hi, bf, floatx4{0.f, 0.f, 0.f, 0.f});
-              d = mfma_b(a_.lo, bf, d);
               floatx4& t = tot[i][m][nb];
-              t[0] = fmaf(delta, d[0], t[0]);
-              t[1] = fmaf(delta, d[1], t[1]);
-              t[2] = fmaf(delta, d[2], t[2]);
-              t[3] = fmaf(delta, d[3], t[3]);
+              if constexpr (PIPE == kPipeDecode) {
+                // one token, hi and lo in alternate rows (load_pair): its
+                // sums are rows 0 and 1, lane group 0 elements 0 and 1
+                const floatx4 d = mfma_b(a_.hi, bf, floatx4{0.f, 0.f, 0.f, 0.f});
+                t[0] = fmaf(delta, d[0] + d[1], t[0]);
+              } else {
+                floatx4 d = mfma_b(a_.hi, bf, floatx4{0.f, 0.f, 0.f, 0.f});
+                d = mfma_b(a_.lo, bf, d);
+                t[0] = fmaf(delta, d[0], t[0]);
+                t[1] = fmaf(delta, d[1], t[1]);
+                t[2] = fmaf(delta, d[2], t[2]);
+                t[3] = fmaf(delta, d[3], t[3]);
+              }
             }
           }
       }
@@ -889,7 +904,7 @@ moe_gemm_kernel(MoeGemmArgs args) {
       run_chunk(
           kc, stage,
           [&](int, int j, AF& af) {
-            af.load(reinterpret_cast<const uint16_t*>(stage + Sh::A_OFF) + AF::offset(j, g));
+            af.load_pair(reinterpret_cast<const uint16_t*>(stage + Sh::A_OFF) + AF::offset(j, g), n);
           },
           [&](int, int q) {
             const int gi = min(kc * KS + 4 * q + g, groups - 1) - kc * KS;
@@ -998,16 +1013,13 @@ __device__ __forceinline__ void combine_step(int kc, const uint8_t* stage, uint3
   for (int j = 0; j < KS; ++j) {
     if (FULL || j < valid) {
       AF af;
-      af.load(reinterpret_cast<const uint16_t*>(stage + Sh::A_OFF) + AF::offset(j, g));
+      af.load_pair(reinterpret_cast<const uint16_t*>(stage + Sh::A_OFF) + AF::offset(j, g), n);
       if (j + 1 < KS && (FULL || j + 1 < valid)) fetch(j + 1, raw[(j + 1) & 1], dl[(j + 1) & 1]);
       const typename B::Frag bf = B::decode(raw[j & 1], sh, j, g);
       const float delta = dl[j & 1];
-      floatx4 d = mfma_b(af.hi, bf, floatx4{0.f, 0.f, 0.f, 0.f});
-      d = mfma_b(af.lo, bf, d);
-      tot[0] = fmaf(delta, d[0], tot[0]);
-      tot[1] = fmaf(delta, d[1], tot[1]);
-      tot[2] = fmaf(delta, d[2], tot[2]);
-      tot[3] = fmaf(delta, d[3], tot[3]);
+      // hi and lo in alternate A rows: the token's two sums are rows 0 and 1
+      const floatx4 d = mfma_b(af.hi, bf, floatx4{0.f, 0.f, 0.f, 0.f});
+      tot[0] = fmaf(delta, d[0] + d[1], tot[0]);
     }
   }
   // offsets: group 4q + g of the chunk in K slice g of MFMA q
