@@ -670,7 +670,9 @@ __device__ __forceinline__ void gemv_mfma_body(uint8_t* lds, int wg, int nwg, co
   const int first = min(nbuf, steps);
   if (table_one_batch<IT, kMfmaWaves>(nblk) && first == 1) {
     // one stage per wave: its DMA is issued right behind the table's loads
-    // and streams in while the table is built
+    // and streams in while the table is built (never for a wave without
+    // steps -- small matrices leave some waves no tile -- whose step 0 would
+    // lie past the rows)
     uint32_t o[Ch::kLoads];
     const uint8_t* base_al = stage_src(0, o);
     build_table_overlapped<IT, kMfmaWaves, Ch::kLoads>(table, gsum, x, nblk, f.norm_w,
