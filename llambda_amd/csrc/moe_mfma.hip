@@ -1166,11 +1166,22 @@ moe_down_combine_kernel(MoeGemmArgs a, MoeCombineArgs cb) {
 // types (Q5_0, Q8_0): chunks of up to 64 (token, rank) pairs of one expert,
 // four 16-token tiles.  A workgroup of four waves takes 64 rows per wave (32
 // of gate and 32 of up for silu-gate products) and streams K in stages of two
-// 32-groups through a double-buffered LDS ring, both operands by DMA:
-//   the chunk's split activations and group sums, once per workgroup and
-//   shared by its waves -- stored piece-major, [piece][token][16 bytes], so
-//   that the 16 tokens of one MFMA fragment read 256 contiguous bytes;
-//   each wave's weight rows, piece-major as well, [piece][row][16 bytes].
+// 32-groups through a double-buffered LDS ring, both operands by DMA, with
+// every DMA instruction's 64 lanes reading whole 16-byte runs of a few rows
+// (one row per lane made each instruction touch 64 cache lines and bound the
+// pipeline on the requests):
+//   the chunk's split activations, once per workgroup and shared by its
+//   waves: instruction k takes tokens 4k .. 4k + 3, a token's 256 bytes of
+//   the stage in 16 consecutive lanes, and writes 1 KB block k of the stage
+//   with piece P of token t in 16-byte slot 16 (t & 3) + (P ^ (t & 15)), so
+//   that the 16 tokens of one MFMA fragment fall in 16 different slots of
+//   the 256-byte bank window; the group sums, 16 bytes per token, one lane
+//   per token;
+//   each wave's weight rows (one matrix): row-major lines of PIECES 16-byte
+//   pieces, instruction q taking line slots 64 q .. 64 q + 63 -- a run of
+//   whole lines (a line pitch of 48 or 80 bytes puts the 16 rows of a
+//   fragment in 16 different banks); the silu-gate pair (two matrices)
+//   keeps the piece-major [piece][row][16 bytes] stage, one row per lane.
 // One barrier per stage: after it, every wave's DMA of the stage has landed
 // and every wave is done with the other buffer, which then takes the next
 // stage's DMA while this one computes.  The per-output arithmetic is the
@@ -1206,9 +1217,11 @@ struct GroupShape {
   static constexpr int LDS = 2 * STAGE;
 };
 
-// Dword i of row r of a piece-major weight stage (matrix nb).
-template <int NB>
+// Dword i of row r of a wave's weight stage (matrix nb): row-major lines of
+// P pieces for one matrix, piece-major for two.
+template <int NB, int P>
 __device__ __forceinline__ uint32_t pm_dword(const uint8_t* wbuf, int nb, int r, uint32_t i) {
+  if constexpr (NB == 1) return *reinterpret_cast<const uint32_t*>(wbuf + r * (16 * P) + 4 * i);
   return *reinterpret_cast<const uint32_t*>(wbuf + (((i >> 2) * NB + nb) * 64 + r) * 16 + 4 * (i & 3));
 }
 
@@ -1220,19 +1233,22 @@ __device__ __forceinline__ typename GemmB<TYPE>::Raw group_fetch(const uint8_t* 
   if constexpr (TYPE == kQ5_0) {
     const uint32_t o = sh + 22u * (uint32_t)j;
     const uint32_t os = (o + 6u + 8u * (uint32_t)(g & 1)) >> 2, ob = (o + 2u + (uint32_t)g) >> 2;
-    return u32x4{pm_dword<NB>(wbuf, nb, r, os), pm_dword<NB>(wbuf, nb, r, os + 1u),
-                 pm_dword<NB>(wbuf, nb, r, os + 2u), pm_dword<NB>(wbuf, nb, r, ob)};
+    constexpr int P = GroupB<TYPE>::kPieces;
+    return u32x4{pm_dword<NB, P>(wbuf, nb, r, os), pm_dword<NB, P>(wbuf, nb, r, os + 1u),
+                 pm_dword<NB, P>(wbuf, nb, r, os + 2u), pm_dword<NB, P>(wbuf, nb, r, ob)};
   } else {
     const uint32_t os = (sh + 34u * (uint32_t)j + 2u + 8u * (uint32_t)g) >> 2;
-    return u32x4{pm_dword<NB>(wbuf, nb, r, os), pm_dword<NB>(wbuf, nb, r, os + 1u),
-                 pm_dword<NB>(wbuf, nb, r, os + 2u), 0u};
+    constexpr int P = GroupB<TYPE>::kPieces;
+    return u32x4{pm_dword<NB, P>(wbuf, nb, r, os), pm_dword<NB, P>(wbuf, nb, r, os + 1u),
+                 pm_dword<NB, P>(wbuf, nb, r, os + 2u), 0u};
   }
 }
 template <int TYPE, int NB>
 __device__ __forceinline__ void group_scale(const uint8_t* wbuf, int nb, int r, uint32_t sh, int j,
                                             float& delta, float& c) {
   const uint32_t o = sh + (uint32_t)GroupB<TYPE>::kBlock * (uint32_t)j;  // even
-  const uint32_t bits = (pm_dword<NB>(wbuf, nb, r, o >> 2) >> (8 * (o & 3u))) & 0xFFFFu;
+  const uint32_t bits =
+      (pm_dword<NB, GroupB<TYPE>::kPieces>(wbuf, nb, r, o >> 2) >> (8 * (o & 3u))) & 0xFFFFu;
   delta = half_bits_to_float(bits);
   if constexpr (TYPE == kQ5_0) c = 144.f * delta;
   else c = 128.f * delta;
@@ -1288,8 +1304,25 @@ __global__ void __launch_bounds__(64 * kGroupWaves, 2) moe_group_kernel(MoeGemmA
   base[0] = uniform_ptr(a.w0 + (int64_t)expert * a.expert_stride);
   if constexpr (NB == 2) base[1] = uniform_ptr(a.w1 + (int64_t)expert * a.expert_stride);
   const uint32_t rb = (uint32_t)a.row_bytes;
-  // DMA lane l: row (l mod ROWS) of each matrix
+  // weight DMA: two matrices, lane l takes row (l mod ROWS) of each; one
+  // matrix, instruction q takes line slot 64 q + l = row r, piece c
+  // (offsets without the stage's, 4-byte aligned: a stage spans a multiple
+  // of 4 bytes)
   const uint32_t brow = (uint32_t)min(n0 + (lane & (Sh::ROWS - 1)), a.N - 1) * rb;
+  uint32_t wdma[Sh::PIECES];
+#pragma unroll
+  for (int q = 0; q < Sh::PIECES; ++q) {
+    const int slot = 64 * q + lane, r = slot / Sh::PIECES, c = slot - r * Sh::PIECES;
+    wdma[q] = (((uint32_t)min(n0 + r, a.N - 1) * rb) & ~3u) + 16u * (uint32_t)c;
+  }
+  // activation DMA: this wave's instructions k = wave + 4 u take token
+  // 4 k + (l >> 4) and piece (l & 15) ^ (token & 15) into slot l of block k
+  uint32_t adma[4];
+#pragma unroll
+  for (int u = 0; u < 4; ++u) {
+    const int t = 4 * (wave + 4 * u) + (lane >> 4);
+    adma[u] = (uint32_t)__shfl((int)a_off, t) + 16u * (uint32_t)((lane & 15) ^ (t & 15));
+  }
   // fetch rows 16 m + n: their byte shift within a dword is the same at
   // every stage (2 blocks span a multiple of 4 bytes) and for every m (rows
   // 16 apart: row_bytes * 16 is a multiple of 4), so the subtiles' LDS words
@@ -1306,17 +1339,23 @@ __global__ void __launch_bounds__(64 * kGroupWaves, 2) moe_group_kernel(MoeGemmA
 
   auto issue = [&](int st, int buf) {
     const uint32_t stg = lds0 + (uint32_t)(buf * Sh::STAGE);
-    for (int p = wave; p < kGroupAPieces; p += kGroupWaves) {
-      if (p < 16) load_lds16(aq_base, a_off + 256u * (uint32_t)st + 16u * (uint32_t)p, stg + 1024u * p);
-      else load_lds16(as_base, s_off + 16u * (uint32_t)st, stg + 1024u * 16u);
-    }
+#pragma unroll
+    for (int u = 0; u < 4; ++u)
+      load_lds16(aq_base, adma[u] + 256u * (uint32_t)st, stg + 1024u * (uint32_t)(wave + 4 * u));
+    if (wave == 0) load_lds16(as_base, s_off + 16u * (uint32_t)st, stg + 1024u * 16u);
     const uint32_t wst = stg + Sh::A_BYTES + (uint32_t)wave * Sh::B_BYTES;
-    const uint32_t off = (brow + (uint32_t)st * (uint32_t)(2 * BB)) & ~3u;
+    const uint32_t sto = (uint32_t)st * (uint32_t)(2 * BB);
+    if constexpr (NB == 1) {
 #pragma unroll
-    for (int k = 0; k < Sh::PIECES; ++k)
+      for (int q = 0; q < Sh::PIECES; ++q) load_lds16(base[0], wdma[q] + sto, wst + 1024u * (uint32_t)q);
+    } else {
+      const uint32_t off = (brow + sto) & ~3u;
 #pragma unroll
-      for (int nb = 0; nb < NB; ++nb)
-        load_lds16(base[nb], off + 16u * (uint32_t)k, wst + (uint32_t)((k * NB + nb) * 1024));
+      for (int k = 0; k < Sh::PIECES; ++k)
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb)
+          load_lds16(base[nb], off + 16u * (uint32_t)k, wst + (uint32_t)((k * NB + nb) * 1024));
+    }
   };
 
   floatx4 tot[MT][NS][NB];
@@ -1381,12 +1420,13 @@ __global__ void __launch_bounds__(64 * kGroupWaves, 2) moe_group_kernel(MoeGemmA
             cneg[m][nb][0] = (mine && j8 < 4) ? -c : cneg[m][nb][0];
             cneg[m][nb][1] = (mine && j8 >= 4) ? -c : cneg[m][nb][1];
           }
+        // token 16 i + n: block 4 i + (n >> 2), slot 16 (n & 3) + (piece ^ n)
         bf16x8 hi[NT], lo[NT];
+        const uint8_t* at = stg + (n >> 2) * 1024 + (n & 3) * 256;
 #pragma unroll
         for (int i = 0; i < NT; ++i) {
-          const uint8_t* ap = stg + ((jj * 8 + g) * 64 + 16 * i + n) * 16;
-          hi[i] = *reinterpret_cast<const bf16x8*>(ap);
-          lo[i] = *reinterpret_cast<const bf16x8*>(ap + 4 * 1024);
+          hi[i] = *reinterpret_cast<const bf16x8*>(at + 4096 * i + 16 * ((jj * 8 + g) ^ n));
+          lo[i] = *reinterpret_cast<const bf16x8*>(at + 4096 * i + 16 * ((jj * 8 + 4 + g) ^ n));
         }
 #pragma unroll
         for (int m = 0; m < NS; ++m)
@@ -1425,7 +1465,6 @@ __global__ void __launch_bounds__(64 * kGroupWaves, 2) moe_group_kernel(MoeGemmA
   };
 
   // epilogue: lane (n, g) holds tokens 16 i + 4 g + r of rows n0 + 16 m + n
-  // (the pairs they belong to are read here, not held through the products)
   auto finish = [&](auto ntc) {
     constexpr int NT = decltype(ntc)::value;
 #pragma unroll
@@ -1434,7 +1473,8 @@ __global__ void __launch_bounds__(64 * kGroupWaves, 2) moe_group_kernel(MoeGemmA
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const int tk = 16 * i + 4 * g + r;
-        qout[r] = tk < count ? a.perm[start + tk] : 0;
+        const int q = __shfl(q_l, tk);  // lane tk holds the pair of token tk
+        qout[r] = tk < count ? q : 0;
       }
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
