@@ -1267,11 +1267,14 @@ __global__ void __launch_bounds__(64 * kGroupWaves, 2) moe_group_kernel(MoeGemmA
   const int bx = (L / (8 * T)) * 8 + (L & 7);
   const int by = (L >> 3) % T;
   const int* cc = args.chunk_counts;
-  const MoeChunk ch = args.chunks[(!args.joint && args.group ? cc[0] : 0) + bx];
   const int nchunks = args.joint ? cc[0] + cc[1] : cc[args.group];
   if (bx >= nchunks) return;  // the whole workgroup, before any barrier
+  // a joint launch takes the shared expert's chunks (all full) first, so
+  // that routed chunks, many of them short, make up the launch's last round
+  const int cx = args.joint ? (bx < cc[1] ? cc[0] + bx : bx - cc[1]) : bx;
+  const MoeChunk ch = args.chunks[(!args.joint && args.group ? cc[0] : 0) + cx];
   MoeGemmArgs a = args;
-  if (args.joint && bx >= cc[0]) {
+  if (args.joint && cx >= cc[0]) {
     a.w0 = args.s_w0;
     a.w1 = args.s_w1;
     a.row_bytes = args.s_row_bytes;
@@ -1337,12 +1340,17 @@ __global__ void __launch_bounds__(64 * kGroupWaves, 2) moe_group_kernel(MoeGemmA
   const int nstage = (groups + 1) >> 1;
   const uint32_t lds0 = lds_address(lds);
 
+  // (the token blocks of tiles past the chunk's are never read; a wave
+  // whose rows all lie past the last loads no rows and computes nothing)
+  const bool live = n0 < a.N;
   auto issue = [&](int st, int buf) {
     const uint32_t stg = lds0 + (uint32_t)(buf * Sh::STAGE);
 #pragma unroll
     for (int u = 0; u < 4; ++u)
-      load_lds16(aq_base, adma[u] + 256u * (uint32_t)st, stg + 1024u * (uint32_t)(wave + 4 * u));
+      if (wave + 4 * u < 4 * nt)
+        load_lds16(aq_base, adma[u] + 256u * (uint32_t)st, stg + 1024u * (uint32_t)(wave + 4 * u));
     if (wave == 0) load_lds16(as_base, s_off + 16u * (uint32_t)st, stg + 1024u * 16u);
+    if (!live) return;
     const uint32_t wst = stg + Sh::A_BYTES + (uint32_t)wave * Sh::B_BYTES;
     const uint32_t sto = (uint32_t)st * (uint32_t)(2 * BB);
     if constexpr (NB == 1) {
@@ -1525,8 +1533,10 @@ __global__ void __launch_bounds__(64 * kGroupWaves, 2) moe_group_kernel(MoeGemmA
     __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
     __syncthreads();
     if (st + 1 < nstage) issue(st + 1, 1 - decltype(bufc)::value);
-    compute(ntc, st, bufc);
-    if ((st & 3) == 3 && st + 1 < nstage) apply_offsets(ntc);
+    if (live) {
+      compute(ntc, st, bufc);
+      if ((st & 3) == 3 && st + 1 < nstage) apply_offsets(ntc);
+    }
   };
   auto run = [&](auto ntc) {
     issue(0, 0);
@@ -1534,8 +1544,10 @@ __global__ void __launch_bounds__(64 * kGroupWaves, 2) moe_group_kernel(MoeGemmA
       stage(ntc, st, std::integral_constant<int, 0>{});
       if (st + 1 < nstage) stage(ntc, st + 1, std::integral_constant<int, 1>{});
     }
-    apply_offsets(ntc);
-    finish(ntc);
+    if (live) {
+      apply_offsets(ntc);
+      finish(ntc);
+    }
   };
   switch (nt) {
     case 1: run(std::integral_constant<int, 1>{}); break;
