@@ -52,6 +52,7 @@ __global__ void __launch_bounds__(256) topk_gate_kernel(MoePlan p, int tokens, i
 // that groups (token, rank) pairs by expert.  Pair id p = token * k + rank;
 // the shared expert's pairs are tokens * k + token.
 constexpr int kScanThreads = 1024;
+constexpr int kMaxChunkPairs = 64;  // pairs per chunk: 16, 32 or 64
 
 __global__ void __launch_bounds__(kScanThreads) moe_scan_kernel(MoePlan p, int tokens, int nt,
                                                                 int has_shared) {
@@ -106,15 +107,33 @@ __global__ void __launch_bounds__(kScanThreads) moe_scan_kernel(MoePlan p, int t
   }
   __syncthreads();
   const int routed_pairs = s_off[E], routed_chunks = s_coff[E];
+  // The chunk table in decreasing pair count -- every full chunk, then the
+  // experts' partial last chunks, counting-sorted by size -- so that the
+  // launch's last workgroups are its shortest.  (A chunk's outputs do not
+  // depend on where it sits in the table.)
+  __shared__ int s_hoff[kMaxChunkPairs + 1];
+  __shared__ int s_full;
+  if (tid <= kMaxChunkPairs) s_hoff[tid] = 0;
+  if (tid == 0) s_full = 0;
+  __syncthreads();
   for (int e = tid; e < E; e += kScanThreads) {
-    const int c = s_cnt[e];
-    for (int j = 0; j * nt < c; ++j) {
-      MoeChunk ch;
-      ch.expert = e;
-      ch.start = s_off[e] + j * nt;
-      ch.count = min(nt, c - j * nt);
-      p.chunks[s_coff[e] + j] = ch;
+    const int r = s_cnt[e] % nt;
+    if (r) atomicAdd(&s_hoff[r], 1);
+  }
+  __syncthreads();
+  if (tid == 0) {
+    int run = routed_chunks;  // the partial chunks end the routed table
+    for (int v = 1; v < nt; ++v) {
+      run -= s_hoff[v];
+      s_hoff[v] = run;
     }
+  }
+  __syncthreads();
+  for (int e = tid; e < E; e += kScanThreads) {
+    const int c = s_cnt[e], f = c / nt, r = c - f * nt;
+    const int base = f ? atomicAdd(&s_full, f) : 0;
+    for (int j = 0; j < f; ++j) p.chunks[base + j] = MoeChunk{e, s_off[e] + j * nt, nt};
+    if (r) p.chunks[atomicAdd(&s_hoff[r], 1)] = MoeChunk{e, s_off[e] + f * nt, r};
   }
   int shared_chunks = 0;
   if (has_shared) {
