@@ -285,6 +285,26 @@ def test_long_chunks(hip, variant, types, tokens):
         session.close()
 
 
+# The group pipeline (every tensor a 32-weight type, 64-pair chunks) where
+# rows end inside a wave and whole waves lie past the last row: ffn 160 (up
+# rows 128-159 in a wave of 64, the fourth wave past them), hidden 544 (down
+# rows 512-543, then three waves past them), a shared expert of 96 rows.
+@pytest.mark.parametrize("types", [(ggml.Q5_0, ggml.Q5_0), (ggml.Q8_0, ggml.Q8_0)])
+def test_group_pipeline_ragged_rows(hip, types):
+    rng = np.random.default_rng(41)
+    layer = synthetic_nemotron_h(rng, hidden=544, experts=8, top_k=3, ffn=160, shared_ffn=96,
+                                 expert_type=types[0], down_type=types[1])
+    tokens = 72
+    assert tokens * layer.top_k / layer.expert_count > 16
+    x = synthetic.activations(rng, tokens, layer.hidden)
+    y, _ = check_layer(layer, x, f"{types} ragged group pipeline")
+    session = HipMoeSession(layer)
+    try:
+        np.testing.assert_array_equal(session.run(x[3:8]), y[3:8])
+    finally:
+        session.close()
+
+
 # The same long chunks for 32-weight block experts beside a K-quant shared
 # expert: the group pipeline needs every tensor in a 32-weight type, so these
 # run on the wide pipeline; ffn 224 makes the down rows 154 (Q5_0) or 238
