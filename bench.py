@@ -252,6 +252,11 @@ def bench_moe(torch, timer, layer, tokens, steps, warmup, seed):
     def step():
         session.run_device(x.data_ptr(), y.data_ptr(), tokens, timer.handle)
 
+    # the layer's upload leaves the GPU idle, and the first ~30 ms of launches
+    # after idling run slower while the clocks come back: warm up for at
+    # least 60 ms whatever the step count asks
+    probe = timer.time(step, 3, 1)
+    warmup = max(warmup, min(4000, int(60.0 / max(probe, 1e-3))))
     ms = timer.time(step, steps, warmup)
     session.sync(timer.handle)
     session.close()
