@@ -311,7 +311,10 @@ def bench_llama(torch, timer, steps, warmup):
     for graph in (True, False):
         def step():
             sess.step_device(token, pos, logits.data_ptr(), timer.handle, graph=graph)
-        res[graph] = timer.time(step, steps, warmup)
+        # at least 60 ms of warm-up tokens, past the clocks' ramp after the
+        # host-side set-up (the same rule as the MoE layers)
+        probe = timer.time(step, 3, 1)
+        res[graph] = timer.time(step, steps, max(warmup, min(400, int(60.0 / max(probe, 1e-3)))))
     sess.close()
     kv_bytes = 2 * c.layer_count * c.kv_head_count * (pos + 1) * c.head_dim * 4
     return res[True], res[False], wbytes, kv_bytes
