@@ -99,35 +99,50 @@ __device__ __forceinline__ void split_octet(const float* __restrict__ xrow, int 
 // -------------------------------------------------------------------- router
 // Router logits sum_h x[t][h] R[e][h] (dot-product-with-f32-tensor-data,
 // llambda.lisp:4096-4107, in another fp32 order), in one fixed order for
-// every batch size: K is cut into slices of 512; workgroup (e-tile, t-tile,
-// slice) adds its slice's 32 pieces of 16 elements for a 16 x 16 tile on
+// every batch size: K is cut into slices of 512; for each 16 x 16 (token,
+// expert) tile and slice, the slice's 32 pieces of 16 elements are added on
 // v_mfma_f32_16x16x4_f32 -- wave w of 8 takes pieces 4w .. 4w+3, adds them as
 // (p0 + p1) + (p2 + p3), and the wave sums meet as ((w0 + w1) + (w2 + w3)) +
-// ((w4 + w5) + (w6 + w7)) -- and writes the slice's partial sum to
-// part[slice][t][e]; the top-k kernel adds the slices in order.  Expert-tile
-// 0 workgroups also write their tokens' split rows over their slice.
+// ((w4 + w5) + (w6 + w7)) -- and the slice's partial sum goes to
+// part[slice][t][e]; the top-k kernel adds the slices in order.  A workgroup
+// takes one token tile, one slice and GE expert tiles; those of the first
+// expert tiles also write their tokens' split rows over their slice.
 constexpr int kRouterWaves = 8;
 constexpr int kRouterSlice = 512;
 
+// GE expert tiles per workgroup: each wave loads its token tile's x pieces
+// once and runs the expert tiles' products in turn (a batch's x is then read
+// once per GE expert tiles instead of once per tile); wave w < GE adds the
+// eight wave sums of expert tile w.  Every tile's arithmetic is the same for
+// any GE.
+template <int GE>
 __global__ void __launch_bounds__(64 * kRouterWaves)
 router_mfma_kernel(const float* __restrict__ x, int T, const float* __restrict__ R, int Er, int H,
                    float* __restrict__ part, int ld, uint16_t* __restrict__ q, int64_t q_stride,
                    float* __restrict__ s, int64_t s_stride) {
-  __shared__ floatx4 red[kRouterWaves][64];
+  __shared__ floatx4 red[GE][kRouterWaves][64];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int i = lane & 15, kg = lane >> 4;
-  const int t0 = blockIdx.y * 16, e0 = blockIdx.x * 16, k0 = blockIdx.z * kRouterSlice;
+  const int t0 = blockIdx.y * 16, eg = blockIdx.x * 16 * GE, k0 = blockIdx.z * kRouterSlice;
+  const int tiles = min(GE, (Er - eg + 15) >> 4);  // expert tiles of this workgroup
   // the products' operands are requested first, so that the split below
-  // (expert-tile 0) overlaps their round trip instead of preceding it
+  // (expert-group 0) overlaps their round trip instead of preceding it
   const float* xr = x + (int64_t)min(t0 + i, T - 1) * H + 4 * kg;
-  const float* rr = R + (int64_t)min(e0 + i, Er - 1) * H + 4 * kg;
+  auto load_r = [&](int e0, float4 (&rb)[4]) {
+    const float* rr = R + (int64_t)min(e0 + i, Er - 1) * H + 4 * kg;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      const int k = k0 + 64 * wave + 16 * c;
+      rb[c] = k < H ? *reinterpret_cast<const float4*>(rr + k) : float4{0.f, 0.f, 0.f, 0.f};
+    }
+  };
   float4 xa[4], rb[4];
 #pragma unroll
   for (int c = 0; c < 4; ++c) {
     const int k = k0 + 64 * wave + 16 * c;
     xa[c] = k < H ? *reinterpret_cast<const float4*>(xr + k) : float4{0.f, 0.f, 0.f, 0.f};
-    rb[c] = k < H ? *reinterpret_cast<const float4*>(rr + k) : float4{0.f, 0.f, 0.f, 0.f};
   }
+  load_r(eg, rb);
   if (blockIdx.x == 0) {
     const int octets = min(kRouterSlice, H - k0) >> 3, ofirst = k0 >> 3;
     for (int idx = threadIdx.x; idx < 16 * octets; idx += 64 * kRouterWaves) {
@@ -137,29 +152,41 @@ router_mfma_kernel(const float* __restrict__ x, int T, const float* __restrict__
                     s + (int64_t)(t0 + tt) * s_stride);
     }
   }
-  floatx4 acc[4];
 #pragma unroll
-  for (int c = 0; c < 4; ++c) {
-    acc[c] = floatx4{0.f, 0.f, 0.f, 0.f};
-    if (k0 + 64 * wave + 16 * c < H) {
-      acc[c] = mfma4f32(xa[c].x, rb[c].x, acc[c]);
-      acc[c] = mfma4f32(xa[c].y, rb[c].y, acc[c]);
-      acc[c] = mfma4f32(xa[c].z, rb[c].z, acc[c]);
-      acc[c] = mfma4f32(xa[c].w, rb[c].w, acc[c]);
+  for (int ge = 0; ge < GE; ++ge) {
+    if (ge < tiles) {
+      float4 rn[4];
+      if (ge + 1 < tiles) load_r(eg + 16 * (ge + 1), rn);
+      floatx4 acc[4];
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        acc[c] = floatx4{0.f, 0.f, 0.f, 0.f};
+        if (k0 + 64 * wave + 16 * c < H) {
+          acc[c] = mfma4f32(xa[c].x, rb[c].x, acc[c]);
+          acc[c] = mfma4f32(xa[c].y, rb[c].y, acc[c]);
+          acc[c] = mfma4f32(xa[c].z, rb[c].z, acc[c]);
+          acc[c] = mfma4f32(xa[c].w, rb[c].w, acc[c]);
+        }
+      }
+      red[ge][wave][lane] = (acc[0] + acc[1]) + (acc[2] + acc[3]);
+      if (ge + 1 < tiles)
+#pragma unroll
+        for (int c = 0; c < 4; ++c) rb[c] = rn[c];
     }
   }
-  red[wave][lane] = (acc[0] + acc[1]) + (acc[2] + acc[3]);
   __syncthreads();
-  if (wave != 0) return;
-  const floatx4 v = ((red[0][lane] + red[1][lane]) + (red[2][lane] + red[3][lane])) +
-                    ((red[4][lane] + red[5][lane]) + (red[6][lane] + red[7][lane]));
-  const int e = e0 + i;
-  if (e >= Er) return;
-  float* out = part + (int64_t)blockIdx.z * T * ld;
+  for (int ge = wave; ge < tiles; ge += kRouterWaves) {
+    const floatx4(&r8)[kRouterWaves][64] = red[ge];
+    const floatx4 v = ((r8[0][lane] + r8[1][lane]) + (r8[2][lane] + r8[3][lane])) +
+                      ((r8[4][lane] + r8[5][lane]) + (r8[6][lane] + r8[7][lane]));
+    const int e = eg + 16 * ge + i;
+    if (e >= Er) continue;
+    float* out = part + (int64_t)blockIdx.z * T * ld;
 #pragma unroll
-  for (int r = 0; r < 4; ++r) {
-    const int t = t0 + 4 * kg + r;
-    if (t < T) out[(int64_t)t * ld + e] = v[r];
+    for (int r = 0; r < 4; ++r) {
+      const int t = t0 + 4 * kg + r;
+      if (t < T) out[(int64_t)t * ld + e] = v[r];
+    }
   }
 }
 
@@ -168,9 +195,18 @@ int router_slices(int H) { return (H + kRouterSlice - 1) / kRouterSlice; }
 hipError_t router_mfma_launch(const float* x, int T, const float* R, int Er, int H, float* part,
                               int ld, uint16_t* q, int64_t q_stride, float* s, int64_t s_stride,
                               hipStream_t stream) {
-  const dim3 grid((Er + 15) / 16, (T + 15) / 16, router_slices(H));
-  hipLaunchKernelGGL(router_mfma_kernel, grid, dim3(64 * kRouterWaves), 0, stream, x, T, R, Er, H,
-                     part, ld, q, q_stride, s, s_stride);
+  // batches of 16 token tiles or more take eight expert tiles per
+  // workgroup; smaller ones one (their grid is already short)
+  const int etiles = (Er + 15) / 16, ttiles = (T + 15) / 16;
+  if (ttiles >= 16) {
+    const dim3 grid((etiles + 7) / 8, ttiles, router_slices(H));
+    hipLaunchKernelGGL(router_mfma_kernel<8>, grid, dim3(64 * kRouterWaves), 0, stream, x, T, R, Er,
+                       H, part, ld, q, q_stride, s, s_stride);
+  } else {
+    const dim3 grid(etiles, ttiles, router_slices(H));
+    hipLaunchKernelGGL(router_mfma_kernel<1>, grid, dim3(64 * kRouterWaves), 0, stream, x, T, R, Er,
+                       H, part, ld, q, q_stride, s, s_stride);
+  }
   return hipGetLastError();
 }
 
