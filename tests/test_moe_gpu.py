@@ -257,6 +257,24 @@ def test_small_qwen_shapes(hip):
     check_layer(layer, x, "qwen small")
 
 
+def test_router_expert_groups_ragged(hip):
+    """300 tokens (19 token tiles, the last partial) take the router launch
+    with eight expert tiles per workgroup; 40 experts + the shared gate row
+    are 41 router rows, three tiles of one group, the last partial.  Against
+    the oracle, and bit for bit against the same tokens in a batch of 20 (one
+    expert tile per workgroup)."""
+    rng = np.random.default_rng(42)
+    layer = synthetic_qwen3next(rng, hidden=768, experts=40, top_k=4, ffn=64, shared_ffn=64,
+                                gate_type=ggml.Q8_0, down_type=ggml.Q5_0)
+    x = synthetic.activations(rng, 300, layer.hidden)
+    y, _ = check_layer(layer, x, "router expert groups")
+    session = HipMoeSession(layer)
+    try:
+        np.testing.assert_array_equal(session.run(x[280:300]), y[280:300])
+    finally:
+        session.close()
+
+
 # Batches whose average load per expert (tokens * k / E) is above 16 pairs:
 # chunks of two token tiles (the wide pipeline) against the oracle.  Every
 # weight type, relu^2 (one matrix) and silu-gate (two side by side) products.
