@@ -323,6 +323,27 @@ def test_group_pipeline_ragged_rows(hip, types):
         session.close()
 
 
+# The group pipeline with the shared expert in another 32-weight type than
+# the routed ones (Q8_0 beside Q5_0): routed and shared chunks then take
+# separate launches instead of one joint launch.
+def test_group_pipeline_separate_shared_launches(hip):
+    rng = np.random.default_rng(43)
+    layer = synthetic_nemotron_h(rng, hidden=512, experts=8, top_k=3, ffn=256, shared_ffn=160,
+                                 expert_type=ggml.Q5_0, down_type=ggml.Q5_0)
+    gen = synthetic.packed
+    layer = dataclasses.replace(layer, shared_up=(ggml.Q8_0, gen(ggml.Q8_0, rng, 160, 512)),
+                                shared_down=(ggml.Q8_0, gen(ggml.Q8_0, rng, 512, 160)))
+    tokens = 80
+    assert tokens * layer.top_k / layer.expert_count > 16
+    x = synthetic.activations(rng, tokens, layer.hidden)
+    y, _ = check_layer(layer, x, "group pipeline, separate shared launches")
+    session = HipMoeSession(layer)
+    try:
+        np.testing.assert_array_equal(session.run(x[3:8]), y[3:8])
+    finally:
+        session.close()
+
+
 # The same long chunks for 32-weight block experts beside a K-quant shared
 # expert: the group pipeline needs every tensor in a 32-weight type, so these
 # run on the wide pipeline; ffn 224 makes the down rows 154 (Q5_0) or 238
