@@ -462,9 +462,27 @@ struct GemmShape {
   static constexpr int WG_ROWS = PIPE == kPipeDecode ? ROWS : kWaves * ROWS;
 };
 
+// The double pipeline with 16-byte activation fragments: the chunk's split
+// activations (16 tokens x 1 KB) go into LDS once per workgroup, a quarter
+// loaded by each wave, instead of every wave holding all 16 KB of the
+// current and the next chunk in its registers; with one row stage per wave
+// (the next chunk's rows load once the products have read the stage) the
+// workgroup fits 53 KB and 160 registers, three workgroups per CU instead of
+// two, whose waves cover each other's waits (Qwen3Next B=256 gate|up:
+// 0.493 -> 0.452 ms for the layer).
+constexpr int kShareABytes = 16 * 1024;
+template <int TYPE, int EPI, int PIPE>
+constexpr bool gemm_share_a() {
+  using Sh = GemmShape<TYPE, EPI, PIPE>;
+  return PIPE == kPipeDouble && GemmB<TYPE>::kWide &&
+         Sh::RED + Sh::kWaves * (Sh::STAGE + Sh::TABLE) + kShareABytes <= 53 * 1024;
+}
+
 template <int TYPE, int EPI, int PIPE>
 constexpr int gemm_lds_bytes(int depth) {
   using Sh = GemmShape<TYPE, EPI, PIPE>;
+  if constexpr (gemm_share_a<TYPE, EPI, PIPE>())
+    return Sh::RED + Sh::kWaves * (Sh::STAGE + Sh::TABLE) + kShareABytes;
   return Sh::RED + Sh::kWaves * (depth * Sh::STAGE + Sh::TABLE);
 }
 
@@ -574,8 +592,11 @@ moe_gemm_kernel(MoeGemmArgs args) {
   // tiles_per_wg consecutive row tiles of the chunk, one after the other)
   const int n0 = PIPE == kPipeDecode ? by * Sh::ROWS
                                      : by * a.tiles_per_wg * Sh::WG_ROWS + wave * Sh::ROWS;
-  if (n0 >= a.N) return;  // uniform over the workgroup for the decode pipeline
-  const int depth = PIPE == kPipeDecode ? a.depth : Sh::DEPTH;
+  // shared activations: every wave of the workgroup takes part in their
+  // loads and barriers, also one whose rows lie past the last
+  constexpr bool SHARE_A = gemm_share_a<TYPE, EPI, PIPE>();
+  if (SHARE_A ? n0 - wave * Sh::ROWS >= a.N : n0 >= a.N) return;  // uniform (decode, SHARE_A)
+  const int depth = PIPE == kPipeDecode ? a.depth : SHARE_A ? 1 : Sh::DEPTH;
   uint8_t* wlds = lds + Sh::RED + wave * (depth * Sh::STAGE + Sh::TABLE);
   float2* table = reinterpret_cast<float2*>(wlds + depth * Sh::STAGE);
   const uint32_t wlds_addr = lds_address(wlds);
@@ -691,7 +712,7 @@ moe_gemm_kernel(MoeGemmArgs args) {
     // group j + 1 and, in the wide pipeline, whose activations come from
     // memory, those of group j + 2 are requested before group j decodes and
     // multiplies, so that neither latency stalls the group's MFMAs.
-    constexpr int kAhead = PIPE == kPipeWide ? 2 : 0;
+    constexpr int kAhead = PIPE == kPipeWide ? 2 : SHARE_A ? 1 : 0;
     typename B::Raw raw[2][NS][NB];
     float dl[2][NS][NB];
     AF af[kAhead + 1][MT];
@@ -866,6 +887,92 @@ moe_gemm_kernel(MoeGemmArgs args) {
           },
           [&](int i, int q) { return sv[i][q]; });
       __builtin_amdgcn_s_waitcnt(kWaitLgkm0);
+    }
+  } else if constexpr (PIPE == kPipeDouble && SHARE_A) {
+    // As below, with the chunk's activations in LDS: wave w loads tokens
+    // 4w .. 4w+3 (lane l: token 4w + (l >> 4), 16-byte pieces 4 (l & 15) ..
+    // +3 of its 1 KB) into registers while the step computes, and stores
+    // them once every wave is done with the step's; piece P of token t sits
+    // in slot P ^ t of the token's 1 KB, so a fragment's 16 tokens read 16
+    // different bank quads.  The steps and barriers are the workgroup's: a
+    // wave without rows in a tile loads its quarter and waits with the rest.
+    const int n0w = n0 - wave * Sh::ROWS;
+    const int ntile = min(a.tiles_per_wg, (a.N - n0w + Sh::WG_ROWS - 1) / Sh::WG_ROWS);
+    const int steps = ntile * nchunk;
+    uint8_t* alds = lds + Sh::RED + Sh::kWaves * (Sh::STAGE + Sh::TABLE);
+    const int qt = 4 * wave + (lane >> 4);
+    const uint64_t ap = reinterpret_cast<uint64_t>(arow[0]);  // lane qt holds token qt's row
+    const uint32_t ap_lo = (uint32_t)__shfl((int)(uint32_t)ap, qt);
+    const uint32_t ap_hi = (uint32_t)__shfl((int)(uint32_t)(ap >> 32), qt);
+    const uint16_t* qrow = reinterpret_cast<const uint16_t*>(((uint64_t)ap_hi << 32) | ap_lo);
+    u32x4 qa[4];
+    auto load_quarter = [&](int kc) {
+      const int valid = min(KS, groups - kc * KS);
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        const int piece = 4 * (lane & 15) + k;  // group piece >> 3
+        qa[k] = (piece >> 3) < valid
+                    ? *reinterpret_cast<const u32x4*>(qrow + 512 * kc + 8 * piece)
+                    : u32x4{0u, 0u, 0u, 0u};
+      }
+    };
+    auto store_quarter = [&]() {
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        const int piece = 4 * (lane & 15) + k;
+        *reinterpret_cast<u32x4*>(alds + qt * 1024 + 16 * (piece ^ qt)) = qa[k];
+      }
+    };
+    auto load_sums = [&](int kc, float (&sr)[NQ]) {
+#pragma unroll
+      for (int q = 0; q < NQ; ++q) sr[q] = row_sum(srow[0], min(kc * KS + 4 * q + g, groups - 1));
+    };
+    auto get_a_lds = [&](int, int j, AF& af) {
+      af.hi = *reinterpret_cast<const bf16x8*>(alds + n * 1024 + 16 * ((8 * j + g) ^ n));
+      af.lo = *reinterpret_cast<const bf16x8*>(alds + n * 1024 + 16 * ((8 * j + 4 + g) ^ n));
+    };
+    float scur[NQ], snext[NQ];
+    if (n0 < a.N) issue(0, 0, n0);
+    load_quarter(0);
+    load_sums(0, scur);
+    __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
+    store_quarter();
+    __syncthreads();
+    for (int st = 0, tt = 0, kc = 0; st < steps; ++st) {
+      const bool more = st + 1 < steps;
+      const int kc1 = kc + 1 < nchunk ? kc + 1 : 0;
+      const int tt1 = kc + 1 < nchunk ? tt : tt + 1;
+      const bool live = n0 + tt * Sh::WG_ROWS < a.N;
+      if (more) {
+        load_quarter(kc1);
+        load_sums(kc1, snext);
+      }
+      if (live)
+        run_chunk(kc, wlds, get_a_lds, [&](int, int q) { return scur[q]; });
+      // one row stage per wave: the next step's rows load once this step's
+      // products have read them (the other workgroups' waves cover the wait)
+      __builtin_amdgcn_s_waitcnt(kWaitLgkm0);
+      if (more && n0 + tt1 * Sh::WG_ROWS < a.N) issue(kc1, 0, n0 + tt1 * Sh::WG_ROWS);
+      __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
+      if (kc + 1 == nchunk) {
+        if (live) finish(n0 + tt * Sh::WG_ROWS);
+#pragma unroll
+        for (int i = 0; i < MT; ++i)
+#pragma unroll
+          for (int m = 0; m < NS; ++m)
+#pragma unroll
+            for (int nb = 0; nb < NB; ++nb) tot[i][m][nb] = floatx4{0.f, 0.f, 0.f, 0.f};
+        if (more && !ALIGNED) set_rows(n0 + tt1 * Sh::WG_ROWS);
+      }
+      __syncthreads();  // every wave is done with this chunk's activations
+      if (more) {
+        store_quarter();
+#pragma unroll
+        for (int q = 0; q < NQ; ++q) scur[q] = snext[q];
+      }
+      __syncthreads();  // the next chunk's activations are in place
+      kc = kc1;
+      tt = tt1;
     }
   } else if constexpr (PIPE == kPipeDouble) {
     // Steps (tile, chunk) over the workgroup's row tiles that hold rows of
