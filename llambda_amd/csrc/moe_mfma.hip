@@ -478,11 +478,25 @@ constexpr bool gemm_share_a() {
          Sh::RED + Sh::kWaves * (Sh::STAGE + Sh::TABLE) + kShareABytes <= 53 * 1024;
 }
 
+// The double pipeline otherwise (8-byte fragments, or rows too wide to
+// share the activations beside them): when one row stage per wave and the
+// scale tables fit 53 KB, it runs the wide pipeline's loop -- one stage,
+// each group's activations loaded two groups ahead -- so that no wave holds
+// a whole chunk's activations (current and next) in registers and three
+// workgroups share a CU.
+template <int TYPE, int EPI, int PIPE>
+constexpr bool gemm_jit_a() {
+  using Sh = GemmShape<TYPE, EPI, PIPE>;
+  return PIPE == kPipeDouble && !gemm_share_a<TYPE, EPI, PIPE>() &&
+         Sh::RED + Sh::kWaves * (Sh::STAGE + Sh::TABLE) <= 53 * 1024;
+}
+
 template <int TYPE, int EPI, int PIPE>
 constexpr int gemm_lds_bytes(int depth) {
   using Sh = GemmShape<TYPE, EPI, PIPE>;
   if constexpr (gemm_share_a<TYPE, EPI, PIPE>())
     return Sh::RED + Sh::kWaves * (Sh::STAGE + Sh::TABLE) + kShareABytes;
+  if constexpr (gemm_jit_a<TYPE, EPI, PIPE>()) return Sh::RED + Sh::kWaves * (Sh::STAGE + Sh::TABLE);
   return Sh::RED + Sh::kWaves * (depth * Sh::STAGE + Sh::TABLE);
 }
 
@@ -595,8 +609,9 @@ moe_gemm_kernel(MoeGemmArgs args) {
   // shared activations: every wave of the workgroup takes part in their
   // loads and barriers, also one whose rows lie past the last
   constexpr bool SHARE_A = gemm_share_a<TYPE, EPI, PIPE>();
+  constexpr bool JIT_A = gemm_jit_a<TYPE, EPI, PIPE>();
   if (SHARE_A ? n0 - wave * Sh::ROWS >= a.N : n0 >= a.N) return;  // uniform (decode, SHARE_A)
-  const int depth = PIPE == kPipeDecode ? a.depth : SHARE_A ? 1 : Sh::DEPTH;
+  const int depth = PIPE == kPipeDecode ? a.depth : SHARE_A || JIT_A ? 1 : Sh::DEPTH;
   uint8_t* wlds = lds + Sh::RED + wave * (depth * Sh::STAGE + Sh::TABLE);
   float2* table = reinterpret_cast<float2*>(wlds + depth * Sh::STAGE);
   const uint32_t wlds_addr = lds_address(wlds);
@@ -712,7 +727,7 @@ moe_gemm_kernel(MoeGemmArgs args) {
     // group j + 1 and, in the wide pipeline, whose activations come from
     // memory, those of group j + 2 are requested before group j decodes and
     // multiplies, so that neither latency stalls the group's MFMAs.
-    constexpr int kAhead = PIPE == kPipeWide ? 2 : SHARE_A ? 1 : 0;
+    constexpr int kAhead = PIPE == kPipeWide || JIT_A ? 2 : SHARE_A ? 1 : 0;
     typename B::Raw raw[2][NS][NB];
     float dl[2][NS][NB];
     AF af[kAhead + 1][MT];
@@ -856,7 +871,7 @@ moe_gemm_kernel(MoeGemmArgs args) {
     }
   };
 
-  if constexpr (PIPE == kPipeWide) {
+  if constexpr (PIPE == kPipeWide || JIT_A) {
     for (int kc = 0; kc < nchunk; ++kc) {
       const int gbase = kc * KS;
       // The chunk's group sums and its first group's activations are
@@ -1076,7 +1091,7 @@ moe_gemm_kernel(MoeGemmArgs args) {
       }
   }
 
-  if constexpr (PIPE != kPipeDouble) finish(n0);
+  if constexpr (PIPE != kPipeDouble || JIT_A) finish(n0);
 }
 
 // ------------------------------------------------ one token: down + combine
@@ -1727,7 +1742,7 @@ static hipError_t launch_gemm_t(const MoeGemmArgs& a_in, int max_chunks, hipStre
   // most 4 chunks), so that their prologue is paid once for both (measured
   // on Qwen3Next B=256: one, two and four tiles within 2% of each other,
   // two ahead)
-  a.tiles_per_wg = PIPE == kPipeDouble && nchunk <= 4 ? 2 : 1;
+  a.tiles_per_wg = PIPE == kPipeDouble && nchunk <= 4 && !gemm_jit_a<TYPE, EPI, PIPE>() ? 2 : 1;
   a.row_tiles = (tiles + a.tiles_per_wg - 1) / a.tiles_per_wg;
   // batch pipelines: the XCD-grouped 1-D grid (chunks padded to a multiple of 8)
   const dim3 grid = PIPE == kPipeDecode ? dim3(max_chunks, tiles)
