@@ -37,16 +37,24 @@
 //                other waves of the SIMD, the MFMA work per chunk is long.
 //                The chunk's group sums and first group's activations load
 //                with its rows, later groups' activations two groups ahead.
-//   kPipeDouble  1 token tile: 4 waves x 32 rows, two LDS stages per wave;
-//                chunk kc + 1 (rows by DMA, activations and group sums into
-//                registers) loads while chunk kc computes; with at most four
-//                chunks in K a workgroup takes two row tiles in a row.
+//   kPipeDouble  1 token tile: 4 waves x 32 rows (16 + 16 for gate and
+//                up), in one of three forms chosen by what fits:
+//                16-byte fragments whose rows fit 53 KB with the chunk's
+//                activations: those shared through LDS (a quarter loaded by
+//                each wave), one row stage per wave, three workgroups per
+//                CU; otherwise, when one row stage fits 53 KB, the wide
+//                loop above with one row stage; else two LDS stages per
+//                wave, chunk kc + 1 (rows by DMA, activations and group sums
+//                into registers) loading while chunk kc computes, and with
+//                at most four chunks in K two row tiles per workgroup.
 // In every pipeline the LDS words of group j + 1 are read while group j
 // decodes and multiplies, and rows sit an odd number of 16-byte pieces apart
 // in LDS so that the 16 rows of one read fall in different bank quads.
 //   moe_group_kernel  4 token tiles (chunks of up to 64 pairs), 32-weight
 //                block types only: the chunk's activations staged once per
-//                workgroup by DMA and shared by its four waves (see below).
+//                workgroup by DMA and shared by its four waves, every DMA
+//                instruction reading whole 16-byte runs of a few rows (see
+//                below).
 //   kPipeDecode  one token: 4 waves share 32 rows and split K (wave w takes
 //                chunks w, w + 4, ...), each through a ring of up to 8 LDS
 //                stages of rows, the token's activations and group sums,
