@@ -374,7 +374,7 @@ def main():
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported "
-              f"(this build has no multi-GPU path)", file=sys.stderr)
+              f"(the library runs on one GPU; sharding across GPUs is not implemented)", file=sys.stderr)
         return 2
     torch = _torch()
     if native.lib().llambda_hip_probe() != 1:
