@@ -261,6 +261,8 @@ struct GemmB<kQ4_K> {
   static constexpr int kSpan = 144, kPieces = 9, kPitch = odd_pitch(kPieces), kSteps = 8,
                        kStepK = 32;
   static constexpr bool kWide = true;
+  // c = kCd * delta (0: c also carries the block minimum)
+  static constexpr float kCd = 0.f;
   typedef bf16x8 Frag;
   typedef uint2 Raw;
   static __device__ __forceinline__ Raw fetch(const uint8_t* row, uint32_t, int j, int g) {
@@ -301,6 +303,7 @@ struct GemmB<kQ6_K> {
   static constexpr int kSpan = 210, kPieces = 14, kPitch = odd_pitch(kPieces), kSteps = 16,
                        kStepK = 16;
   static constexpr bool kWide = false;
+  static constexpr float kCd = 160.f;
   typedef shortx4 Frag;
   typedef u32x4 Raw;
   static __device__ __forceinline__ Raw fetch(const uint8_t* row, uint32_t, int u, int g) {
@@ -337,6 +340,7 @@ struct GemmB<kQ5_0> {
   static constexpr int kSpan = 176, kPieces = 12, kPitch = odd_pitch(kPieces), kSteps = 8,
                        kStepK = 32;
   static constexpr bool kWide = true;
+  static constexpr float kCd = 144.f;
   typedef bf16x8 Frag;
   typedef u32x4 Raw;  // three words from the qs bytes' dword, the qh byte's word
   static __device__ __forceinline__ Raw fetch(const uint8_t* row, uint32_t sh, int j, int g) {
@@ -370,6 +374,7 @@ struct GemmB<kQ8_0> {
   static constexpr int kSpan = 272, kPieces = 18, kPitch = odd_pitch(kPieces), kSteps = 8,
                        kStepK = 32;
   static constexpr bool kWide = true;
+  static constexpr float kCd = 128.f;
   typedef bf16x8 Frag;
   static __device__ __forceinline__ uint32_t pack2(uint32_t u, int k) {
     const float f0 = (float)((u >> (8 * k)) & 0xFFu), f1 = (float)((u >> (8 * k + 8)) & 0xFFu);
@@ -458,7 +463,8 @@ struct GemmShape {
   static constexpr int LOADS = (PIECES + 63) / 64;                  // per matrix
   static constexpr int MATBUF = 1024 * LOADS;                       // one matrix's rows
   static constexpr int ROWBUF = MATBUF * NB;                        // rows of one chunk
-  static constexpr int TABLE = NS * NB * B::kSteps * 16 * 8;        // (delta, -c) per group and row
+  // (delta, -c) per group and row; delta alone where c = kCd * delta
+  static constexpr int TABLE = NS * NB * B::kSteps * 16 * (B::kCd != 0.f ? 4 : 8);
   static constexpr int A_OFF = ROWBUF;                              // decode: the token's chunk
   static constexpr int S_OFF = ROWBUF + 1024;                       // decode: its 16 group sums
   static constexpr int STAGE = PIPE == kPipeDecode ? ROWBUF + 1024 + 256 : ROWBUF;
@@ -621,7 +627,8 @@ moe_gemm_kernel(MoeGemmArgs args) {
   if (SHARE_A ? n0 - wave * Sh::ROWS >= a.N : n0 >= a.N) return;  // uniform (decode, SHARE_A)
   const int depth = PIPE == kPipeDecode ? a.depth : SHARE_A || JIT_A ? 1 : Sh::DEPTH;
   uint8_t* wlds = lds + Sh::RED + wave * (depth * Sh::STAGE + Sh::TABLE);
-  float2* table = reinterpret_cast<float2*>(wlds + depth * Sh::STAGE);
+  using TableEntry = std::conditional_t<B::kCd != 0.f, float, float2>;
+  TableEntry* table = reinterpret_cast<TableEntry*>(wlds + depth * Sh::STAGE);
   const uint32_t wlds_addr = lds_address(wlds);
 
   // split rows of this lane's tokens (tile row t = n of each token tile)
@@ -728,7 +735,8 @@ moe_gemm_kernel(MoeGemmArgs args) {
           float delta, c;
           B::scale(row, sh[m], j, delta, c);
           const bool ok = j < valid;
-          table[((m * NB + nb) * KS + j) * 16 + n] = float2{ok ? delta : 0.f, ok ? -c : 0.f};
+          if constexpr (B::kCd != 0.f) table[((m * NB + nb) * KS + j) * 16 + n] = ok ? delta : 0.f;
+          else table[((m * NB + nb) * KS + j) * 16 + n] = float2{ok ? delta : 0.f, ok ? -c : 0.f};
         }
       }
     // Software pipeline over the groups: the LDS words (codes and delta) of
@@ -746,7 +754,8 @@ moe_gemm_kernel(MoeGemmArgs args) {
         for (int nb = 0; nb < NB; ++nb) {
           const uint8_t* row = stage + nb * Sh::MATBUF + (16 * m + n) * B::kPitch;
           r[m][nb] = B::fetch(row, sh[m], j, g);
-          d[m][nb] = table[((m * NB + nb) * KS + j) * 16 + n].x;
+          if constexpr (B::kCd != 0.f) d[m][nb] = table[((m * NB + nb) * KS + j) * 16 + n];
+          else d[m][nb] = table[((m * NB + nb) * KS + j) * 16 + n].x;
         }
     };
 #pragma unroll
@@ -796,7 +805,13 @@ moe_gemm_kernel(MoeGemmArgs args) {
 #pragma unroll
       for (int m = 0; m < NS; ++m)
 #pragma unroll
-        for (int nb = 0; nb < NB; ++nb) cb[m][nb] = table[((m * NB + nb) * KS + 4 * q + g) * 16 + n].y;
+        for (int nb = 0; nb < NB; ++nb) {
+          // -c as the table held it: -(kCd * delta), 0 for a group past K
+          if constexpr (B::kCd != 0.f)
+            cb[m][nb] = 4 * q + g < valid ? -(B::kCd * table[((m * NB + nb) * KS + 4 * q + g) * 16 + n])
+                                          : 0.f;
+          else cb[m][nb] = table[((m * NB + nb) * KS + 4 * q + g) * 16 + n].y;
+        }
 #pragma unroll
       for (int i = 0; i < MT; ++i) {
         const float sv = get_s(i, q);
