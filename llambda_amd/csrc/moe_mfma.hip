@@ -496,8 +496,8 @@ constexpr bool gemm_share_a() {
 // share the activations beside them): when one row stage per wave and the
 // scale tables fit 53 KB, it runs the wide pipeline's loop -- one stage,
 // each group's activations loaded two groups ahead -- so that no wave holds
-// a whole chunk's activations (current and next) in registers and three
-// workgroups share a CU.
+// a whole chunk's activations (current and next) in registers and three or
+// four workgroups share a CU (Q6_K: 112 registers, 40 KB).
 template <int TYPE, int EPI, int PIPE>
 constexpr bool gemm_jit_a() {
   using Sh = GemmShape<TYPE, EPI, PIPE>;
