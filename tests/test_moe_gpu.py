@@ -257,6 +257,26 @@ def test_small_qwen_shapes(hip):
     check_layer(layer, x, "qwen small")
 
 
+def test_double_pipeline_shared_activations_ragged(hip):
+    """Batches of at most 16 pairs per expert on 32-weight blocks: the
+    gate|up products (Q5_0, 16-byte fragments) share the chunk's activations
+    through LDS, the down products (Q8_0) run the one-stage loop.  ffn 224:
+    the gate|up rows end inside a workgroup (two of its waves have none) and
+    the down K ends inside a chunk.  Against the oracle, and bit for bit
+    against a batch of 5."""
+    rng = np.random.default_rng(44)
+    layer = synthetic_qwen3next(rng, hidden=512, experts=16, top_k=4, ffn=224, shared_ffn=224,
+                                gate_type=ggml.Q5_0, down_type=ggml.Q8_0)
+    x = synthetic.activations(rng, 24, layer.hidden)
+    assert 24 * layer.top_k / layer.expert_count <= 16
+    y, _ = check_layer(layer, x, "double pipeline, shared activations")
+    session = HipMoeSession(layer)
+    try:
+        np.testing.assert_array_equal(session.run(x[3:8]), y[3:8])
+    finally:
+        session.close()
+
+
 def test_router_expert_groups_ragged(hip):
     """300 tokens (19 token tiles, the last partial) take the router launch
     with eight expert tiles per workgroup; 40 experts + the shared gate row
