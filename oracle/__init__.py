@@ -59,6 +59,9 @@ class MoeDesc(ctypes.Structure):
         ("shared_gate_type", ctypes.c_int), ("shared_gate", ctypes.c_void_p),
         ("shared_up_type", ctypes.c_int), ("shared_up", ctypes.c_void_p),
         ("shared_down_type", ctypes.c_int), ("shared_down", ctypes.c_void_p),
+        ("latent", ctypes.c_int64),
+        ("latent_down_type", ctypes.c_int), ("latent_down", ctypes.c_void_p),
+        ("latent_up_type", ctypes.c_int), ("latent_up", ctypes.c_void_p),
     ]
 
 
@@ -275,6 +278,15 @@ def moe_forward(layer, x: np.ndarray, threads: int = 1) -> MoeResult:
         else:
             setattr(d, name + "_type", pair[0])
             setattr(d, field, arr(pair[1], np.uint8))
+    latent_down = getattr(layer, "latent_down", None)
+    latent_up = getattr(layer, "latent_up", None)
+    if latent_down is not None:
+        d.latent = np.asarray(latent_down[1]).size // row_bytes(latent_down[0], layer.hidden)
+        d.latent_down_type = latent_down[0]
+        d.latent_down = arr(latent_down[1], np.uint8)
+    if latent_up is not None:
+        d.latent_up_type = latent_up[0]
+        d.latent_up = arr(latent_up[1], np.uint8)
     y = np.empty_like(x)
     idx = np.empty((tokens, layer.top_k), dtype=np.int64)
     w = np.empty((tokens, layer.top_k), dtype=np.float32)

@@ -24,6 +24,9 @@
  *   select_top_k         stable descending sort with NaN excluded
  *   sigmoid/silu/relu2   float64 closed forms
  *   MoE layers           float64 restatement from dequantised weights
+ *   Nemotron latent      float64 restatement with ffn_latent_down/up; identity
+ *                        down and permutation up equal the latent-free layer
+ *                        permuted, bit for bit
  *                        (independent of the fused kernels)
  *   rms_norm, silu,      reference KATs tests.lisp:298-345 (rms-norm of
  *   rope, softmax        (3 4) by (1 2), silu 2, rotation by cos/sin 1,
@@ -120,6 +123,13 @@ typedef struct oracle_moe_desc {
   int shared_gate_type; const uint8_t* shared_gate; /* [Fs][H], qwen3next */
   int shared_up_type;   const uint8_t* shared_up;   /* [Fs][H] */
   int shared_down_type; const uint8_t* shared_down; /* [H][Fs] */
+  /* nemotron only, optional (llambda.lisp:5845-5864): ffn_latent_down [Lt][H]
+   * and ffn_latent_up [H][Lt]; with them the routed experts run on the
+   * latent vector (up_exps [E*F][Lt], down_exps [E*Lt][F]).  latent = 0 when
+   * the layer has none. */
+  int64_t latent;               /* Lt */
+  int latent_down_type; const uint8_t* latent_down;
+  int latent_up_type;   const uint8_t* latent_up;
 } oracle_moe_desc;
 
 /* llambda.lisp:5321-5426 (qwen3next-moe-into) and 5827-5949

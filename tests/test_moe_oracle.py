@@ -3,6 +3,8 @@ independent float64 evaluation built from the dequantised weights, the
 closed-form routing (stable descending sort) and the gating formulas.  The
 reference's own suite has no test of either MoE function, so these are the
 pins.  CPU only."""
+import dataclasses
+
 import numpy as np
 import pytest
 
@@ -125,3 +127,84 @@ def test_combine_order_is_rank_order():
         d = oracle.gemv(layer.down[0], layer.down[1][e * H * rb_down:], H, F, h.astype(np.float32))
         dest = (dest + (ref.top_weights[0, r] * d).astype(np.float32)).astype(np.float32)
     assert np.array_equal(dest, ref.y[0])
+
+
+def nemotron_with_latent(rng, hidden, latent, latent_type, **kw):
+    """A Nemotron-H layer whose routed experts run on a `latent`-wide vector:
+    router and shared expert from an H-wide layer, experts from an Lt-wide one,
+    ffn_latent_down [Lt][H] and ffn_latent_up [H][Lt] of `latent_type`."""
+    outer = synthetic_nemotron_h(rng, hidden=hidden, **kw)
+    inner = synthetic_nemotron_h(rng, hidden=latent, **kw)
+    return dataclasses.replace(
+        outer, up=inner.up, down=inner.down,
+        latent_down=(latent_type, synthetic.packed(latent_type, rng, latent, hidden)),
+        latent_up=(latent_type, synthetic.packed(latent_type, rng, hidden, latent)))
+
+
+def float64_latent_layer(layer, x, latent):
+    """nemotron-h-moe-ffn-into with ffn_latent_down/up (llambda.lisp:5845-5864,
+    5883-5887, 5933-5938) in float64 from the dequantised weights."""
+    H, E, K, F, Fs = (layer.hidden, layer.expert_count, layer.top_k, layer.expert_ffn,
+                      layer.shared_ffn)
+    up = dq(layer.up, E * F, latent).reshape(E, F, latent)
+    down = dq(layer.down, E * latent, F).reshape(E, latent, F)
+    ld = dq(layer.latent_down, latent, H)
+    lu = dq(layer.latent_up, H, latent)
+    ys = []
+    for xt in x.astype(np.float64):
+        logits = layer.router.astype(np.float64) @ xt + layer.router_bias
+        order = sorted(range(E), key=lambda e: (-logits[e], e))[:K]
+        w = sig(logits[order])
+        if layer.expert_weights_norm:
+            w = w / w.sum()
+        w = w * layer.expert_weights_scale
+        ein = ld @ xt
+        m = np.zeros(latent)
+        for r, e in enumerate(order):
+            m += w[r] * (down[e] @ (np.maximum(up[e] @ ein, 0.0) ** 2))
+        y = lu @ m
+        if Fs:
+            y += dq(layer.shared_down, H, Fs) @ (np.maximum(dq(layer.shared_up, Fs, H) @ xt, 0.0) ** 2)
+        ys.append(y)
+    return np.array(ys)
+
+
+@pytest.mark.parametrize("latent_type", [ggml.Q8_0, ggml.F32])
+def test_nemotron_latent_oracle_vs_float64(latent_type):
+    rng = np.random.default_rng(11)
+    layer = nemotron_with_latent(rng, 256, 128, latent_type, experts=16, top_k=3, ffn=96,
+                                 shared_ffn=64, router_std=0.1)
+    x = synthetic.activations(rng, 4, layer.hidden)
+    ref = oracle.moe_forward(layer, x, threads=2)
+    y64 = float64_latent_layer(layer, x, 128)
+    assert np.all(np.abs(ref.y - y64) <= 1e-5 * scale_of(y64))
+
+
+def test_nemotron_latent_permutation_is_exact():
+    """ffn_latent_down = I and ffn_latent_up = a permutation P (F32, Lt = H): the
+    layer's output is the latent-free layer's output with its entries taken in
+    P's order, bit for bit.  A transposed or misplaced latent product fails it."""
+    rng = np.random.default_rng(12)
+    H = 128
+    base = synthetic_nemotron_h(rng, hidden=H, experts=8, top_k=2, ffn=64, shared_ffn=0,
+                                router_std=0.1)
+    pi = rng.permutation(H)
+    assert np.any(pi[pi] != np.arange(H))  # not an involution: P and P^T differ
+    perm = np.zeros((H, H), np.float32)
+    perm[np.arange(H), pi] = 1.0
+    eye = np.eye(H, dtype=np.float32)
+    lat = dataclasses.replace(base, latent_down=(ggml.F32, eye.view(np.uint8).ravel()),
+                              latent_up=(ggml.F32, perm.view(np.uint8).ravel()))
+    x = synthetic.activations(rng, 3, H)
+    want = oracle.moe_forward(base, x).y
+    got = oracle.moe_forward(lat, x).y
+    assert np.array_equal(got, want[:, pi])
+
+
+def test_latent_needs_both_tensors():
+    rng = np.random.default_rng(13)
+    layer = synthetic_nemotron_h(rng, hidden=64, experts=4, top_k=2, ffn=32, shared_ffn=0)
+    half = dataclasses.replace(layer, latent_down=(ggml.F32, np.eye(64, dtype=np.float32)
+                                                   .view(np.uint8).ravel()))
+    with pytest.raises(Exception, match="latent projections"):
+        oracle.moe_forward(half, synthetic.activations(rng, 1, 64))
