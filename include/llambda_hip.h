@@ -8,6 +8,12 @@
  *   - status ints: 0 = success, -1 = failure with llambda_hip_last_error()
  *     describing it (thread-local; cleared on entry of every call that can
  *     fail); C++ exceptions never cross the boundary;
+ *   - status -2 (MoE runs only, LLAMBDA_HIP_INPUT_ERROR): the reference's
+ *     own error for this input, last_error holding its text; the session
+ *     is healthy and the next call runs normally.  The adapter signals a
+ *     plain error for it, not the backend's condition, so the runtime
+ *     fallback re-signals it without disabling the layer, as the
+ *     reference's CPU body would for that call alone;
  *   - sessions are opaque, owned by the caller, destroyed with a null-safe
  *     destroy; element-count getters return 0 for null;
  *   - a run is synchronous on host pointers: input copied to the device, the
@@ -30,6 +36,8 @@
 #ifdef __cplusplus
 extern "C" {
 #endif
+
+#define LLAMBDA_HIP_INPUT_ERROR (-2)
 
 typedef struct llambda_hip_session llambda_hip_session;
 typedef struct llambda_hip_moe_session llambda_hip_moe_session;
@@ -183,9 +191,11 @@ size_t llambda_hip_moe_session_expert_count(const llambda_hip_moe_session* sessi
  * input[batch][H], token by token as the reference computes it.  Synchronous.
  * top_indices / top_weights (optional, [batch][k]) receive the selected
  * experts in rank order and their final weights; router_logits (optional,
- * [batch][E]) the router logits (after the bias for nemotron).  Returns -1
- * with the reference's error text when it would have signalled one
- * (non-positive weight sum, fewer than k finite logits). */
+ * [batch][E]) the router logits (after the bias for nemotron).  Returns
+ * LLAMBDA_HIP_INPUT_ERROR (-2) with the reference's error text when it would
+ * have signalled one for this input (non-positive weight sum,
+ * llambda.lisp:5373-5375 and 5903-5905; fewer than k selectable logits);
+ * output then holds no result.  -1 for every other failure. */
 int llambda_hip_moe_session_run(llambda_hip_moe_session* session, const float* input,
                                 size_t input_element_count, float* output,
                                 size_t output_element_count, size_t batch,
@@ -199,7 +209,8 @@ int llambda_hip_moe_session_run_device(llambda_hip_moe_session* session, const f
                                        float* output, size_t batch, void* stream);
 
 /* Wait for `stream` (null = the session's stream) and report any error flag
- * raised by the kernels since the last check. */
+ * raised by the kernels since the last check (LLAMBDA_HIP_INPUT_ERROR, as
+ * llambda_hip_moe_session_run). */
 int llambda_hip_moe_session_sync(llambda_hip_moe_session* session, void* stream);
 
 /* The device-resident run above with no allocation of any kind (no hipMalloc,
@@ -212,9 +223,13 @@ int llambda_hip_moe_session_sync(llambda_hip_moe_session* session, void* stream)
  * more (the layer's per-token scratch times `batch`; e.g. Qwen3Next-shaped
  * layers up to 251 tokens, Nemotron-H-shaped ones up to 166) is
  * refused with an error, before anything is enqueued.  Every call on a GPU
- * shares that GPU's array: calls that overlap on one GPU (on different
- * streams, or from different sessions) race.  Errors raised by the kernels
- * reach the session's flag and are reported by llambda_hip_moe_session_sync. */
+ * shares that GPU's array, which keeps the last call's contents, so the calls
+ * are ordered on the device: each call's stream first waits for the previous
+ * call's last launch (an event recorded on its stream), whatever stream or
+ * session it came from.  Under stream capture no wait or record is made:
+ * the graph orders its own calls, and replays of graphs holding such calls
+ * must not overlap on one GPU.  Errors raised by the kernels reach the
+ * session's flag and are reported by llambda_hip_moe_session_sync. */
 int llambda_hip_moe_session_run_device_noalloc(llambda_hip_moe_session* session,
                                                const float* input, float* output, size_t batch,
                                                void* stream);

@@ -39,6 +39,12 @@ struct Failure : std::runtime_error {
   using std::runtime_error::runtime_error;
 };
 
+// The reference's own error for this input (the MoE functions' `error`
+// calls): the call fails with status -2 and the session stays usable.
+struct InputError : Failure {
+  using Failure::Failure;
+};
+
 [[noreturn]] void failf(const char* fmt, ...) {
   char buf[1024];
   va_list ap;
@@ -59,6 +65,9 @@ int guarded(F&& f) {
   try {
     f();
     return 0;
+  } catch (const InputError& e) {
+    g_last_error = e.what();
+    return -2;
   } catch (const std::exception& e) {
     g_last_error = e.what();
   } catch (...) {
@@ -552,13 +561,22 @@ struct llambda_hip_moe_session {
   }
 };
 
-static void raise_moe_error(int flag, int variant) {
+// The kernels' error word: bit 1 = a non-positive top-k weight sum
+// (llambda.lisp:5373-5375, 5903-5905), bit 0 = fewer than k selectable
+// logits, where the reference's expert lookup fails on index -1.  Both are
+// the reference's own errors for the input, so they take status -2.
+[[noreturn]] static void raise_moe_error(int flag, int variant) {
   const char* layer = variant == kQwen3Next ? "Qwen3Next" : "Nemotron-H MoE";
-  if (flag & 2) failf("%s layer router produced non-positive top-k weight sum.", layer);
-  if (flag & 1)
-    failf("%s layer router produced fewer than top-k selectable logits (Expert index -1 is out of range).",
-          layer);
-  failf("%s layer failed (error flags %d)", layer, flag);
+  char buf[256];
+  if (flag & 2)
+    snprintf(buf, sizeof buf, "%s layer router produced non-positive top-k weight sum.", layer);
+  else if (flag & 1)
+    snprintf(buf, sizeof buf,
+             "%s layer router produced fewer than top-k selectable logits (Expert index -1 is out of range).",
+             layer);
+  else
+    failf("%s layer failed (error flags %d)", layer, flag);
+  throw InputError(buf);
 }
 
 extern "C" {
@@ -794,12 +812,18 @@ static __device__ __align__(256) uint8_t scratch[kMoeNoallocScratchBytes];
 namespace {
 
 constexpr int kMaxScratchDevices = 64;
+// g_scratch_mutex is held across a whole call (wait, launches, record), so
+// the calls' order on the device is the order they took the mutex.
 std::mutex g_scratch_mutex;
 uint8_t* g_scratch[kMaxScratchDevices];
+// Recorded after each call's last launch on its stream; the next call's
+// stream waits for it first, so calls on one GPU never overlap on the device
+// whatever stream or session they come from.
+hipEvent_t g_scratch_done[kMaxScratchDevices];
 
-// The device address of `scratch` on `device`, which must be current.
+// Set-up, once per device (current): the device address of `scratch` and
+// the ordering event.  The caller holds g_scratch_mutex.
 uint8_t* noalloc_scratch(int device) {
-  std::lock_guard<std::mutex> lock(g_scratch_mutex);
   if (device < 0 || device >= kMaxScratchDevices)
     failf("moe_session_run_device_noalloc: device %d beyond the %d tracked", device,
           kMaxScratchDevices);
@@ -807,6 +831,8 @@ uint8_t* noalloc_scratch(int device) {
     void* ptr = nullptr;
     HIPC(hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)));
     if (!ptr) failf("moe_session_run_device_noalloc: no device address for the scratch array");
+    if (!g_scratch_done[device])
+      HIPC(hipEventCreateWithFlags(&g_scratch_done[device], hipEventDisableTiming));
     g_scratch[device] = static_cast<uint8_t*>(ptr);
   }
   return g_scratch[device];
@@ -868,9 +894,17 @@ int llambda_hip_moe_session_run_device_noalloc(llambda_hip_moe_session* s, const
             "the no-allocation entry point holds %zu (run fewer tokens per call, or use "
             "llambda_hip_moe_session_run_device)",
             batch, need, kMoeNoallocScratchBytes);
+    std::lock_guard<std::mutex> order(g_scratch_mutex);
     uint8_t* base = noalloc_scratch(s->device);
     carve_moe_scratch(p, T, base, kMoeNoallocScratchBytes);
     const hipStream_t st = stream ? static_cast<hipStream_t>(stream) : s->stream;
+    // Outside stream capture, wait for the previous call's last launch.  A
+    // captured call is ordered by the graph it joins: replays of graphs that
+    // hold such calls must not overlap on one GPU.
+    hipStreamCaptureStatus capture = hipStreamCaptureStatusNone;
+    HIPC(hipStreamIsCapturing(st, &capture));
+    const bool ordered = capture == hipStreamCaptureStatusNone;
+    if (ordered) HIPC(hipStreamWaitEvent(st, g_scratch_done[s->device], 0));
     // the error flag must start at zero (the array keeps the last call's
     // contents); a fill kernel, not a memset, so that a captured graph
     // replays it faithfully
@@ -878,6 +912,7 @@ int llambda_hip_moe_session_run_device_noalloc(llambda_hip_moe_session* s, const
     HIPC(moe_forward_launch(p, input, output, T, st));
     // errors reach the session's own flag, reported by moe_session_sync
     HIPC(moe_error_merge_launch(p.error, s->plan.error, st));
+    if (ordered) HIPC(hipEventRecord(g_scratch_done[s->device], st));
   });
 }
 

@@ -48,6 +48,7 @@ class MoeLayer:
     shared_down: Optional[Packed] = None      # [H][Fs]       ffn_down_shexp
     latent_down: Optional[Packed] = None      # [Lt][H]       ffn_latent_down (nemotron)
     latent_up: Optional[Packed] = None        # [H][Lt]       ffn_latent_up (nemotron)
+    layer_index: Optional[int] = None         # blk.N, for the reference's error texts
 
     def weight_bytes(self) -> int:
         """Packed bytes of every tensor the layer can read."""
@@ -87,6 +88,25 @@ class MoeLayer:
         if self.shared_gate_inp is not None:
             n += self.shared_gate_inp.nbytes
         return n
+
+
+class MoeLayerInputError(RuntimeError):
+    """The reference's own error for a token (status -2 from the library):
+    a non-positive top-k weight sum (llambda.lisp:5373-5375, 5903-5905) or
+    fewer than k selectable router logits.  Deliberately not a
+    HipBackendError: the backend's error predicate does not select it, so
+    the runtime fallback re-signals it and the layer stays on the device,
+    as the reference's CPU body signals it for that call alone."""
+
+
+def _check_moe(status: int, what: str, layer_index: Optional[int]) -> None:
+    if status == native.INPUT_ERROR:
+        text = native.last_error()
+        if layer_index is not None:
+            # the reference's texts name the layer: "<variant> layer N router ..."
+            text = text.replace(" layer router ", f" layer {layer_index} router ", 1)
+        raise MoeLayerInputError(text)
+    _check(status, what)
 
 
 class HipMoeSession:
@@ -156,9 +176,9 @@ class HipMoeSession:
         for a, what in ((dest, "destination"), (vector, "input")):
             if not (isinstance(a, np.ndarray) and a.dtype == np.float32 and a.flags.c_contiguous):
                 raise HipBackendError(f"HIP MoE {what} must be a contiguous float32 array.")
-        _check(native.lib().llambda_hip_moe_session_run(
+        _check_moe(native.lib().llambda_hip_moe_session_run(
             self._live(), vector.ctypes.data, vector.size, dest.ctypes.data, dest.size, 1,
-            None, None, None), "HIP MoE run")
+            None, None, None), "HIP MoE run", self.layer.layer_index)
         return dest
 
     def run(self, x: np.ndarray, with_routing: bool = False):
@@ -173,11 +193,12 @@ class HipMoeSession:
             idx = np.empty((tokens, L.top_k), dtype=np.int64)
             w = np.empty((tokens, L.top_k), dtype=np.float32)
             logits = np.empty((tokens, L.expert_count), dtype=np.float32)
-        _check(native.lib().llambda_hip_moe_session_run(
+        _check_moe(native.lib().llambda_hip_moe_session_run(
             self._live(), x.ctypes.data, x.size, y.ctypes.data, y.size, tokens,
             idx.ctypes.data if idx is not None else None,
             w.ctypes.data if w is not None else None,
-            logits.ctypes.data if logits is not None else None), "HIP MoE run")
+            logits.ctypes.data if logits is not None else None), "HIP MoE run",
+            self.layer.layer_index)
         return (y, idx, w, logits) if with_routing else y
 
     def run_device(self, x_ptr: int, y_ptr: int, tokens: int, stream: int = 0) -> None:
@@ -186,8 +207,8 @@ class HipMoeSession:
                "HIP MoE device run")
 
     def sync(self, stream: int = 0) -> None:
-        _check(native.lib().llambda_hip_moe_session_sync(self._live(), stream or None),
-               "HIP MoE sync")
+        _check_moe(native.lib().llambda_hip_moe_session_sync(self._live(), stream or None),
+                   "HIP MoE sync", self.layer.layer_index)
 
 
 def moe_layer_from_model(model, layer_index: int, variant: int, *, expert_used_count: int,
@@ -231,7 +252,8 @@ def moe_layer_from_model(model, layer_index: int, variant: int, *, expert_used_c
         shared_gate=packed("ffn_gate_shexp"), shared_up=packed("ffn_up_shexp"),
         shared_down=packed("ffn_down_shexp"),
         latent_down=packed("ffn_latent_down") if variant == NEMOTRON_H else None,
-        latent_up=packed("ffn_latent_up") if variant == NEMOTRON_H else None)
+        latent_up=packed("ffn_latent_up") if variant == NEMOTRON_H else None,
+        layer_index=layer_index)
 
 
 def select_top_k(logits: np.ndarray, k: int):

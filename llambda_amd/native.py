@@ -17,6 +17,10 @@ LIB_PATH = os.environ.get("LLAMBDA_HIP_LIBRARY", os.path.join(HERE, "libllambda_
 _lock = threading.Lock()
 _lib = None
 
+# LLAMBDA_HIP_INPUT_ERROR: a MoE run met the reference's own error for its
+# input; the session stays usable
+INPUT_ERROR = -2
+
 c_int = ctypes.c_int
 c_size = ctypes.c_size_t
 c_i64 = ctypes.c_int64

@@ -366,6 +366,46 @@ def test_moe_hook_priority_fallback_and_its_own_table():
         acc.unregister_accelerator_backend("fake-mnpu")
 
 
+def test_moe_hook_reraises_a_reference_input_error_and_keeps_the_layer():
+    """An error that is not the backend's condition (the reference's own error
+    for a token, e.g. moe.MoeLayerInputError) is re-signalled by the runtime
+    fallback: no warning, nothing unregistered or closed, no CPU body, and
+    the next token runs on the same session (llambda.lisp:4660-4676)."""
+    from llambda_amd.moe import MoeLayerInputError
+    closed = []
+    state = {"bad": True}
+
+    def run(session, dest, vector):
+        if state["bad"]:
+            raise MoeLayerInputError("Qwen3Next layer 0 router produced non-positive top-k "
+                                     "weight sum.")
+        dest[:] = 5.0
+        return dest
+
+    b = make_fake_backend("fake-minput", 1, lambda d, s, v: d, lambda s: closed.append(s.name))
+    acc.register_accelerator_backend(b, replace=True)
+    try:
+        model = moe_model()
+        projection.register_model_accelerator_moe_layer(model, b, 0,
+                                                        FakeMoeSession("m0", 4, 3, run))
+        out = np.zeros(4, dtype=np.float32)
+        x = np.ones(4, dtype=np.float32)
+
+        def cpu_body():
+            raise AssertionError("the CPU body must not run")
+
+        with warnings.catch_warnings():
+            warnings.simplefilter("error")
+            with pytest.raises(MoeLayerInputError, match="non-positive top-k weight sum"):
+                projection.moe_layer_into(out, model, 0, x, cpu_body)
+        assert closed == [] and projection.model_accelerator_moe_layer(model, b, 0) is not None
+        state["bad"] = False
+        projection.moe_layer_into(out, model, 0, x, cpu_body)
+        assert out[0] == 5.0
+    finally:
+        acc.unregister_accelerator_backend("fake-minput")
+
+
 def test_moe_hook_registration_checks_the_router_shape():
     closed = []
     b = make_fake_backend("fake-mreg", 1, lambda d, s, v: d, lambda s: closed.append(s.name))

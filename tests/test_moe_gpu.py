@@ -18,8 +18,8 @@ import pytest
 import oracle
 from llambda_amd import ggml, synthetic
 from llambda_amd.hip_backend import HipBackendError
-from llambda_amd.moe import (NEMOTRON_H, QWEN3NEXT, HipMoeSession, select_top_k,
-                             synthetic_nemotron_h, synthetic_qwen3next)
+from llambda_amd.moe import (NEMOTRON_H, QWEN3NEXT, HipMoeSession, MoeLayerInputError,
+                             select_top_k, synthetic_nemotron_h, synthetic_qwen3next)
 
 from helpers import REL
 
@@ -407,11 +407,61 @@ def test_nan_input_reports_reference_error(hip):
     x = np.full((1, 256), np.nan, dtype=np.float32)
     session = HipMoeSession(layer)
     try:
-        with pytest.raises(HipBackendError, match="router"):
+        # the reference's own error (status -2), not the backend's condition.
+        # Every slot stays (-1, -FLT_MAX), each weight sigmoid(-FLT_MAX) = 0,
+        # and the weight-sum check comes before any expert is looked up
+        # (llambda.lisp:5364-5375)
+        with pytest.raises(MoeLayerInputError,
+                           match="Qwen3Next layer router produced non-positive top-k weight sum"
+                           ) as info:
             session.run(x)
+        assert not isinstance(info.value, HipBackendError)
         # the session stays usable after the error
         good = synthetic.activations(rng, 2, 256)
         assert np.isfinite(session.run(good)).all()
+    finally:
+        session.close()
+
+
+def test_nan_input_without_normalisation_reports_the_expert_lookup(hip):
+    """Nemotron-H without expert_weights_norm has no weight-sum check: a NaN
+    token reaches the expert lookup with index -1 (llambda.lisp:5898-5912)."""
+    rng = np.random.default_rng(13)
+    layer = synthetic_nemotron_h(rng, hidden=256, experts=16, top_k=2, ffn=64, shared_ffn=0,
+                                 expert_type=ggml.Q8_0, down_type=ggml.Q8_0, weights_norm=False)
+    session = HipMoeSession(layer)
+    try:
+        bad = synthetic.activations(rng, 5, 256)
+        bad[3] = np.nan
+        with pytest.raises(MoeLayerInputError, match="fewer than top-k selectable logits"):
+            session.run(bad)
+        good = bad[[0, 1, 2, 4]]
+        ref = oracle.moe_forward(layer, good)
+        y, idx, _, _ = session.run(good, with_routing=True)
+        assert np.array_equal(idx, ref.top_indices)
+    finally:
+        session.close()
+
+
+def test_non_positive_weight_sum_reports_reference_error(hip):
+    """Every biased router logit near -200: each top-k sigmoid rounds to 0 in
+    single precision, the normalised Nemotron-H gating finds a zero weight sum
+    and the reference signals its error (llambda.lisp:5903-5905)."""
+    rng = np.random.default_rng(12)
+    layer = synthetic_nemotron_h(rng, hidden=256, experts=16, top_k=2, ffn=64, shared_ffn=64,
+                                 expert_type=ggml.Q8_0, down_type=ggml.Q8_0, weights_norm=True)
+    layer.router_bias = np.full(16, -200.0, dtype=np.float32)
+    layer.layer_index = 7
+    x = synthetic.activations(rng, 3, 256)
+    with pytest.raises(RuntimeError, match="non-positive top-k weight sum"):
+        oracle.moe_forward(layer, x[:1])
+    session = HipMoeSession(layer)
+    try:
+        for batch in (x[:1], x):  # the single-token and the batch pipelines
+            with pytest.raises(MoeLayerInputError,
+                               match="Nemotron-H MoE layer 7 router produced non-positive "
+                                     "top-k weight sum"):
+                session.run(batch)
     finally:
         session.close()
 

@@ -14,8 +14,8 @@ import oracle
 from llambda_amd import accelerator as acc
 from llambda_amd import ggml, native, projection, synthetic
 from llambda_amd.hip_backend import PACKED_MAGIC, make_hip_session_packed, register_hip_backend
-from llambda_amd.moe import (NEMOTRON_H, QWEN3NEXT, HipMoeSession, moe_layer_from_model,
-                             synthetic_nemotron_h, synthetic_qwen3next)
+from llambda_amd.moe import (NEMOTRON_H, QWEN3NEXT, HipMoeSession, MoeLayerInputError,
+                             moe_layer_from_model, synthetic_nemotron_h, synthetic_qwen3next)
 
 from helpers import REL, abs_dot_bound, assert_within_bound
 from test_moe_gpu import _shared_weights, output_bounds
@@ -161,6 +161,43 @@ def test_moe_hook_on_the_device(hip_backend, variant):
         projection.moe_layer_into(dest, model, 0, longer, cpu_body_first)
     assert np.array_equal(dest, ref.y[0])
     assert not model.accelerator_moe_layers
+
+
+def test_moe_hook_input_error_keeps_the_layer_on_the_device(hip_backend):
+    """A token the reference itself rejects (NaN input: no selectable router
+    logit, so a zero top-k weight sum) raises the reference's error for that call
+    alone: no warning, the layer stays bound, and the next token runs on the
+    device, not on the CPU body (llambda.lisp:4660-4676 re-signals any
+    condition its backend's error predicate does not select)."""
+    rng = np.random.default_rng(45)
+    layer = synthetic_qwen3next(rng, hidden=512, experts=32, top_k=4, ffn=256, shared_ffn=256)
+    model = _moe_model(layer, index=3)
+
+    def make(m, i):
+        return HipMoeSession(moe_layer_from_model(m, i, QWEN3NEXT, expert_used_count=4))
+
+    assert projection.try_enable_model_accelerator_moe_layers(model, "hip", [3], make) is True
+    cpu_runs = []
+
+    def cpu_body():
+        cpu_runs.append(1)
+        raise AssertionError("the CPU body must not run")
+
+    dest = np.empty(layer.hidden, dtype=np.float32)
+    bad = np.full(layer.hidden, np.nan, dtype=np.float32)
+    with warnings.catch_warnings():
+        warnings.simplefilter("error")  # a warning would mean the layer was disabled
+        with pytest.raises(MoeLayerInputError,
+                           match=r"Qwen3Next layer 3 router produced non-positive top-k"):
+            projection.moe_layer_into(dest, model, 3, bad, cpu_body)
+    assert [p.backend.name for p in model.accelerator_moe_layers[3]] == ["hip"]
+    x = synthetic.activations(rng, 1, layer.hidden)
+    ref = oracle.moe_forward(layer, x)
+    S = output_bounds(layer, x, ref.top_indices, ref.top_weights, _shared_weights(layer, x))
+    projection.moe_layer_into(dest, model, 3, x[0], cpu_body)
+    assert cpu_runs == []
+    assert np.all(np.abs(dest.astype(np.float64) - ref.y[0]) <= REL * S[0])
+    projection.clear_model_accelerator_projections(model)
 
 
 def test_moe_hook_refuses_a_layer_it_cannot_run(hip_backend):
