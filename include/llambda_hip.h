@@ -160,14 +160,18 @@ typedef struct llambda_hip_moe_desc {
   const void* shared_up;
   int shared_down_type;       /* ffn_down_shexp [H][Fs] */
   const void* shared_down;
-  /* ffn_latent_down [Lt][H] and ffn_latent_up [H][Lt] (nemotron, optional,
-   * llambda.lisp:5845-5864, 5883-5887, 5933-5938): the routed experts' input
-   * and output pass through them.  Not supported: a layer that has them is
-   * refused at creation, and the host runs its CPU body. */
+  /* ffn_latent_down [Li][H] and ffn_latent_up [H][Lo] (nemotron, each
+   * optional, llambda.lisp:5845-5864, 5883-5887, 5933-5938).  With
+   * ffn_latent_down the routed experts' input is ffn_latent_down * x, Li
+   * wide (ffn_up_exps [E*F][Li]); with ffn_latent_up their weighted sum is
+   * Lo wide (ffn_down_exps [E*Lo][F]) and ffn_latent_up maps it back to H
+   * before the shared expert is added.  Types: F32, Q4_K, Q6_K, Q5_0, Q8_0. */
   int latent_down_type;
   const void* latent_down;
   int latent_up_type;
   const void* latent_up;
+  int64_t latent_in;          /* Li: rows of ffn_latent_down; 0 = none */
+  int64_t latent_out;         /* Lo: columns of ffn_latent_up; 0 = none */
 } llambda_hip_moe_desc;
 
 /* Upload one layer.  No counterpart in the reference's bridge (its routed

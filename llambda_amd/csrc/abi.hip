@@ -463,7 +463,7 @@ int llambda_hip_session_dequantize(llambda_hip_session* s, float* output, size_t
 // the kernels index them.
 struct MoeScratchBytes {
   size_t logits, router_part, top_idx, top_w, shared_w, perm, chunks, down_out, xq, xsum, aq,
-      asum;
+      asum, lat, lq, lsum, lat_y;
 };
 
 static MoeScratchBytes moe_scratch_bytes(const MoePlan& p, size_t T) {
@@ -481,7 +481,7 @@ static MoeScratchBytes moe_scratch_bytes(const MoePlan& p, size_t T) {
   // grid, which is padded to a multiple of 8, before they compare its index
   // with the count)
   b.chunks = (size_t)(moe_max_chunks(p, (int64_t)T, 1) + 8) * sizeof(MoeChunk);
-  b.down_out = pairs * H * sizeof(float);
+  b.down_out = pairs * (size_t)p.out_w * sizeof(float);
   // the decode pipeline stages whole 256-element chunks (1 KB of split row)
   // of a row's last, partial chunk: 1 KB of readable slack
   b.xq = T * 2 * H * sizeof(uint16_t) + 1024;
@@ -490,6 +490,13 @@ static MoeScratchBytes moe_scratch_bytes(const MoePlan& p, size_t T) {
   b.xsum = T * (H / 16) * sizeof(float) + 256;
   b.aq = pairs * 2 * act_w * sizeof(uint16_t) + 1024;
   b.asum = pairs * (act_w / 16) * sizeof(float) + 256;
+  // latent layers: the experts' input (then their weighted sum), its split
+  // rows (the same slack as x's), the ffn_latent_up output
+  const size_t Li = (size_t)p.latent_in, Lo = (size_t)p.latent_out;
+  b.lat = T * std::max(Li, Lo) * sizeof(float);
+  b.lq = Li ? T * 2 * Li * sizeof(uint16_t) + 1024 : 0;
+  b.lsum = Li ? T * (Li / 16) * sizeof(float) + 256 : 0;
+  b.lat_y = Lo ? T * H * sizeof(float) : 0;
   return b;
 }
 
@@ -498,9 +505,9 @@ struct llambda_hip_moe_session {
   int device = 0;
   hipStream_t stream = nullptr;
   MoePlan plan{};
-  DevBuf router, bias, gate, up, down, sh_gate, sh_up, sh_down;
+  DevBuf router, bias, gate, up, down, sh_gate, sh_up, sh_down, lat_down, lat_up;
   DevBuf logits, router_part, top_idx, top_w, shared_w, perm, chunks, chunk_counts,
-      down_out, error, xq, xsum, aq, asum;
+      down_out, error, xq, xsum, aq, asum, lat, lq, lsum, lat_y;
   DevBuf x, y;     // device staging for the host-pointer runs
   HostBuf hx, hy;  // their pinned host side; hy is mapped, the error word after the rows
   int staged = 0;
@@ -525,6 +532,10 @@ struct llambda_hip_moe_session {
     xsum.alloc(b.xsum, "input group sums");
     aq.alloc(b.aq, "split activations");
     asum.alloc(b.asum, "activation group sums");
+    lat.alloc(b.lat, "latent vectors");
+    lq.alloc(b.lq, "split latent input");
+    lsum.alloc(b.lsum, "latent input group sums");
+    lat_y.alloc(b.lat_y, "ffn_latent_up output");
     p.capacity = tokens;
     p.router_part = router_part.as<float>();
     p.xq = xq.as<uint16_t>();
@@ -538,6 +549,10 @@ struct llambda_hip_moe_session {
     p.perm = perm.as<int>();
     p.chunks = chunks.as<MoeChunk>();
     p.down_out = down_out.as<float>();
+    p.lat = lat.as<float>();
+    p.lq = lq.as<uint16_t>();
+    p.lsum = lsum.as<float>();
+    p.lat_y = lat_y.as<float>();
   }
   void ensure_staging(int tokens) {
     if (tokens <= staged) return;
@@ -590,6 +605,9 @@ int llambda_hip_moe_session_create(const llambda_hip_moe_desc* d,
     if (d->variant != LLAMBDA_HIP_MOE_QWEN3NEXT && d->variant != LLAMBDA_HIP_MOE_NEMOTRON_H)
       failf("moe_session_create: unknown variant %d", d->variant);
     const bool qwen = d->variant == LLAMBDA_HIP_MOE_QWEN3NEXT;
+    const int64_t Li = d->latent_in, Lo = d->latent_out;
+    if ((d->latent_down || d->latent_up || Li || Lo) && qwen)
+      failf("moe_session_create: ffn_latent_down / ffn_latent_up belong to Nemotron-H layers");
     const int64_t H = d->hidden, E = d->expert_count, K = d->top_k, F = d->expert_ffn,
                   Fs = d->shared_ffn;
     if (H <= 0 || H % 32 || H > (1 << 16)) failf("moe_session_create: hidden %lld unsupported", (long long)H);
@@ -605,9 +623,13 @@ int llambda_hip_moe_session_create(const llambda_hip_moe_desc* d,
     if (qwen && d->gate_type != d->up_type)
       failf("moe_session_create: ffn_gate_exps and ffn_up_exps must share a type");
     if (!qwen && !d->router_bias) failf("moe_session_create: missing exp_probs_b.bias");
-    if (d->latent_down || d->latent_up)
-      failf("moe_session_create: layers with ffn_latent_down / ffn_latent_up are not supported "
-            "(the host runs the layer's CPU body)");
+    if ((Li != 0) != (d->latent_down != nullptr) || Li < 0 || Li % 32 || Li > (1 << 16))
+      failf("moe_session_create: ffn_latent_down needs its row count (latent_in %lld), a positive "
+            "multiple of 32 up to 65536", (long long)Li);
+    if ((Lo != 0) != (d->latent_up != nullptr) || Lo < 0 || Lo > (1 << 16))
+      failf("moe_session_create: ffn_latent_up needs its column count (latent_out %lld), "
+            "positive and up to 65536", (long long)Lo);
+    const int64_t din = Li ? Li : H, dout = Lo ? Lo : H;
     if (Fs > 0) {
       if (!d->shared_up || !d->shared_down) failf("moe_session_create: missing shared expert tensors");
       if (qwen && (!d->shared_gate || !d->shared_gate_inp))
@@ -620,12 +642,14 @@ int llambda_hip_moe_session_create(const llambda_hip_moe_desc* d,
     for (int t : types)
       if (t == kF32 || !supported_type(t))
         failf("moe_session_create: expert tensors must be Q4_K, Q6_K, Q5_0 or Q8_0 (got tag %d)", t);
-    const int64_t up_rb = checked_row_bytes(d->up_type, H, "ffn_up_exps");
+    const int64_t up_rb = checked_row_bytes(d->up_type, din, "ffn_up_exps");
     const int64_t down_rb = checked_row_bytes(d->down_type, F, "ffn_down_exps");
     // the expert kernels address one expert's slab with 32-bit offsets
     if (F * up_rb + (int64_t)kWeightPad >= ((int64_t)1 << 31) ||
-        H * down_rb + (int64_t)kWeightPad >= ((int64_t)1 << 31))
+        dout * down_rb + (int64_t)kWeightPad >= ((int64_t)1 << 31))
       failf("moe_session_create: one expert's slab exceeds 2 GiB");
+    const int64_t ld_rb = Li ? checked_row_bytes(d->latent_down_type, H, "ffn_latent_down") : 0;
+    const int64_t lu_rb = Lo ? checked_row_bytes(d->latent_up_type, Lo, "ffn_latent_up") : 0;
 
     auto* s = new llambda_hip_moe_session();
     try {
@@ -655,8 +679,8 @@ int llambda_hip_moe_session_create(const llambda_hip_moe_desc* d,
                             hipMemcpyHostToDevice, s->stream));
         p.bias = s->bias.as<float>();
       }
-      const int64_t up_blocks = E * F * (H / block_weights(d->up_type));
-      const int64_t down_blocks = E * H * (F / block_weights(d->down_type));
+      const int64_t up_blocks = E * F * (din / block_weights(d->up_type));
+      const int64_t down_blocks = E * dout * (F / block_weights(d->down_type));
       p.up_type = d->up_type;
       p.down_type = d->down_type;
       p.gate_type = qwen ? d->gate_type : d->up_type;
@@ -667,10 +691,25 @@ int llambda_hip_moe_session_create(const llambda_hip_moe_desc* d,
       }
       upload_weights(s->up, d->up_exps, (size_t)(E * F * up_rb), d->up_type, up_blocks, s->stream,
                      "ffn_up_exps");
-      upload_weights(s->down, d->down_exps, (size_t)(E * H * down_rb), d->down_type, down_blocks,
+      upload_weights(s->down, d->down_exps, (size_t)(E * dout * down_rb), d->down_type, down_blocks,
                      s->stream, "ffn_down_exps");
       p.up = s->up.as<uint8_t>();
       p.down = s->down.as<uint8_t>();
+      p.latent_in = (int)Li;
+      p.latent_out = (int)Lo;
+      p.out_w = (int)std::max(H, Lo);
+      if (Li) {
+        upload_weights(s->lat_down, d->latent_down, (size_t)(Li * ld_rb), d->latent_down_type,
+                       Li * (H / block_weights(d->latent_down_type)), s->stream, "ffn_latent_down");
+        p.lat_down_type = d->latent_down_type;
+        p.lat_down = s->lat_down.as<uint8_t>();
+      }
+      if (Lo) {
+        upload_weights(s->lat_up, d->latent_up, (size_t)(H * lu_rb), d->latent_up_type,
+                       H * (Lo / block_weights(d->latent_up_type)), s->stream, "ffn_latent_up");
+        p.lat_up_type = d->latent_up_type;
+        p.lat_up = s->lat_up.as<uint8_t>();
+      }
       if (Fs > 0) {
         const int64_t sh_up_rb = checked_row_bytes(d->shared_up_type, H, "ffn_up_shexp");
         const int64_t sh_down_rb = checked_row_bytes(d->shared_down_type, Fs, "ffn_down_shexp");
@@ -844,7 +883,7 @@ size_t carve_moe_scratch(MoePlan& p, int T, uint8_t* base, size_t limit) {
   const MoeScratchBytes b = moe_scratch_bytes(p, (size_t)T);
   const size_t sizes[] = {b.logits, b.router_part, b.top_idx, b.top_w, b.shared_w, b.perm,
                           b.chunks, b.down_out, b.xq, b.xsum, b.aq, b.asum, 2 * sizeof(int),
-                          sizeof(int)};
+                          sizeof(int), b.lat, b.lq, b.lsum, b.lat_y};
   constexpr int kBuffers = sizeof(sizes) / sizeof(sizes[0]);
   size_t off[kBuffers], total = 0;
   for (int i = 0; i < kBuffers; ++i) {
@@ -866,6 +905,10 @@ size_t carve_moe_scratch(MoePlan& p, int T, uint8_t* base, size_t limit) {
   p.asum = reinterpret_cast<float*>(base + off[11]);
   p.chunk_counts = reinterpret_cast<int*>(base + off[12]);
   p.error = reinterpret_cast<int*>(base + off[13]);
+  p.lat = reinterpret_cast<float*>(base + off[14]);
+  p.lq = reinterpret_cast<uint16_t*>(base + off[15]);
+  p.lsum = reinterpret_cast<float*>(base + off[16]);
+  p.lat_y = reinterpret_cast<float*>(base + off[17]);
   p.router_ks = router_slices(p.hidden);
   p.capacity = T;
   return total;

@@ -11,6 +11,10 @@
 //     activation fused (silu(g)*u, or relu(u)^2)
 //   5 grouped down: down rows against the chunk's activations, per pair
 //   6 combine in rank order, then the shared expert
+// A Nemotron-H layer with ffn_latent_down also runs that projection on x
+// and splits its output after 1 (the routed up products read it); with
+// ffn_latent_up, 6 forms the latent-wide weighted sum, then ffn_latent_up and
+// the shared expert's addition follow.
 #pragma once
 
 #include "gemv.h"
@@ -46,6 +50,15 @@ struct MoePlan {
   const uint8_t* sh_gate;  // [shared_ffn] rows of hidden (qwen3next)
   const uint8_t* sh_up;    // [shared_ffn] rows of hidden
   const uint8_t* sh_down;  // [hidden] rows of shared_ffn
+  // ffn_latent_down [latent_in] rows of hidden and ffn_latent_up [hidden]
+  // rows of latent_out (nemotron, each optional: 0 = absent).  The routed
+  // up rows are latent_in (else hidden) wide, the routed down rows number
+  // latent_out (else hidden).
+  int latent_in, latent_out;
+  int lat_down_type, lat_up_type;
+  const uint8_t* lat_down;
+  const uint8_t* lat_up;
+  int out_w;           // row stride of down_out: max(hidden, latent_out)
   // scratch, sized for `capacity` tokens
   int capacity;
   float* logits;       // [capacity][experts + 1]
@@ -62,7 +75,13 @@ struct MoePlan {
   float* xsum;         // [capacity][hidden/16]          16-group sums
   uint16_t* aq;        // [capacity * (top_k + 1)][2 act_width]  activations
   float* asum;         // [capacity * (top_k + 1)][act_width/16]
-  float* down_out;     // [capacity * (top_k + 1)][hidden]
+  float* down_out;     // [capacity * (top_k + 1)][out_w]
+  // latent layers only
+  float* lat;          // [capacity][latent_in], later [capacity][latent_out]:
+                       // the experts' input, then their weighted sum
+  uint16_t* lq;        // [capacity][2 latent_in]        its split rows
+  float* lsum;         // [capacity][latent_in/16]       and their sums
+  float* lat_y;        // [capacity][hidden]             ffn_latent_up output
   int* error;          // [1] nonzero after a run that hit a reference error
 };
 
@@ -125,6 +144,10 @@ int router_slices(int H);
 hipError_t router_mfma_launch(const float* x, int T, const float* R, int Er, int H, float* part,
                               int ld, uint16_t* q, int64_t q_stride, float* s, int64_t s_stride,
                               hipStream_t stream);
+// The split rows (format above router_mfma_launch's q, s) of T rows of K
+// fp32 elements, K % 32 == 0, rows x_stride floats apart.
+hipError_t split_rows_launch(const float* x, int T, int K, int64_t x_stride, uint16_t* q,
+                             int64_t q_stride, float* s, int64_t s_stride, hipStream_t stream);
 // mt: 0 = one token (K split over four wavefronts), 1 = chunks of up to 16
 // pairs (double-buffered), 2 = chunks of up to 32 pairs, 4 = chunks of up to
 // 64 pairs, activations shared by the workgroup (32-weight block types only:

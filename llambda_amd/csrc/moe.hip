@@ -163,19 +163,22 @@ __global__ void __launch_bounds__(kScanThreads) moe_scan_kernel(MoePlan p, int t
 // Weighted combine in rank order, then the shared expert, every product and
 // sum rounded separately as in vector-add-scaled-in-place /
 // vector-add-bias-in-place (llambda.lisp:3465-3489; 5359, 5409, 5426, 5914,
-// 5932, 5949).
+// 5932, 5949).  `width` outputs per token (hidden; latent_out where
+// ffn_latent_up follows, then without the shared expert, which
+// moe_latent_finish_kernel adds after it).
 __global__ void __launch_bounds__(256) moe_combine_kernel(MoePlan p, float* __restrict__ y,
-                                                          int tokens, int has_shared,
+                                                          int tokens, int width, int has_shared,
                                                           int* __restrict__ error_out) {
 #pragma clang fp contract(off)
   const int t = blockIdx.y;
   const int i = blockIdx.x * blockDim.x + threadIdx.x;
-  const int H = p.hidden, K = p.top_k;
+  const int K = p.top_k;
+  const int64_t ow = p.out_w;
   if (error_out && i == 0 && t == 0) *error_out = *p.error;
-  if (i >= H) return;
+  if (i >= width) return;
   // the ranks' outputs (just written by another launch, on other XCDs) are
   // loaded 8 ranks at a time before the sums, which run in rank order
-  const float dsh = has_shared ? p.down_out[(int64_t)(tokens * K + t) * H + i] : 0.f;
+  const float dsh = has_shared ? p.down_out[(int64_t)(tokens * K + t) * ow + i] : 0.f;
   float acc = 0.f;
   constexpr int kBatch = 8;
   for (int r0 = 0; r0 < K; r0 += kBatch) {
@@ -186,7 +189,7 @@ __global__ void __launch_bounds__(256) moe_combine_kernel(MoePlan p, float* __re
       const int q = t * K + min(r0 + b, K - 1);
       ix[b] = p.top_idx[q];
       wv[b] = p.top_w[q];
-      d[b] = p.down_out[(int64_t)q * H + i];
+      d[b] = p.down_out[(int64_t)q * ow + i];
     }
 #pragma unroll
     for (int b = 0; b < kBatch; ++b) {
@@ -204,7 +207,23 @@ __global__ void __launch_bounds__(256) moe_combine_kernel(MoePlan p, float* __re
       acc = acc + d;
     }
   }
-  y[(int64_t)t * H + i] = acc;
+  y[(int64_t)t * width + i] = acc;
+}
+
+// After ffn_latent_up (llambda.lisp:5933-5938): y = its output, plus the
+// shared expert's (vector-add-bias-in-place, :5939-5949) when there is one.
+__global__ void __launch_bounds__(256) moe_latent_finish_kernel(MoePlan p, float* __restrict__ y,
+                                                                int tokens, int has_shared,
+                                                                int* __restrict__ error_out) {
+#pragma clang fp contract(off)
+  const int t = blockIdx.y;
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  const int H = p.hidden;
+  if (error_out && i == 0 && t == 0) *error_out = *p.error;
+  if (i >= H) return;
+  float v = p.lat_y[(int64_t)t * H + i];
+  if (has_shared) v = v + p.down_out[(int64_t)(tokens * p.top_k + t) * p.out_w + i];
+  y[(int64_t)t * H + i] = v;
 }
 
 __global__ void moe_reset_kernel(int* error) {
@@ -262,7 +281,7 @@ static int moe_mfma_tiles(const MoePlan& p, int tokens) {
                                             moe_group_pipeline_types(p.sh_down_type)));
   const int64_t act_w = std::max(p.ffn, p.shared_ffn);
   const int64_t split_bytes = std::max((int64_t)tokens * (p.top_k + 1) * 4 * act_w,
-                                       (int64_t)tokens * 4 * p.hidden);
+                                       (int64_t)tokens * 4 * std::max(p.hidden, p.latent_in));
   return types && split_bytes < ((int64_t)1 << 31) ? 4 : 2;
 }
 static int moe_chunk_tokens(int mt) { return mt == 0 ? 1 : 16 * mt; }
@@ -277,15 +296,29 @@ hipError_t moe_forward_launch(const MoePlan& p, const float* x, float* y, int to
   if (reinterpret_cast<uintptr_t>(x) & 15u) return hipErrorInvalidValue;
   const int has_shared = p.shared_ffn > 0;
   const int H = p.hidden, E = p.experts, K = p.top_k;
+  const int Li = p.latent_in, Lo = p.latent_out;
+  const int din = Li ? Li : H, dout = Lo ? Lo : H;  // routed experts' input, output widths
   const int act_w = std::max(p.ffn, p.shared_ffn);
   const int64_t xs_stride = H / 16, as_stride = act_w / 16;
   const int er = E + ((p.variant == kQwen3Next && has_shared) ? 1 : 0);
   hipError_t e = router_mfma_launch(x, tokens, p.router, er, H, p.router_part, E + 1, p.xq,
                                     2 * (int64_t)H, p.xsum, xs_stride, s);
   if (e != hipSuccess) return e;
+  if (Li) {
+    // the experts' input ffn_latent_down * x (llambda.lisp:5883-5887) and
+    // its split rows; the router and the shared expert keep x's
+    GemvProblem g{p.lat_down_type, p.lat_down, row_bytes_of(p.lat_down_type, H), Li, H, x, H,
+                  tokens, p.lat, Li};
+    e = gemv_launch(g, s);
+    if (e != hipSuccess) return e;
+    e = split_rows_launch(p.lat, tokens, Li, Li, p.lq, 2 * (int64_t)Li, p.lsum, Li / 16, s);
+    if (e != hipSuccess) return e;
+  }
   const int single = tokens == 1;
   const int mt = moe_mfma_tiles(p, tokens), nt = moe_chunk_tokens(mt);
-  const bool joint_up = has_shared && p.sh_up_type == p.up_type;
+  // routed and shared up products share a launch when they share a weight
+  // type and an input
+  const bool joint_up = has_shared && p.sh_up_type == p.up_type && !Li;
   // one token whose up products run in one launch: that launch selects and
   // gates the token itself (one launch fewer)
   const bool fuse_gate = single && mt == 0 && (!has_shared || joint_up) && K <= kMoeMaxTopK &&
@@ -331,9 +364,16 @@ hipError_t moe_forward_launch(const MoePlan& p, const float* x, float* y, int to
   // routed, then shared, gate/up products: one launch when the types agree
   MoeGemmArgs a = up;
   a.group = 0;
+  if (Li) {
+    a.aq = p.lq;
+    a.aq_stride = 2 * (int64_t)Li;
+    a.as = p.lsum;
+    a.as_stride = Li / 16;
+    a.K = Li;
+  }
   a.w0 = p.variant == kQwen3Next ? p.gate : p.up;
   a.w1 = p.up;
-  a.row_bytes = row_bytes_of(p.up_type, H);
+  a.row_bytes = row_bytes_of(p.up_type, din);
   a.expert_stride = a.row_bytes * p.ffn;
   a.N = p.ffn;
   if (joint_up) {
@@ -379,13 +419,14 @@ hipError_t moe_forward_launch(const MoePlan& p, const float* x, float* y, int to
   down.as_stride = as_stride;
   down.N = H;
   down.out = p.down_out;
-  down.out_stride = H;
+  down.out_stride = p.out_w;
   a = down;
   a.group = 0;
   a.K = p.ffn;
+  a.N = dout;
   a.w0 = p.down;
   a.row_bytes = row_bytes_of(p.down_type, p.ffn);
-  a.expert_stride = a.row_bytes * H;
+  a.expert_stride = a.row_bytes * dout;
   const bool joint_down = has_shared && p.sh_down_type == p.down_type;
   if (joint_down) {
     a.joint = 1;
@@ -395,7 +436,8 @@ hipError_t moe_forward_launch(const MoePlan& p, const float* x, float* y, int to
     a.s_K = p.shared_ffn;
   }
   // one token: the down products and the combine in one launch
-  if (single && (!has_shared || joint_down) && moe_down_combine_supported(p.down_type, a)) {
+  if (single && !Lo && (!has_shared || joint_down) &&
+      moe_down_combine_supported(p.down_type, a)) {
     MoeCombineArgs c{};
     c.y = y;
     c.top_w = p.top_w;
@@ -420,8 +462,19 @@ hipError_t moe_forward_launch(const MoePlan& p, const float* x, float* y, int to
   // (a separate launch: combining in the last workgroup of each row tile,
   // behind a device-scope fence and an atomic per workgroup, measured 10 us
   // slower for one Qwen3Next token)
-  return launch(moe_combine_kernel, dim3((H + 255) / 256, tokens), dim3(256), 0, s, p, y, tokens,
-                has_shared, error_out);
+  if (!Lo)
+    return launch(moe_combine_kernel, dim3((H + 255) / 256, tokens), dim3(256), 0, s, p, y, tokens,
+                  H, has_shared, error_out);
+  // the Lo-wide weighted sum, ffn_latent_up, then the shared expert
+  e = launch(moe_combine_kernel, dim3((Lo + 255) / 256, tokens), dim3(256), 0, s, p, p.lat, tokens,
+             Lo, 0, static_cast<int*>(nullptr));
+  if (e != hipSuccess) return e;
+  GemvProblem g{p.lat_up_type, p.lat_up, row_bytes_of(p.lat_up_type, Lo), H, Lo, p.lat, Lo, tokens,
+                p.lat_y, H};
+  e = gemv_launch(g, s);
+  if (e != hipSuccess) return e;
+  return launch(moe_latent_finish_kernel, dim3((H + 255) / 256, tokens), dim3(256), 0, s, p, y,
+                tokens, has_shared, error_out);
 }
 
 hipError_t moe_reset_launch(const MoePlan& p, hipStream_t s) {

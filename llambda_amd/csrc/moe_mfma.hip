@@ -104,6 +104,29 @@ __device__ __forceinline__ void split_octet(const float* __restrict__ xrow, int 
   if ((o & 1) == 0) srow[o >> 1] = s16;
 }
 
+// One thread per octet of the T rows (a row's K / 8 octets are a multiple of
+// four, so octets o and o ^ 1 always sit in neighbouring lanes).
+__global__ void __launch_bounds__(256)
+split_rows_kernel(const float* __restrict__ x, int T, int K, int64_t x_stride,
+                  uint16_t* __restrict__ q, int64_t q_stride, float* __restrict__ s,
+                  int64_t s_stride) {
+  const int octets = K >> 3;
+  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx >= (int64_t)T * octets) return;
+  const int t = (int)(idx / octets), o = (int)(idx - (int64_t)t * octets);
+  split_octet(x + t * x_stride, o, q + t * q_stride, s + t * s_stride);
+}
+
+hipError_t split_rows_launch(const float* x, int T, int K, int64_t x_stride, uint16_t* q,
+                             int64_t q_stride, float* s, int64_t s_stride, hipStream_t stream) {
+  if (T <= 0) return hipSuccess;
+  if (K <= 0 || K % 32 || x_stride % 4 || q_stride % 8) return hipErrorInvalidValue;
+  const int64_t threads = (int64_t)T * (K >> 3);
+  hipLaunchKernelGGL(split_rows_kernel, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0,
+                     stream, x, T, K, x_stride, q, q_stride, s, s_stride);
+  return hipGetLastError();
+}
+
 // -------------------------------------------------------------------- router
 // Router logits sum_h x[t][h] R[e][h] (dot-product-with-f32-tensor-data,
 // llambda.lisp:4096-4107, in another fp32 order), in one fixed order for

@@ -46,14 +46,30 @@ class MoeLayer:
     shared_gate: Optional[Packed] = None      # [Fs][H]       ffn_gate_shexp (qwen3next)
     shared_up: Optional[Packed] = None        # [Fs][H]       ffn_up_shexp
     shared_down: Optional[Packed] = None      # [H][Fs]       ffn_down_shexp
-    latent_down: Optional[Packed] = None      # [Lt][H]       ffn_latent_down (nemotron)
-    latent_up: Optional[Packed] = None        # [H][Lt]       ffn_latent_up (nemotron)
+    latent_down: Optional[Packed] = None      # [Li][H]       ffn_latent_down (nemotron)
+    latent_up: Optional[Packed] = None        # [H][Lo]       ffn_latent_up (nemotron)
     layer_index: Optional[int] = None         # blk.N, for the reference's error texts
+
+    @property
+    def latent_in(self) -> int:
+        """Li: rows of ffn_latent_down (0 without it)."""
+        if self.latent_down is None:
+            return 0
+        return self.latent_down[1].size // ggml.row_bytes(self.latent_down[0], self.hidden)
+
+    @property
+    def latent_out(self) -> int:
+        """Lo: columns of ffn_latent_up (0 without it)."""
+        if self.latent_up is None:
+            return 0
+        t, data = self.latent_up
+        return data.size // self.hidden // ggml.block_bytes(t) * ggml.block_elements(t)
 
     def weight_bytes(self) -> int:
         """Packed bytes of every tensor the layer can read."""
         n = self.router.nbytes
-        for t in (self.gate, self.up, self.down, self.shared_gate, self.shared_up, self.shared_down):
+        for t in (self.gate, self.up, self.down, self.shared_gate, self.shared_up, self.shared_down,
+                  self.latent_down, self.latent_up):
             if t is not None:
                 n += t[1].nbytes
         for v in (self.shared_gate_inp, self.router_bias):
@@ -63,20 +79,23 @@ class MoeLayer:
 
     def expert_bytes(self) -> int:
         """Packed bytes of one routed expert (gate + up + down)."""
-        per = ggml.row_bytes(self.up[0], self.hidden) * self.expert_ffn
+        din, dout = self.latent_in or self.hidden, self.latent_out or self.hidden
+        per = ggml.row_bytes(self.up[0], din) * self.expert_ffn
         if self.gate is not None:
             per += ggml.row_bytes(self.gate[0], self.hidden) * self.expert_ffn
-        per += ggml.row_bytes(self.down[0], self.expert_ffn) * self.hidden
+        per += ggml.row_bytes(self.down[0], self.expert_ffn) * dout
         return per
 
     def flops_per_token(self) -> int:
         """2 x the multiply-adds of one token: the router (and the shared-expert
         gate row), k routed experts (gate, up and down rows), the shared expert."""
         H, F, Fs = self.hidden, self.expert_ffn, self.shared_ffn
-        per_expert = (3 if self.gate is not None else 2) * F * H
+        din, dout = self.latent_in or H, self.latent_out or H
+        per_expert = (2 if self.gate is not None else 1) * F * din + F * dout
         shared = ((3 if self.shared_gate is not None else 2) * Fs * H) if Fs else 0
         router = self.expert_count * H + (H if self.shared_gate_inp is not None else 0)
-        return 2 * (self.top_k * per_expert + shared + router)
+        latent = (self.latent_in + self.latent_out) * H
+        return 2 * (self.top_k * per_expert + shared + router + latent)
 
     def shared_bytes(self) -> int:
         if not self.shared_ffn:
@@ -141,6 +160,8 @@ class HipMoeSession:
             if pair is not None:
                 setattr(d, name + "_type", pair[0])
                 setattr(d, field, arr(pair[1], np.uint8))
+        d.latent_in = layer.latent_in
+        d.latent_out = layer.latent_out
         handle = ctypes.c_void_p()
         _check(native.lib().llambda_hip_moe_session_create(ctypes.byref(d), ctypes.byref(handle)),
                "HIP MoE session creation")
@@ -303,17 +324,26 @@ def zipf_bias(rng: np.random.Generator, experts: int, s: float = 1.1, c: float =
 def synthetic_nemotron_h(rng: np.random.Generator, *, hidden=2688, experts=128, top_k=6, ffn=1856,
                          shared_ffn=3712, expert_type=ggml.Q5_0, down_type=ggml.Q5_0,
                          router_std=0.02, zipf_s=1.1, zipf_c=0.5, weights_scale=1.0,
-                         weights_norm=True) -> MoeLayer:
-    """A Nemotron-H-MoE-shaped layer: relu^2 experts, biased sigmoid routing."""
+                         weights_norm=True, latent_in=0, latent_out=0,
+                         latent_type=ggml.Q8_0) -> MoeLayer:
+    """A Nemotron-H-MoE-shaped layer: relu^2 experts, biased sigmoid routing.
+    latent_in > 0 adds ffn_latent_down [latent_in][hidden] (the routed
+    experts' input is then latent_in wide), latent_out > 0 adds
+    ffn_latent_up [hidden][latent_out] (their weighted sum is latent_out
+    wide), both of latent_type."""
     gen = synthetic.packed
+    din = latent_in or hidden
+    dout = latent_out or hidden
     return MoeLayer(
         variant=NEMOTRON_H, hidden=hidden, expert_count=experts, top_k=top_k, expert_ffn=ffn,
         shared_ffn=shared_ffn,
         router=rng.normal(0.0, router_std, size=(experts, hidden)).astype(np.float32),
         router_bias=zipf_bias(rng, experts, zipf_s, zipf_c),
         expert_weights_scale=weights_scale, expert_weights_norm=weights_norm,
-        up=(expert_type, gen(expert_type, rng, experts * ffn, hidden)),
-        down=(down_type, gen(down_type, rng, experts * hidden, ffn)),
+        up=(expert_type, gen(expert_type, rng, experts * ffn, din)),
+        down=(down_type, gen(down_type, rng, experts * dout, ffn)),
         shared_up=(expert_type, gen(expert_type, rng, shared_ffn, hidden)) if shared_ffn else None,
         shared_down=(down_type, gen(down_type, rng, hidden, shared_ffn)) if shared_ffn else None,
+        latent_down=(latent_type, gen(latent_type, rng, latent_in, hidden)) if latent_in else None,
+        latent_up=(latent_type, gen(latent_type, rng, hidden, latent_out)) if latent_out else None,
     )

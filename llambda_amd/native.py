@@ -51,6 +51,8 @@ class MoeDesc(ctypes.Structure):
         ("shared_down_type", c_int), ("shared_down", c_void_p),
         ("latent_down_type", c_int), ("latent_down", c_void_p),
         ("latent_up_type", c_int), ("latent_up", c_void_p),
+        ("latent_in", c_i64),
+        ("latent_out", c_i64),
     ]
 
 

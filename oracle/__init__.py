@@ -59,9 +59,10 @@ class MoeDesc(ctypes.Structure):
         ("shared_gate_type", ctypes.c_int), ("shared_gate", ctypes.c_void_p),
         ("shared_up_type", ctypes.c_int), ("shared_up", ctypes.c_void_p),
         ("shared_down_type", ctypes.c_int), ("shared_down", ctypes.c_void_p),
-        ("latent", ctypes.c_int64),
+        ("latent_in", ctypes.c_int64),
         ("latent_down_type", ctypes.c_int), ("latent_down", ctypes.c_void_p),
         ("latent_up_type", ctypes.c_int), ("latent_up", ctypes.c_void_p),
+        ("latent_out", ctypes.c_int64),
     ]
 
 
@@ -160,6 +161,15 @@ def row_bytes(type_tag: int, columns: int) -> int:
     if n < 0:
         raise OracleError(lib().oracle_last_error().decode())
     return n
+
+
+def columns_of(type_tag: int, row_byte_count: int) -> int:
+    """Columns of one packed row of row_byte_count bytes (its smallest block
+    of 1, 32 or 256 weights, whichever the type takes)."""
+    for block in (1, 32, 256):
+        if lib().oracle_row_bytes(type_tag, block) > 0:
+            return row_byte_count // row_bytes(type_tag, block) * block
+    raise OracleError(f"unknown GGML type tag {type_tag}")
 
 
 def fp16_to_f32(bits: int) -> float:
@@ -280,11 +290,12 @@ def moe_forward(layer, x: np.ndarray, threads: int = 1) -> MoeResult:
             setattr(d, field, arr(pair[1], np.uint8))
     latent_down = getattr(layer, "latent_down", None)
     latent_up = getattr(layer, "latent_up", None)
-    if latent_down is not None:
-        d.latent = np.asarray(latent_down[1]).size // row_bytes(latent_down[0], layer.hidden)
+    if latent_down is not None:  # [Li][H]
+        d.latent_in = np.asarray(latent_down[1]).size // row_bytes(latent_down[0], layer.hidden)
         d.latent_down_type = latent_down[0]
         d.latent_down = arr(latent_down[1], np.uint8)
-    if latent_up is not None:
+    if latent_up is not None:  # [H][Lo]
+        d.latent_out = columns_of(latent_up[0], np.asarray(latent_up[1]).size // layer.hidden)
         d.latent_up_type = latent_up[0]
         d.latent_up = arr(latent_up[1], np.uint8)
     y = np.empty_like(x)

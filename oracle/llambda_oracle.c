@@ -632,31 +632,32 @@ static int qwen3next_token(const oracle_moe_desc* m, const float* x, float* dest
   return 0;
 }
 
-/* nemotron-h-moe-ffn-into, llambda.lisp:5827-5949, for one token.  With the
- * optional latent projections (m->latent > 0) the experts' input is
- * ffn_latent_down * x (:5883-5887), their weighted sum is Lt wide, and
- * ffn_latent_up maps it back to H before the shared expert is added
- * (:5933-5938); the router and the shared expert read x itself. */
+/* nemotron-h-moe-ffn-into, llambda.lisp:5827-5949, for one token.  The
+ * optional latent projections are independent, as in the reference: with
+ * ffn_latent_down the experts' input is ffn_latent_down * x (:5883-5887),
+ * Li wide; with ffn_latent_up their weighted sum is Lo wide and
+ * ffn_latent_up maps it back to H (:5933-5938); without it the sum is
+ * formed in dest.  The router and the shared expert read x itself. */
 static int nemotron_token(const oracle_moe_desc* m, const float* x, float* dest,
                           int64_t* top_idx, float* top_w, float* logits, float* work,
                           int threads) {
   const int64_t H = m->hidden, E = m->expert_count, K = m->top_k, F = m->expert_ffn,
                 Fs = m->shared_ffn;
-  float* top_logits = work;
-  int64_t FF = F > Fs ? F : Fs;
+  const int64_t Li = m->latent_in, Lo = m->latent_out;
+  const int64_t Din = Li > 0 ? Li : H;      /* width of the experts' input */
+  const int64_t Dout = Lo > 0 ? Lo : H;     /* width of their outputs */
+  const int64_t FF = F > Fs ? F : Fs;
+  float* top_logits = work;                 /* [K] */
   float* up = top_logits + K;               /* [FF] */
-  float* down = up + FF;                    /* [H] */
-  const int64_t Lt = m->latent;
-  const int64_t D = Lt > 0 ? Lt : H;        /* width of the experts' input and output */
-  float* expert_in = down + H;              /* [Lt] */
-  float* moe_out = expert_in + Lt;          /* [Lt] */
+  float* down = up + FF;                    /* [max(H, Lo)] */
+  float* expert_in = down + (H > Lo ? H : Lo); /* [Li] */
+  float* moe_out = expert_in + Li;          /* [Lo] */
   const float* ein = x;
-  float* acc = dest;
-  if (Lt > 0) {                                                         /* :5883-5887 */
-    if (oracle_gemv(m->latent_down_type, m->latent_down, Lt, H, x, expert_in, threads))
+  float* acc = Lo > 0 ? moe_out : dest;
+  if (Li > 0) {                                                         /* :5883-5887 */
+    if (oracle_gemv(m->latent_down_type, m->latent_down, Li, H, x, expert_in, threads))
       return -1;
     ein = expert_in;
-    acc = moe_out;
   }
   if (oracle_gemv(ORACLE_TYPE_F32, (const uint8_t*)m->router, E, H, x, logits, threads))
     return -1;                                                          /* :5888-5891 */
@@ -674,17 +675,17 @@ static int nemotron_token(const oracle_moe_desc* m, const float* x, float* dest,
     for (int64_t r = 0; r < K; ++r) top_w[r] = top_w[r] / weight_sum;
   }
   for (int64_t r = 0; r < K; ++r) top_w[r] = m->expert_weights_scale * top_w[r];
-  for (int64_t i = 0; i < D; ++i) acc[i] = 0.0f;                       /* :5914 */
+  for (int64_t i = 0; i < Dout; ++i) acc[i] = 0.0f;                    /* :5914 */
   for (int64_t r = 0; r < K; ++r) {                                     /* :5915-5932 */
     int64_t e = top_idx[r];
     if (e < 0 || e >= E) return fail("Expert index %lld is out of range.", (long long)e);
-    if (expert_gemv(m->up_type, m->up_exps, e, F, D, ein, up, threads)) return -1;
+    if (expert_gemv(m->up_type, m->up_exps, e, F, Din, ein, up, threads)) return -1;
     for (int64_t i = 0; i < F; ++i) up[i] = oracle_relu_squared(up[i]);
-    if (expert_gemv(m->down_type, m->down_exps, e, D, F, up, down, threads)) return -1;
-    for (int64_t i = 0; i < D; ++i) acc[i] = acc[i] + top_w[r] * down[i];
+    if (expert_gemv(m->down_type, m->down_exps, e, Dout, F, up, down, threads)) return -1;
+    for (int64_t i = 0; i < Dout; ++i) acc[i] = acc[i] + top_w[r] * down[i];
   }
-  if (Lt > 0 &&                                                         /* :5933-5938 */
-      oracle_gemv(m->latent_up_type, m->latent_up, H, Lt, moe_out, dest, threads))
+  if (Lo > 0 &&                                                         /* :5933-5938 */
+      oracle_gemv(m->latent_up_type, m->latent_up, H, Lo, moe_out, dest, threads))
     return -1;
   if (Fs > 0) {                                                         /* :5939-5949 */
     if (oracle_gemv(m->shared_up_type, m->shared_up, Fs, H, x, up, threads)) return -1;
@@ -701,14 +702,20 @@ int oracle_moe_forward(const oracle_moe_desc* m, const float* x, float* y, int64
   if (!m || !x || !y) return fail("null argument");
   if (m->top_k <= 0 || m->top_k > m->expert_count) return fail("top_k out of range");
   int64_t FF = m->expert_ffn > m->shared_ffn ? m->expert_ffn : m->shared_ffn;
-  if (m->latent < 0 || (m->latent > 0 && (m->variant != 1 || !m->latent_down || !m->latent_up)))
-    return fail("latent projections need a Nemotron-H layer with both tensors");
-  size_t work_floats = (size_t)(m->top_k + 2 * FF + m->hidden + m->expert_count +
-                                2 * (m->latent > 0 ? m->latent : 0));
-  float* work = (float*)malloc(work_floats * sizeof(float));
+  const int64_t Li = m->latent_in, Lo = m->latent_out;
+  if (Li < 0 || Lo < 0 || (Li > 0) != (m->latent_down != NULL) ||
+      (Lo > 0) != (m->latent_up != NULL))
+    return fail("latent projections: a width for each tensor given, and only for those");
+  if ((Li > 0 || Lo > 0) && m->variant != 1)
+    return fail("latent projections belong to Nemotron-H layers");
+  /* qwen3next: top logits, gate, up, down [H]; nemotron: top logits, up,
+   * down [max(H, Lo)], expert input [Li], weighted sum [Lo] */
+  const int64_t wide = m->hidden > Lo ? m->hidden : Lo;
+  size_t work_floats = (size_t)(m->top_k + 2 * FF + wide + Li + Lo);
+  float* work = (float*)malloc((work_floats + (size_t)m->expert_count) * sizeof(float));
   int64_t* idx = (int64_t*)malloc((size_t)m->top_k * sizeof(int64_t));
   float* w = (float*)malloc((size_t)m->top_k * sizeof(float));
-  float* logits = work + m->top_k + 2 * FF + m->hidden + 2 * (m->latent > 0 ? m->latent : 0);
+  float* logits = work + work_floats;
   int status = 0;
   for (int64_t t = 0; t < tokens && status == 0; ++t) {
     const float* xt = x + t * m->hidden;

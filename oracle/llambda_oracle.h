@@ -123,13 +123,14 @@ typedef struct oracle_moe_desc {
   int shared_gate_type; const uint8_t* shared_gate; /* [Fs][H], qwen3next */
   int shared_up_type;   const uint8_t* shared_up;   /* [Fs][H] */
   int shared_down_type; const uint8_t* shared_down; /* [H][Fs] */
-  /* nemotron only, optional (llambda.lisp:5845-5864): ffn_latent_down [Lt][H]
-   * and ffn_latent_up [H][Lt]; with them the routed experts run on the
-   * latent vector (up_exps [E*F][Lt], down_exps [E*Lt][F]).  latent = 0 when
-   * the layer has none. */
-  int64_t latent;               /* Lt */
+  /* nemotron only, each optional (llambda.lisp:5845-5864): ffn_latent_down
+   * [Li][H] gives the routed experts an Li-wide input (up_exps [E*F][Li]);
+   * ffn_latent_up [H][Lo] maps their Lo-wide weighted sum back to H
+   * (down_exps [E*Lo][F]).  0 when the layer has no such tensor. */
+  int64_t latent_in;            /* Li: rows of ffn_latent_down */
   int latent_down_type; const uint8_t* latent_down;
   int latent_up_type;   const uint8_t* latent_up;
+  int64_t latent_out;           /* Lo: columns of ffn_latent_up */
 } oracle_moe_desc;
 
 /* llambda.lisp:5321-5426 (qwen3next-moe-into) and 5827-5949

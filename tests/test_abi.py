@@ -98,29 +98,40 @@ def test_packed_create_validates_geometry():
     assert "unsupported GGML tensor type" in native.last_error()
 
 
-def test_moe_session_refuses_latent_projections():
+def test_moe_session_checks_latent_projections():
     """nemotron-h-moe-ffn-into's optional ffn_latent_down / ffn_latent_up
-    (llambda.lisp:5845-5864, 5883-5887, 5933-5938) are refused at creation --
-    before any device work -- so the host keeps the layer's CPU body."""
+    (llambda.lisp:5845-5864, 5883-5887, 5933-5938): the layer reads them with
+    their widths (rows of ffn_latent_down, columns of ffn_latent_up), and
+    session creation refuses inconsistent descriptions before any device
+    work."""
+    import dataclasses
+
     from llambda_amd import ggml, projection, synthetic
     from llambda_amd.hip_backend import HipBackendError
     from llambda_amd.moe import NEMOTRON_H, HipMoeSession, moe_layer_from_model
 
     rng = np.random.default_rng(3)
-    H, E, F, Lt = 256, 8, 64, 128
+    H, E, F, Li, Lo = 256, 8, 64, 128, 96
     t = projection.TensorInfo
     names = {
         "ffn_gate_inp.weight": (ggml.F32, (H, E), synthetic.f32(rng, E, H)),
         "exp_probs_b.bias": (ggml.F32, (E,), synthetic.f32(rng, 1, E)),
-        "ffn_up_exps.weight": (ggml.Q8_0, (Lt, F, E), synthetic.q8_0(rng, E * F, Lt)),
-        "ffn_down_exps.weight": (ggml.Q8_0, (F, Lt, E), synthetic.q8_0(rng, E * Lt, F)),
-        "ffn_latent_down.weight": (ggml.Q8_0, (H, Lt), synthetic.q8_0(rng, Lt, H)),
-        "ffn_latent_up.weight": (ggml.Q8_0, (Lt, H), synthetic.q8_0(rng, H, Lt)),
+        "ffn_up_exps.weight": (ggml.Q8_0, (Li, F, E), synthetic.q8_0(rng, E * F, Li)),
+        "ffn_down_exps.weight": (ggml.Q8_0, (F, Lo, E), synthetic.q8_0(rng, E * Lo, F)),
+        "ffn_latent_down.weight": (ggml.Q8_0, (H, Li), synthetic.q8_0(rng, Li, H)),
+        "ffn_latent_up.weight": (ggml.Q8_0, (Lo, H), synthetic.q8_0(rng, H, Lo)),
     }
     model = projection.ProjectionModel([t(f"blk.0.{n}", ty, dims, data)
                                         for n, (ty, dims, data) in names.items()], layer_count=1)
     layer = moe_layer_from_model(model, 0, NEMOTRON_H, expert_used_count=2)
-    assert layer.latent_down is not None and layer.latent_up is not None
+    assert (layer.latent_in, layer.latent_out) == (Li, Lo)
     assert (layer.hidden, layer.expert_count, layer.top_k, layer.expert_ffn) == (H, E, 2, F)
-    with pytest.raises(HipBackendError, match="ffn_latent_down / ffn_latent_up are not supported"):
-        HipMoeSession(layer)
+    # Li must be a multiple of 32 (the experts' up rows are Li wide)
+    odd = dataclasses.replace(layer, latent_down=(ggml.F32, synthetic.f32(rng, 100, H)))
+    assert odd.latent_in == 100
+    with pytest.raises(HipBackendError, match="ffn_latent_down needs its row count"):
+        HipMoeSession(odd)
+    # a Qwen3Next layer has no latent projections
+    qwen = dataclasses.replace(layer, variant=0)
+    with pytest.raises(HipBackendError, match="belong to Nemotron-H"):
+        HipMoeSession(qwen)

@@ -129,27 +129,22 @@ def test_combine_order_is_rank_order():
     assert np.array_equal(dest, ref.y[0])
 
 
-def nemotron_with_latent(rng, hidden, latent, latent_type, **kw):
-    """A Nemotron-H layer whose routed experts run on a `latent`-wide vector:
-    router and shared expert from an H-wide layer, experts from an Lt-wide one,
-    ffn_latent_down [Lt][H] and ffn_latent_up [H][Lt] of `latent_type`."""
-    outer = synthetic_nemotron_h(rng, hidden=hidden, **kw)
-    inner = synthetic_nemotron_h(rng, hidden=latent, **kw)
-    return dataclasses.replace(
-        outer, up=inner.up, down=inner.down,
-        latent_down=(latent_type, synthetic.packed(latent_type, rng, latent, hidden)),
-        latent_up=(latent_type, synthetic.packed(latent_type, rng, hidden, latent)))
-
-
-def float64_latent_layer(layer, x, latent):
-    """nemotron-h-moe-ffn-into with ffn_latent_down/up (llambda.lisp:5845-5864,
-    5883-5887, 5933-5938) in float64 from the dequantised weights."""
+def float64_latent_layer(layer, x):
+    """nemotron-h-moe-ffn-into with its optional ffn_latent_down / ffn_latent_up
+    (llambda.lisp:5845-5864, 5883-5887, 5933-5938), each independently, in
+    float64 from the dequantised weights."""
     H, E, K, F, Fs = (layer.hidden, layer.expert_count, layer.top_k, layer.expert_ffn,
                       layer.shared_ffn)
-    up = dq(layer.up, E * F, latent).reshape(E, F, latent)
-    down = dq(layer.down, E * latent, F).reshape(E, latent, F)
-    ld = dq(layer.latent_down, latent, H)
-    lu = dq(layer.latent_up, H, latent)
+    ld = lu = None
+    din = dout = H
+    if layer.latent_down is not None:
+        din = layer.latent_down[1].size // ggml.row_bytes(layer.latent_down[0], H)
+        ld = dq(layer.latent_down, din, H)
+    if layer.latent_up is not None:
+        dout = oracle.columns_of(layer.latent_up[0], layer.latent_up[1].size // H)
+        lu = dq(layer.latent_up, H, dout)
+    up = dq(layer.up, E * F, din).reshape(E, F, din)
+    down = dq(layer.down, E * dout, F).reshape(E, dout, F)
     ys = []
     for xt in x.astype(np.float64):
         logits = layer.router.astype(np.float64) @ xt + layer.router_bias
@@ -158,32 +153,42 @@ def float64_latent_layer(layer, x, latent):
         if layer.expert_weights_norm:
             w = w / w.sum()
         w = w * layer.expert_weights_scale
-        ein = ld @ xt
-        m = np.zeros(latent)
+        ein = ld @ xt if ld is not None else xt
+        m = np.zeros(dout)
         for r, e in enumerate(order):
             m += w[r] * (down[e] @ (np.maximum(up[e] @ ein, 0.0) ** 2))
-        y = lu @ m
+        y = lu @ m if lu is not None else m
         if Fs:
             y += dq(layer.shared_down, H, Fs) @ (np.maximum(dq(layer.shared_up, Fs, H) @ xt, 0.0) ** 2)
         ys.append(y)
     return np.array(ys)
 
 
-@pytest.mark.parametrize("latent_type", [ggml.Q8_0, ggml.F32])
-def test_nemotron_latent_oracle_vs_float64(latent_type):
+@pytest.mark.parametrize("latent_in,latent_out,latent_type", [
+    (128, 128, ggml.Q8_0), (128, 128, ggml.F32), (160, 0, ggml.Q5_0), (0, 96, ggml.Q8_0),
+    (96, 160, ggml.Q8_0), (128, 0, ggml.Q6_K), (0, 256, ggml.Q4_K)])
+def test_nemotron_latent_oracle_vs_float64(latent_in, latent_out, latent_type):
     rng = np.random.default_rng(11)
-    layer = nemotron_with_latent(rng, 256, 128, latent_type, experts=16, top_k=3, ffn=96,
-                                 shared_ffn=64, router_std=0.1)
+    layer = synthetic_nemotron_h(rng, hidden=256, experts=16, top_k=3, ffn=96, shared_ffn=64,
+                                 router_std=0.1, expert_type=ggml.Q8_0, down_type=ggml.Q8_0,
+                                 latent_in=latent_in, latent_out=latent_out,
+                                 latent_type=latent_type)
     x = synthetic.activations(rng, 4, layer.hidden)
     ref = oracle.moe_forward(layer, x, threads=2)
-    y64 = float64_latent_layer(layer, x, 128)
+    y64 = float64_latent_layer(layer, x)
     assert np.all(np.abs(ref.y - y64) <= 1e-5 * scale_of(y64))
+
+
+def _f32(a):
+    return (ggml.F32, np.ascontiguousarray(a, dtype=np.float32).view(np.uint8).ravel())
 
 
 def test_nemotron_latent_permutation_is_exact():
     """ffn_latent_down = I and ffn_latent_up = a permutation P (F32, Lt = H): the
     layer's output is the latent-free layer's output with its entries taken in
-    P's order, bit for bit.  A transposed or misplaced latent product fails it."""
+    P's order, bit for bit; with ffn_latent_down = I alone it is the latent-free
+    output itself, and with ffn_latent_up = P alone the permuted one.  A
+    transposed or misplaced latent product fails it."""
     rng = np.random.default_rng(12)
     H = 128
     base = synthetic_nemotron_h(rng, hidden=H, experts=8, top_k=2, ffn=64, shared_ffn=0,
@@ -193,18 +198,20 @@ def test_nemotron_latent_permutation_is_exact():
     perm = np.zeros((H, H), np.float32)
     perm[np.arange(H), pi] = 1.0
     eye = np.eye(H, dtype=np.float32)
-    lat = dataclasses.replace(base, latent_down=(ggml.F32, eye.view(np.uint8).ravel()),
-                              latent_up=(ggml.F32, perm.view(np.uint8).ravel()))
     x = synthetic.activations(rng, 3, H)
     want = oracle.moe_forward(base, x).y
-    got = oracle.moe_forward(lat, x).y
-    assert np.array_equal(got, want[:, pi])
+    both = dataclasses.replace(base, latent_down=_f32(eye), latent_up=_f32(perm))
+    assert np.array_equal(oracle.moe_forward(both, x).y, want[:, pi])
+    down_only = dataclasses.replace(base, latent_down=_f32(eye))
+    assert np.array_equal(oracle.moe_forward(down_only, x).y, want)
+    up_only = dataclasses.replace(base, latent_up=_f32(perm))
+    assert np.array_equal(oracle.moe_forward(up_only, x).y, want[:, pi])
 
 
-def test_latent_needs_both_tensors():
+def test_latent_projections_only_on_nemotron():
     rng = np.random.default_rng(13)
-    layer = synthetic_nemotron_h(rng, hidden=64, experts=4, top_k=2, ffn=32, shared_ffn=0)
-    half = dataclasses.replace(layer, latent_down=(ggml.F32, np.eye(64, dtype=np.float32)
-                                                   .view(np.uint8).ravel()))
-    with pytest.raises(Exception, match="latent projections"):
-        oracle.moe_forward(half, synthetic.activations(rng, 1, 64))
+    layer = synthetic_qwen3next(rng, hidden=256, experts=4, top_k=2, ffn=32, shared_ffn=32,
+                                down_type=ggml.Q8_0)
+    lat = dataclasses.replace(layer, latent_down=_f32(np.eye(256, dtype=np.float32)))
+    with pytest.raises(Exception, match="latent projections belong to Nemotron-H"):
+        oracle.moe_forward(lat, synthetic.activations(rng, 1, 256))

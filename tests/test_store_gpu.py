@@ -200,24 +200,42 @@ def test_moe_hook_input_error_keeps_the_layer_on_the_device(hip_backend):
     projection.clear_model_accelerator_projections(model)
 
 
-def test_moe_hook_refuses_a_layer_it_cannot_run(hip_backend):
-    """A layer the device path does not run (here: Nemotron-H with
-    ffn_latent_down / ffn_latent_up) stays on its CPU body: setup warns and
-    nothing is bound."""
+def test_moe_hook_runs_a_latent_layer(hip_backend):
+    """A Nemotron-H layer with ffn_latent_down / ffn_latent_up runs through the
+    hook on the device (llambda.lisp:5845-5864, 5883-5887, 5933-5938): the
+    session is bound, the CPU body never runs, and each token agrees with the
+    oracle."""
+    from test_moe_latent_gpu import absolute_layer
     rng = np.random.default_rng(44)
-    layer = synthetic_nemotron_h(rng, hidden=256, experts=16, top_k=2, ffn=64, shared_ffn=0,
-                                 expert_type=ggml.Q8_0, down_type=ggml.Q8_0)
+    layer = synthetic_nemotron_h(rng, hidden=256, experts=16, top_k=2, ffn=64, shared_ffn=64,
+                                 expert_type=ggml.Q8_0, down_type=ggml.Q8_0, latent_in=128,
+                                 latent_out=96, latent_type=ggml.Q5_0, router_std=0.05)
     model = _moe_model(layer)
-    for name, rows, cols in (("ffn_latent_down", 128, 256), ("ffn_latent_up", 256, 128)):
+    Li, Lo = layer.latent_in, layer.latent_out
+    model.tensors["blk.0.ffn_up_exps.weight"] = projection.TensorInfo(
+        "blk.0.ffn_up_exps.weight", layer.up[0], (Li, 64, 16), layer.up[1])
+    model.tensors["blk.0.ffn_down_exps.weight"] = projection.TensorInfo(
+        "blk.0.ffn_down_exps.weight", layer.down[0], (64, Lo, 16), layer.down[1])
+    for name, pair, dims in (("ffn_latent_down", layer.latent_down, (256, Li)),
+                             ("ffn_latent_up", layer.latent_up, (Lo, 256))):
         model.tensors[f"blk.0.{name}.weight"] = projection.TensorInfo(
-            f"blk.0.{name}.weight", ggml.Q8_0, (cols, rows),
-            synthetic.packed(ggml.Q8_0, rng, rows, cols))
+            f"blk.0.{name}.weight", pair[0], dims, pair[1])
 
     def make(m, i):
         return HipMoeSession(moe_layer_from_model(m, i, NEMOTRON_H, expert_used_count=2))
 
-    with warnings.catch_warnings(record=True) as w:
-        warnings.simplefilter("always")
-        assert projection.try_enable_model_accelerator_moe_layers(model, "hip", [0], make) is None
-    assert any("ffn_latent_down" in str(x.message) for x in w)
-    assert not model.accelerator_moe_layers
+    assert projection.try_enable_model_accelerator_moe_layers(model, "hip", [0], make) is True
+    bound = model.accelerator_moe_layers[0][0].session.layer
+    assert (bound.latent_in, bound.latent_out) == (Li, Lo)
+    xs = synthetic.activations(rng, 3, layer.hidden)
+    ref = oracle.moe_forward(layer, xs)
+    A = absolute_layer(layer, xs, ref.top_indices, ref.top_weights)
+
+    def cpu_body():
+        raise AssertionError("the CPU body must not run")
+
+    for t in range(xs.shape[0]):
+        dest = np.empty(layer.hidden, dtype=np.float32)
+        projection.moe_layer_into(dest, model, 0, xs[t], cpu_body)
+        assert np.all(np.abs(dest.astype(np.float64) - ref.y[t]) <= REL * A[t]), t
+    projection.clear_model_accelerator_projections(model)

@@ -25,13 +25,18 @@ def _layer(variant, rng):
     one token (fused gating, down + combine), 16-pair chunks (at most 16
     pairs per expert on average), the wide pipeline (K-quant experts, more
     than 16 pairs per expert) and the group pipeline (32-weight block types,
-    more than 16 pairs per expert: 300 tokens x 2 of 8 experts = 75)."""
+    more than 16 pairs per expert: 300 tokens x 2 of 8 experts = 75), and a
+    Nemotron-H layer with ffn_latent_down / ffn_latent_up."""
     if variant == "qwen3next":
         return synthetic_qwen3next(rng, hidden=1024, experts=64, top_k=6, ffn=256,
                                    shared_ffn=256), (40, 7)
     if variant == "nemotron":
         return synthetic_nemotron_h(rng, hidden=768, experts=32, top_k=4, ffn=320,
                                     shared_ffn=640), (33, 1)
+    if variant == "latent":
+        return synthetic_nemotron_h(rng, hidden=512, experts=8, top_k=2, ffn=288, shared_ffn=320,
+                                    expert_type=ggml.Q8_0, down_type=ggml.Q5_0, latent_in=256,
+                                    latent_out=192, latent_type=ggml.Q5_0), (300, 1)
     if variant == "wide":
         return synthetic_qwen3next(rng, hidden=512, experts=8, top_k=2, ffn=256,
                                    shared_ffn=256), (300, 120)
@@ -39,7 +44,7 @@ def _layer(variant, rng):
                                 expert_type=ggml.Q8_0, down_type=ggml.Q5_0), (300, 90)
 
 
-@pytest.mark.parametrize("variant", ["qwen3next", "nemotron", "wide", "group"])
+@pytest.mark.parametrize("variant", ["qwen3next", "nemotron", "wide", "group", "latent"])
 def test_noalloc_matches_the_allocating_run(hip, variant):
     import torch
     rng = np.random.default_rng(70)
