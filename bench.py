@@ -148,6 +148,81 @@ def bench_gemv(torch, timer, type_tag, rows, columns, steps, warmup, seed=1, cop
     return ms, nbytes
 
 
+def bench_stream_read(torch, timer, nbytes, steps, warmup, sustained):
+    """llambda_hip_stream_read over one nbytes buffer: the read rate the device
+    sustains, timed exactly as the GEMV beside it (ms per launch, then the
+    sustained figure)."""
+    buf = torch.empty(nbytes, dtype=torch.uint8, device="cuda").fill_(7)
+    out = torch.empty(native.STREAM_READ_WORDS, dtype=torch.int32, device="cuda")
+    lib = native.lib()
+
+    def step():
+        if lib.llambda_hip_stream_read(buf.data_ptr(), nbytes, out.data_ptr(), timer.handle):
+            raise RuntimeError(native.last_error())
+
+    ms = timer.time(step, steps, warmup)
+    settle, launches = sustained
+    ms_sus = timer.time(step, launches, settle)
+    del buf, out
+    return ms, ms_sus
+
+
+REPORT_WARMUP, REPORT_RUNS = 3, 20  # benchmark-gguf-projection-backends' defaults
+
+
+def projection_report(torch, timer, name, type_tag, rows, columns, seed):
+    """benchmark-gguf-projection-backends (llambda.lisp:4825-4949) for one
+    synthetic tensor: the reference's deterministic input x[i] = ((17 i + 11)
+    mod 257)/128 - 1 (:4870-4874), 3 warm-up and 20 timed runs per backend,
+    ms per run, GFLOP/s = 2 N K / time, speedup over the CPU and the maximum
+    absolute difference from the CPU output (:4752-4787).  Backends: the CPU
+    oracle on the host's cores; the HIP session on device-resident x and y
+    (HIP events); the HIP session through the synchronous host-pointer entry
+    point the Lisp adapter calls (wall clock)."""
+    import oracle
+    rng = np.random.default_rng(seed)
+    w = synthetic.packed(type_tag, rng, rows, columns)
+    x_host = synthetic.reference_input(columns)
+    flops = 2.0 * rows * columns
+    y_cpu = np.empty(rows, np.float32)
+
+    def cpu():
+        y_cpu[:] = oracle.gemv(type_tag, w, rows, columns, x_host, threads=CPU_THREADS)
+
+    ms_cpu = _per_call_us(cpu, REPORT_RUNS, REPORT_WARMUP) / 1e3
+    sess = make_hip_session_packed(w, type_tag, rows, columns)
+    x = torch.from_numpy(x_host).cuda()
+    y = torch.empty(rows, device="cuda", dtype=torch.float32)
+    ms_dev = timer.time(lambda: sess.run_device(x.data_ptr(), y.data_ptr(), 1, timer.handle),
+                        REPORT_RUNS, REPORT_WARMUP)
+    y_dev = y.cpu().numpy()
+    y_host = np.empty(rows, np.float32)
+    ms_host = _per_call_us(lambda: sess.run_into(y_host, x_host), REPORT_RUNS, REPORT_WARMUP) / 1e3
+    sess.close()
+
+    def row(backend, ms, out, **extra):
+        r = {"backend": backend, "ms_per_run": round(ms, 4), "gflops": round(flops / ms / 1e6, 2),
+             "speedup_vs_cpu": round(ms_cpu / ms, 2),
+             "max_absolute_error": float(np.max(np.abs(out - y_cpu)))}
+        r.update(extra)
+        return r
+
+    results = [row("CPU", ms_cpu, y_cpu, threads=CPU_THREADS, kind="oracle (C restatement)"),
+               row("HIP", ms_dev, y_dev, pointers="device"),
+               row("HIP", ms_host, y_host, pointers="host (synchronous, as run-hip-session-into)")]
+    log(f"Projection {name!r} ({rows} x {columns}), {REPORT_WARMUP} warmup and "
+        f"{REPORT_RUNS} timed runs")
+    log(f"{'Backend':<12} {'ms/run':<12} {'GFLOP/s':<12} {'speedup':<10} max abs error")
+    for r in results:
+        label = r["backend"] + ("" if r["backend"] == "CPU" else
+                                "/dev" if r["pointers"] == "device" else "/host")
+        log(f"{label:<12} {r['ms_per_run']:<12.3f} {r['gflops']:<12.3f} "
+            f"{r['speedup_vs_cpu']:<9.2f}x {r['max_absolute_error']:<14.6g}")
+    return {"tensor": name, "type": ggml.NAMES[type_tag], "rows": rows, "columns": columns,
+            "input": "x[i] = ((17 i + 11) mod 257) / 128 - 1", "warmup_runs": REPORT_WARMUP,
+            "timed_runs": REPORT_RUNS, "results": results}
+
+
 def bench_head_sampling(torch, timer, rows, columns, steps, warmup):
     """Output head then sample-token-id-from-logits on the device (top-k 40,
     top-p 0.9, temperature 1, repetition penalty over a 64-token history,
@@ -367,7 +442,8 @@ def main():
     # fresh process, head launches 26-75 run ~15% slower than the settled
     # rate reached ~30 ms in)
     ap.add_argument("--warmup", type=int, default=300)
-    ap.add_argument("--only", choices=["head", "q4k", "moe", "llama", "copy", "none"], default=None,
+    ap.add_argument("--only", choices=["head", "report", "q4k", "moe", "llama", "copy", "none"],
+                    default=None,
                     help="run one workload group only (profiling)")
     ap.add_argument("--cpu-seconds", type=float, default=8.0,
                     help="bound on each CPU-baseline sample (0 disables)")
@@ -395,6 +471,12 @@ def main():
         gbs_sus = nbytes / (ms_sus * 1e-3) / 1e9
         log(f"Q6_K head: {ms * 1e3:.1f} us/launch, {gbs:.0f} GB/s; sustained "
             f"{ms_sus * 1e3:.1f} us/launch, {gbs_sus:.0f} GB/s")
+        # the device's own ceiling: a plain read of as many bytes, timed alike
+        rd_ms, rd_ms_sus = bench_stream_read(torch, timer, nbytes, steps, warmup, (300, 800))
+        rd_gbs = nbytes / (rd_ms * 1e-3) / 1e9
+        rd_gbs_sus = nbytes / (rd_ms_sus * 1e-3) / 1e9
+        log(f"streaming read of {nbytes} B: {rd_ms * 1e3:.1f} us/launch, {rd_gbs:.0f} GB/s; "
+            f"sustained {rd_ms_sus * 1e3:.1f} us, {rd_gbs_sus:.0f} GB/s")
         cpu = None
         if args.cpu_seconds > 0:
             cpu_gbs, n = cpu_gemv_baseline(ggml.Q6_K, rows, cols, args.cpu_seconds)
@@ -417,12 +499,31 @@ def main():
                        "rows": rows, "columns": cols, "algorithmic_bytes": nbytes},
             "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS,
                          "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4),
-                         "traffic": traffic},
+                         "traffic": traffic,
+                         "ceiling": {"kernel": "llambda_hip_stream_read (each of 4096 waves "
+                                               "streams one contiguous slice, 16-byte loads)",
+                                     "bytes": nbytes, "GB/s": round(rd_gbs, 1),
+                                     "frac_of_peak": round(rd_gbs / HBM_PEAK_GBS, 4),
+                                     "gemv_frac_of_ceiling": round(gbs / rd_gbs, 4),
+                                     "sustained_GB/s": round(rd_gbs_sus, 1),
+                                     "gemv_sustained_frac_of_ceiling":
+                                         round(gbs_sus / rd_gbs_sus, 4)}},
             "sustained": {"launches": 800, "after_launches": steps + warmup + 300,
                           "us_per_launch": round(ms_sus * 1e3, 2), "GB/s": round(gbs_sus, 1),
                           "frac": round(gbs_sus / HBM_PEAK_GBS, 4)},
             "cpu_baseline": cpu,
         }
+
+    if args.only in (None, "report") and args.cpu_seconds > 0:
+        reports = [projection_report(torch, timer, "output.weight", ggml.Q6_K, 128256, 4096, 41),
+                   projection_report(torch, timer, "blk.0.attn_q.weight", ggml.Q4_K, 4096, 4096,
+                                     42),
+                   projection_report(torch, timer, "blk.0.ffn_down.weight", ggml.Q6_K, 4096,
+                                     14336, 43)]
+        if line is not None:
+            line["projection_report"] = reports
+        else:
+            workloads.append({"workload": "projection report", "projection_report": reports})
 
     if args.only in (None, "q4k"):
         ms_hot, nbytes = bench_gemv(torch, timer, ggml.Q4_K, 4096, 4096, steps, warmup)

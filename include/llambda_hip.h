@@ -247,6 +247,19 @@ int llambda_hip_moe_session_run_device_noalloc(llambda_hip_moe_session* session,
 int llambda_hip_select_top_k(const float* logits, size_t n, size_t k, size_t batch,
                              int64_t* top_indices, float* top_logits);
 
+/* ---- measurement ------------------------------------------------------ */
+
+#define LLAMBDA_HIP_STREAM_READ_WORDS 4096
+
+/* A plain streaming read of `bytes` of device memory (16-byte aligned, a
+ * multiple of 16): LLAMBDA_HIP_STREAM_READ_WORDS wavefronts each read one
+ * contiguous slice with 16-byte loads and store the XOR of what they read in
+ * out[wave] (device memory, LLAMBDA_HIP_STREAM_READ_WORDS words).  Enqueued
+ * on `stream` (null = the null stream), not waited for.  No counterpart in
+ * the reference: it measures the HBM read rate the device sustains, the
+ * ceiling beside 8 TB/s against which bench.py reads the GEMV figures. */
+int llambda_hip_stream_read(const void* data, size_t bytes, uint32_t* out, void* stream);
+
 /* ---- Llama-layout decode token ---------------------------------------- */
 
 /* One packed 2-D tensor: GGML type tag and its rows (rows * row_bytes bytes,

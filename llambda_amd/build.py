@@ -2,7 +2,8 @@
 
 ``python -m llambda_amd.build`` or ``llambda_amd.build.build()``.  Objects go
 to ``llambda_amd/_build/``; the shared library to
-``llambda_amd/libllambda_hip.so``.
+``llambda_amd/libllambda_hip.so``, and the command-line check
+``llambda_amd/llambda_hip_smoke`` (linked against it) beside it.
 """
 from __future__ import annotations
 
@@ -16,6 +17,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 OBJ = os.path.join(HERE, "_build")
 LIB = os.path.join(HERE, "libllambda_hip.so")
+SMOKE = os.path.join(HERE, "llambda_hip_smoke")
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 ARCH = "gfx950"
 
@@ -66,6 +68,12 @@ def build(verbose: bool = False, defines=(), obj_dir: str = OBJ, lib_path: str =
     tmp = lib_path + ".tmp"
     _run([HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp, *objs])
     shutil.move(tmp, lib_path)
+    if lib_path == LIB:
+        # the smoke CLI finds the library beside itself
+        tmp = SMOKE + ".tmp"
+        _run(["g++", *CXX_FLAGS, os.path.join(CSRC, "smoke.cpp"), "-o", tmp, f"-L{HERE}",
+              "-lllambda_hip", "-Wl,-rpath,$ORIGIN"])
+        shutil.move(tmp, SMOKE)
     return lib_path
 
 

@@ -959,6 +959,17 @@ int llambda_hip_moe_session_run_device_noalloc(llambda_hip_moe_session* s, const
   });
 }
 
+int llambda_hip_stream_read(const void* data, size_t bytes, uint32_t* out, void* stream) {
+  return guarded([&] {
+    static_assert(LLAMBDA_HIP_STREAM_READ_WORDS == kStreamReadWords, "one out word per wave");
+    if (!data || !out) failf("stream_read: null argument");
+    if (bytes == 0 || bytes % 16 || reinterpret_cast<uintptr_t>(data) % 16)
+      failf("stream_read: %zu bytes at %p: need a positive multiple of 16, 16-byte aligned", bytes,
+            data);
+    HIPC(stream_read_launch(data, bytes, out, static_cast<hipStream_t>(stream)));
+  });
+}
+
 int llambda_hip_select_top_k(const float* logits, size_t n, size_t k, size_t batch,
                              int64_t* top_indices, float* top_logits) {
   return guarded([&] {

@@ -81,6 +81,12 @@ hipError_t dequant_launch(int type, const uint8_t* w, int64_t row_bytes, int64_t
                           int64_t columns, float* out, hipStream_t stream,
                           const int* row_sel = nullptr);
 
+// A plain read of `bytes` (a multiple of 16, 16-byte aligned device memory)
+// by kStreamReadWords waves, each streaming one contiguous slice; out
+// (kStreamReadWords words) receives each wave's XOR of what it read.
+constexpr int kStreamReadWords = 4096;
+hipError_t stream_read_launch(const void* data, size_t bytes, uint32_t* out, hipStream_t stream);
+
 // *first_bad = min(*first_bad, index of the first block whose fp16 scale
 // field is Inf/NaN).
 hipError_t validate_launch(int type, const uint8_t* w, int64_t nblocks,

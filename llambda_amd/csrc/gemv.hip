@@ -481,3 +481,48 @@ hipError_t validate_launch(int type, const uint8_t* w, int64_t nblocks,
 }
 
 }  // namespace llhip
+
+// ------------------------------------------------------- streaming read
+// The read rate this device sustains over one contiguous buffer: the
+// ceiling the GEMV kernels are measured against.  Each wave streams one
+// contiguous slice with 16-byte loads, four in flight per lane; the XOR of
+// everything a wave read goes to out[wave], so the loads cannot be dropped.
+namespace llhip {
+
+constexpr int kStreamWaves = 8;
+
+__global__ void __launch_bounds__(64 * kStreamWaves)
+stream_read_kernel(const u32x4a4* __restrict__ p, int64_t n16, uint32_t* __restrict__ out) {
+  const int lane = threadIdx.x & 63;
+  const int64_t wave = (int64_t)blockIdx.x * kStreamWaves + (threadIdx.x >> 6);
+  const int64_t waves = (int64_t)gridDim.x * kStreamWaves;
+  const int64_t per = (((n16 + waves - 1) / waves) + 63) & ~(int64_t)63;  // whole wave rows
+  const int64_t begin = wave * per;
+  const int64_t end = begin + per < n16 ? begin + per : n16;
+  uint32_t acc = 0;
+  int64_t j = begin;
+  for (; j + 256 <= end; j += 256) {
+    const u32x4a4 a = p[j + lane], b = p[j + 64 + lane], c = p[j + 128 + lane],
+                  d = p[j + 192 + lane];
+    acc ^= (a.x ^ a.y ^ a.z ^ a.w) ^ (b.x ^ b.y ^ b.z ^ b.w) ^ (c.x ^ c.y ^ c.z ^ c.w) ^
+           (d.x ^ d.y ^ d.z ^ d.w);
+  }
+  for (; j < end; j += 64)
+    if (j + lane < end) {
+      const u32x4a4 a = p[j + lane];
+      acc ^= a.x ^ a.y ^ a.z ^ a.w;
+    }
+  for (int off = 32; off; off >>= 1) acc ^= (uint32_t)__shfl_xor((int)acc, off);
+  if (lane == 0) out[wave] = acc;
+}
+
+hipError_t stream_read_launch(const void* data, size_t bytes, uint32_t* out, hipStream_t stream) {
+  if (!data || !out || bytes == 0 || bytes % 16 || reinterpret_cast<uintptr_t>(data) % 16)
+    return hipErrorInvalidValue;
+  hipLaunchKernelGGL(stream_read_kernel, dim3(kStreamReadWords / kStreamWaves),
+                     dim3(64 * kStreamWaves), 0, stream, static_cast<const u32x4a4*>(data),
+                     (int64_t)(bytes / 16), out);
+  return hipGetLastError();
+}
+
+}  // namespace llhip

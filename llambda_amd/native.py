@@ -20,6 +20,8 @@ _lib = None
 # LLAMBDA_HIP_INPUT_ERROR: a MoE run met the reference's own error for its
 # input; the session stays usable
 INPUT_ERROR = -2
+# LLAMBDA_HIP_STREAM_READ_WORDS: words of llambda_hip_stream_read's output
+STREAM_READ_WORDS = 4096
 
 c_int = ctypes.c_int
 c_size = ctypes.c_size_t
@@ -140,6 +142,7 @@ SIGNATURES = {
     "llambda_hip_moe_session_run_device_noalloc": (c_int, [c_void_p, c_void_p, c_void_p, c_size,
                                                            c_void_p]),
     "llambda_hip_select_top_k": (c_int, [c_void_p, c_size, c_size, c_size, c_void_p, c_void_p]),
+    "llambda_hip_stream_read": (c_int, [c_void_p, c_size, c_void_p, c_void_p]),
     "llambda_hip_llama_session_create": (c_int, [ctypes.POINTER(LlamaDesc),
                                                  ctypes.POINTER(c_void_p)]),
     "llambda_hip_llama_session_destroy": (None, [c_void_p]),
