@@ -485,8 +485,9 @@ hipError_t validate_launch(int type, const uint8_t* w, int64_t nblocks,
 // ------------------------------------------------------- streaming read
 // The read rate this device sustains over one contiguous buffer: the
 // ceiling the GEMV kernels are measured against.  Each wave streams one
-// contiguous slice with 16-byte loads, four in flight per lane; the XOR of
-// everything a wave read goes to out[wave], so the loads cannot be dropped.
+// contiguous slice with 16-byte non-temporal loads (the policy the weight
+// streams use), four in flight per lane; the XOR of everything a wave read
+// goes to out[wave], so the loads cannot be dropped.
 namespace llhip {
 
 constexpr int kStreamWaves = 8;
@@ -502,14 +503,16 @@ stream_read_kernel(const u32x4a4* __restrict__ p, int64_t n16, uint32_t* __restr
   uint32_t acc = 0;
   int64_t j = begin;
   for (; j + 256 <= end; j += 256) {
-    const u32x4a4 a = p[j + lane], b = p[j + 64 + lane], c = p[j + 128 + lane],
-                  d = p[j + 192 + lane];
+    const u32x4a4 a = __builtin_nontemporal_load(p + j + lane),
+                  b = __builtin_nontemporal_load(p + j + 64 + lane),
+                  c = __builtin_nontemporal_load(p + j + 128 + lane),
+                  d = __builtin_nontemporal_load(p + j + 192 + lane);
     acc ^= (a.x ^ a.y ^ a.z ^ a.w) ^ (b.x ^ b.y ^ b.z ^ b.w) ^ (c.x ^ c.y ^ c.z ^ c.w) ^
            (d.x ^ d.y ^ d.z ^ d.w);
   }
   for (; j < end; j += 64)
     if (j + lane < end) {
-      const u32x4a4 a = p[j + lane];
+      const u32x4a4 a = __builtin_nontemporal_load(p + j + lane);
       acc ^= a.x ^ a.y ^ a.z ^ a.w;
     }
   for (int off = 32; off; off >>= 1) acc ^= (uint32_t)__shfl_xor((int)acc, off);

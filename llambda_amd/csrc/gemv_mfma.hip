@@ -550,6 +550,11 @@ struct MfmaArgs {
   float* y;
   GemvFuse f;
   int nbuf;
+  // weight stages with the non-temporal policy: launches of eight rounds or
+  // more, whose rows stream far past what the caches keep (the Q6_K head
+  // 128256 x 4096: 76.9 -> 74.3 us); shorter ones keep the default policy,
+  // under which they measured faster (4096^2 Q4_K 5.7 us against 5.9)
+  int nt;
 };
 
 // Workgroup `wg` of `nwg` working on one GEMV (the body of gemv_mfma_kernel
@@ -660,8 +665,13 @@ __device__ __forceinline__ void gemv_mfma_body(uint8_t* lds, int wg, int nwg, co
     uint32_t o[Ch::kLoads];
     const uint8_t* base_al = stage_src(s, o);
     const uint32_t dst = stage_lds + (uint32_t)((s % nbuf) * Ch::kBuffer);
+    if (args.nt) {
 #pragma unroll
-    for (int i = 0; i < Ch::kLoads; ++i) load_lds16(base_al, o[i], dst + 1024u * i);
+      for (int i = 0; i < Ch::kLoads; ++i) load_lds16_nt(base_al, o[i], dst + 1024u * i);
+    } else {
+#pragma unroll
+      for (int i = 0; i < Ch::kLoads; ++i) load_lds16(base_al, o[i], dst + 1024u * i);
+    }
   };
 
   for (int i = threadIdx.x; i < T::kZero / 16; i += blockDim.x)
@@ -910,7 +920,7 @@ static hipError_t launch_mfma(const GemvProblem& p, const GemvFuse& f, hipStream
   // 4 instead of 512 of 3 or 4, +0.2%).
   const int nrounds = (needed + cap - 1) / cap;
   const int grid = std::max(1, nrounds >= 8 ? (needed + nrounds - 1) / nrounds : std::min(needed, cap));
-  const MfmaArgs args{p.weights, p.row_bytes, (int)p.rows, nblk, p.x, p.y, f, nbuf};
+  const MfmaArgs args{p.weights, p.row_bytes, (int)p.rows, nblk, p.x, p.y, f, nbuf, nrounds >= 8};
   hipLaunchKernelGGL(kernel, dim3(grid), dim3(64 * kMfmaWaves), lds, stream, args);
   return hipGetLastError();
 }

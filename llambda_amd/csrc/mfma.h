@@ -98,6 +98,19 @@ __device__ __forceinline__ void load_lds16(const uint8_t* base, uint32_t voff, u
       : "memory");
 }
 
+// load_lds16 with the non-temporal policy: for streams read once (packed
+// weight rows), which then stay out of the caches' way.  Measured on one
+// MI355X over a 431 MB buffer: 7.0 TB/s against 6.0 TB/s with the default
+// policy.
+__device__ __forceinline__ void load_lds16_nt(const uint8_t* base, uint32_t voff, uint32_t lds) {
+  asm volatile(
+      "s_nop 0\n\t"
+      "global_load_lds_dwordx4 %0, %1 nt"
+      :
+      : "v"(voff), "s"(base), "{m0}"(lds)
+      : "memory");
+}
+
 // 64 lanes x 4 bytes from base + voff[lane] to LDS lds + 4 * lane.
 __device__ __forceinline__ void load_lds4(const uint8_t* base, uint32_t voff, uint32_t lds) {
   asm volatile(
