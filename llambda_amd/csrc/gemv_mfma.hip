@@ -790,6 +790,159 @@ __global__ void __launch_bounds__(64 * kMfmaWaves) gemv_mfma_kernel(const MfmaAr
   gemv_mfma_body<TYPE, C, ALIGNED, D, S>(lds, blockIdx.x, gridDim.x, args);
 }
 
+// ------------------------------------------------------------ tile rounds
+// The batch-1 GEMV of long launches whose row is one chunk per wave (K =
+// C x kMfmaWaves blocks, dword-aligned rows): a round is one 16-row tile of
+// the workgroup's contiguous range, and its bytes -- contiguous in HBM --
+// come in by non-temporal DMA as one contiguous run per wave into a tile
+// buffer whose rows sit an odd number of 16-byte pieces apart (a row's pad
+// piece re-reads its last piece, in the same instruction).  Each wave then
+// reads its own chunk of the 16 rows from the buffer and computes it exactly
+// as gemv_mfma_body does, and wave 0 adds the eight partial sums in wave
+// order: the outputs are that kernel's, bit for bit.  (There each wave DMAs
+// its chunk of every row, so the 128-byte lines on chunk boundaries are two
+// waves' requests; non-temporal, they are fetched twice: 1.07x the bytes.
+// One run per wave reads 1.00x.)
+constexpr int kTileMaxLoads = 8;  // DMA instructions (1 KB) per wave and tile
+
+__host__ __device__ constexpr int tile_pitch_pieces(int64_t row_bytes) {
+  return (int)(row_bytes / 16) | 1;  // odd: a fragment's 16 rows in 16 bank quads
+}
+__host__ __device__ constexpr int tile_loads(int64_t row_bytes) {
+  return (16 * tile_pitch_pieces(row_bytes) + 63) / 64;
+}
+// LDS: [0, kZero) zeros | table | group sums | tile buffer | partials (two
+// rounds x waves x 16 rows)
+template <int TYPE>
+constexpr size_t tile_lds_bytes(int nblk, int64_t row_bytes) {
+  using T = MfmaType<TYPE>;
+  return (size_t)T::kZero + (size_t)nblk * (T::kTable + 4 * T::kSums) +
+         1024 * (size_t)tile_loads(row_bytes) + 2 * kMfmaWaves * 16 * sizeof(float);
+}
+
+template <int TYPE, int C>
+__global__ void __launch_bounds__(64 * kMfmaWaves) gemv_tile_kernel(const MfmaArgs args) {
+  extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+  constexpr int S = kMfmaWaves;
+  using T = MfmaType<TYPE>;
+  const uint8_t* __restrict__ w = args.w;
+  const int64_t row_bytes = args.row_bytes;
+  const int rows = args.rows, nblk = args.nblk;
+  const GemvFuse& f = args.f;
+  const int pitch = tile_pitch_pieces(row_bytes), loads = tile_loads(row_bytes);
+  uint8_t* table = lds + T::kZero;
+  float* gsum = reinterpret_cast<float*>(table + nblk * T::kTable);
+  uint8_t* tbuf = reinterpret_cast<uint8_t*>(gsum + nblk * T::kSums);
+  float* partial = reinterpret_cast<float*>(tbuf + 1024 * loads);
+  const uint32_t tbuf_lds = lds_address(tbuf);
+
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int n = lane & 15, g = lane >> 4, a = lane & 15;
+  const uint32_t table_off = T::kZero;
+  uint32_t a_base;
+  bool a_m[4];
+  if constexpr (TYPE == kQ4_K) {
+    a_base = (g == (a >> 2)) ? table_off + (uint32_t)(a * 16) : 0u;
+  } else {
+    const bool act = ((a >> 1) & 1) == (g >> 1);
+    a_base = table_off + (uint32_t)(((a & 3) * 2 + (g & 1)) * 16);
+#pragma unroll
+    for (int m = 0; m < 4; ++m) a_m[m] = act && (a >> 2) == m;
+  }
+  const uint32_t a_stride = (TYPE == kQ4_K && a_base == 0u) ? 0u : (uint32_t)T::kTable;
+
+  // the workgroup's contiguous tile range (workgroups b and b + nwg / 2 --
+  // one CU when the grid is two per CU -- take adjacent ranges)
+  const int tiles = (rows + 15) >> 4, nwg = gridDim.x, wg = blockIdx.x;
+  const int half = (nwg + 1) >> 1;
+  const int rix = wg < half ? 2 * wg : 2 * (wg - half) + 1;
+  const int wg_first = (int)(((int64_t)rix * tiles) / nwg);
+  const int wg_end = (int)(((int64_t)(rix + 1) * tiles) / nwg);
+  const int ntiles = wg_end - wg_first;
+
+  // this wave's run: loads [l0, l0 + nl) of the tile; lane i of load l
+  // writes slot 64 l + i = (row, piece) of the buffer
+  const int per = loads / S, extra = loads - per * S;
+  const int l0 = wave * per + min(wave, extra), nl = per + (wave < extra ? 1 : 0);
+  const uint32_t rb = (uint32_t)row_bytes;
+  const int rp = (int)(row_bytes / 16);  // pieces of a row
+  uint32_t voff[kTileMaxLoads];
+  int vrow[kTileMaxLoads];
+#pragma unroll
+  for (int l = 0; l < kTileMaxLoads; ++l) {
+    const int slot = min(64 * (l0 + l) + lane, 16 * pitch - 1);
+    const int r = slot / pitch;
+    vrow[l] = r;
+    voff[l] = (uint32_t)r * rb + 16u * (uint32_t)min(slot - r * pitch, rp - 1);
+  }
+  auto issue = [&](int tile) {
+    const uint8_t* base = uniform_ptr(w + (int64_t)tile * 16 * row_bytes);
+    const int rmax = rows - 1 - tile * 16;  // rows past the end re-read the last one
+#pragma unroll
+    for (int l = 0; l < kTileMaxLoads; ++l) {
+      if (l < nl) {
+        const uint32_t o = rmax >= 15 ? voff[l]
+                                      : voff[l] - (uint32_t)(vrow[l] - min(vrow[l], rmax)) * rb;
+        load_lds16_nt(base, o, tbuf_lds + 1024u * (uint32_t)(l0 + l));
+      }
+    }
+  };
+
+  for (int i = threadIdx.x; i < T::kZero / 16; i += blockDim.x)
+    reinterpret_cast<u32x4*>(lds)[i] = u32x4{0u, 0u, 0u, 0u};
+  using IT = std::conditional_t<TYPE == kQ4_K, Q4Items, Q6Items>;
+  build_table<IT, S>(table, gsum, args.x, nblk, f.norm_w, f.norm_eps, partial);
+  if (ntiles > 0) issue(wg_first);
+  __syncthreads();
+
+  auto finish_round = [&](int r) {  // wave 0: the round's row sums, in wave order
+    const float* part = partial + (r & 1) * (S * 16);
+    float t = part[n];
+#pragma unroll
+    for (int k = 1; k < S; ++k) t = t + part[k * 16 + n];
+    store_row(f, args.y, rows, (wg_first + r) * 16 + n, t, g == 0);
+  };
+  using Raw = std::conditional_t<TYPE == kQ4_K, Q4Raw, Q6Raw>;
+  const uint8_t* rowp = tbuf + n * (16 * pitch) + wave * (C * T::kBB);
+  for (int r = 0; r < ntiles; ++r) {
+    __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
+    __syncthreads();  // the tile is in LDS; the last round's partial sums too
+    if (r > 0 && wave == 0) finish_round(r - 1);
+    Raw raw[C];
+    [&]<int... BL>(std::integer_sequence<int, BL...>) {
+      ((raw[BL] = [&] {
+         const uint8_t* p = rowp + BL * T::kBB;
+         if constexpr (TYPE == kQ4_K) return q4k_fetch(p, g);
+         else return q6k_fetch<(BL * 210) & 3>(p, g);
+       }()), ...);
+    }(std::make_integer_sequence<int, C>{});
+    __builtin_amdgcn_s_waitcnt(kWaitLgkm0);
+    __syncthreads();  // every wave has its chunk: the buffer takes the next tile
+    if (r + 1 < ntiles) issue(wg_first + r + 1);
+    float acc = 0.f;
+#pragma unroll
+    for (int bl = 0; bl < C; ++bl) {
+      const int b = wave * C + bl;
+      const float* gs = gsum + b * T::kSums;
+      if constexpr (TYPE == kQ4_K) {
+        acc += q4k_block(raw[bl], lds, a_base + (uint32_t)b * a_stride, gs, g);
+      } else {
+        const uint32_t ab = a_base + (uint32_t)b * (uint32_t)T::kTable;
+        const uint32_t am[4] = {a_m[0] ? ab : 0u, a_m[1] ? ab : 0u, a_m[2] ? ab : 0u,
+                                a_m[3] ? ab : 0u};
+        acc += q6k_block(raw[bl], lds, am, gs, g);
+      }
+    }
+    const float v = sum_lane_groups(acc);
+    if (g == 0) partial[(r & 1) * (S * 16) + wave * 16 + n] = v;
+  }
+  if (ntiles > 0) {
+    __syncthreads();
+    if (wave == 0) finish_round(ntiles - 1);
+  }
+}
+
 // Two independent GEMVs in one launch (the decoder's q|k and v rows): the
 // first `grid_a` workgroups run the first, the rest the second, so the
 // second's fixed latency (table, first loads, epilogue) overlaps the first's
@@ -893,6 +1046,31 @@ bool gemv_mfma_supported(const GemvProblem& p) {
   return false;
 }
 
+// The tile-round kernel, on the same persistent grid rule as launch_mfma;
+// hipErrorInvalidValue when its LDS does not allow one workgroup per CU.
+template <int TYPE, int C>
+static hipError_t launch_tile(const GemvProblem& p, const MfmaArgs& args, int tiles,
+                              hipStream_t stream) {
+  const size_t lds = tile_lds_bytes<TYPE>(args.nblk, p.row_bytes);
+  if (lds > kMaxLdsBytes) return hipErrorInvalidValue;
+  const auto kernel = gemv_tile_kernel<TYPE, C>;
+  if (lds > 65536) {
+    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kernel),
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    if (e != hipSuccess) return e;
+  }
+  int per_cu = 0;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, reinterpret_cast<const void*>(kernel),
+                                                   64 * kMfmaWaves, lds) != hipSuccess ||
+      per_cu < 1)
+    per_cu = 1;
+  const int cap = device_cu_count() * per_cu;
+  const int nrounds = (tiles + cap - 1) / cap;
+  const int grid = std::max(1, (tiles + nrounds - 1) / nrounds);
+  hipLaunchKernelGGL(kernel, dim3(grid), dim3(64 * kMfmaWaves), lds, stream, args);
+  return hipGetLastError();
+}
+
 template <int TYPE, int C, bool ALIGNED, int D, int S>
 static hipError_t launch_mfma(const GemvProblem& p, const GemvFuse& f, hipStream_t stream) {
   const int nblk = (int)(p.columns / 256);
@@ -921,6 +1099,11 @@ static hipError_t launch_mfma(const GemvProblem& p, const GemvFuse& f, hipStream
   const int nrounds = (needed + cap - 1) / cap;
   const int grid = std::max(1, nrounds >= 8 ? (needed + nrounds - 1) / nrounds : std::min(needed, cap));
   const MfmaArgs args{p.weights, p.row_bytes, (int)p.rows, nblk, p.x, p.y, f, nbuf, nrounds >= 8};
+  if constexpr (ALIGNED && S == kMfmaWaves) {
+    if (nrounds >= 8 && nblk == C * S && p.row_bytes % 16 == 0 &&
+        tile_loads(p.row_bytes) <= kTileMaxLoads * S)
+      return launch_tile<TYPE, C>(p, args, tiles, stream);
+  }
   hipLaunchKernelGGL(kernel, dim3(grid), dim3(64 * kMfmaWaves), lds, stream, args);
   return hipGetLastError();
 }

@@ -128,6 +128,31 @@ def test_batch_matches_oracle(hip):
             s.close()
 
 
+@pytest.mark.parametrize("type_tag", [ggml.Q6_K, ggml.Q4_K])
+def test_tile_rounds_equal_the_short_launch_kernel(hip, type_tag):
+    """A long launch (128256 rows x 4096: tile rounds, one contiguous DMA run
+    per wave) and short launches over slices of the same rows (the per-wave
+    chunk staging) compute each row with the same arithmetic in the same
+    order: equal bit for bit, first, middle and last (partial) tiles."""
+    rows, columns = 128256 - 7, 4096
+    w, x = make_gemv(type_tag, rows, columns, 23)
+    rb = ggml.row_bytes(type_tag, columns)
+    s = make_hip_session_packed(w, type_tag, rows, columns)
+    try:
+        y = np.empty(rows, dtype=np.float32)
+        s.run_into(y, x)
+    finally:
+        s.close()
+    for first, count in ((0, 4096), (61440, 1000), (rows - 100, 100)):
+        part = make_hip_session_packed(w[first * rb:(first + count) * rb], type_tag, count, columns)
+        try:
+            yp = np.empty(count, dtype=np.float32)
+            part.run_into(yp, x)
+        finally:
+            part.close()
+        assert np.array_equal(yp, y[first:first + count]), (first, count)
+
+
 def test_scaling_is_exact(hip):
     """y(2x) = 2 y(x) bit for bit: power-of-two scaling commutes with every
     rounding, so any mismatch is a kernel bug."""
