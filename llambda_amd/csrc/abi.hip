@@ -506,6 +506,7 @@ struct llambda_hip_moe_session {
   hipStream_t stream = nullptr;
   MoePlan plan{};
   DevBuf router, bias, gate, up, down, sh_gate, sh_up, sh_down, lat_down, lat_up;
+  DevBuf up_g, down_g, sh_up_g, sh_down_g;  // stage-major copies (group pipeline)
   DevBuf logits, router_part, top_idx, top_w, shared_w, perm, chunks, chunk_counts,
       down_out, error, xq, xsum, aq, asum, lat, lq, lsum, lat_y;
   DevBuf x, y;     // device staging for the host-pointer runs
@@ -727,6 +728,30 @@ int llambda_hip_moe_session_create(const llambda_hip_moe_desc* d,
                        H * (Fs / block_weights(d->shared_down_type)), s->stream, "ffn_down_shexp");
         p.sh_up = s->sh_up.as<uint8_t>();
         p.sh_down = s->sh_down.as<uint8_t>();
+      }
+      // the group pipeline's stage-major copies of the one-matrix launches
+      // weights (Q5_0 / Q8_0 relu^2 up and every down), made on the device
+      auto stage_major = [&](DevBuf& dst, const DevBuf& src, int type, int64_t slabs, int64_t rows,
+                             int64_t columns, const char* what) -> const uint8_t* {
+        if (!moe_group_pipeline_types(type)) return nullptr;
+        dst.alloc((size_t)moe_repack_bytes(type, slabs, rows, columns) + kWeightPad, what);
+        HIPC(moe_repack_launch(type, src.as<uint8_t>(), slabs, rows, columns, dst.as<uint8_t>(),
+                               s->stream));
+        return dst.as<uint8_t>();
+      };
+      if (!qwen) {
+        p.up_g = stage_major(s->up_g, s->up, d->up_type, E, F, din, "ffn_up_exps (stage-major)");
+        p.up_g_stride = moe_repack_bytes(d->up_type, 1, F, din);
+      }
+      p.down_g = stage_major(s->down_g, s->down, d->down_type, E, dout, F,
+                             "ffn_down_exps (stage-major)");
+      p.down_g_stride = moe_repack_bytes(d->down_type, 1, dout, F);
+      if (Fs > 0) {
+        if (!qwen)
+          p.sh_up_g = stage_major(s->sh_up_g, s->sh_up, d->shared_up_type, 1, Fs, H,
+                                  "ffn_up_shexp (stage-major)");
+        p.sh_down_g = stage_major(s->sh_down_g, s->sh_down, d->shared_down_type, 1, H, Fs,
+                                  "ffn_down_shexp (stage-major)");
       }
       s->chunk_counts.alloc(2 * sizeof(int), "chunk counts");
       s->error.alloc(sizeof(int), "error flag");

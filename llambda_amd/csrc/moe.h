@@ -59,6 +59,13 @@ struct MoePlan {
   const uint8_t* lat_down;
   const uint8_t* lat_up;
   int out_w;           // row stride of down_out: max(hidden, latent_out)
+  // the group pipeline's one-matrix launches (Q5_0 / Q8_0: relu^2 up, down)
+  // read these stage-major copies (moe_repack_launch); slab strides in bytes
+  const uint8_t* up_g;
+  const uint8_t* down_g;
+  const uint8_t* sh_up_g;
+  const uint8_t* sh_down_g;
+  int64_t up_g_stride, down_g_stride;
   // scratch, sized for `capacity` tokens
   int capacity;
   float* logits;       // [capacity][experts + 1]
@@ -155,6 +162,13 @@ hipError_t split_rows_launch(const float* x, int T, int K, int64_t x_stride, uin
 hipError_t moe_gemm_launch(int type, int epi, const MoeGemmArgs& a, int mt, int max_chunks,
                            hipStream_t stream);
 bool moe_group_pipeline_types(int type);
+// The stage-major copy of `slabs` slabs of `rows` packed rows of `columns`
+// (Q5_0 / Q8_0) that the group pipeline's one-matrix launches read: per slab,
+// per 64-row tile, per stage of two 32-blocks, the 64 rows' two blocks back
+// to back (zeros past the slab's rows and past an odd block count).
+int64_t moe_repack_bytes(int type, int64_t slabs, int64_t rows, int64_t columns);
+hipError_t moe_repack_launch(int type, const uint8_t* src, int64_t slabs, int64_t rows,
+                             int64_t columns, uint8_t* dst, hipStream_t stream);
 
 // One token's down products and their combine in one launch (moe_mfma.hip):
 // a.chunks / a.chunk_counts / a.perm as topk_gate_kernel writes them for a

@@ -389,6 +389,12 @@ hipError_t moe_forward_launch(const MoePlan& p, const float* x, float* y, int to
     a.gate_jpl = jpl_for(E);
     a.plan = p;
   }
+  const bool staged_up = mt == 4 && epi == kEpiRelu2;  // one matrix: the stage-major copies
+  if (staged_up) {
+    a.w0 = p.up_g;
+    a.expert_stride = p.up_g_stride;
+    a.s_w0 = p.sh_up_g;
+  }
   e = moe_gemm_launch(p.up_type, epi, a, mt,
                       fuse_gate ? K + (joint_up ? 1 : 0)
                                 : routed_chunks + (joint_up ? shared_chunks : 0),
@@ -397,7 +403,7 @@ hipError_t moe_forward_launch(const MoePlan& p, const float* x, float* y, int to
   if (has_shared && !joint_up) {
     a = up;
     a.group = 1;
-    a.w0 = p.variant == kQwen3Next ? p.sh_gate : p.sh_up;
+    a.w0 = staged_up ? p.sh_up_g : p.variant == kQwen3Next ? p.sh_gate : p.sh_up;
     a.w1 = p.sh_up;
     a.row_bytes = row_bytes_of(p.sh_up_type, H);
     a.expert_stride = 0;
@@ -447,13 +453,18 @@ hipError_t moe_forward_launch(const MoePlan& p, const float* x, float* y, int to
     c.error_out = error_out;
     return moe_down_combine_launch(p.down_type, a, c, s);
   }
+  if (mt == 4) {
+    a.w0 = p.down_g;
+    a.expert_stride = p.down_g_stride;
+    a.s_w0 = p.sh_down_g;
+  }
   e = moe_gemm_launch(p.down_type, kEpiDown, a, mt, routed_chunks + (joint_down ? shared_chunks : 0), s);
   if (e != hipSuccess) return e;
   if (has_shared && !joint_down) {
     a = down;
     a.group = 1;
     a.K = p.shared_ffn;
-    a.w0 = p.sh_down;
+    a.w0 = mt == 4 ? p.sh_down_g : p.sh_down;
     a.row_bytes = row_bytes_of(p.sh_down_type, p.shared_ffn);
     a.expert_stride = 0;
     e = moe_gemm_launch(p.sh_down_type, kEpiDown, a, mt, shared_chunks, s);

@@ -1411,6 +1411,7 @@ struct GroupB<kQ8_0> {
 template <int TYPE, int EPI>
 struct GroupShape {
   static constexpr int NB = EPI == kEpiSwiglu ? 2 : 1;
+  static constexpr int RUN = 128 * GroupB<TYPE>::kBlock;  // stage-major run: 64 rows x 2 blocks
   static constexpr int ROWS = 64 / NB;  // rows per matrix and wave
   static constexpr int NS = ROWS / 16;
   static constexpr int WG_ROWS = kGroupWaves * ROWS;
@@ -1421,11 +1422,11 @@ struct GroupShape {
   static constexpr int LDS = 2 * STAGE;
 };
 
-// Dword i of row r of a wave's weight stage (matrix nb): row-major lines of
-// P pieces for one matrix, piece-major for two.
-template <int NB, int P>
+// Dword i of row r of a wave's weight stage (matrix nb): one matrix, the
+// stage-major run (rows RP = two blocks' bytes apart); two, piece-major.
+template <int NB, int P, int RP>
 __device__ __forceinline__ uint32_t pm_dword(const uint8_t* wbuf, int nb, int r, uint32_t i) {
-  if constexpr (NB == 1) return *reinterpret_cast<const uint32_t*>(wbuf + r * (16 * P) + 4 * i);
+  if constexpr (NB == 1) return *reinterpret_cast<const uint32_t*>(wbuf + r * RP + 4 * i);
   return *reinterpret_cast<const uint32_t*>(wbuf + (((i >> 2) * NB + nb) * 64 + r) * 16 + 4 * (i & 3));
 }
 
@@ -1437,22 +1438,22 @@ __device__ __forceinline__ typename GemmB<TYPE>::Raw group_fetch(const uint8_t* 
   if constexpr (TYPE == kQ5_0) {
     const uint32_t o = sh + 22u * (uint32_t)j;
     const uint32_t os = (o + 6u + 8u * (uint32_t)(g & 1)) >> 2, ob = (o + 2u + (uint32_t)g) >> 2;
-    constexpr int P = GroupB<TYPE>::kPieces;
-    return u32x4{pm_dword<NB, P>(wbuf, nb, r, os), pm_dword<NB, P>(wbuf, nb, r, os + 1u),
-                 pm_dword<NB, P>(wbuf, nb, r, os + 2u), pm_dword<NB, P>(wbuf, nb, r, ob)};
+    constexpr int P = GroupB<TYPE>::kPieces, RP = 2 * GroupB<TYPE>::kBlock;
+    return u32x4{pm_dword<NB, P, RP>(wbuf, nb, r, os), pm_dword<NB, P, RP>(wbuf, nb, r, os + 1u),
+                 pm_dword<NB, P, RP>(wbuf, nb, r, os + 2u), pm_dword<NB, P, RP>(wbuf, nb, r, ob)};
   } else {
     const uint32_t os = (sh + 34u * (uint32_t)j + 2u + 8u * (uint32_t)g) >> 2;
-    constexpr int P = GroupB<TYPE>::kPieces;
-    return u32x4{pm_dword<NB, P>(wbuf, nb, r, os), pm_dword<NB, P>(wbuf, nb, r, os + 1u),
-                 pm_dword<NB, P>(wbuf, nb, r, os + 2u), 0u};
+    constexpr int P = GroupB<TYPE>::kPieces, RP = 2 * GroupB<TYPE>::kBlock;
+    return u32x4{pm_dword<NB, P, RP>(wbuf, nb, r, os), pm_dword<NB, P, RP>(wbuf, nb, r, os + 1u),
+                 pm_dword<NB, P, RP>(wbuf, nb, r, os + 2u), 0u};
   }
 }
 template <int TYPE, int NB>
 __device__ __forceinline__ void group_scale(const uint8_t* wbuf, int nb, int r, uint32_t sh, int j,
                                             float& delta, float& c) {
   const uint32_t o = sh + (uint32_t)GroupB<TYPE>::kBlock * (uint32_t)j;  // even
-  const uint32_t bits =
-      (pm_dword<NB, GroupB<TYPE>::kPieces>(wbuf, nb, r, o >> 2) >> (8 * (o & 3u))) & 0xFFFFu;
+  const uint32_t bits = (pm_dword<NB, GroupB<TYPE>::kPieces, 2 * GroupB<TYPE>::kBlock>(
+                             wbuf, nb, r, o >> 2) >> (8 * (o & 3u))) & 0xFFFFu;
   delta = half_bits_to_float(bits);
   if constexpr (TYPE == kQ5_0) c = 144.f * delta;
   else c = 128.f * delta;
@@ -1516,12 +1517,12 @@ __global__ void __launch_bounds__(64 * kGroupWaves, 2) moe_group_kernel(MoeGemmA
   // (offsets without the stage's, 4-byte aligned: a stage spans a multiple
   // of 4 bytes)
   const uint32_t brow = (uint32_t)min(n0 + (lane & (Sh::ROWS - 1)), a.N - 1) * rb;
+  // one matrix: the stage-major layout (moe_repack_launch), this wave's run
+  // of each stage read whole -- instruction q takes its bytes 1024 q ..
+  // 1024 q + 1023, lanes past the run re-reading its last piece
   uint32_t wdma[Sh::PIECES];
 #pragma unroll
-  for (int q = 0; q < Sh::PIECES; ++q) {
-    const int slot = 64 * q + lane, r = slot / Sh::PIECES, c = slot - r * Sh::PIECES;
-    wdma[q] = (((uint32_t)min(n0 + r, a.N - 1) * rb) & ~3u) + 16u * (uint32_t)c;
-  }
+  for (int q = 0; q < Sh::PIECES; ++q) wdma[q] = (uint32_t)min(16 * (64 * q + lane), Sh::RUN - 16);
   // activation DMA: this wave's instructions k = wave + 4 u take token
   // 4 k + (l >> 4) and piece (l & 15) ^ (token & 15) into slot l of block k
   uint32_t adma[4];
@@ -1535,7 +1536,7 @@ __global__ void __launch_bounds__(64 * kGroupWaves, 2) moe_group_kernel(MoeGemmA
   // 16 apart: row_bytes * 16 is a multiple of 4), so the subtiles' LDS words
   // sit at constant offsets from one address.  (A row past the last one
   // reads the clamped row's bytes at this shift; its outputs are dropped.)
-  const uint32_t sh0 = ((uint32_t)(n0 + n) * rb) & 3u;
+  const uint32_t sh0 = NB == 1 ? 0u : ((uint32_t)(n0 + n) * rb) & 3u;  // runs: rows on dwords
   uint32_t sh[NS];
 #pragma unroll
   for (int m = 0; m < NS; ++m) sh[m] = sh0;
@@ -1558,8 +1559,10 @@ __global__ void __launch_bounds__(64 * kGroupWaves, 2) moe_group_kernel(MoeGemmA
     const uint32_t wst = stg + Sh::A_BYTES + (uint32_t)wave * Sh::B_BYTES;
     const uint32_t sto = (uint32_t)st * (uint32_t)(2 * BB);
     if constexpr (NB == 1) {
+      const uint8_t* run =
+          uniform_ptr(base[0] + (int64_t)((n0 >> 6) * nstage + st) * Sh::RUN);
 #pragma unroll
-      for (int q = 0; q < Sh::PIECES; ++q) load_lds16(base[0], wdma[q] + sto, wst + 1024u * (uint32_t)q);
+      for (int q = 0; q < Sh::PIECES; ++q) load_lds16(run, wdma[q], wst + 1024u * (uint32_t)q);
     } else {
       const uint32_t off = (brow + sto) & ~3u;
 #pragma unroll
@@ -1864,6 +1867,50 @@ static hipError_t launch_group_epi(int type, const MoeGemmArgs& a, int max_chunk
 }
 
 bool moe_group_pipeline_types(int type) { return type == kQ5_0 || type == kQ8_0; }
+
+// The stage-major layout of the group pipeline's one-matrix launches: per
+// slab, per 64-row tile, per stage of two blocks, the tile's 64 rows' two
+// blocks back to back (a wave's stage then comes in as one contiguous run;
+// rows past the slab's and the block past an odd count are zeros).
+static int64_t repack_slab_bytes(int type, int64_t rows, int64_t columns) {
+  const int64_t bb = block_bytes(type), nblk = columns / 32;
+  return (rows + 63) / 64 * ((nblk + 1) / 2) * 128 * bb;
+}
+int64_t moe_repack_bytes(int type, int64_t slabs, int64_t rows, int64_t columns) {
+  return slabs * repack_slab_bytes(type, rows, columns);
+}
+
+__global__ void __launch_bounds__(256)
+moe_repack_kernel(const uint8_t* __restrict__ src, int64_t rows, int64_t rb, int nblk, int bb,
+                  int ntile, int nstage, uint8_t* __restrict__ dst, int64_t total) {
+  const int64_t run = 128 * (int64_t)bb;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total;
+       i += (int64_t)gridDim.x * blockDim.x) {
+    int64_t q = i / run;
+    const int o = (int)(i - q * run);
+    const int stage = (int)(q % nstage);
+    q /= nstage;
+    const int tile = (int)(q % ntile);
+    const int64_t slab = q / ntile;
+    const int r = o / (2 * bb), rest = o - r * 2 * bb, j = rest / bb, b = rest - j * bb;
+    const int64_t row = (int64_t)tile * 64 + r;
+    const int blk = 2 * stage + j;
+    dst[i] = row < rows && blk < nblk ? src[(slab * rows + row) * rb + (int64_t)blk * bb + b] : 0;
+  }
+}
+
+hipError_t moe_repack_launch(int type, const uint8_t* src, int64_t slabs, int64_t rows,
+                             int64_t columns, uint8_t* dst, hipStream_t stream) {
+  if (!moe_group_pipeline_types(type) || columns % 32 || rows <= 0 || slabs <= 0)
+    return hipErrorInvalidValue;
+  const int bb = block_bytes(type), nblk = (int)(columns / 32);
+  const int ntile = (int)((rows + 63) / 64), nstage = (nblk + 1) / 2;
+  const int64_t total = moe_repack_bytes(type, slabs, rows, columns);
+  const int grid = (int)std::min<int64_t>((total + 255) / 256, 65536);
+  hipLaunchKernelGGL(moe_repack_kernel, dim3(grid), dim3(256), 0, stream, src, rows,
+                     nblk * (int64_t)bb, nblk, bb, ntile, nstage, dst, total);
+  return hipGetLastError();
+}
 
 template <int TYPE, bool ALIGNED>
 static hipError_t launch_combine_t(const MoeGemmArgs& a_in, const MoeCombineArgs& c,
