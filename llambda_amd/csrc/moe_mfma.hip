@@ -1393,6 +1393,25 @@ moe_down_combine_kernel(MoeGemmArgs a, MoeCombineArgs cb) {
 // then lo MFMA, per-group delta fma in group order, the -c * sum offsets of
 // each 256-element chunk after its eight groups), so a token's output does
 // not depend on the pipeline, and hence on the batch, it runs in.
+// Q5_0 in the stage-major lane order (moe_repack_launch): row r of a wave's
+// stage holds dwords [4j + g] = lane g's nibbles of block j, [8 + j] = the
+// block's qh, [10] = both deltas.  Codes and scales equal GemmB<kQ5_0>'s.
+__device__ __forceinline__ u32x4 staged_q5_fetch(const uint8_t* row, int j, int g) {
+  const uint32_t* w = reinterpret_cast<const uint32_t*>(row);
+  return u32x4{w[4 * j + g], w[8 + j], 0u, 0u};
+}
+__device__ __forceinline__ bf16x8 staged_q5_decode(const u32x4& w, int g) {
+  const uint32_t hb = __builtin_amdgcn_ubfe(w[1], 8u * (uint32_t)g, 8u);
+  const uint32_t c0 = (w[0] & 0x0F0F0F0Fu) | (spread_nibble(hb & 15u) << 4);
+  const uint32_t c1 = ((w[0] >> 4) & 0x0F0F0F0Fu) | (spread_nibble(hb >> 4) << 4);
+  return codes_to_b(c0, c1);
+}
+__device__ __forceinline__ void staged_q5_scale(const uint8_t* row, int j, float& delta, float& c) {
+  const uint32_t d = reinterpret_cast<const uint32_t*>(row)[10];
+  delta = half_bits_to_float(j ? d >> 16 : d & 0xFFFFu);
+  c = 144.f * delta;
+}
+
 constexpr int kGroupWaves = 4;
 constexpr int kGroupTiles = 4;    // 16-token tiles per chunk
 constexpr int kGroupAPieces = 17; // 16 pieces of split activations + 1 of group sums
@@ -1412,6 +1431,7 @@ template <int TYPE, int EPI>
 struct GroupShape {
   static constexpr int NB = EPI == kEpiSwiglu ? 2 : 1;
   static constexpr int RUN = 128 * GroupB<TYPE>::kBlock;  // stage-major run: 64 rows x 2 blocks
+  static constexpr int RP = 2 * GroupB<TYPE>::kBlock;     // a row's bytes in the run
   static constexpr int ROWS = 64 / NB;  // rows per matrix and wave
   static constexpr int NS = ROWS / 16;
   static constexpr int WG_ROWS = kGroupWaves * ROWS;
@@ -1464,6 +1484,7 @@ __global__ void __launch_bounds__(64 * kGroupWaves, 2) moe_group_kernel(MoeGemmA
   using B = GemmB<TYPE>;
   using Sh = GroupShape<TYPE, EPI>;
   constexpr int NB = Sh::NB, NS = Sh::NS, MT = kGroupTiles;
+  constexpr bool kStagedQ5 = TYPE == kQ5_0 && NB == 1;  // the lane-ordered stage-major rows
   constexpr int BB = GroupB<TYPE>::kBlock;
   extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
 
@@ -1627,9 +1648,15 @@ __global__ void __launch_bounds__(64 * kGroupWaves, 2) moe_group_kernel(MoeGemmA
         for (int m = 0; m < NS; ++m)
 #pragma unroll
           for (int nb = 0; nb < NB; ++nb) {
-            raw[m][nb] = group_fetch<TYPE, NB>(wbuf, nb, 16 * m + n, sh[m], jj, g);
             float c;
-            group_scale<TYPE, NB>(wbuf, nb, 16 * m + n, sh[m], jj, dl[m][nb], c);
+            if constexpr (kStagedQ5) {
+              const uint8_t* row = wbuf + (16 * m + n) * Sh::RP;
+              raw[m][nb] = staged_q5_fetch(row, jj, g);
+              staged_q5_scale(row, jj, dl[m][nb], c);
+            } else {
+              raw[m][nb] = group_fetch<TYPE, NB>(wbuf, nb, 16 * m + n, sh[m], jj, g);
+              group_scale<TYPE, NB>(wbuf, nb, 16 * m + n, sh[m], jj, dl[m][nb], c);
+            }
             // (q = j8 >> 2 is uniform: a select per lane, not an indexed write)
             const bool mine = (j8 & 3) == g;
             cneg[m][nb][0] = (mine && j8 < 4) ? -c : cneg[m][nb][0];
@@ -1647,7 +1674,9 @@ __global__ void __launch_bounds__(64 * kGroupWaves, 2) moe_group_kernel(MoeGemmA
         for (int m = 0; m < NS; ++m)
 #pragma unroll
           for (int nb = 0; nb < NB; ++nb) {
-            const typename B::Frag bf = B::decode(raw[m][nb], sh[m], jj, g);
+            typename B::Frag bf;
+            if constexpr (kStagedQ5) bf = staged_q5_decode(raw[m][nb], g);
+            else bf = B::decode(raw[m][nb], sh[m], jj, g);
             const float delta = dl[m][nb];
 #pragma unroll
             for (int i = 0; i < NT; ++i) {
@@ -1871,7 +1900,10 @@ bool moe_group_pipeline_types(int type) { return type == kQ5_0 || type == kQ8_0;
 // The stage-major layout of the group pipeline's one-matrix launches: per
 // slab, per 64-row tile, per stage of two blocks, the tile's 64 rows' two
 // blocks back to back (a wave's stage then comes in as one contiguous run;
-// rows past the slab's and the block past an odd count are zeros).
+// rows past the slab's and the block past an odd count are zeros).  Q8_0
+// blocks keep their bytes; a Q5_0 row's 44 bytes are reordered so that MFMA
+// lane g finds its eight codes' nibbles in one aligned dword and their high
+// bits in byte g of the block's qh word (staged_q5_decode).
 static int64_t repack_slab_bytes(int type, int64_t rows, int64_t columns) {
   const int64_t bb = block_bytes(type), nblk = columns / 32;
   return (rows + 63) / 64 * ((nblk + 1) / 2) * 128 * bb;
@@ -1892,10 +1924,39 @@ moe_repack_kernel(const uint8_t* __restrict__ src, int64_t rows, int64_t rb, int
     q /= nstage;
     const int tile = (int)(q % ntile);
     const int64_t slab = q / ntile;
-    const int r = o / (2 * bb), rest = o - r * 2 * bb, j = rest / bb, b = rest - j * bb;
+    const int r = o / (2 * bb), rest = o - r * 2 * bb;
     const int64_t row = (int64_t)tile * 64 + r;
-    const int blk = 2 * stage + j;
-    dst[i] = row < rows && blk < nblk ? src[(slab * rows + row) * rb + (int64_t)blk * bb + b] : 0;
+    const uint8_t* rsrc = src + (slab * rows + row) * rb;
+    uint8_t v = 0;
+    if (bb == 22) {
+      // Q5_0, lane order: [0, 32) the nibble dwords N[j][g] (block j, lane
+      // g: byte b = code 8g + b | code 8g + 4 + b << 4), [32, 40) the qh
+      // words of blocks 0 and 1, [40, 44) their deltas
+      int j, off;
+      if (rest < 32) j = rest >> 4;
+      else if (rest < 40) j = (rest - 32) >> 2;
+      else j = (rest - 40) >> 1;
+      const int blk = 2 * stage + j;
+      if (row < rows && blk < nblk) {
+        const uint8_t* blkp = rsrc + (int64_t)blk * bb;
+        if (rest < 32) {
+          const int g = (rest & 15) >> 2, b = rest & 3;
+          auto nib = [&](int e) { return e < 16 ? blkp[6 + e] & 15 : blkp[6 + e - 16] >> 4; };
+          v = (uint8_t)(nib(8 * g + b) | (nib(8 * g + 4 + b) << 4));
+        } else if (rest < 40) {
+          off = (rest - 32) & 3;
+          v = blkp[2 + off];
+        } else {
+          off = (rest - 40) & 1;
+          v = blkp[off];
+        }
+      }
+    } else {
+      const int j = rest / bb, b = rest - j * bb;
+      const int blk = 2 * stage + j;
+      if (row < rows && blk < nblk) v = rsrc[(int64_t)blk * bb + b];
+    }
+    dst[i] = v;
   }
 }
 
