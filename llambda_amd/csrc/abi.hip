@@ -133,6 +133,10 @@ struct DevBuf {
   }
   template <typename T>
   T* as() const { return static_cast<T*>(ptr); }
+  void swap(DevBuf& o) {
+    std::swap(ptr, o.ptr);
+    std::swap(bytes, o.bytes);
+  }
 };
 
 // Pinned host memory staging the host-pointer runs.  A copy from or to it
@@ -645,9 +649,12 @@ int llambda_hip_moe_session_create(const llambda_hip_moe_desc* d,
         failf("moe_session_create: expert tensors must be Q4_K, Q6_K, Q5_0 or Q8_0 (got tag %d)", t);
     const int64_t up_rb = checked_row_bytes(d->up_type, din, "ffn_up_exps");
     const int64_t down_rb = checked_row_bytes(d->down_type, F, "ffn_down_exps");
-    // the expert kernels address one expert's slab with 32-bit offsets
-    if (F * up_rb + (int64_t)kWeightPad >= ((int64_t)1 << 31) ||
-        dout * down_rb + (int64_t)kWeightPad >= ((int64_t)1 << 31))
+    // the expert kernels address one expert's slab (in its device layout)
+    // with 32-bit offsets
+    if (std::max(F * up_rb, moe_slab_bytes(d->up_type, F, din)) + (int64_t)kWeightPad >=
+            ((int64_t)1 << 31) ||
+        std::max(dout * down_rb, moe_slab_bytes(d->down_type, dout, F)) + (int64_t)kWeightPad >=
+            ((int64_t)1 << 31))
       failf("moe_session_create: one expert's slab exceeds 2 GiB");
     const int64_t ld_rb = Li ? checked_row_bytes(d->latent_down_type, H, "ffn_latent_down") : 0;
     const int64_t lu_rb = Lo ? checked_row_bytes(d->latent_up_type, Lo, "ffn_latent_up") : 0;
@@ -752,6 +759,31 @@ int llambda_hip_moe_session_create(const llambda_hip_moe_desc* d,
                                   "ffn_up_shexp (stage-major)");
         p.sh_down_g = stage_major(s->sh_down_g, s->sh_down, d->shared_down_type, 1, H, Fs,
                                   "ffn_down_shexp (stage-major)");
+      }
+      // K-quant expert tensors: the tile-major layout replaces the packed rows
+      auto tile_major = [&](DevBuf& buf, int type, int64_t slabs, int64_t rows, int64_t columns,
+                            const uint8_t*& ptr, const char* what) {
+        if (!moe_tiled_type(type)) return;
+        const int64_t bytes = slabs * moe_slab_bytes(type, rows, columns);
+        DevBuf t;
+        t.alloc((size_t)bytes + kWeightPad, what);
+        HIPC(hipMemsetAsync(t.as<uint8_t>() + bytes, 0, kWeightPad, s->stream));
+        HIPC(moe_tile_launch(type, buf.as<uint8_t>(), slabs, rows, columns, t.as<uint8_t>(),
+                             s->stream));
+        HIPC(hipStreamSynchronize(s->stream));
+        buf.swap(t);
+        ptr = buf.as<uint8_t>();
+      };
+      if (qwen) tile_major(s->gate, d->gate_type, E, F, din, p.gate, "ffn_gate_exps (tile-major)");
+      tile_major(s->up, d->up_type, E, F, din, p.up, "ffn_up_exps (tile-major)");
+      tile_major(s->down, d->down_type, E, dout, F, p.down, "ffn_down_exps (tile-major)");
+      if (Fs > 0) {
+        if (qwen)
+          tile_major(s->sh_gate, d->shared_gate_type, 1, Fs, H, p.sh_gate,
+                     "ffn_gate_shexp (tile-major)");
+        tile_major(s->sh_up, d->shared_up_type, 1, Fs, H, p.sh_up, "ffn_up_shexp (tile-major)");
+        tile_major(s->sh_down, d->shared_down_type, 1, H, Fs, p.sh_down,
+                   "ffn_down_shexp (tile-major)");
       }
       s->chunk_counts.alloc(2 * sizeof(int), "chunk counts");
       s->error.alloc(sizeof(int), "error flag");

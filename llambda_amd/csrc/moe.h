@@ -39,7 +39,9 @@ struct MoePlan {
   int hidden, experts, top_k, ffn, shared_ffn;
   float weights_scale;
   int weights_norm;
-  // weights
+  // weights.  Expert tensors of a K-quant type (Q4_K, Q6_K) are held in the
+  // tile-major layout (moe_tile_launch), the others as packed GGUF rows;
+  // moe_slab_bytes gives one expert's bytes in either.
   const float* router;   // [(experts + (variant == qwen3next && shared)) ][hidden]
   const float* bias;     // [experts], nemotron
   int gate_type, up_type, down_type;
@@ -169,6 +171,17 @@ bool moe_group_pipeline_types(int type);
 int64_t moe_repack_bytes(int type, int64_t slabs, int64_t rows, int64_t columns);
 hipError_t moe_repack_launch(int type, const uint8_t* src, int64_t slabs, int64_t rows,
                              int64_t columns, uint8_t* dst, hipStream_t stream);
+// The tile-major layout of K-quant (Q4_K, Q6_K) expert tensors, which the
+// grouped products and the one-token down+combine read: per slab, per
+// 16-row tile, per 256-weight chunk, the 16 rows' chunks back to back, each
+// padded to a dword (Q4_K 144 bytes, Q6_K 212); rows past the slab's are
+// zeros.  A wave's stage of a chunk is then one contiguous run whose rows
+// start on dwords.  moe_slab_bytes: one slab's bytes in the device layout of
+// `type` (tile-major for K-quants, packed rows otherwise).
+bool moe_tiled_type(int type);
+int64_t moe_slab_bytes(int type, int64_t rows, int64_t columns);
+hipError_t moe_tile_launch(int type, const uint8_t* src, int64_t slabs, int64_t rows,
+                           int64_t columns, uint8_t* dst, hipStream_t stream);
 
 // One token's down products and their combine in one launch (moe_mfma.hip):
 // a.chunks / a.chunk_counts / a.perm as topk_gate_kernel writes them for a

@@ -374,7 +374,7 @@ hipError_t moe_forward_launch(const MoePlan& p, const float* x, float* y, int to
   a.w0 = p.variant == kQwen3Next ? p.gate : p.up;
   a.w1 = p.up;
   a.row_bytes = row_bytes_of(p.up_type, din);
-  a.expert_stride = a.row_bytes * p.ffn;
+  a.expert_stride = moe_slab_bytes(p.up_type, p.ffn, din);
   a.N = p.ffn;
   if (joint_up) {
     a.joint = 1;
@@ -432,7 +432,7 @@ hipError_t moe_forward_launch(const MoePlan& p, const float* x, float* y, int to
   a.N = dout;
   a.w0 = p.down;
   a.row_bytes = row_bytes_of(p.down_type, p.ffn);
-  a.expert_stride = a.row_bytes * dout;
+  a.expert_stride = moe_slab_bytes(p.down_type, dout, p.ffn);
   const bool joint_down = has_shared && p.sh_down_type == p.down_type;
   if (joint_down) {
     a.joint = 1;

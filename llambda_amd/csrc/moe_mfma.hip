@@ -283,6 +283,7 @@ template <>
 struct GemmB<kQ4_K> {
   static constexpr int kSpan = 144, kPieces = 9, kPitch = odd_pitch(kPieces), kSteps = 8,
                        kStepK = 32;
+  static constexpr int kTilePitch = 144;  // tile-major row chunk (0: packed rows)
   static constexpr bool kWide = true;
   // c = kCd * delta (0: c also carries the block minimum)
   static constexpr float kCd = 0.f;
@@ -325,6 +326,7 @@ template <>
 struct GemmB<kQ6_K> {
   static constexpr int kSpan = 210, kPieces = 14, kPitch = odd_pitch(kPieces), kSteps = 16,
                        kStepK = 16;
+  static constexpr int kTilePitch = 212;
   static constexpr bool kWide = false;
   static constexpr float kCd = 160.f;
   typedef shortx4 Frag;
@@ -362,6 +364,7 @@ template <>
 struct GemmB<kQ5_0> {
   static constexpr int kSpan = 176, kPieces = 12, kPitch = odd_pitch(kPieces), kSteps = 8,
                        kStepK = 32;
+  static constexpr int kTilePitch = 0;
   static constexpr bool kWide = true;
   static constexpr float kCd = 144.f;
   typedef bf16x8 Frag;
@@ -396,6 +399,7 @@ template <>
 struct GemmB<kQ8_0> {
   static constexpr int kSpan = 272, kPieces = 18, kPitch = odd_pitch(kPieces), kSteps = 8,
                        kStepK = 32;
+  static constexpr int kTilePitch = 0;
   static constexpr bool kWide = true;
   static constexpr float kCd = 128.f;
   typedef bf16x8 Frag;
@@ -552,6 +556,8 @@ moe_gemm_kernel(MoeGemmArgs args) {
   using B = GemmB<TYPE>;
   using Sh = GemmShape<TYPE, EPI, PIPE>;
   constexpr int NB = Sh::NB, NS = Sh::NS, NQ = B::kSteps / 4, KS = B::kSteps;
+  constexpr bool TILED = B::kTilePitch != 0;  // tile-major weights (K-quants)
+  static_assert(!TILED || ALIGNED, "tile-major rows start on dwords");
   typedef AFrag<B::kWide> AF;
   extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
 
@@ -691,14 +697,18 @@ moe_gemm_kernel(MoeGemmArgs args) {
 
   const int groups = a.K / B::kStepK;
   const int nchunk = (a.K + 255) >> 8;
+  const int last_tile = (a.N - 1) >> 4;  // tile-major: the slab's last 16-row tile
 
   // Issue chunk kc's loads into stage `slot`: the rows; for the decode
   // pipeline also the token's 256 split elements (1 KB) and 16 group sums.
   // Lane l of load instruction i carries piece 64 i + l of the stage: row
   // r = piece / PPR, its 16-byte piece p = piece % PPR (the pad piece p =
-  // PPR - 1 repeats the last one).  The offsets are formed anew at every
-  // issue (the empty asm keeps the compiler from holding them in registers
-  // across the products, where the wide pipeline has none to spare).
+  // PPR - 1 repeats the last one).  Tile-major weights: the stage's rows of
+  // one 16-row tile are one contiguous run (row r at r * kTilePitch); a
+  // tile past the slab's last re-reads that one, whose outputs are dropped.
+  // The offsets are formed anew at every issue (the empty asm keeps the
+  // compiler from holding them in registers across the products, where the
+  // wide pipeline has none to spare).
   auto issue = [&](int kc, int slot, int n0t) {
     const uint32_t koff = (uint32_t)kc * (uint32_t)B::kSpan;
     const uint32_t st = wlds_addr + (uint32_t)(slot * Sh::STAGE);
@@ -708,8 +718,15 @@ moe_gemm_kernel(MoeGemmArgs args) {
     for (int i = 0; i < Sh::LOADS; ++i) {
       const int idx = min(64 * i + lane_v, Sh::PIECES - 1);
       const int r = idx / Sh::PPR;
-      const uint32_t off = (((uint32_t)min(n0t + r, a.N - 1) * rb + koff) & ~3u) +
-                           16u * (uint32_t)min(idx - r * Sh::PPR, B::kPieces - 1);
+      const uint32_t piece = 16u * (uint32_t)min(idx - r * Sh::PPR, B::kPieces - 1);
+      uint32_t off;
+      if constexpr (TILED) {
+        const uint32_t tile = (uint32_t)min((n0t + r) >> 4, last_tile);
+        off = ((tile * (uint32_t)nchunk + (uint32_t)kc) * 16u + (uint32_t)(r & 15)) *
+                  (uint32_t)B::kTilePitch + piece;
+      } else {
+        off = (((uint32_t)min(n0t + r, a.N - 1) * rb + koff) & ~3u) + piece;
+      }
 #pragma unroll
       for (int nb = 0; nb < NB; ++nb)
         load_lds16(base[nb], off, st + (uint32_t)(nb * Sh::MATBUF + 1024 * i));
@@ -745,7 +762,8 @@ moe_gemm_kernel(MoeGemmArgs args) {
     const int valid = FULL ? KS : min(KS, groups - kc * KS);
     uint32_t sh[NS];
 #pragma unroll
-    for (int m = 0; m < NS; ++m) sh[m] = ALIGNED ? (koff & 3u) : ((brow[m] + koff) & 3u);
+    for (int m = 0; m < NS; ++m)
+      sh[m] = TILED ? 0u : ALIGNED ? (koff & 3u) : ((brow[m] + koff) & 3u);
     // scale table: lane (n, g) decodes groups g*KS/4 .. +KS/4-1 of row n
 #pragma unroll
     for (int m = 0; m < NS; ++m)
@@ -1195,7 +1213,7 @@ __device__ __forceinline__ void combine_step(int kc, const uint8_t* stage, uint3
   typedef AFrag<B::kWide> AF;
   const uint32_t koff = (uint32_t)kc * (uint32_t)B::kSpan;
   const int valid = FULL ? KS : min(KS, groups - kc * KS);
-  const uint32_t sh = ALIGNED ? (koff & 3u) : ((brow + koff) & 3u);
+  const uint32_t sh = B::kTilePitch ? 0u : ALIGNED ? (koff & 3u) : ((brow + koff) & 3u);
   const uint8_t* row = stage + n * B::kPitch;
   // scale table: lane (n, g) decodes groups g*KS/4 .. +KS/4-1 of row n
 #pragma unroll
@@ -1291,12 +1309,17 @@ moe_down_combine_kernel(MoeGemmArgs a, MoeCombineArgs cb) {
     const int Kc = __builtin_amdgcn_readlane(kv, c);
     const uint32_t koff = (uint32_t)kc * (uint32_t)B::kSpan;
     const uint32_t st = wlds_addr + (uint32_t)(slot * Sh::STAGE);
+    // tile-major weights: this workgroup's tile of chunk kc, one run
+    const uint32_t run = ((uint32_t)blockIdx.x * (uint32_t)((Kc + 255) >> 8) + (uint32_t)kc) *
+                         16u * (uint32_t)B::kTilePitch;
 #pragma unroll
     for (int l = 0; l < Sh::LOADS; ++l) {
       const int idx = min(64 * l + lane, Sh::PIECES - 1);
       const int r = idx / Sh::PPR;
-      const uint32_t off = (((uint32_t)min(n0 + r, a.N - 1) * rb + koff) & ~3u) +
-                           16u * (uint32_t)min(idx - r * Sh::PPR, B::kPieces - 1);
+      const uint32_t piece = 16u * (uint32_t)min(idx - r * Sh::PPR, B::kPieces - 1);
+      const uint32_t off =
+          B::kTilePitch ? run + (uint32_t)r * (uint32_t)B::kTilePitch + piece
+                        : (((uint32_t)min(n0 + r, a.N - 1) * rb + koff) & ~3u) + piece;
       load_lds16(base, off, st + (uint32_t)(1024 * l));
     }
     const uint8_t* abase = uniform_ptr(
@@ -1844,11 +1867,12 @@ static hipError_t launch_gemm_mt(const MoeGemmArgs& a, int mt, int max_chunks, h
 
 template <int TYPE, int EPI>
 static hipError_t launch_gemm_al(const MoeGemmArgs& a, int mt, int max_chunks, hipStream_t s) {
-  // Q4_K rows are always whole 144-byte blocks (16-byte multiples); a joint
-  // launch is aligned only if the shared expert's rows are too
+  // tile-major (K-quant) rows start on dwords; packed rows are aligned when
+  // their bytes are dword multiples (a joint launch: the shared expert's too)
+  constexpr bool kTiled = GemmB<TYPE>::kTilePitch != 0;
   const bool aligned = a.row_bytes % 4 == 0 && (!a.joint || a.s_row_bytes % 4 == 0);
-  if (TYPE == kQ4_K || aligned) return launch_gemm_mt<TYPE, EPI, true>(a, mt, max_chunks, s);
-  if constexpr (TYPE != kQ4_K) return launch_gemm_mt<TYPE, EPI, false>(a, mt, max_chunks, s);
+  if (kTiled || aligned) return launch_gemm_mt<TYPE, EPI, true>(a, mt, max_chunks, s);
+  if constexpr (!kTiled) return launch_gemm_mt<TYPE, EPI, false>(a, mt, max_chunks, s);
   return hipErrorInvalidValue;
 }
 
@@ -1973,6 +1997,54 @@ hipError_t moe_repack_launch(int type, const uint8_t* src, int64_t slabs, int64_
   return hipGetLastError();
 }
 
+// The tile-major copy (moe.h): the grid strides over the destination's
+// 16-bit halves (every chunk length and offset is even), each one row r of
+// tile t, chunk kc of slab s: zeros in a row's dword pad and past the slab.
+__global__ void __launch_bounds__(256)
+moe_tile_kernel(const uint16_t* __restrict__ src, int64_t rows, int64_t row_halves, int nchunk,
+                int span_halves, int pitch_halves, int64_t tiles, uint16_t* __restrict__ dst,
+                int64_t total) {
+  const int64_t chunk_halves = 16 * (int64_t)pitch_halves;
+  const int64_t tile_halves = nchunk * chunk_halves;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total;
+       i += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t t_all = i / tile_halves;  // slab * tiles + tile
+    const int64_t in_tile = i - t_all * tile_halves;
+    const int kc = (int)(in_tile / chunk_halves);
+    const int in_chunk = (int)(in_tile - kc * chunk_halves);
+    const int r = in_chunk / pitch_halves, h = in_chunk - r * pitch_halves;
+    const int64_t slab = t_all / tiles, row = (t_all - slab * tiles) * 16 + r;
+    uint16_t v = 0;
+    if (row < rows && h < span_halves)
+      v = src[(slab * rows + row) * row_halves + (int64_t)kc * span_halves + h];
+    dst[i] = v;
+  }
+}
+
+bool moe_tiled_type(int type) { return type == kQ4_K || type == kQ6_K; }
+
+int64_t moe_slab_bytes(int type, int64_t rows, int64_t columns) {
+  if (!moe_tiled_type(type)) return rows * (columns / block_weights(type)) * block_bytes(type);
+  const int pitch = type == kQ4_K ? GemmB<kQ4_K>::kTilePitch : GemmB<kQ6_K>::kTilePitch;
+  return (rows + 15) / 16 * (columns / 256) * 16 * pitch;
+}
+
+hipError_t moe_tile_launch(int type, const uint8_t* src, int64_t slabs, int64_t rows,
+                           int64_t columns, uint8_t* dst, hipStream_t stream) {
+  if (!moe_tiled_type(type) || columns % 256 || rows <= 0 || slabs <= 0)
+    return hipErrorInvalidValue;
+  const int span = type == kQ4_K ? GemmB<kQ4_K>::kSpan : GemmB<kQ6_K>::kSpan;
+  const int pitch = type == kQ4_K ? GemmB<kQ4_K>::kTilePitch : GemmB<kQ6_K>::kTilePitch;
+  const int nchunk = (int)(columns / 256);
+  const int64_t total = slabs * moe_slab_bytes(type, rows, columns) / 2;
+  const int grid = (int)std::min<int64_t>((total + 255) / 256, 65536);
+  hipLaunchKernelGGL(moe_tile_kernel, dim3(grid), dim3(256), 0, stream,
+                     reinterpret_cast<const uint16_t*>(src), rows, (int64_t)nchunk * span / 2,
+                     nchunk, span / 2, pitch / 2, (rows + 15) / 16,
+                     reinterpret_cast<uint16_t*>(dst), total);
+  return hipGetLastError();
+}
+
 template <int TYPE, bool ALIGNED>
 static hipError_t launch_combine_t(const MoeGemmArgs& a_in, const MoeCombineArgs& c,
                                    hipStream_t stream) {
@@ -2004,10 +2076,9 @@ hipError_t moe_down_combine_launch(int type, const MoeGemmArgs& a, const MoeComb
   if (!moe_down_combine_supported(type, a)) return hipErrorInvalidValue;
   const bool aligned = a.row_bytes % 4 == 0 && (!a.joint || a.s_row_bytes % 4 == 0);
   switch (type) {
+    // (K-quants: tile-major rows, which start on dwords)
     case kQ4_K: return launch_combine_t<kQ4_K, true>(a, c, stream);
-    case kQ6_K:
-      return aligned ? launch_combine_t<kQ6_K, true>(a, c, stream)
-                     : launch_combine_t<kQ6_K, false>(a, c, stream);
+    case kQ6_K: return launch_combine_t<kQ6_K, true>(a, c, stream);
     case kQ5_0:
       return aligned ? launch_combine_t<kQ5_0, true>(a, c, stream)
                      : launch_combine_t<kQ5_0, false>(a, c, stream);
