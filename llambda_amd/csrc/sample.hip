@@ -26,10 +26,9 @@
 //     (sample-from-probabilities, 1253-1270): masked logits have probability
 //     exactly 0, so the reference's serial sums over the whole row equal the
 //     serial sums over the survivors in index order, done here by one thread.
-// With top-k the result is the reference's token bit for bit.  Without top-k
-// (k = 0 or k >= n; top-p must then be 1) every logit survives and the sums
-// run as a parallel tree: the token then matches wherever the random value
-// is not within rounding of a cumulative boundary.
+// With top-k the result is the reference's token bit for bit.  Rows without
+// top-k (k = 0 or k >= n) take sample_exp_kernel (the exponentials, over the
+// slices) and sample_row_kernel instead of steps 2-5.
 #include "sample.h"
 
 #include <cmath>
@@ -159,6 +158,9 @@ struct PrepScratch {
   int* count;
   int* nan;
   uint32_t* cut;
+  float* smax;  // the slice's maximum of x / T
+  float* ssum;  // rows without top-k: the slice's sum of exp(x / T - max)
+  int* sact;    // and its logits above the mask value
 };
 __device__ __host__ inline PrepScratch prep_scratch(float* work, int n) {
   float* base = work + ((n + 3) & ~3);
@@ -168,32 +170,23 @@ __device__ __host__ inline PrepScratch prep_scratch(float* work, int n) {
   ps.count = ps.idx + kPrepGroups * kPrepCap;
   ps.nan = ps.count + kPrepGroups;
   ps.cut = reinterpret_cast<uint32_t*>(ps.nan + kPrepGroups);
+  ps.smax = reinterpret_cast<float*>(ps.cut + kPrepGroups);
+  ps.ssum = ps.smax + kPrepGroups;
+  ps.sact = reinterpret_cast<int*>(ps.ssum + kPrepGroups);
   return ps;
 }
 
-// Top-p without top-k: the row's (sort key << 32 | token id) words, twice
-// (the radix passes alternate between the two copies), after the prep
-// scratch.
-struct ToppScratch {
-  uint64_t* item[2];
-};
+// Top-p without top-k: the row's exponentials, after the prep scratch.
 __device__ __host__ inline size_t prep_work_floats(int n) {
-  return (size_t)((n + 3) & ~3) + 2 * kPrepGroups * kPrepCap + 3 * kPrepGroups;
+  return (size_t)((n + 3) & ~3) + 2 * kPrepGroups * kPrepCap + 6 * kPrepGroups;
 }
-__device__ __host__ inline ToppScratch topp_scratch(float* work, int n) {
-  const size_t n4 = (size_t)((n + 3) & ~3);
-  // prep_work_floats(n) is even (n4 + 2 * 64 * 64 + 3 * 64), so the words
-  // are 8-byte aligned
-  uint64_t* base = reinterpret_cast<uint64_t*>(work + prep_work_floats(n));
-  ToppScratch t;
-  t.item[0] = base;
-  t.item[1] = base + n4;
-  return t;
+static_assert((2 * kPrepGroups * kPrepCap + 6 * kPrepGroups) % 4 == 0,
+              "the exponentials start on 16 bytes");
+__device__ __host__ inline float* topp_scratch(float* work, int n) {
+  return work + prep_work_floats(n);
 }
 
-size_t sample_work_floats(int n) { return prep_work_floats(n) + 4 * (size_t)((n + 3) & ~3); }
-static_assert(2 * kPrepGroups * kPrepCap % 2 == 0 && 3 * kPrepGroups % 2 == 0,
-              "the top-p words must stay 8-byte aligned");
+size_t sample_work_floats(int n) { return prep_work_floats(n) + (size_t)((n + 3) & ~3); }
 
 __global__ void __launch_bounds__(kPrepThreads)
 sample_prep_kernel(const float* __restrict__ logits, float* __restrict__ work, SampleParams p) {
@@ -203,6 +196,7 @@ sample_prep_kernel(const float* __restrict__ logits, float* __restrict__ work, S
   __shared__ int hist[256];
   __shared__ uint32_t sel[3];
   __shared__ int nan_flag, count;
+  __shared__ float wmax[kPrepThreads / 64];
   const int g = blockIdx.x, tid = threadIdx.x, n = p.n;
   const int lo = (int)((int64_t)g * n / kPrepGroups), hi = (int)((int64_t)(g + 1) * n / kPrepGroups);
   const int m = hi - lo;
@@ -228,6 +222,7 @@ sample_prep_kernel(const float* __restrict__ logits, float* __restrict__ work, S
     lv[j] = i < m ? logits[lo + i] : 0.f;
   }
   int nan = 0;
+  float vmax = -INFINITY;
 #pragma unroll
   for (int j = 0; j < kPer; ++j) {
     const int i = tid + kPrepThreads * j;
@@ -240,9 +235,12 @@ sample_prep_kernel(const float* __restrict__ logits, float* __restrict__ work, S
       nan |= v != v;
       work[lo + i] = v;
       vals[i] = v;
+      vmax = fmaxf(vmax, v / p.temperature);
     }
   }
   if (nan) nan_flag = 1;
+  vmax = wave_max(vmax);
+  if ((tid & 63) == 0) wmax[tid >> 6] = vmax;
   __syncthreads();
   const bool topk = p.top_k > 0 && p.top_k < n;
   uint32_t ck = 0u;
@@ -267,6 +265,71 @@ sample_prep_kernel(const float* __restrict__ logits, float* __restrict__ work, S
     ps.count[g] = count;
     ps.nan[g] = nan_flag;
     ps.cut[g] = ck;
+    float sm = wmax[0];
+    for (int w = 1; w < kPrepThreads / 64; ++w) sm = fmaxf(sm, wmax[w]);
+    ps.smax[g] = sm;
+  }
+}
+
+// Rows without top-k: exp(x / T - max) rounded to single (computed in double
+// as the reference computes it) per position of the slice, into the scratch
+// after the prep words, with the slice's sum (threads' strided sums, added
+// in wave order) and its logits above the mask value.  The maximum is the
+// slices' (written by the prep launch).
+__global__ void __launch_bounds__(kPrepThreads)
+sample_exp_kernel(float* __restrict__ work, SampleParams p) {
+#pragma clang fp contract(off)
+  __shared__ float wred[kPrepThreads / 64];
+  __shared__ int wact[kPrepThreads / 64];
+  __shared__ float s_mx;
+  const int g = blockIdx.x, tid = threadIdx.x, n = p.n, lane = tid & 63, wave = tid >> 6;
+  const int lo = (int)((int64_t)g * n / kPrepGroups), hi = (int)((int64_t)(g + 1) * n / kPrepGroups);
+  const PrepScratch ps = prep_scratch(work, n);
+  if (wave == 0) {
+    float v = lane < kPrepGroups ? ps.smax[lane] : -INFINITY;
+    v = wave_max(v);
+    if (lane == 0) s_mx = v;
+  }
+  __syncthreads();
+  const float mx = s_mx;
+  float* ex = topp_scratch(work, n);
+  constexpr int kPer = kPrepSlice / kPrepThreads;
+  float xv[kPer];
+#pragma unroll
+  for (int j = 0; j < kPer; ++j) {
+    const int i = lo + tid + kPrepThreads * j;
+    xv[j] = i < hi ? work[i] : 0.f;
+  }
+  float local = 0.f;
+  int act = 0;
+#pragma unroll
+  for (int j = 0; j < kPer; ++j) {
+    const int i = lo + tid + kPrepThreads * j;
+    if (i < hi) {
+      const float e = (float)exp((double)(xv[j] / p.temperature - mx));
+      ex[i] = e;
+      local += e;
+      act += xv[j] > kMaskedLogit;
+    }
+  }
+  for (int o = 32; o > 0; o >>= 1) {
+    local += __shfl_xor(local, o, 64);
+    act += __shfl_xor(act, o, 64);
+  }
+  if (lane == 0) {
+    wred[wave] = local;
+    wact[wave] = act;
+  }
+  __syncthreads();
+  if (tid == 0) {
+    float t = wred[0];
+    int a = wact[0];
+    for (int w = 1; w < kPrepThreads / 64; ++w) {
+      t += wred[w];
+      a += wact[w];
+    }
+    ps.ssum[g] = t;
+    ps.sact[g] = a;
   }
 }
 
@@ -311,44 +374,6 @@ sample_kernel(float* __restrict__ work, SampleParams p, int* __restrict__ result
     if (tid == 0) {
       result[0] = -1;
       result[1] = kSampleErrNaN;
-    }
-    return;
-  }
-
-  const bool topk = p.top_k > 0 && p.top_k < n;
-  if (!topk) {
-    // every logit survives: the tree path (top-p must be 1); thread t owns
-    // the contiguous range [t * per, (t + 1) * per) so that its prefix sums
-    // follow index order
-    const int per = (n + kSampleThreads - 1) / kSampleThreads;
-    const int lo = min(n, tid * per), hi = min(n, lo + per);
-    float m = -INFINITY;
-    for (int i = lo; i < hi; ++i) m = fmaxf(m, work[i] / p.temperature);
-    for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
-    if ((tid & 63) == 0) fred[tid >> 6] = m;
-    __syncthreads();
-    float mx = fred[0];
-    for (int w = 1; w < kSampleThreads / 64; ++w) mx = fmaxf(mx, fred[w]);
-    __syncthreads();
-    float local = 0.f;
-    for (int i = lo; i < hi; ++i) local += (float)exp((double)(work[i] / p.temperature - mx));
-    const float sum = block_sum(local, fred);
-    float mine = 0.f;
-    for (int i = lo; i < hi; ++i) mine += (float)exp((double)(work[i] / p.temperature - mx)) / sum;
-    float run = block_exclusive_scan(mine, fred);
-    if (tid == 0) flag = n - 1;
-    __syncthreads();
-    for (int i = lo; i < hi; ++i) {
-      run += (float)exp((double)(work[i] / p.temperature - mx)) / sum;
-      if (p.roll <= run) {
-        atomicMin(&flag, i);
-        break;
-      }
-    }
-    __syncthreads();
-    if (tid == 0) {
-      result[0] = flag;
-      result[1] = 0;
     }
     return;
   }
@@ -642,176 +667,248 @@ sample_kernel(float* __restrict__ work, SampleParams p, int* __restrict__ result
   }
 }
 
-// Exclusive prefix sum of one int per thread over the block, in thread order.
-__device__ int block_exclusive_scan_int(int v, int* red) {
+// Rows without top-k (k = 0 or k >= n: every logit survives apply-top-k).
+// Top-p (apply-top-p-with-workspace, llambda.lisp:1163-1240), when p < 1:
+// the logits above the mask value ranked by value, descending, exp(x / T -
+// max / T) per rank, and the first rank at which the running sum of
+// exp / sum reaches p gives the cut value; every logit below it is masked
+// (ties with the cut kept).  Only the cut value is needed, not the ranking:
+// it is the value whose keys' probability mass first brings the running sum
+// to p, found by a radix select over descending keys (12, 8, 8 and 4 bits a
+// pass, most significant first) that carries each bin's mass.  Masses are 32-bit
+// fixed-point probabilities (floor(2^32 exp / sum), exp / sum rounded to
+// single as the reference forms it) added in 64-bit integers, so every order
+// of addition gives the same bins; the sums are exact where the reference's
+// serial single sums round (the cut can move by a rank where the running sum
+// meets p within that rounding).  A row whose total never reaches p keeps
+// every logit (the reference's cut is then its smallest one).
+// Then apply-temperature, softmax (1009-1034) and the draw
+// (sample-from-probabilities, 1253-1270) over the masked row: masked logits
+// have probability exactly 0.  Wavefront w owns a contiguous segment of the
+// row, read 256 positions at a time (lane l: positions 4l .. 4l+3, one
+// float4), so the running sums follow index order up to the rounding of
+// the wavefront scans and of the scan over the segments' totals; the
+// reference adds serially, so the token matches wherever the random value is
+// not within rounding of a cumulative boundary.  The exponentials, the
+// slices' sums and their active counts come from sample_exp_kernel.
+constexpr int kRowWaves = kSampleThreads / 64;
+
+// Exclusive prefix sum of one 64-bit integer per thread over the block, in
+// thread order (red: kRowWaves words of LDS).
+__device__ unsigned long long block_exclusive_scan_u64(unsigned long long v,
+                                                       unsigned long long* red) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  int inc = v;
+  unsigned long long inc = v;
   for (int o = 1; o < 64; o <<= 1) {
-    const int t = __shfl_up(inc, o, 64);
+    const unsigned long long t = __shfl_up(inc, o, 64);
     if (lane >= o) inc += t;
   }
   if (lane == 63) red[wave] = inc;
   __syncthreads();
-  if (threadIdx.x == 0) {
-    int acc = 0;
-    for (int w = 0; w < kSampleThreads / 64; ++w) {
-      const int t = red[w];
-      red[w] = acc;
-      acc += t;
-    }
-  }
+  unsigned long long before = 0;
+  for (int w = 0; w < wave; ++w) before += red[w];
   __syncthreads();
-  const int r = red[wave] + inc - v;
-  __syncthreads();
-  return r;
+  return before + inc - v;
 }
 
-// Top-p without top-k (apply-top-p-with-workspace, llambda.lisp:1163-1240,
-// after apply-top-k with k = 0 or k >= n): the logits above the mask value
-// ranked by value, descending, equal values in index order (the reference's
-// stable insertion sort; -0 and +0 compare equal), exp(x / T - max / T) per
-// rank, the first rank at which the running sum of exp / sum reaches p gives
-// the cut value, and every logit below it is masked in the row.  The ranking
-// is a stable LSD radix sort in eight 4-bit passes over the row; thread t
-// owns a contiguous range of positions, so counts laid out digit-major and
-// scanned in order give each (digit, thread) its output range.  The sums run
-// in a fixed tree order (the reference adds serially): the cut can move by a
-// rank where the running sum meets p within its rounding.  The draw itself
-// is sample_kernel's path for rows without top-k, over the masked row.
+// Inclusive scan of v over the wavefront's lanes, in lane order.
+__device__ __forceinline__ float wave_inclusive_scan(float v) {
+  const int lane = threadIdx.x & 63;
+  for (int o = 1; o < 64; o <<= 1) {
+    const float t = __shfl_up(v, o, 64);
+    if (lane >= o) v += t;
+  }
+  return v;
+}
+
 __global__ void __launch_bounds__(kSampleThreads)
-sample_topp_kernel(float* __restrict__ work, SampleParams p) {
+sample_row_kernel(float* __restrict__ work, SampleParams p, int* __restrict__ result) {
 #pragma clang fp contract(off)
-  __shared__ int cnt[16 * kSampleThreads];
-  __shared__ int ired[kSampleThreads / 64];
-  __shared__ float fred[kSampleThreads / 64 + 1];
-  __shared__ int s_nan, s_active, s_first;
-  const int n = p.n, tid = threadIdx.x;
+  __shared__ unsigned long long mass[4096];
+  __shared__ unsigned long long ured[kRowWaves];
+  __shared__ float fred[kRowWaves + 1];
+  __shared__ float wtot[kRowWaves];
+  __shared__ int s_active, s_token, s_none;
+  __shared__ uint32_t s_key;  // descending key of the selected prefix
+  __shared__ unsigned long long s_before;
+  const int n = p.n, tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const PrepScratch ps = prep_scratch(work, n);
   if (tid == 0) {
-    int any = 0;
-    for (int g = 0; g < kPrepGroups; ++g) any |= ps.nan[g];
-    s_nan = any;  // reported by the draw's launch
     s_active = 0;
-    s_first = INT_MAX;
+    s_token = n - 1;
+    s_none = 0;
+    s_key = 0;
+    s_before = 0;
   }
-  __syncthreads();
-  if (s_nan) return;
-  const ToppScratch t = topp_scratch(work, n);
-  const int per = (n + kSampleThreads - 1) / kSampleThreads;
-  const int lo = min(n, tid * per), hi = min(n, lo + per);
-  // Every loop over a thread's range loads kB elements in one round before
-  // using them (the row was just written by another launch, and each
-  // dependent round of loads costs a full memory round trip).
-  constexpr int kB = 16;
-  int act = 0;
-  for (int i0 = lo; i0 < hi; i0 += kB) {
-    float xb[kB];
-#pragma unroll
-    for (int b = 0; b < kB; ++b) xb[b] = i0 + b < hi ? work[i0 + b] : 0.f;
-#pragma unroll
-    for (int b = 0; b < kB; ++b) {
-      if (i0 + b >= hi) break;
-      float x = xb[b];
-      act += x > kMaskedLogit;
-      if (x == 0.0f) x = 0.0f;  // -0 ranks with +0
-      // ascending key order = descending value; equal keys keep index order
-      t.item[0][i0 + b] = ((uint64_t)~float_key(x) << 32) | (uint32_t)(i0 + b);
+  // NaN in any slice is the reference's error (the slices' words were just
+  // written on other XCDs: one round of loads)
+  if (__syncthreads_or(tid < kPrepGroups ? ps.nan[tid] : 0)) {
+    if (tid == 0) {
+      result[0] = -1;
+      result[1] = kSampleErrNaN;
     }
+    return;
   }
-  atomicAdd(&s_active, act);
-  __syncthreads();
-  for (int pass = 0; pass < 8; ++pass) {
-    // (selected, not indexed: an index into the pointer pair put it in
-    // scratch memory)
-    const uint64_t* in = (pass & 1) ? t.item[1] : t.item[0];
-    uint64_t* out = (pass & 1) ? t.item[0] : t.item[1];
-    const int sh = 32 + 4 * pass;
-#pragma unroll
-    for (int d = 0; d < 16; ++d) cnt[d * kSampleThreads + tid] = 0;
-    for (int i0 = lo; i0 < hi; i0 += kB) {
-      uint64_t kb[kB];
-#pragma unroll
-      for (int b = 0; b < kB; ++b) kb[b] = i0 + b < hi ? in[i0 + b] : 0ull;
-#pragma unroll
-      for (int b = 0; b < kB; ++b)
-        if (i0 + b < hi) ++cnt[(int)((kb[b] >> sh) & 15u) * kSampleThreads + tid];
-    }
-    __syncthreads();
-    int v[16], local = 0;
-#pragma unroll
-    for (int e = 0; e < 16; ++e) {
-      v[e] = cnt[16 * tid + e];
-      local += v[e];
-    }
-    int base = block_exclusive_scan_int(local, ired);
-#pragma unroll
-    for (int e = 0; e < 16; ++e) {
-      cnt[16 * tid + e] = base;
-      base += v[e];
-    }
-    __syncthreads();
-    for (int i0 = lo; i0 < hi; i0 += kB) {
-      uint64_t kb[kB];
-#pragma unroll
-      for (int b = 0; b < kB; ++b) kb[b] = i0 + b < hi ? in[i0 + b] : 0ull;
+  float* ex = topp_scratch(work, n);
+  // this wavefront's segment [wlo, whi): a multiple of 256 positions long
+  const int seg = (n + 256 * kRowWaves - 1) / (256 * kRowWaves) * 256;
+  const int wlo = min(n, wave * seg), whi = min(n, wlo + seg);
+  constexpr int kB = 8;  // float4 loads per lane in flight
+  // each round of kB chunks of 256: the row's (and, with EX, the
+  // exponentials') float4s loaded at once, then visit(chunk start, x[4],
+  // e[4], count) per chunk in order; the row is padded to 4 floats, so a
+  // float4 that starts inside it is read whole
+  auto sweep = [&](auto with_ex, auto&& visit) {
+    constexpr bool EX = decltype(with_ex)::value;
+    for (int c0 = wlo; c0 < whi; c0 += 256 * kB) {
+      float4 xv[kB], ev[kB];
 #pragma unroll
       for (int b = 0; b < kB; ++b) {
-        if (i0 + b >= hi) break;
-        const int pos = cnt[(int)((kb[b] >> sh) & 15u) * kSampleThreads + tid]++;
-        out[pos] = kb[b];
+        const int i = c0 + 256 * b + 4 * lane;
+        xv[b] = i < whi ? *reinterpret_cast<const float4*>(work + i) : make_float4(0.f, 0.f, 0.f, 0.f);
+        if constexpr (EX)
+          ev[b] = i < whi ? *reinterpret_cast<const float4*>(ex + i) : make_float4(0.f, 0.f, 0.f, 0.f);
+        else
+          ev[b] = make_float4(0.f, 0.f, 0.f, 0.f);
+      }
+#pragma unroll
+      for (int b = 0; b < kB; ++b) {
+        const int c = c0 + 256 * b;
+        if (c >= whi) break;  // uniform
+        const int i = c + 4 * lane;
+        const float xs[4] = {xv[b].x, xv[b].y, xv[b].z, xv[b].w};
+        const float es[4] = {ev[b].x, ev[b].y, ev[b].z, ev[b].w};
+        visit(i, xs, es, max(0, min(4, whi - i)));
       }
     }
-    __syncthreads();
-  }
-  // eight passes: the ranking is in copy 0; rank r < active holds the r-th
-  // largest logit above the mask value
-  const int active = s_active;
-  if (active <= 1) return;
-  const uint64_t* ranked = t.item[0];
-  auto rank = [&](int r) { return (int)(uint32_t)ranked[r]; };
-  const float max_scaled = work[rank(0)] / p.temperature;
-  const int rper = (active + kSampleThreads - 1) / kSampleThreads;
-  const int rlo = min(active, tid * rper), rhi = min(active, rlo + rper);
-  // this thread's ranks' exponentials, kept in rank order in copy 1 (no
-  // longer needed) for the three passes over them
-  float* ex = reinterpret_cast<float*>(t.item[1]);
-  float local = 0.f;
-  for (int r0 = rlo; r0 < rhi; r0 += kB) {
-    int rb[kB];
-#pragma unroll
-    for (int b = 0; b < kB; ++b) rb[b] = r0 + b < rhi ? rank(r0 + b) : 0;
-    float vb[kB];
-#pragma unroll
-    for (int b = 0; b < kB; ++b) vb[b] = work[rb[b]];
-#pragma unroll
-    for (int b = 0; b < kB; ++b) {
-      if (r0 + b >= rhi) break;
-      const float e = (float)exp((double)(vb[b] / p.temperature - max_scaled));
-      ex[r0 + b] = e;
-      local += e;
+  };
+  using NoEx = std::integral_constant<bool, false>;
+  using WithEx = std::integral_constant<bool, true>;
+
+  // the row's sum of exponentials (the slices' sums in slice order) and its
+  // logits above the mask value
+  if (tid == 0) {
+    float t = 0.f;
+    int a = 0;
+    for (int g = 0; g < kPrepGroups; ++g) {
+      t += ps.ssum[g];
+      a += ps.sact[g];
     }
-  }
-  const float sum = block_sum(local, fred);
-  float mine = 0.f;
-  for (int r = rlo; r < rhi; ++r) mine += ex[r] / sum;
-  float run = block_exclusive_scan(mine, fred);
-  for (int r = rlo; r < rhi; ++r) {
-    run += ex[r] / sum;
-    if (run >= p.top_p) {
-      atomicMin(&s_first, r);
-      break;
-    }
+    fred[0] = t;
+    s_active = a;
   }
   __syncthreads();
-  const float cut = work[rank(s_first == INT_MAX ? active - 1 : s_first)];
+  const float sum = fred[0];
   __syncthreads();
-  for (int i0 = lo; i0 < hi; i0 += kB) {
-    float xb[kB];
+
+  float cut = -INFINITY;  // logits below it are masked
+  if (p.top_p < 1.0f && s_active > 1) {
+    const unsigned long long target = (unsigned long long)ceil((double)p.top_p * 4294967296.0);
+    auto dkey = [](float x) { return ~float_key(x == 0.0f ? 0.0f : x); };  // -0 ranks with +0
+    // passes over key bits 31..20 (sign, exponent, 3 mantissa bits: a
+    // row's logits spread over many bins, so few lanes of an instruction
+    // add to one), 19..12, 11..4 and 3..0
+    constexpr int kShift[4] = {20, 12, 4, 0}, kWidth[4] = {12, 8, 8, 4};
+    for (int pass = 0; pass < 4; ++pass) {
+      const int shift = kShift[pass], width = kWidth[pass], nb = 1 << width;
+      for (int i = tid; i < nb; i += kSampleThreads) mass[i] = 0ull;
+      __syncthreads();
+      const uint32_t prefix = s_key;
+      const int top = shift + width;  // bits above the pass's are the prefix's
+      sweep(WithEx{}, [&](int, const float (&x)[4], const float (&e)[4], int cnt) {
 #pragma unroll
-    for (int b = 0; b < kB; ++b) xb[b] = i0 + b < hi ? work[i0 + b] : 0.f;
+        for (int u = 0; u < 4; ++u) {
+          if (u >= cnt || !(x[u] > kMaskedLogit)) continue;
+          const uint32_t k = dkey(x[u]);
+          if (top < 32 && (k >> top) != (prefix >> top)) continue;
+          // floor(2^32 q): the scaling is exact in single, the conversion truncates
+          const float qs = (e[u] / sum) * 4294967296.0f;
+          const uint32_t q = qs < 4294967296.0f ? (uint32_t)qs : 0xFFFFFFFFu;
+          if (q) atomicAdd(&mass[(k >> shift) & (uint32_t)(nb - 1)], (unsigned long long)q);
+        }
+      });
+      __syncthreads();
+      // thread t: bins 4t .. 4t+3; the running mass before them; the one
+      // thread whose bins bring it to the target picks the bin
+      unsigned long long mine = 0;
+      if (4 * tid < nb)
+        for (int j = 0; j < 4; ++j) mine += mass[4 * tid + j];
+      unsigned long long run = s_before + block_exclusive_scan_u64(mine, ured);
+      if (4 * tid < nb && run < target && run + mine >= target) {
+        for (int j = 0; j < 4; ++j) {
+          const unsigned long long bm = mass[4 * tid + j];
+          if (run + bm >= target) {
+            s_key = (prefix & ~((uint32_t)(nb - 1) << shift)) | ((uint32_t)(4 * tid + j) << shift);
+            s_before = run;
+            break;
+          }
+          run += bm;
+        }
+        s_none = 2;  // picked
+      }
+      __syncthreads();
+      const bool picked = s_none == 2;
+      __syncthreads();
+      if (!picked) break;  // the total never reaches p (first pass): no cut
+      if (tid == 0) s_none = 0;
+      if (pass == 3) cut = key_float(~s_key);
+    }
+  }
+
+  // the draw over the masked row: its sum, each chunk's running sums of
+  // exp / sum (lanes' four in order, then a lane scan), chunks in order, the
+  // segments' totals scanned in wavefront order; the first position whose
+  // running sum reaches the roll
+  float msum = sum;
+  if (cut > -INFINITY) {
+    float ls = 0.f;
+    sweep(WithEx{}, [&](int, const float (&x)[4], const float (&e)[4], int cnt) {
 #pragma unroll
-    for (int b = 0; b < kB; ++b)
-      if (i0 + b < hi && xb[b] < cut) work[i0 + b] = kMaskedLogit;
+      for (int u = 0; u < 4; ++u)
+        if (u < cnt && x[u] >= cut) ls += e[u];
+    });
+    msum = block_sum(ls, fred);
+  }
+  auto probs = [&](const float (&x)[4], const float (&e)[4], int cnt, float (&q)[4]) {
+#pragma unroll
+    for (int u = 0; u < 4; ++u) q[u] = u < cnt && x[u] >= cut ? e[u] / msum : 0.f;
+  };
+  float seg_run = 0.f;  // the segment's running sum at its current chunk
+  sweep(WithEx{}, [&](int, const float (&x)[4], const float (&e)[4], int cnt) {
+    float q[4];
+    probs(x, e, cnt, q);
+    const float incl = wave_inclusive_scan(((q[0] + q[1]) + q[2]) + q[3]);
+    seg_run += __shfl(incl, 63, 64);
+  });
+  if (lane == 0) wtot[wave] = seg_run;
+  __syncthreads();
+  float run = 0.f;  // the running sum before this segment
+  for (int w = 0; w < wave; ++w) run += wtot[w];
+  bool found = false;
+  sweep(WithEx{}, [&](int i, const float (&x)[4], const float (&e)[4], int cnt) {
+    if (found) return;  // uniform
+    float q[4];
+    probs(x, e, cnt, q);
+    const float incl = wave_inclusive_scan(((q[0] + q[1]) + q[2]) + q[3]);
+    const float before = __shfl_up(incl, 1, 64);
+    float r = run + (lane > 0 ? before : 0.f);
+    int hit = 4;
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      r += q[u];
+      if (hit == 4 && u < cnt && p.roll <= r) hit = u;
+    }
+    const uint64_t any = __ballot(hit < 4);
+    if (any) {
+      if (lane == __builtin_ctzll(any)) atomicMin(&s_token, i + hit);
+      found = true;
+    }
+    run += __shfl(incl, 63, 64);
+  });
+  __syncthreads();
+  if (tid == 0) {
+    result[0] = s_token;
+    result[1] = 0;
   }
 }
 
@@ -821,15 +918,12 @@ hipError_t sample_launch(const float* logits, float* work, const SampleParams& p
   hipLaunchKernelGGL(sample_prep_kernel, dim3(kPrepGroups), dim3(kPrepThreads), 0, stream, logits,
                      work, p);
   const bool topk = p.top_k > 0 && p.top_k < p.n;
-  if (!topk && p.top_p < 1.0f) {
-    // top-p alone: cut the row, then draw from it as without top-p
-    hipLaunchKernelGGL(sample_topp_kernel, dim3(1), dim3(kSampleThreads), 0, stream, work, p);
-    SampleParams q = p;
-    q.top_p = 1.0f;
-    hipLaunchKernelGGL(sample_kernel, dim3(1), dim3(kSampleThreads), 0, stream, work, q, result);
-    return hipGetLastError();
+  if (topk) {
+    hipLaunchKernelGGL(sample_kernel, dim3(1), dim3(kSampleThreads), 0, stream, work, p, result);
+  } else {
+    hipLaunchKernelGGL(sample_exp_kernel, dim3(kPrepGroups), dim3(kPrepThreads), 0, stream, work, p);
+    hipLaunchKernelGGL(sample_row_kernel, dim3(1), dim3(kSampleThreads), 0, stream, work, p, result);
   }
-  hipLaunchKernelGGL(sample_kernel, dim3(1), dim3(kSampleThreads), 0, stream, work, p, result);
   return hipGetLastError();
 }
 
