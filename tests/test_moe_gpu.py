@@ -39,9 +39,12 @@ def _silu(v):
     return v / (1.0 + np.exp(-v))
 
 
-def output_bounds(layer, x, idx, w, shared_w):
-    """S_i per token (see module docstring), float64."""
+def layer64(layer, x, idx, w, shared_w):
+    """The layer's output under the routing (idx, w) and the shared weights,
+    and S_i per token (see module docstring), both in float64 from the
+    exact dequantised weights (a layer without latent projections)."""
     H, F, Fs = layer.hidden, layer.expert_ffn, layer.shared_ffn
+    Y = np.zeros((x.shape[0], H))
     S = np.zeros((x.shape[0], H))
     x64 = x.astype(np.float64)
     by_expert = {}
@@ -57,15 +60,25 @@ def output_bounds(layer, x, idx, w, shared_w):
             h = _silu(g) * up
         else:
             h = np.maximum(up, 0.0) ** 2
-        S[ts] += np.abs(ws)[:, None] * (np.abs(_dq(layer.down, H, F, e * H)) @ np.abs(h)).T
+        down = _dq(layer.down, H, F, e * H)
+        # a token may take an expert once: np.add.at for the general case
+        np.add.at(Y, ts, ws[:, None] * (down @ h).T)
+        np.add.at(S, ts, np.abs(ws)[:, None] * (np.abs(down) @ np.abs(h)).T)
     if Fs:
         up = _dq(layer.shared_up, Fs, H) @ x64.T
         if layer.variant == QWEN3NEXT:
             h = _silu(_dq(layer.shared_gate, Fs, H) @ x64.T) * up
         else:
             h = np.maximum(up, 0.0) ** 2
-        S += np.abs(shared_w)[:, None] * (np.abs(_dq(layer.shared_down, H, Fs)) @ np.abs(h)).T
-    return S
+        down = _dq(layer.shared_down, H, Fs)
+        Y += shared_w[:, None] * (down @ h).T
+        S += np.abs(shared_w)[:, None] * (np.abs(down) @ np.abs(h)).T
+    return Y, S
+
+
+def output_bounds(layer, x, idx, w, shared_w):
+    """S_i per token (see module docstring), float64."""
+    return layer64(layer, x, idx, w, shared_w)[1]
 
 
 def _shared_weights(layer, x):
@@ -209,6 +222,16 @@ def test_nemotron_h_1024_batch_invariance(hip):
     err = np.abs(y[sub].astype(np.float64) - ref.y.astype(np.float64))
     bad = (err > REL * S) & same_set[:, None]
     assert not bad.any(), f"B=1024: {int(bad.sum())} outputs of the sampled tokens exceed 1e-4*S"
+    # every token of the batch against the float64 restatement of the
+    # expert products and the combine under the device's own routing (its
+    # expert set and gating weights, checked above on the sampled tokens):
+    # the per-chunk arithmetic of every hot expert's every 64-pair chunk
+    print("nemotron B=1024: float64 products of all 1024 tokens", flush=True)
+    Y64, S64 = layer64(layer, x, idx, w.astype(np.float64), np.ones(x.shape[0]))
+    err = np.abs(y.astype(np.float64) - Y64)
+    bad = err > REL * S64
+    assert not bad.any(), (f"B=1024: {int(bad.sum())} outputs exceed 1e-4*S against float64 "
+                           f"(tokens {sorted(set(np.nonzero(bad)[0].tolist()))[:10]})")
 
 
 # One token through each single-token launch sequence: the up launch that
