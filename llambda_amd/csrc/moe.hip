@@ -52,7 +52,7 @@ __global__ void __launch_bounds__(256) topk_gate_kernel(MoePlan p, int tokens, i
 // that groups (token, rank) pairs by expert.  Pair id p = token * k + rank;
 // the shared expert's pairs are tokens * k + token.
 constexpr int kScanThreads = 1024;
-constexpr int kMaxChunkPairs = 64;  // pairs per chunk: 16, 32 or 64
+constexpr int kMaxChunkPairs = 128;  // pairs per chunk: 16, 32, 64 or 128
 
 __global__ void __launch_bounds__(kScanThreads) moe_scan_kernel(MoePlan p, int tokens, int nt,
                                                                 int has_shared) {
@@ -269,7 +269,11 @@ static int64_t row_bytes_of(int type, int64_t columns) {
 
 // Pipeline of the grouped MFMA products and its chunk size: 0 = the
 // single-token pipeline, 1 = one 16-token tile per chunk (double-buffered),
-// 2 = two 16-token tiles per chunk (32 pairs).
+// 2 = two 16-token tiles per chunk (32 pairs), 4 and 8 = the group pipeline
+// with one or two wave sets (64 or 128 pairs per chunk).
+#ifndef LLHIP_GROUP_PAIRS
+#define LLHIP_GROUP_PAIRS 64
+#endif
 static int moe_mfma_tiles(const MoePlan& p, int tokens) {
   if (tokens == 1) return 0;
   const int64_t avg = ((int64_t)tokens * p.top_k + p.experts - 1) / p.experts;
@@ -282,7 +286,8 @@ static int moe_mfma_tiles(const MoePlan& p, int tokens) {
   const int64_t act_w = std::max(p.ffn, p.shared_ffn);
   const int64_t split_bytes = std::max((int64_t)tokens * (p.top_k + 1) * 4 * act_w,
                                        (int64_t)tokens * 4 * std::max(p.hidden, p.latent_in));
-  return types && split_bytes < ((int64_t)1 << 31) ? 4 : 2;
+  if (!types || split_bytes >= ((int64_t)1 << 31)) return 2;
+  return LLHIP_GROUP_PAIRS / 16;
 }
 static int moe_chunk_tokens(int mt) { return mt == 0 ? 1 : 16 * mt; }
 
@@ -389,7 +394,7 @@ hipError_t moe_forward_launch(const MoePlan& p, const float* x, float* y, int to
     a.gate_jpl = jpl_for(E);
     a.plan = p;
   }
-  const bool staged_up = mt == 4 && epi == kEpiRelu2;  // one matrix: the stage-major copies
+  const bool staged_up = mt >= 4 && epi == kEpiRelu2;  // one matrix: the stage-major copies
   if (staged_up) {
     a.w0 = p.up_g;
     a.expert_stride = p.up_g_stride;
@@ -453,7 +458,7 @@ hipError_t moe_forward_launch(const MoePlan& p, const float* x, float* y, int to
     c.error_out = error_out;
     return moe_down_combine_launch(p.down_type, a, c, s);
   }
-  if (mt == 4) {
+  if (mt >= 4) {
     a.w0 = p.down_g;
     a.expert_stride = p.down_g_stride;
     a.s_w0 = p.sh_down_g;
@@ -464,7 +469,7 @@ hipError_t moe_forward_launch(const MoePlan& p, const float* x, float* y, int to
     a = down;
     a.group = 1;
     a.K = p.shared_ffn;
-    a.w0 = mt == 4 ? p.sh_down_g : p.sh_down;
+    a.w0 = mt >= 4 ? p.sh_down_g : p.sh_down;
     a.row_bytes = row_bytes_of(p.sh_down_type, p.shared_ffn);
     a.expert_stride = 0;
     e = moe_gemm_launch(p.sh_down_type, kEpiDown, a, mt, shared_chunks, s);

@@ -1435,9 +1435,8 @@ __device__ __forceinline__ void staged_q5_scale(const uint8_t* row, int j, float
   c = 144.f * delta;
 }
 
-constexpr int kGroupWaves = 4;
-constexpr int kGroupTiles = 4;    // 16-token tiles per chunk
-constexpr int kGroupAPieces = 17; // 16 pieces of split activations + 1 of group sums
+constexpr int kGroupWaves = 4;    // waves of one set: 64 rows each
+constexpr int kGroupTiles = 4;    // 16-token tiles per set
 
 template <int TYPE>
 struct GroupB;
@@ -1450,17 +1449,22 @@ struct GroupB<kQ8_0> {
   static constexpr int kBlock = 34, kPieces = 5;
 };
 
-template <int TYPE, int EPI>
+// SETS wave sets share the workgroup's weight rows: set s takes token tiles
+// 4 s .. 4 s + 3 of a chunk of up to 64 SETS pairs, so each stage of rows
+// comes from HBM once for 64 SETS tokens.
+template <int TYPE, int EPI, int SETS>
 struct GroupShape {
   static constexpr int NB = EPI == kEpiSwiglu ? 2 : 1;
   static constexpr int RUN = 128 * GroupB<TYPE>::kBlock;  // stage-major run: 64 rows x 2 blocks
   static constexpr int RP = 2 * GroupB<TYPE>::kBlock;     // a row's bytes in the run
   static constexpr int ROWS = 64 / NB;  // rows per matrix and wave
   static constexpr int NS = ROWS / 16;
+  static constexpr int WAVES = kGroupWaves * SETS;
   static constexpr int WG_ROWS = kGroupWaves * ROWS;
   static constexpr int PIECES = GroupB<TYPE>::kPieces;
-  static constexpr int A_BYTES = kGroupAPieces * 1024;
-  static constexpr int B_BYTES = PIECES * NB * 1024;  // per wave
+  static constexpr int TOKENS = 64 * SETS;                  // pairs per chunk
+  static constexpr int A_BYTES = TOKENS * 256 + TOKENS * 16;  // + each token's 4 group sums
+  static constexpr int B_BYTES = PIECES * NB * 1024;  // per wave of a set
   static constexpr int STAGE = A_BYTES + kGroupWaves * B_BYTES;
   static constexpr int LDS = 2 * STAGE;
 };
@@ -1502,10 +1506,11 @@ __device__ __forceinline__ void group_scale(const uint8_t* wbuf, int nb, int r, 
   else c = 128.f * delta;
 }
 
-template <int TYPE, int EPI>
-__global__ void __launch_bounds__(64 * kGroupWaves, 2) moe_group_kernel(MoeGemmArgs args) {
+template <int TYPE, int EPI, int SETS>
+__global__ void __launch_bounds__(64 * kGroupWaves * SETS, SETS == 1 ? 2 : 1)
+moe_group_kernel(MoeGemmArgs args) {
   using B = GemmB<TYPE>;
-  using Sh = GroupShape<TYPE, EPI>;
+  using Sh = GroupShape<TYPE, EPI, SETS>;
   constexpr int NB = Sh::NB, NS = Sh::NS, MT = kGroupTiles;
   constexpr bool kStagedQ5 = TYPE == kQ5_0 && NB == 1;  // the lane-ordered stage-major rows
   constexpr int BB = GroupB<TYPE>::kBlock;
@@ -1535,21 +1540,30 @@ __global__ void __launch_bounds__(64 * kGroupWaves, 2) moe_group_kernel(MoeGemmA
   if (wg_row0 >= a.N) return;  // the whole workgroup
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int rw = wave & (kGroupWaves - 1), set = wave / kGroupWaves;  // row group, token set
   const int n = lane & 15, g = lane >> 4;
   // rows of this wave (a wave past the last row still takes part in every
   // barrier: its rows clamp to the last one and its outputs are dropped)
-  const int n0 = wg_row0 + wave * Sh::ROWS;
+  const int n0 = wg_row0 + rw * Sh::ROWS;
   const int count = __builtin_amdgcn_readfirstlane(ch.count);
   const int start = __builtin_amdgcn_readfirstlane(ch.start);
   const int expert = __builtin_amdgcn_readfirstlane(ch.expert);
   const int nt = (count + 15) >> 4;  // token tiles holding pairs
+  const int nt_set = min(max(nt - kGroupTiles * set, 0), kGroupTiles);  // this wave's
 
-  // lane l = token l of the chunk: its split row and group sums (tokens past
-  // the count read the first token's)
-  const int q_l = a.perm[start + (lane < count ? lane : 0)];
-  const int64_t r_l = a.a_by_token ? (q_l < a.pairs ? q_l / a.top_k : q_l - a.pairs) : q_l;
-  const uint32_t a_off = (uint32_t)(r_l * a.aq_stride * 2);
-  const uint32_t s_off = (uint32_t)(r_l * a.as_stride * 4);
+  // lane l = token l of the chunk (and token 64 + l with two sets): its
+  // split row and group sums (tokens past the count read the first token's)
+  uint32_t a_off[SETS], s_off[SETS];
+  int q_l[SETS];
+#pragma unroll
+  for (int k = 0; k < SETS; ++k) {
+    const int tk = 64 * k + lane;
+    q_l[k] = a.perm[start + (tk < count ? tk : 0)];
+    const int64_t r_l = a.a_by_token ? (q_l[k] < a.pairs ? q_l[k] / a.top_k : q_l[k] - a.pairs)
+                                     : q_l[k];
+    a_off[k] = (uint32_t)(r_l * a.aq_stride * 2);
+    s_off[k] = (uint32_t)(r_l * a.as_stride * 4);
+  }
   const uint8_t* aq_base = uniform_ptr(reinterpret_cast<const uint8_t*>(a.aq));
   const uint8_t* as_base = uniform_ptr(reinterpret_cast<const uint8_t*>(a.as));
   const uint8_t* base[NB];
@@ -1567,13 +1581,18 @@ __global__ void __launch_bounds__(64 * kGroupWaves, 2) moe_group_kernel(MoeGemmA
   uint32_t wdma[Sh::PIECES];
 #pragma unroll
   for (int q = 0; q < Sh::PIECES; ++q) wdma[q] = (uint32_t)min(16 * (64 * q + lane), Sh::RUN - 16);
-  // activation DMA: this wave's instructions k = wave + 4 u take token
+  // activation DMA: this wave's instructions k = wave + WAVES u take token
   // 4 k + (l >> 4) and piece (l & 15) ^ (token & 15) into slot l of block k
   uint32_t adma[4];
 #pragma unroll
   for (int u = 0; u < 4; ++u) {
-    const int t = 4 * (wave + 4 * u) + (lane >> 4);
-    adma[u] = (uint32_t)__shfl((int)a_off, t) + 16u * (uint32_t)((lane & 15) ^ (t & 15));
+    const int t = 4 * (wave + Sh::WAVES * u) + (lane >> 4);
+    int ao = __shfl((int)a_off[0], t & 63);
+    if constexpr (SETS == 2) {
+      const int ao1 = __shfl((int)a_off[1], t & 63);
+      ao = t < 64 ? ao : ao1;
+    }
+    adma[u] = (uint32_t)ao + 16u * (uint32_t)((lane & 15) ^ (t & 15));
   }
   // fetch rows 16 m + n: their byte shift within a dword is the same at
   // every stage (2 blocks span a multiple of 4 bytes) and for every m (rows
@@ -1590,17 +1609,22 @@ __global__ void __launch_bounds__(64 * kGroupWaves, 2) moe_group_kernel(MoeGemmA
   const uint32_t lds0 = lds_address(lds);
 
   // (the token blocks of tiles past the chunk's are never read; a wave
-  // whose rows all lie past the last loads no rows and computes nothing)
+  // whose rows all lie past the last loads no rows and computes nothing, nor
+  // does a wave whose set holds no token tile; the first set loads the rows)
   const bool live = n0 < a.N;
+  const bool work = live && nt_set > 0;
   auto issue = [&](int st, int buf) {
     const uint32_t stg = lds0 + (uint32_t)(buf * Sh::STAGE);
 #pragma unroll
     for (int u = 0; u < 4; ++u)
-      if (wave + 4 * u < 4 * nt)
-        load_lds16(aq_base, adma[u] + 256u * (uint32_t)st, stg + 1024u * (uint32_t)(wave + 4 * u));
-    if (wave == 0) load_lds16(as_base, s_off + 16u * (uint32_t)st, stg + 1024u * 16u);
-    if (!live) return;
-    const uint32_t wst = stg + Sh::A_BYTES + (uint32_t)wave * Sh::B_BYTES;
+      if (wave + Sh::WAVES * u < 4 * nt)
+        load_lds16(aq_base, adma[u] + 256u * (uint32_t)st,
+                   stg + 1024u * (uint32_t)(wave + Sh::WAVES * u));
+    if (wave < SETS)  // wave k: the sums of tokens 64 k .. 64 k + 63
+      load_lds16(as_base, (wave == 0 ? s_off[0] : s_off[SETS - 1]) + 16u * (uint32_t)st,
+                 stg + (uint32_t)(Sh::TOKENS * 256 + 1024 * wave));
+    if (!live || set > 0) return;
+    const uint32_t wst = stg + Sh::A_BYTES + (uint32_t)rw * Sh::B_BYTES;
     const uint32_t sto = (uint32_t)st * (uint32_t)(2 * BB);
     if constexpr (NB == 1) {
       const uint8_t* run =
@@ -1659,7 +1683,7 @@ __global__ void __launch_bounds__(64 * kGroupWaves, 2) moe_group_kernel(MoeGemmA
   auto compute = [&](auto ntc, int st, auto bufc) {
     constexpr int NT = decltype(ntc)::value;
     const uint8_t* stg = lds + decltype(bufc)::value * Sh::STAGE;
-    const uint8_t* wbuf = stg + Sh::A_BYTES + wave * Sh::B_BYTES;
+    const uint8_t* wbuf = stg + Sh::A_BYTES + rw * Sh::B_BYTES;
     const int ls = st & 3;  // stage within the 256-element chunk
 #pragma unroll
     for (int jj = 0; jj < 2; ++jj) {
@@ -1685,9 +1709,10 @@ __global__ void __launch_bounds__(64 * kGroupWaves, 2) moe_group_kernel(MoeGemmA
             cneg[m][nb][0] = (mine && j8 < 4) ? -c : cneg[m][nb][0];
             cneg[m][nb][1] = (mine && j8 >= 4) ? -c : cneg[m][nb][1];
           }
-        // token 16 i + n: block 4 i + (n >> 2), slot 16 (n & 3) + (piece ^ n)
+        // token 16 i + n of the set: block 4 i + (n >> 2), slot 16 (n & 3) +
+        // (piece ^ n)
         bf16x8 hi[NT], lo[NT];
-        const uint8_t* at = stg + (n >> 2) * 1024 + (n & 3) * 256;
+        const uint8_t* at = stg + set * 16384 + (n >> 2) * 1024 + (n & 3) * 256;
 #pragma unroll
         for (int i = 0; i < NT; ++i) {
           hi[i] = *reinterpret_cast<const bf16x8*>(at + 4096 * i + 16 * ((jj * 8 + g) ^ n));
@@ -1722,7 +1747,8 @@ __global__ void __launch_bounds__(64 * kGroupWaves, 2) moe_group_kernel(MoeGemmA
       const bool ok = 2 * st + (g & 1) < groups;
 #pragma unroll
       for (int i = 0; i < NT; ++i) {
-        const float* sp = reinterpret_cast<const float*>(stg + 16 * 1024 + (16 * i + n) * 16);
+        const float* sp = reinterpret_cast<const float*>(
+            stg + Sh::TOKENS * 256 + (64 * set + 16 * i + n) * 16);
         const float v = sp[2 * (g & 1)] + sp[2 * (g & 1) + 1];
         const float val = ok ? v : 0.f;
         sv[i][0] = (mine && ls < 2) ? val : sv[i][0];
@@ -1739,13 +1765,17 @@ __global__ void __launch_bounds__(64 * kGroupWaves, 2) moe_group_kernel(MoeGemmA
       int qout[4];
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        const int tk = 16 * i + 4 * g + r;
-        const int q = __shfl(q_l, tk);  // lane tk holds the pair of token tk
+        const int tk = 64 * set + 16 * i + 4 * g + r;
+        int q = __shfl(q_l[0], tk & 63);  // lane tk holds the pair of token tk
+        if constexpr (SETS == 2) {
+          const int q1 = __shfl(q_l[1], tk & 63);
+          q = tk < 64 ? q : q1;
+        }
         qout[r] = tk < count ? q : 0;
       }
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        const int tk = 16 * i + 4 * g + r;
+        const int tk = 64 * set + 16 * i + 4 * g + r;
         const bool ok_t = tk < count;
         const int q = qout[r];
         if constexpr (EPI == kEpiDown) {
@@ -1792,7 +1822,7 @@ __global__ void __launch_bounds__(64 * kGroupWaves, 2) moe_group_kernel(MoeGemmA
     __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
     __syncthreads();
     if (st + 1 < nstage) issue(st + 1, 1 - decltype(bufc)::value);
-    if (live) {
+    if (work) {
       compute(ntc, st, bufc);
       if ((st & 3) == 3 && st + 1 < nstage) apply_offsets(ntc);
     }
@@ -1803,12 +1833,12 @@ __global__ void __launch_bounds__(64 * kGroupWaves, 2) moe_group_kernel(MoeGemmA
       stage(ntc, st, std::integral_constant<int, 0>{});
       if (st + 1 < nstage) stage(ntc, st + 1, std::integral_constant<int, 1>{});
     }
-    if (live) {
+    if (work) {
       apply_offsets(ntc);
       finish(ntc);
     }
   };
-  switch (nt) {
+  switch (nt_set) {
     case 1: run(std::integral_constant<int, 1>{}); break;
     case 2: run(std::integral_constant<int, 2>{}); break;
     case 3: run(std::integral_constant<int, 3>{}); break;
@@ -1888,11 +1918,11 @@ static hipError_t launch_gemm_epi(int type, const MoeGemmArgs& a, int mt, int ma
   }
 }
 
-template <int TYPE, int EPI>
+template <int TYPE, int EPI, int SETS>
 static hipError_t launch_group_t(const MoeGemmArgs& a_in, int max_chunks, hipStream_t stream) {
-  using Sh = GroupShape<TYPE, EPI>;
+  using Sh = GroupShape<TYPE, EPI, SETS>;
   MoeGemmArgs a = a_in;
-  const auto kernel = moe_group_kernel<TYPE, EPI>;
+  const auto kernel = moe_group_kernel<TYPE, EPI, SETS>;
   if (Sh::LDS > 65536) {
     hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kernel),
                                        hipFuncAttributeMaxDynamicSharedMemorySize, Sh::LDS);
@@ -1903,18 +1933,18 @@ static hipError_t launch_group_t(const MoeGemmArgs& a_in, int max_chunks, hipStr
   a.tiles_per_wg = 1;
   a.depth = 2;
   const dim3 grid(((max_chunks + 7) / 8) * 8 * a.row_tiles);
-  hipLaunchKernelGGL(kernel, grid, dim3(64 * kGroupWaves), Sh::LDS, stream, a);
+  hipLaunchKernelGGL(kernel, grid, dim3(64 * Sh::WAVES), Sh::LDS, stream, a);
   return hipGetLastError();
 }
 
-template <int EPI>
+template <int EPI, int SETS>
 static hipError_t launch_group_epi(int type, const MoeGemmArgs& a, int max_chunks, hipStream_t s) {
   // the stage offsets (256 bytes of split row, 16 of sums per stage) are
   // 32-bit: the launcher only chooses this pipeline when they fit
   if (a.K % 32 || (a.joint && a.s_K % 32)) return hipErrorInvalidValue;
   switch (type) {
-    case kQ5_0: return launch_group_t<kQ5_0, EPI>(a, max_chunks, s);
-    case kQ8_0: return launch_group_t<kQ8_0, EPI>(a, max_chunks, s);
+    case kQ5_0: return launch_group_t<kQ5_0, EPI, SETS>(a, max_chunks, s);
+    case kQ8_0: return launch_group_t<kQ8_0, EPI, SETS>(a, max_chunks, s);
     default: return hipErrorInvalidValue;
   }
 }
@@ -2092,11 +2122,18 @@ hipError_t moe_down_combine_launch(int type, const MoeGemmArgs& a, const MoeComb
 hipError_t moe_gemm_launch(int type, int epi, const MoeGemmArgs& a, int mt, int max_chunks,
                            hipStream_t stream) {
   if (max_chunks <= 0 || a.N <= 0) return hipSuccess;
-  if (mt == 4) {
+  if (mt == 4 || mt == 8) {
+    const bool two = mt == 8;
     switch (epi) {
-      case kEpiSwiglu: return launch_group_epi<kEpiSwiglu>(type, a, max_chunks, stream);
-      case kEpiRelu2: return launch_group_epi<kEpiRelu2>(type, a, max_chunks, stream);
-      case kEpiDown: return launch_group_epi<kEpiDown>(type, a, max_chunks, stream);
+      case kEpiSwiglu:
+        return two ? launch_group_epi<kEpiSwiglu, 2>(type, a, max_chunks, stream)
+                   : launch_group_epi<kEpiSwiglu, 1>(type, a, max_chunks, stream);
+      case kEpiRelu2:
+        return two ? launch_group_epi<kEpiRelu2, 2>(type, a, max_chunks, stream)
+                   : launch_group_epi<kEpiRelu2, 1>(type, a, max_chunks, stream);
+      case kEpiDown:
+        return two ? launch_group_epi<kEpiDown, 2>(type, a, max_chunks, stream)
+                   : launch_group_epi<kEpiDown, 1>(type, a, max_chunks, stream);
       default: return hipErrorInvalidValue;
     }
   }
