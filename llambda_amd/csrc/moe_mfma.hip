@@ -478,10 +478,13 @@ __device__ __forceinline__ floatx4 mfma_b(const shortx4& a, const shortx4& b, co
 // ------------------------------------------------------------ tile shape
 enum GemmPipe : int { kPipeWide = 0, kPipeDouble = 1, kPipeDecode = 2 };
 
+#ifndef LLHIP_DECODE_WAVES
+#define LLHIP_DECODE_WAVES 4
+#endif
 template <int TYPE, int EPI, int PIPE>
 struct GemmShape {
   using B = GemmB<TYPE>;
-  static constexpr int kWaves = 4;
+  static constexpr int kWaves = PIPE == kPipeDecode ? LLHIP_DECODE_WAVES : 4;
   static constexpr int NB = EPI == kEpiSwiglu ? 2 : 1;             // gate and up side by side
   static constexpr int NS = (PIPE == kPipeWide ? 4 : 2) / NB;      // 16-row subtiles per matrix
   static constexpr int ROWS = 16 * NS;                              // rows per matrix and wave
@@ -1163,7 +1166,7 @@ moe_gemm_kernel(MoeGemmArgs args) {
 // order, then the shared expert) and their weighted combine, in one launch.
 // Workgroup r takes rows 16 r .. 16 r + 15 of every chunk.  The work units
 // are the chunks' 256-element K steps (chunk by chunk, steps in order); wave
-// w of 8 takes units w, w + 8, ..., streaming each unit's rows by DMA with
+// w of 16 takes units w, w + 16, ..., streaming each unit's rows by DMA with
 // the pair's 256 split activations and their 16 group sums through a ring of
 // LDS stages filled ahead of use.  A unit leaves the partial sums of its 16
 // rows in LDS; after one barrier lanes 0..15 of wave 0 add each chunk's
@@ -1179,7 +1182,10 @@ constexpr int kCombineUnits = 128;  // (chunk, K step) units of one token
 template <int TYPE>
 struct CombineShape {
   using B = GemmB<TYPE>;
-  static constexpr int kWaves = 8;
+  // sixteen waves: a unit's decode and products are a chain of dependent
+  // VALU work, so four waves per SIMD cover each other's latencies where two
+  // did not (Qwen3Next B=1 25.3 -> 23.0 us; the ring is one stage deep then)
+  static constexpr int kWaves = 16;
   static constexpr int PPR = B::kPitch / 16;       // 16-byte pieces per row
   static constexpr int PIECES = 16 * PPR;          // 16 rows
   static constexpr int LOADS = (PIECES + 63) / 64;
