@@ -15,7 +15,7 @@ import torch
 
 from llambda_amd import ggml, synthetic
 from llambda_amd.hip_backend import HipBackendError, make_hip_session_packed
-from llambda_amd.moe import HipMoeSession, synthetic_qwen3next
+from llambda_amd.moe import HipMoeSession, MoeLayerInputError, synthetic_qwen3next
 
 pytestmark = pytest.mark.gpu
 
@@ -72,15 +72,16 @@ def test_moe_host_runs_equal_device_runs(hip):
 
 
 def test_moe_host_run_error_word_then_good_run(hip):
-    """A NaN token reports the reference's router error through the error word
-    stored by the final launch; the flag is cleared, and the next one-token run
-    succeeds and matches the device-pointer run."""
+    """A NaN token reports the reference's router error (its own input error,
+    status -2: non-positive top-k weight sum, llambda.lisp:5373) through the
+    error word stored by the final launch; the flag is cleared, and the next
+    one-token run succeeds and matches the device-pointer run."""
     rng = np.random.default_rng(61)
     layer = synthetic_qwen3next(rng, hidden=256, experts=16, top_k=2, ffn=256, shared_ffn=256)
     s = HipMoeSession(layer)
     try:
         bad = np.full(layer.hidden, np.nan, dtype=np.float32)
-        with pytest.raises(HipBackendError, match="router"):
+        with pytest.raises(MoeLayerInputError, match="router produced non-positive top-k weight sum"):
             s.run_into(np.empty(layer.hidden, dtype=np.float32), bad)
         x = synthetic.activations(rng, 1, layer.hidden)
         y = np.empty(layer.hidden, dtype=np.float32)
