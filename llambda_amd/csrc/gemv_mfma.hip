@@ -892,8 +892,10 @@ __global__ void __launch_bounds__(64 * kMfmaWaves) gemv_tile_kernel(const MfmaAr
   for (int i = threadIdx.x; i < T::kZero / 16; i += blockDim.x)
     reinterpret_cast<u32x4*>(lds)[i] = u32x4{0u, 0u, 0u, 0u};
   using IT = std::conditional_t<TYPE == kQ4_K, Q4Items, Q6Items>;
-  build_table<IT, S>(table, gsum, args.x, nblk, f.norm_w, f.norm_eps, partial);
+  // the first tile's DMA streams in while the activation table is built
+  // (the table's loads wait behind it; head 71.3 -> 70.5 us by events)
   if (ntiles > 0) issue(wg_first);
+  build_table<IT, S>(table, gsum, args.x, nblk, f.norm_w, f.norm_eps, partial);
   __syncthreads();
 
   auto finish_round = [&](int r) {  // wave 0: the round's row sums, in wave order
