@@ -1423,22 +1423,43 @@ moe_down_combine_kernel(MoeGemmArgs a, MoeCombineArgs cb) {
 // each 256-element chunk after its eight groups), so a token's output does
 // not depend on the pipeline, and hence on the batch, it runs in.
 // Q5_0 in the stage-major lane order (moe_repack_launch): row r of a wave's
-// stage holds dwords [4j + g] = lane g's nibbles of block j, [8 + j] = the
-// block's qh, [10] = both deltas.  Codes and scales equal GemmB<kQ5_0>'s.
+// stage holds dwords [4j + g] = lane g's code fields of block j (byte b: all
+// five bits of code 8g + b, the low three of code 8g + 4 + b above them),
+// [8 + j] = the block's word of the other bits, [10] = both deltas.  Codes
+// and scales equal GemmB<kQ5_0>'s.
 __device__ __forceinline__ u32x4 staged_q5_fetch(const uint8_t* row, int j, int g) {
   const uint32_t* w = reinterpret_cast<const uint32_t*>(row);
   return u32x4{w[4 * j + g], w[8 + j], 0u, 0u};
 }
 __device__ __forceinline__ bf16x8 staged_q5_decode(const u32x4& w, int g) {
-  const uint32_t hb = __builtin_amdgcn_ubfe(w[1], 8u * (uint32_t)g, 8u);
-  const uint32_t c0 = (w[0] & 0x0F0F0F0Fu) | (spread_nibble(hb & 15u) << 4);
-  const uint32_t c1 = ((w[0] >> 4) & 0x0F0F0F0Fu) | (spread_nibble(hb >> 4) << 4);
+  // the word rotated right by 2g puts bits 3 and 4 of code 8g + 4 + b at
+  // bits 8b + 3 and 8b + 4
+  const uint32_t r = __builtin_amdgcn_alignbit(w[1], w[1], 2u * (uint32_t)g);
+  const uint32_t c0 = w[0] & 0x1F1F1F1Fu;
+  const uint32_t c1 = ((w[0] >> 5) & 0x07070707u) | (r & 0x18181818u);
   return codes_to_b(c0, c1);
 }
 __device__ __forceinline__ void staged_q5_scale(const uint8_t* row, int j, float& delta, float& c) {
   const uint32_t d = reinterpret_cast<const uint32_t*>(row)[10];
   delta = half_bits_to_float(j ? d >> 16 : d & 0xFFFFu);
   c = 144.f * delta;
+}
+// Q8_0 in the stage-major order: row r holds the codes q + 128 of blocks 0
+// and 1 in dwords [0, 16), both deltas in [16].  Codes and scales equal
+// GemmB<kQ8_0>'s.
+__device__ __forceinline__ u32x4 staged_q8_fetch(const uint8_t* row, int j, int g) {
+  const uint32_t* w = reinterpret_cast<const uint32_t*>(row);
+  return u32x4{w[8 * j + 2 * g], w[8 * j + 2 * g + 1], 0u, 0u};
+}
+__device__ __forceinline__ bf16x8 staged_q8_decode(const u32x4& w) {
+  using B = GemmB<kQ8_0>;
+  u32x4 v = {B::pack2(w[0], 0), B::pack2(w[0], 2), B::pack2(w[1], 0), B::pack2(w[1], 2)};
+  return __builtin_bit_cast(bf16x8, v);
+}
+__device__ __forceinline__ void staged_q8_scale(const uint8_t* row, int j, float& delta, float& c) {
+  const uint32_t d = reinterpret_cast<const uint32_t*>(row)[16];
+  delta = half_bits_to_float(j ? d >> 16 : d & 0xFFFFu);
+  c = 128.f * delta;
 }
 
 constexpr int kGroupWaves = 4;    // waves of one set: 64 rows each
@@ -1518,7 +1539,8 @@ moe_group_kernel(MoeGemmArgs args) {
   using B = GemmB<TYPE>;
   using Sh = GroupShape<TYPE, EPI, SETS>;
   constexpr int NB = Sh::NB, NS = Sh::NS, MT = kGroupTiles;
-  constexpr bool kStagedQ5 = TYPE == kQ5_0 && NB == 1;  // the lane-ordered stage-major rows
+  // one matrix: the stage-major rows in lane order
+  constexpr bool kStagedQ5 = TYPE == kQ5_0 && NB == 1, kStagedQ8 = TYPE == kQ8_0 && NB == 1;
   constexpr int BB = GroupB<TYPE>::kBlock;
   extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
 
@@ -1706,6 +1728,10 @@ moe_group_kernel(MoeGemmArgs args) {
               const uint8_t* row = wbuf + (16 * m + n) * Sh::RP;
               raw[m][nb] = staged_q5_fetch(row, jj, g);
               staged_q5_scale(row, jj, dl[m][nb], c);
+            } else if constexpr (kStagedQ8) {
+              const uint8_t* row = wbuf + (16 * m + n) * Sh::RP;
+              raw[m][nb] = staged_q8_fetch(row, jj, g);
+              staged_q8_scale(row, jj, dl[m][nb], c);
             } else {
               raw[m][nb] = group_fetch<TYPE, NB>(wbuf, nb, 16 * m + n, sh[m], jj, g);
               group_scale<TYPE, NB>(wbuf, nb, 16 * m + n, sh[m], jj, dl[m][nb], c);
@@ -1730,6 +1756,7 @@ moe_group_kernel(MoeGemmArgs args) {
           for (int nb = 0; nb < NB; ++nb) {
             typename B::Frag bf;
             if constexpr (kStagedQ5) bf = staged_q5_decode(raw[m][nb], g);
+            else if constexpr (kStagedQ8) bf = staged_q8_decode(raw[m][nb]);
             else bf = B::decode(raw[m][nb], sh[m], jj, g);
             const float delta = dl[m][nb];
 #pragma unroll
@@ -1960,10 +1987,12 @@ bool moe_group_pipeline_types(int type) { return type == kQ5_0 || type == kQ8_0;
 // The stage-major layout of the group pipeline's one-matrix launches: per
 // slab, per 64-row tile, per stage of two blocks, the tile's 64 rows' two
 // blocks back to back (a wave's stage then comes in as one contiguous run;
-// rows past the slab's and the block past an odd count are zeros).  Q8_0
-// blocks keep their bytes; a Q5_0 row's 44 bytes are reordered so that MFMA
-// lane g finds its eight codes' nibbles in one aligned dword and their high
-// bits in byte g of the block's qh word (staged_q5_decode).
+// rows past the slab's and the block past an odd count are zeros).  A row's
+// two blocks are reordered so that MFMA lane g decodes its eight codes from
+// aligned dwords in a few instructions: Q8_0 as the 64 codes q + 128 then the
+// two deltas (staged_q8_decode); Q5_0 as one dword of five- and three-bit
+// fields per lane and block plus a word of the remaining bits, rotated into
+// place per lane (staged_q5_decode).
 static int64_t repack_slab_bytes(int type, int64_t rows, int64_t columns) {
   const int64_t bb = block_bytes(type), nblk = columns / 32;
   return (rows + 63) / 64 * ((nblk + 1) / 2) * 128 * bb;
@@ -1989,32 +2018,51 @@ moe_repack_kernel(const uint8_t* __restrict__ src, int64_t rows, int64_t rb, int
     const uint8_t* rsrc = src + (slab * rows + row) * rb;
     uint8_t v = 0;
     if (bb == 22) {
-      // Q5_0, lane order: [0, 32) the nibble dwords N[j][g] (block j, lane
-      // g: byte b = code 8g + b | code 8g + 4 + b << 4), [32, 40) the qh
-      // words of blocks 0 and 1, [40, 44) their deltas
-      int j, off;
+      // Q5_0, lane order: [0, 32) the code dwords N[j][g] (block j, lane g:
+      // byte b = code 8g + b | (code 8g + 4 + b & 7) << 5), [32, 40) the
+      // words H[j] holding bits 3 and 4 of code 8g + 4 + b at bits
+      // (8b + 3 + 2g) and (8b + 4 + 2g) mod 32, [40, 44) the deltas
+      int j;
       if (rest < 32) j = rest >> 4;
       else if (rest < 40) j = (rest - 32) >> 2;
       else j = (rest - 40) >> 1;
       const int blk = 2 * stage + j;
       if (row < rows && blk < nblk) {
         const uint8_t* blkp = rsrc + (int64_t)blk * bb;
+        const uint32_t qh = blkp[2] | (uint32_t)blkp[3] << 8 | (uint32_t)blkp[4] << 16 |
+                            (uint32_t)blkp[5] << 24;
+        auto code = [&](int e) -> uint32_t {  // q of element e (0..31)
+          const uint32_t nib = e < 16 ? blkp[6 + e] & 15 : blkp[6 + e - 16] >> 4;
+          return nib | ((qh >> e) & 1u) << 4;
+        };
         if (rest < 32) {
           const int g = (rest & 15) >> 2, b = rest & 3;
-          auto nib = [&](int e) { return e < 16 ? blkp[6 + e] & 15 : blkp[6 + e - 16] >> 4; };
-          v = (uint8_t)(nib(8 * g + b) | (nib(8 * g + 4 + b) << 4));
+          v = (uint8_t)(code(8 * g + b) | (code(8 * g + 4 + b) & 7u) << 5);
         } else if (rest < 40) {
-          off = (rest - 32) & 3;
-          v = blkp[2 + off];
+          const int byte = (rest - 32) & 3;
+          uint32_t bits = 0;
+          for (int k = 0; k < 8; ++k) {
+            const int p = 8 * byte + k;
+            // the one lane g whose bit (8b + 3 + t + 2g) mod 32 is p
+            for (int g = 0; g < 4; ++g) {
+              const int s = (p - 3 - 2 * g) & 31;
+              if ((s & 7) < 2) bits |= ((code(8 * g + 4 + (s >> 3)) >> (3 + (s & 7))) & 1u) << k;
+            }
+          }
+          v = (uint8_t)bits;
         } else {
-          off = (rest - 40) & 1;
-          v = blkp[off];
+          v = blkp[(rest - 40) & 1];
         }
       }
     } else {
-      const int j = rest / bb, b = rest - j * bb;
+      // Q8_0: [0, 64) the two blocks' codes as q + 128 (q ^ 0x80), [64, 68)
+      // the deltas
+      const int j = rest < 64 ? rest >> 5 : (rest - 64) >> 1;
       const int blk = 2 * stage + j;
-      if (row < rows && blk < nblk) v = rsrc[(int64_t)blk * bb + b];
+      if (row < rows && blk < nblk) {
+        const uint8_t* blkp = rsrc + (int64_t)blk * bb;
+        v = rest < 64 ? (uint8_t)(blkp[2 + (rest & 31)] ^ 0x80u) : blkp[(rest - 64) & 1];
+      }
     }
     dst[i] = v;
   }
