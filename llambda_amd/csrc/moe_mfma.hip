@@ -75,6 +75,22 @@ namespace llhip {
 // [6:4], lgkmcnt [11:8]).  Issued through the builtin so the compiler's own
 // wait insertion knows the counters were drained.
 constexpr int waitcnt_vm(int n) { return 0x0F70 | (n & 15) | ((n >> 4) << 14); }
+
+// s_waitcnt vmcnt(n) for a wave-uniform n in 0..24 (larger n: 24)
+__device__ __forceinline__ void wait_vm_count(int n) {
+  switch (n) {
+#define LLHIP_WAIT_CASE(k) \
+  case k: __builtin_amdgcn_s_waitcnt(waitcnt_vm(k)); break;
+    LLHIP_WAIT_CASE(0) LLHIP_WAIT_CASE(1) LLHIP_WAIT_CASE(2) LLHIP_WAIT_CASE(3)
+    LLHIP_WAIT_CASE(4) LLHIP_WAIT_CASE(5) LLHIP_WAIT_CASE(6) LLHIP_WAIT_CASE(7)
+    LLHIP_WAIT_CASE(8) LLHIP_WAIT_CASE(9) LLHIP_WAIT_CASE(10) LLHIP_WAIT_CASE(11)
+    LLHIP_WAIT_CASE(12) LLHIP_WAIT_CASE(13) LLHIP_WAIT_CASE(14) LLHIP_WAIT_CASE(15)
+    LLHIP_WAIT_CASE(16) LLHIP_WAIT_CASE(17) LLHIP_WAIT_CASE(18) LLHIP_WAIT_CASE(19)
+    LLHIP_WAIT_CASE(20) LLHIP_WAIT_CASE(21) LLHIP_WAIT_CASE(22) LLHIP_WAIT_CASE(23)
+#undef LLHIP_WAIT_CASE
+    default: __builtin_amdgcn_s_waitcnt(waitcnt_vm(24)); break;
+  }
+}
 constexpr int kWaitLgkm0 = 0xC07F;
 
 // ------------------------------------------------------------ split rows
@@ -1462,8 +1478,19 @@ __device__ __forceinline__ void staged_q8_scale(const uint8_t* row, int j, float
   c = 128.f * delta;
 }
 
-constexpr int kGroupWaves = 4;    // waves of one set: 64 rows each
+// Row waves per set (64 rows each) and the depth of the LDS stage ring:
+// build knobs.
+#ifndef LLHIP_GROUP_ROW_WAVES
+#define LLHIP_GROUP_ROW_WAVES 4
+#endif
+#ifndef LLHIP_GROUP_RING
+#define LLHIP_GROUP_RING 2
+#endif
+constexpr int kGroupWaves = LLHIP_GROUP_ROW_WAVES;
+constexpr int kGroupRing = LLHIP_GROUP_RING;
 constexpr int kGroupTiles = 4;    // 16-token tiles per set
+static_assert(kGroupWaves == 4 || kGroupWaves == 8, "row waves: 4 or 8");
+static_assert(kGroupRing >= 2 && kGroupRing <= 4, "ring: 2 to 4 stages");
 
 template <int TYPE>
 struct GroupB;
@@ -1486,14 +1513,21 @@ struct GroupShape {
   static constexpr int RP = 2 * GroupB<TYPE>::kBlock;     // a row's bytes in the run
   static constexpr int ROWS = 64 / NB;  // rows per matrix and wave
   static constexpr int NS = ROWS / 16;
-  static constexpr int WAVES = kGroupWaves * SETS;
-  static constexpr int WG_ROWS = kGroupWaves * ROWS;
+  // row waves of a set (the silu-gate pair's two matrices keep four)
+  static constexpr int RW = NB == 2 ? 4 : kGroupWaves;
+  static constexpr int WAVES = RW * SETS;
+  static constexpr int WG_ROWS = RW * ROWS;
   static constexpr int PIECES = GroupB<TYPE>::kPieces;
   static constexpr int TOKENS = 64 * SETS;                  // pairs per chunk
   static constexpr int A_BYTES = TOKENS * 256 + TOKENS * 16;  // + each token's 4 group sums
-  static constexpr int B_BYTES = PIECES * NB * 1024;  // per wave of a set
-  static constexpr int STAGE = A_BYTES + kGroupWaves * B_BYTES;
-  static constexpr int LDS = 2 * STAGE;
+  // per wave of a set: one matrix, the run itself (the last DMA instruction
+  // takes only the lanes inside it); two, piece-major
+  static constexpr int B_BYTES = NB == 1 ? RUN : PIECES * NB * 1024;
+  static constexpr int STAGE = A_BYTES + RW * B_BYTES;
+  static constexpr int RING = kGroupRing * STAGE <= 160 * 1024 ? kGroupRing : 2;
+  static constexpr int LDS = RING * STAGE;
+  static_assert(RUN % 16 == 0 && STAGE % 16 == 0, "16-byte DMA slots");
+  static constexpr bool FITS = LDS <= 160 * 1024;  // else the launch is refused
 };
 
 // Dword i of row r of a wave's weight stage (matrix nb): one matrix, the
@@ -1534,7 +1568,7 @@ __device__ __forceinline__ void group_scale(const uint8_t* wbuf, int nb, int r, 
 }
 
 template <int TYPE, int EPI, int SETS>
-__global__ void __launch_bounds__(64 * kGroupWaves * SETS, SETS == 1 ? 2 : 1)
+__global__ void __launch_bounds__((64 * GroupShape<TYPE, EPI, SETS>::WAVES), 2)
 moe_group_kernel(MoeGemmArgs args) {
   using B = GemmB<TYPE>;
   using Sh = GroupShape<TYPE, EPI, SETS>;
@@ -1568,7 +1602,7 @@ moe_group_kernel(MoeGemmArgs args) {
   if (wg_row0 >= a.N) return;  // the whole workgroup
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int rw = wave & (kGroupWaves - 1), set = wave / kGroupWaves;  // row group, token set
+  const int rw = wave & (Sh::RW - 1), set = wave / Sh::RW;  // row group, token set
   const int n = lane & 15, g = lane >> 4;
   // rows of this wave (a wave past the last row still takes part in every
   // barrier: its rows clamp to the last one and its outputs are dropped)
@@ -1658,7 +1692,9 @@ moe_group_kernel(MoeGemmArgs args) {
       const uint8_t* run =
           uniform_ptr(base[0] + (int64_t)((n0 >> 6) * nstage + st) * Sh::RUN);
 #pragma unroll
-      for (int q = 0; q < Sh::PIECES; ++q) load_lds16(run, wdma[q], wst + 1024u * (uint32_t)q);
+      for (int q = 0; q < Sh::PIECES; ++q)
+        if (16 * (64 * q + lane) < Sh::RUN)  // lane 0 always: every instruction issues
+          load_lds16(run, wdma[q], wst + 1024u * (uint32_t)q);
     } else {
       const uint32_t off = (brow + sto) & ~3u;
 #pragma unroll
@@ -1710,7 +1746,7 @@ moe_group_kernel(MoeGemmArgs args) {
 
   auto compute = [&](auto ntc, int st, auto bufc) {
     constexpr int NT = decltype(ntc)::value;
-    const uint8_t* stg = lds + decltype(bufc)::value * Sh::STAGE;
+    const uint8_t* stg = lds + (int)bufc * Sh::STAGE;
     const uint8_t* wbuf = stg + Sh::A_BYTES + rw * Sh::B_BYTES;
     const int ls = st & 3;  // stage within the 256-element chunk
 #pragma unroll
@@ -1849,8 +1885,8 @@ moe_group_kernel(MoeGemmArgs args) {
 
   // the stages; each 256-element chunk's offsets follow its last stage (the
   // final chunk's after the loop, in line with the epilogue)
-  // (two stages per iteration: the buffer of each is a compile-time
-  // constant, folded into the LDS instructions' offsets)
+  // Two buffers: two stages per iteration, the buffer of each a compile-time
+  // constant folded into the LDS instructions' offsets.
   auto stage = [&](auto ntc, int st, auto bufc) {
     __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
     __syncthreads();
@@ -1860,11 +1896,36 @@ moe_group_kernel(MoeGemmArgs args) {
       if ((st & 3) == 3 && st + 1 < nstage) apply_offsets(ntc);
     }
   };
+  // A deeper ring: RING - 1 stages in flight; stage st waits for its own DMA
+  // by count (this wave's per-stage instruction count times the stages
+  // issued after it), then the barrier, then stage st + RING - 1 goes into
+  // the buffer stage st - 1 left.
+  int n_act = 0;
+#pragma unroll
+  for (int u = 0; u < 4; ++u) n_act += (wave + Sh::WAVES * u < 4 * nt) ? 1 : 0;
+  const int per_stage = n_act + (wave < SETS ? 1 : 0) + (live && set == 0 ? Sh::PIECES * NB : 0);
   auto run = [&](auto ntc) {
-    issue(0, 0);
-    for (int st = 0; st < nstage; st += 2) {
-      stage(ntc, st, std::integral_constant<int, 0>{});
-      if (st + 1 < nstage) stage(ntc, st + 1, std::integral_constant<int, 1>{});
+    if constexpr (Sh::RING == 2) {
+      issue(0, 0);
+      for (int st = 0; st < nstage; st += 2) {
+        stage(ntc, st, std::integral_constant<int, 0>{});
+        if (st + 1 < nstage) stage(ntc, st + 1, std::integral_constant<int, 1>{});
+      }
+    } else {
+      constexpr int R = Sh::RING;
+      for (int s = 0; s < R - 1 && s < nstage; ++s) issue(s, s);
+      int buf = 0, nbuf = R - 1;  // stage st's buffer, and st + R - 1's
+      for (int st = 0; st < nstage; ++st) {
+        wait_vm_count(per_stage * min(R - 2, nstage - 1 - st));
+        __syncthreads();
+        if (st + R - 1 < nstage) issue(st + R - 1, nbuf);
+        if (work) {
+          compute(ntc, st, buf);
+          if ((st & 3) == 3 && st + 1 < nstage) apply_offsets(ntc);
+        }
+        buf = buf == R - 1 ? 0 : buf + 1;
+        nbuf = nbuf == R - 1 ? 0 : nbuf + 1;
+      }
     }
     if (work) {
       apply_offsets(ntc);
@@ -1954,20 +2015,24 @@ static hipError_t launch_gemm_epi(int type, const MoeGemmArgs& a, int mt, int ma
 template <int TYPE, int EPI, int SETS>
 static hipError_t launch_group_t(const MoeGemmArgs& a_in, int max_chunks, hipStream_t stream) {
   using Sh = GroupShape<TYPE, EPI, SETS>;
-  MoeGemmArgs a = a_in;
-  const auto kernel = moe_group_kernel<TYPE, EPI, SETS>;
-  if (Sh::LDS > 65536) {
-    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kernel),
-                                       hipFuncAttributeMaxDynamicSharedMemorySize, Sh::LDS);
-    if (e != hipSuccess) return e;
+  if constexpr (!Sh::FITS) {
+    return hipErrorInvalidValue;  // this build's ring and row waves leave no room
+  } else {
+    MoeGemmArgs a = a_in;
+    const auto kernel = moe_group_kernel<TYPE, EPI, SETS>;
+    if (Sh::LDS > 65536) {
+      hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kernel),
+                                         hipFuncAttributeMaxDynamicSharedMemorySize, Sh::LDS);
+      if (e != hipSuccess) return e;
+    }
+    const int rows = a.joint ? std::max(a.N, a.s_N) : a.N;
+    a.row_tiles = (rows + Sh::WG_ROWS - 1) / Sh::WG_ROWS;
+    a.tiles_per_wg = 1;
+    a.depth = Sh::RING;
+    const dim3 grid(((max_chunks + 7) / 8) * 8 * a.row_tiles);
+    hipLaunchKernelGGL(kernel, grid, dim3(64 * Sh::WAVES), Sh::LDS, stream, a);
+    return hipGetLastError();
   }
-  const int rows = a.joint ? std::max(a.N, a.s_N) : a.N;
-  a.row_tiles = (rows + Sh::WG_ROWS - 1) / Sh::WG_ROWS;
-  a.tiles_per_wg = 1;
-  a.depth = 2;
-  const dim3 grid(((max_chunks + 7) / 8) * 8 * a.row_tiles);
-  hipLaunchKernelGGL(kernel, grid, dim3(64 * Sh::WAVES), Sh::LDS, stream, a);
-  return hipGetLastError();
 }
 
 template <int EPI, int SETS>
