@@ -75,22 +75,6 @@ namespace llhip {
 // [6:4], lgkmcnt [11:8]).  Issued through the builtin so the compiler's own
 // wait insertion knows the counters were drained.
 constexpr int waitcnt_vm(int n) { return 0x0F70 | (n & 15) | ((n >> 4) << 14); }
-
-// s_waitcnt vmcnt(n) for a wave-uniform n in 0..24 (larger n: 24)
-__device__ __forceinline__ void wait_vm_count(int n) {
-  switch (n) {
-#define LLHIP_WAIT_CASE(k) \
-  case k: __builtin_amdgcn_s_waitcnt(waitcnt_vm(k)); break;
-    LLHIP_WAIT_CASE(0) LLHIP_WAIT_CASE(1) LLHIP_WAIT_CASE(2) LLHIP_WAIT_CASE(3)
-    LLHIP_WAIT_CASE(4) LLHIP_WAIT_CASE(5) LLHIP_WAIT_CASE(6) LLHIP_WAIT_CASE(7)
-    LLHIP_WAIT_CASE(8) LLHIP_WAIT_CASE(9) LLHIP_WAIT_CASE(10) LLHIP_WAIT_CASE(11)
-    LLHIP_WAIT_CASE(12) LLHIP_WAIT_CASE(13) LLHIP_WAIT_CASE(14) LLHIP_WAIT_CASE(15)
-    LLHIP_WAIT_CASE(16) LLHIP_WAIT_CASE(17) LLHIP_WAIT_CASE(18) LLHIP_WAIT_CASE(19)
-    LLHIP_WAIT_CASE(20) LLHIP_WAIT_CASE(21) LLHIP_WAIT_CASE(22) LLHIP_WAIT_CASE(23)
-#undef LLHIP_WAIT_CASE
-    default: __builtin_amdgcn_s_waitcnt(waitcnt_vm(24)); break;
-  }
-}
 constexpr int kWaitLgkm0 = 0xC07F;
 
 // ------------------------------------------------------------ split rows
@@ -1478,19 +1462,13 @@ __device__ __forceinline__ void staged_q8_scale(const uint8_t* row, int j, float
   c = 128.f * delta;
 }
 
-// Row waves per set (64 rows each) and the depth of the LDS stage ring:
-// build knobs.
+// Row waves per set (64 rows each): a build knob.
 #ifndef LLHIP_GROUP_ROW_WAVES
 #define LLHIP_GROUP_ROW_WAVES 4
 #endif
-#ifndef LLHIP_GROUP_RING
-#define LLHIP_GROUP_RING 2
-#endif
 constexpr int kGroupWaves = LLHIP_GROUP_ROW_WAVES;
-constexpr int kGroupRing = LLHIP_GROUP_RING;
 constexpr int kGroupTiles = 4;    // 16-token tiles per set
 static_assert(kGroupWaves == 4 || kGroupWaves == 8, "row waves: 4 or 8");
-static_assert(kGroupRing >= 2 && kGroupRing <= 4, "ring: 2 to 4 stages");
 
 template <int TYPE>
 struct GroupB;
@@ -1524,8 +1502,7 @@ struct GroupShape {
   // takes only the lanes inside it); two, piece-major
   static constexpr int B_BYTES = NB == 1 ? RUN : PIECES * NB * 1024;
   static constexpr int STAGE = A_BYTES + RW * B_BYTES;
-  static constexpr int RING = kGroupRing * STAGE <= 160 * 1024 ? kGroupRing : 2;
-  static constexpr int LDS = RING * STAGE;
+  static constexpr int LDS = 2 * STAGE;
   static_assert(RUN % 16 == 0 && STAGE % 16 == 0, "16-byte DMA slots");
   static constexpr bool FITS = LDS <= 160 * 1024;  // else the launch is refused
 };
@@ -1746,7 +1723,7 @@ moe_group_kernel(MoeGemmArgs args) {
 
   auto compute = [&](auto ntc, int st, auto bufc) {
     constexpr int NT = decltype(ntc)::value;
-    const uint8_t* stg = lds + (int)bufc * Sh::STAGE;
+    const uint8_t* stg = lds + decltype(bufc)::value * Sh::STAGE;
     const uint8_t* wbuf = stg + Sh::A_BYTES + rw * Sh::B_BYTES;
     const int ls = st & 3;  // stage within the 256-element chunk
 #pragma unroll
@@ -1885,8 +1862,9 @@ moe_group_kernel(MoeGemmArgs args) {
 
   // the stages; each 256-element chunk's offsets follow its last stage (the
   // final chunk's after the loop, in line with the epilogue)
-  // Two buffers: two stages per iteration, the buffer of each a compile-time
-  // constant folded into the LDS instructions' offsets.
+  // (two stages per iteration: the buffer of each is a compile-time
+  // constant, folded into the LDS instructions' offsets.  Deeper rings, of
+  // both operands or of either, measured slower.)
   auto stage = [&](auto ntc, int st, auto bufc) {
     __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
     __syncthreads();
@@ -1896,36 +1874,11 @@ moe_group_kernel(MoeGemmArgs args) {
       if ((st & 3) == 3 && st + 1 < nstage) apply_offsets(ntc);
     }
   };
-  // A deeper ring: RING - 1 stages in flight; stage st waits for its own DMA
-  // by count (this wave's per-stage instruction count times the stages
-  // issued after it), then the barrier, then stage st + RING - 1 goes into
-  // the buffer stage st - 1 left.
-  int n_act = 0;
-#pragma unroll
-  for (int u = 0; u < 4; ++u) n_act += (wave + Sh::WAVES * u < 4 * nt) ? 1 : 0;
-  const int per_stage = n_act + (wave < SETS ? 1 : 0) + (live && set == 0 ? Sh::PIECES * NB : 0);
   auto run = [&](auto ntc) {
-    if constexpr (Sh::RING == 2) {
-      issue(0, 0);
-      for (int st = 0; st < nstage; st += 2) {
-        stage(ntc, st, std::integral_constant<int, 0>{});
-        if (st + 1 < nstage) stage(ntc, st + 1, std::integral_constant<int, 1>{});
-      }
-    } else {
-      constexpr int R = Sh::RING;
-      for (int s = 0; s < R - 1 && s < nstage; ++s) issue(s, s);
-      int buf = 0, nbuf = R - 1;  // stage st's buffer, and st + R - 1's
-      for (int st = 0; st < nstage; ++st) {
-        wait_vm_count(per_stage * min(R - 2, nstage - 1 - st));
-        __syncthreads();
-        if (st + R - 1 < nstage) issue(st + R - 1, nbuf);
-        if (work) {
-          compute(ntc, st, buf);
-          if ((st & 3) == 3 && st + 1 < nstage) apply_offsets(ntc);
-        }
-        buf = buf == R - 1 ? 0 : buf + 1;
-        nbuf = nbuf == R - 1 ? 0 : nbuf + 1;
-      }
+    issue(0, 0);
+    for (int st = 0; st < nstage; st += 2) {
+      stage(ntc, st, std::integral_constant<int, 0>{});
+      if (st + 1 < nstage) stage(ntc, st + 1, std::integral_constant<int, 1>{});
     }
     if (work) {
       apply_offsets(ntc);
@@ -2016,7 +1969,7 @@ template <int TYPE, int EPI, int SETS>
 static hipError_t launch_group_t(const MoeGemmArgs& a_in, int max_chunks, hipStream_t stream) {
   using Sh = GroupShape<TYPE, EPI, SETS>;
   if constexpr (!Sh::FITS) {
-    return hipErrorInvalidValue;  // this build's ring and row waves leave no room
+    return hipErrorInvalidValue;  // this build's row waves leave no room in LDS
   } else {
     MoeGemmArgs a = a_in;
     const auto kernel = moe_group_kernel<TYPE, EPI, SETS>;
@@ -2028,7 +1981,7 @@ static hipError_t launch_group_t(const MoeGemmArgs& a_in, int max_chunks, hipStr
     const int rows = a.joint ? std::max(a.N, a.s_N) : a.N;
     a.row_tiles = (rows + Sh::WG_ROWS - 1) / Sh::WG_ROWS;
     a.tiles_per_wg = 1;
-    a.depth = Sh::RING;
+    a.depth = 2;
     const dim3 grid(((max_chunks + 7) / 8) * 8 * a.row_tiles);
     hipLaunchKernelGGL(kernel, grid, dim3(64 * Sh::WAVES), Sh::LDS, stream, a);
     return hipGetLastError();
