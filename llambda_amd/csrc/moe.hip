@@ -60,8 +60,8 @@ __global__ void __launch_bounds__(kScanThreads) moe_scan_kernel(MoePlan p, int t
   __shared__ int s_off[kMoeMaxExperts + 1];
   __shared__ int s_coff[kMoeMaxExperts + 1];
   __shared__ int s_cur[kMoeMaxExperts];
-  __shared__ int s_part[kScanThreads];
-  __shared__ int s_cpart[kScanThreads];
+  __shared__ int s_part[kScanThreads / 64];
+  __shared__ int s_cpart[kScanThreads / 64];
   const int E = p.experts, K = p.top_k, tid = threadIdx.x;
   const int P = tokens * K;
   for (int e = tid; e < E; e += kScanThreads) {
@@ -83,18 +83,27 @@ __global__ void __launch_bounds__(kScanThreads) moe_scan_kernel(MoePlan p, int t
     sum += s_cnt[e];
     csum += (s_cnt[e] + nt - 1) / nt;
   }
-  s_part[tid] = sum;
-  s_cpart[tid] = csum;
-  __syncthreads();
-  for (int off = 1; off < kScanThreads; off <<= 1) {
-    const int v = tid >= off ? s_part[tid - off] : 0;
-    const int cv = tid >= off ? s_cpart[tid - off] : 0;
-    __syncthreads();
-    s_part[tid] += v;
-    s_cpart[tid] += cv;
-    __syncthreads();
+  // exclusive prefix sums of both counts in thread order: wavefront scans,
+  // then the wavefronts' totals
+  const int lane = tid & 63, wave = tid >> 6;
+  int inc = sum, cinc = csum;
+  for (int o = 1; o < 64; o <<= 1) {
+    const int v = __shfl_up(inc, o, 64), cv = __shfl_up(cinc, o, 64);
+    if (lane >= o) {
+      inc += v;
+      cinc += cv;
+    }
   }
-  int run = tid ? s_part[tid - 1] : 0, crun = tid ? s_cpart[tid - 1] : 0;
+  if (lane == 63) {
+    s_part[wave] = inc;
+    s_cpart[wave] = cinc;
+  }
+  __syncthreads();
+  int run = inc - sum, crun = cinc - csum;
+  for (int w = 0; w < wave; ++w) {
+    run += s_part[w];
+    crun += s_cpart[w];
+  }
   for (int e = e0; e < e1; ++e) {
     s_off[e] = run;
     s_coff[e] = crun;
@@ -102,8 +111,8 @@ __global__ void __launch_bounds__(kScanThreads) moe_scan_kernel(MoePlan p, int t
     crun += (s_cnt[e] + nt - 1) / nt;
   }
   if (tid == kScanThreads - 1) {
-    s_off[E] = s_part[tid];
-    s_coff[E] = s_cpart[tid];
+    s_off[E] = run;
+    s_coff[E] = crun;
   }
   __syncthreads();
   const int routed_pairs = s_off[E], routed_chunks = s_coff[E];
