@@ -1696,14 +1696,21 @@ moe_group_kernel(MoeGemmArgs args) {
 #pragma unroll
       for (int nb = 0; nb < NB; ++nb) tot[i][m][nb] = floatx4{0.f, 0.f, 0.f, 0.f};
   // offsets of the current 256-element chunk: -c of group 4 q + g of the
-  // lane's rows, and the lane token's sum of that group
+  // lane's rows, and the lane token's sum of that group.  The stage-major
+  // rows keep, instead of -c, the word holding the deltas of the stage
+  // with the lane's group (c is formed from it when the offsets apply, the
+  // same product as the scale's).
+  constexpr bool kStaged = kStagedQ5 || kStagedQ8;
   float cneg[NS][NB][2];
+  uint32_t cdw[NS][2];
   float sv[MT][2];
   auto clear_offsets = [&]() {
 #pragma unroll
-    for (int m = 0; m < NS; ++m)
+    for (int m = 0; m < NS; ++m) {
 #pragma unroll
       for (int nb = 0; nb < NB; ++nb) cneg[m][nb][0] = cneg[m][nb][1] = 0.f;
+      cdw[m][0] = cdw[m][1] = 0u;
+    }
 #pragma unroll
     for (int i = 0; i < MT; ++i) sv[i][0] = sv[i][1] = 0.f;
   };
@@ -1715,6 +1722,18 @@ moe_group_kernel(MoeGemmArgs args) {
   // result needs can be lost on the branch path.
   auto apply_offsets = [&](auto ntc) {
     constexpr int NT = decltype(ntc)::value;
+    if constexpr (kStaged) {
+      // (a cleared word -- a group past the last -- gives -c = -0, which
+      // leaves the sums as +0 does: they start at +0 and never become -0)
+      constexpr float kC = kStagedQ5 ? 144.f : 128.f;
+#pragma unroll
+      for (int m = 0; m < NS; ++m)
+#pragma unroll
+        for (int q = 0; q < 2; ++q) {
+          const uint32_t bits = (g & 1) ? cdw[m][q] >> 16 : cdw[m][q] & 0xFFFFu;
+          cneg[m][0][q] = -(kC * half_bits_to_float(bits));
+        }
+    }
 #pragma unroll
     for (int q = 0; q < 2; ++q)
 #pragma unroll
@@ -1755,10 +1774,12 @@ moe_group_kernel(MoeGemmArgs args) {
               raw[m][nb] = group_fetch<TYPE, NB>(wbuf, nb, 16 * m + n, sh[m], jj, g);
               group_scale<TYPE, NB>(wbuf, nb, 16 * m + n, sh[m], jj, dl[m][nb], c);
             }
-            // (q = j8 >> 2 is uniform: a select per lane, not an indexed write)
-            const bool mine = (j8 & 3) == g;
-            cneg[m][nb][0] = (mine && j8 < 4) ? -c : cneg[m][nb][0];
-            cneg[m][nb][1] = (mine && j8 >= 4) ? -c : cneg[m][nb][1];
+            if constexpr (!kStaged) {
+              // (q = j8 >> 2 is uniform: a select per lane, not an indexed write)
+              const bool mine = (j8 & 3) == g;
+              cneg[m][nb][0] = (mine && j8 < 4) ? -c : cneg[m][nb][0];
+              cneg[m][nb][1] = (mine && j8 >= 4) ? -c : cneg[m][nb][1];
+            }
           }
         // token 16 i + n of the set: block 4 i + (n >> 2), slot 16 (n & 3) +
         // (piece ^ n)
@@ -1793,10 +1814,20 @@ moe_group_kernel(MoeGemmArgs args) {
     }
     // this stage holds groups 2 st and 2 st + 1: lanes whose offset group
     // 4 q + g is one of them take the lane token's sum of it (the sum of
-    // its two 16-halves, as the other pipelines form it)
+    // its two 16-halves, as the other pipelines form it) and, stage-major,
+    // the word of its rows' deltas
     {
       const bool mine = (g >> 1) == (ls & 1);
       const bool ok = 2 * st + (g & 1) < groups;
+      if constexpr (kStaged) {
+#pragma unroll
+        for (int m = 0; m < NS; ++m) {
+          const uint32_t dw = reinterpret_cast<const uint32_t*>(
+              wbuf + (16 * m + n) * Sh::RP)[kStagedQ5 ? 10 : 16];
+          cdw[m][0] = (mine && ok && ls < 2) ? dw : cdw[m][0];
+          cdw[m][1] = (mine && ok && ls >= 2) ? dw : cdw[m][1];
+        }
+      }
 #pragma unroll
       for (int i = 0; i < NT; ++i) {
         const float* sp = reinterpret_cast<const float*>(
