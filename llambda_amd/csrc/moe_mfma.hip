@@ -1428,14 +1428,16 @@ moe_down_combine_kernel(MoeGemmArgs a, MoeCombineArgs cb) {
 // then lo MFMA, per-group delta fma in group order, the -c * sum offsets of
 // each 256-element chunk after its eight groups), so a token's output does
 // not depend on the pipeline, and hence on the batch, it runs in.
-// Q5_0 in the stage-major lane order (moe_repack_launch): row r of a wave's
-// stage holds dwords [4j + g] = lane g's code fields of block j (byte b: all
-// five bits of code 8g + b, the low three of code 8g + 4 + b above them),
-// [8 + j] = the block's word of the other bits, [10] = both deltas.  Codes
+// Q5_0 in the stage-major plane order (moe_repack_launch): a wave's stage
+// of 64 rows is 704 dwords -- [64 (4j + g) + (r ^ 16 g)] = lane g's code
+// fields of block j of row r (byte b: all five bits of code 8g + b, the low
+// three of code 8g + 4 + b above them), [512 + 64 j + r] = block j's word of
+// the other bits, [640 + r] = both deltas -- so that the 64 lanes' reads of
+// one subtile (rows 16 m + n, lanes g) fall in 64 different banks.  Codes
 // and scales equal GemmB<kQ5_0>'s.
-__device__ __forceinline__ u32x4 staged_q5_fetch(const uint8_t* row, int j, int g) {
-  const uint32_t* w = reinterpret_cast<const uint32_t*>(row);
-  return u32x4{w[4 * j + g], w[8 + j], 0u, 0u};
+__device__ __forceinline__ u32x4 staged_q5_fetch(const uint8_t* run, int r, int j, int g) {
+  const uint32_t* w = reinterpret_cast<const uint32_t*>(run);
+  return u32x4{w[64 * (4 * j + g) + (r ^ (16 * g))], w[512 + 64 * j + r], 0u, 0u};
 }
 __device__ __forceinline__ bf16x8 staged_q5_decode(const u32x4& w, int g) {
   // the word rotated right by 2g puts bits 3 and 4 of code 8g + 4 + b at
@@ -1445,8 +1447,12 @@ __device__ __forceinline__ bf16x8 staged_q5_decode(const u32x4& w, int g) {
   const uint32_t c1 = ((w[0] >> 5) & 0x07070707u) | (r & 0x18181818u);
   return codes_to_b(c0, c1);
 }
-__device__ __forceinline__ void staged_q5_scale(const uint8_t* row, int j, float& delta, float& c) {
-  const uint32_t d = reinterpret_cast<const uint32_t*>(row)[10];
+__device__ __forceinline__ uint32_t staged_q5_deltas(const uint8_t* run, int r) {
+  return reinterpret_cast<const uint32_t*>(run)[640 + r];
+}
+__device__ __forceinline__ void staged_q5_scale(const uint8_t* run, int r, int j, float& delta,
+                                                float& c) {
+  const uint32_t d = staged_q5_deltas(run, r);
   delta = half_bits_to_float(j ? d >> 16 : d & 0xFFFFu);
   c = 144.f * delta;
 }
@@ -1763,9 +1769,8 @@ moe_group_kernel(MoeGemmArgs args) {
           for (int nb = 0; nb < NB; ++nb) {
             float c;
             if constexpr (kStagedQ5) {
-              const uint8_t* row = wbuf + (16 * m + n) * Sh::RP;
-              raw[m][nb] = staged_q5_fetch(row, jj, g);
-              staged_q5_scale(row, jj, dl[m][nb], c);
+              raw[m][nb] = staged_q5_fetch(wbuf, 16 * m + n, jj, g);
+              staged_q5_scale(wbuf, 16 * m + n, jj, dl[m][nb], c);
             } else if constexpr (kStagedQ8) {
               const uint8_t* row = wbuf + (16 * m + n) * Sh::RP;
               raw[m][nb] = staged_q8_fetch(row, jj, g);
@@ -1822,8 +1827,9 @@ moe_group_kernel(MoeGemmArgs args) {
       if constexpr (kStaged) {
 #pragma unroll
         for (int m = 0; m < NS; ++m) {
-          const uint32_t dw = reinterpret_cast<const uint32_t*>(
-              wbuf + (16 * m + n) * Sh::RP)[kStagedQ5 ? 10 : 16];
+          const uint32_t dw =
+              kStagedQ5 ? staged_q5_deltas(wbuf, 16 * m + n)
+                        : reinterpret_cast<const uint32_t*>(wbuf + (16 * m + n) * Sh::RP)[16];
           cdw[m][0] = (mine && ok && ls < 2) ? dw : cdw[m][0];
           cdw[m][1] = (mine && ok && ls >= 2) ? dw : cdw[m][1];
         }
@@ -2042,12 +2048,13 @@ bool moe_group_pipeline_types(int type) { return type == kQ5_0 || type == kQ8_0;
 // The stage-major layout of the group pipeline's one-matrix launches: per
 // slab, per 64-row tile, per stage of two blocks, the tile's 64 rows' two
 // blocks back to back (a wave's stage then comes in as one contiguous run;
-// rows past the slab's and the block past an odd count are zeros).  A row's
-// two blocks are reordered so that MFMA lane g decodes its eight codes from
-// aligned dwords in a few instructions: Q8_0 as the 64 codes q + 128 then the
-// two deltas (staged_q8_decode); Q5_0 as one dword of five- and three-bit
-// fields per lane and block plus a word of the remaining bits, rotated into
-// place per lane (staged_q5_decode).
+// rows past the slab's and the block past an odd count are zeros).  The
+// blocks are reordered so that MFMA lane g decodes its eight codes from
+// aligned dwords in a few instructions: Q8_0 rows as the 64 codes q + 128
+// then the two deltas (staged_q8_decode); Q5_0 as planes of one dword of
+// five- and three-bit fields per lane, block and row, swizzled so that a
+// subtile's 64 reads hit 64 banks, a word of the remaining bits per block
+// and row, rotated into place per lane (staged_q5_decode), and the deltas.
 static int64_t repack_slab_bytes(int type, int64_t rows, int64_t columns) {
   const int64_t bb = block_bytes(type), nblk = columns / 32;
   return (rows + 63) / 64 * ((nblk + 1) / 2) * 128 * bb;
@@ -2073,40 +2080,50 @@ moe_repack_kernel(const uint8_t* __restrict__ src, int64_t rows, int64_t rb, int
     const uint8_t* rsrc = src + (slab * rows + row) * rb;
     uint8_t v = 0;
     if (bb == 22) {
-      // Q5_0, lane order: [0, 32) the code dwords N[j][g] (block j, lane g:
-      // byte b = code 8g + b | (code 8g + 4 + b & 7) << 5), [32, 40) the
-      // words H[j] holding bits 3 and 4 of code 8g + 4 + b at bits
-      // (8b + 3 + 2g) and (8b + 4 + 2g) mod 32, [40, 44) the deltas
-      int j;
-      if (rest < 32) j = rest >> 4;
-      else if (rest < 40) j = (rest - 32) >> 2;
-      else j = (rest - 40) >> 1;
+      // Q5_0, plane order (staged_q5_fetch): the run's dword D = o / 4
+      const int D = o >> 2, byte = o & 3;
+      int pr, j, kind, g = 0;  // kind 0: code fields, 1: the word of other bits, 2: deltas
+      if (D < 512) {
+        kind = 0;
+        j = (D >> 6) >> 2;
+        g = (D >> 6) & 3;
+        pr = (D & 63) ^ (16 * g);
+      } else if (D < 640) {
+        kind = 1;
+        j = (D - 512) >> 6;
+        pr = (D - 512) & 63;
+      } else {
+        kind = 2;
+        j = byte >> 1;
+        pr = D - 640;
+      }
+      const int64_t prow = (int64_t)tile * 64 + pr;
       const int blk = 2 * stage + j;
-      if (row < rows && blk < nblk) {
-        const uint8_t* blkp = rsrc + (int64_t)blk * bb;
+      if (prow < rows && blk < nblk) {
+        const uint8_t* blkp = src + (slab * rows + prow) * rb + (int64_t)blk * bb;
         const uint32_t qh = blkp[2] | (uint32_t)blkp[3] << 8 | (uint32_t)blkp[4] << 16 |
                             (uint32_t)blkp[5] << 24;
         auto code = [&](int e) -> uint32_t {  // q of element e (0..31)
           const uint32_t nib = e < 16 ? blkp[6 + e] & 15 : blkp[6 + e - 16] >> 4;
           return nib | ((qh >> e) & 1u) << 4;
         };
-        if (rest < 32) {
-          const int g = (rest & 15) >> 2, b = rest & 3;
-          v = (uint8_t)(code(8 * g + b) | (code(8 * g + 4 + b) & 7u) << 5);
-        } else if (rest < 40) {
-          const int byte = (rest - 32) & 3;
+        if (kind == 0) {
+          v = (uint8_t)(code(8 * g + byte) | (code(8 * g + 4 + byte) & 7u) << 5);
+        } else if (kind == 1) {
+          // bits 3 and 4 of code 8g + 4 + b at bits (8b + 3 + 2g) and
+          // (8b + 4 + 2g) mod 32 of the word
           uint32_t bits = 0;
           for (int k = 0; k < 8; ++k) {
             const int p = 8 * byte + k;
-            // the one lane g whose bit (8b + 3 + t + 2g) mod 32 is p
-            for (int g = 0; g < 4; ++g) {
-              const int s = (p - 3 - 2 * g) & 31;
-              if ((s & 7) < 2) bits |= ((code(8 * g + 4 + (s >> 3)) >> (3 + (s & 7))) & 1u) << k;
+            for (int gg = 0; gg < 4; ++gg) {  // the one lane whose bit p is
+              const int sft = (p - 3 - 2 * gg) & 31;
+              if ((sft & 7) < 2)
+                bits |= ((code(8 * gg + 4 + (sft >> 3)) >> (3 + (sft & 7))) & 1u) << k;
             }
           }
           v = (uint8_t)bits;
         } else {
-          v = blkp[(rest - 40) & 1];
+          v = blkp[byte & 1];
         }
       }
     } else {
