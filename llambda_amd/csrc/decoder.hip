@@ -124,6 +124,16 @@ attention_kernel(const float* __restrict__ q, const float* __restrict__ kc,
       }
     }
   }
+  // the value rows of the weighted sum, requested now so that they load
+  // while the softmax runs: thread (prt, col) takes float4 column col of
+  // slots prt, prt + NP, ...
+  const int col = threadIdx.x % DQ, prt = threadIdx.x / DQ;
+  float4 vr[PPP];
+#pragma unroll
+  for (int i = 0; i < PPP; ++i) {
+    const int p = min(p0 + prt + NP * i, n - 1);
+    vr[i] = *reinterpret_cast<const float4*>(vh + (int64_t)p * D + 4 * col);
+  }
   __syncthreads();
 
   // chunk max, e_p = exp(s_p - m) rounded to single, and the chunk sum
@@ -154,14 +164,6 @@ attention_kernel(const float* __restrict__ q, const float* __restrict__ kc,
 
   // unnormalised weighted sum of the chunk's value rows
   {
-    // thread (prt, col) takes float4 column col of slots prt, prt + NP, ...
-    const int col = threadIdx.x % DQ, prt = threadIdx.x / DQ;
-    float4 vr[PPP];
-#pragma unroll
-    for (int i = 0; i < PPP; ++i) {
-      const int p = min(p0 + prt + NP * i, n - 1);
-      vr[i] = *reinterpret_cast<const float4*>(vh + (int64_t)p * D + 4 * col);
-    }
     float4 acc[G];
 #pragma unroll
     for (int h = 0; h < G; ++h) acc[h] = make_float4(0.f, 0.f, 0.f, 0.f);
