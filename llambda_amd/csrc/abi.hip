@@ -1356,7 +1356,7 @@ int llambda_hip_llama_session_step(llambda_hip_llama_session* s, int64_t token, 
     std::lock_guard<std::mutex> lock(s->run_mutex);
     HIPC(hipSetDevice(s->device));
     HIPC(hipStreamWaitEvent(s->stream, s->done, 0));
-    HIPC(decoder_state_launch(s->plan.state, (int)token, (int)position, s->stream));
+    HIPC(decoder_state_launch(s->plan, (int)token, (int)position, s->stream));
     HIPC(decoder_step_launch(s->plan, s->logits.as<float>(), s->stream));
     HIPC(hipMemcpyAsync(logits, s->logits.ptr, logits_count * sizeof(float), hipMemcpyDeviceToHost,
                         s->stream));
@@ -1395,7 +1395,7 @@ int llambda_hip_llama_session_step_device(llambda_hip_llama_session* s, int64_t 
       s->graph_logits = logits;
     }
     HIPC(hipStreamWaitEvent(st, s->done, 0));
-    HIPC(decoder_state_launch(s->plan.state, (int)token, (int)position, st));
+    HIPC(decoder_state_launch(s->plan, (int)token, (int)position, st));
     if (use_graph) HIPC(hipGraphLaunch(s->exec, st));
     else HIPC(decoder_step_launch(s->plan, logits, st));
     HIPC(hipEventRecord(s->done, st));

@@ -73,12 +73,12 @@ constexpr int kDecoderMaxContext = kAttnChunk * kAttnMaxChunks;
 
 bool decoder_head_supported(int head_dim, int group);
 
-// state <- (token, position), as a kernel so a captured graph that reads the
-// state can follow it on the stream.
-hipError_t decoder_state_launch(int* state, int token, int position, hipStream_t stream);
+// state <- (token, position) and the rotation table of the position, as a
+// kernel so a captured graph that reads them can follow it on the stream.
+hipError_t decoder_state_launch(const DecoderPlan& p, int token, int position, hipStream_t stream);
 
-// Everything after the state: embedding row, rotation table, the layers and
-// the output rows into logits (device, [vocab]).
+// Everything after the state: embedding row, the layers and the output rows
+// into logits (device, [vocab]).
 hipError_t decoder_step_launch(const DecoderPlan& p, float* logits, hipStream_t stream);
 
 // Attention of one layer alone (test hook): q [heads][head_dim] (rotated and

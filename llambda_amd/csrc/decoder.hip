@@ -3,33 +3,36 @@
 // launch sequence over the fused batch-1 GEMV (gemv_mfma.hip).
 #include "decoder.h"
 
+#include <algorithm>
 #include <cmath>
 
 namespace llhip {
 
-__global__ void decoder_state_kernel(int* __restrict__ state, int token, int position) {
-  if (threadIdx.x == 0) {
+// The state word and the rotation table of the position: cos and sin of
+// angle = position / denom[i] per rotary pair (apply-rope-head-in-place,
+// llambda.lisp:3760-3795: the angle in double; denom[i] = factor_i *
+// theta^(2i/d) is formed on the host, +inf where the factor exceeds 1e20 so
+// that the angle is 0).
+__global__ void decoder_state_kernel(int* __restrict__ state, int token, int position,
+                                     const double* __restrict__ denom, int pairs,
+                                     double* __restrict__ cs) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i == 0) {
     state[0] = token;
     state[1] = position;
   }
-}
-
-hipError_t decoder_state_launch(int* state, int token, int position, hipStream_t stream) {
-  hipLaunchKernelGGL(decoder_state_kernel, dim3(1), dim3(64), 0, stream, state, token, position);
-  return hipGetLastError();
-}
-
-// cos and sin of angle = position / denom[i] per rotary pair
-// (apply-rope-head-in-place, llambda.lisp:3760-3795: the angle in double;
-// denom[i] = factor_i * theta^(2i/d) is formed on the host, +inf where the
-// factor exceeds 1e20 so that the angle is 0).
-__global__ void rope_table_kernel(const int* __restrict__ state, const double* __restrict__ denom,
-                                  int pairs, double* __restrict__ cs) {
-  const int i = blockIdx.x * blockDim.x + threadIdx.x;
   if (i >= pairs) return;
-  const double angle = (double)state[1] / denom[i];
+  const double angle = (double)position / denom[i];
   cs[2 * i] = cos(angle);
   cs[2 * i + 1] = sin(angle);
+}
+
+hipError_t decoder_state_launch(const DecoderPlan& p, int token, int position,
+                                hipStream_t stream) {
+  const int blocks = std::max(1, (p.rope_pairs + 63) / 64);
+  hipLaunchKernelGGL(decoder_state_kernel, dim3(blocks), dim3(64), 0, stream, p.state, token,
+                     position, p.rope_denom, p.rope_pairs, p.rope_cs);
+  return hipGetLastError();
 }
 
 // ----------------------------------------------------------------- attention
@@ -313,13 +316,9 @@ static GemvProblem problem(const DecoderMatrix& m, const float* x, float* y) {
 
 hipError_t decoder_step_launch(const DecoderPlan& p, float* logits, hipStream_t st) {
   const int D = p.head_dim;
-  // token row (gguf-model-token-row-into, llambda.lisp:4977-4982), rotation
+  // token row (gguf-model-token-row-into, llambda.lisp:4977-4982); the
+  // rotation table came with the state
   DEC_CHECK(dequant_launch(p.embd.type, p.embd.w, p.embd.row_bytes, 1, p.hidden, p.x, st, p.state));
-  if (p.rope_pairs > 0) {
-    hipLaunchKernelGGL(rope_table_kernel, dim3((p.rope_pairs + 63) / 64), dim3(64), 0, st, p.state,
-                       p.rope_denom, p.rope_pairs, p.rope_cs);
-    DEC_CHECK(hipGetLastError());
-  }
   for (int l = 0; l < p.layer_count; ++l) {
     const DecoderLayer& L = p.layers[l];
     GemvFuse rope;
