@@ -556,11 +556,14 @@ constexpr int gemm_lds_bytes(int depth) {
 // GATE (single-token pipeline, one token): the launch also selects and
 // gates the token (gate_token) instead of reading a chunk table.
 template <int TYPE, int EPI, int MT, int PIPE, bool ALIGNED, bool GATE = false>
-// (the wide pipeline asks for two workgroups per CU, except for the
-// 32-weight block types, whose decode state does not fit the registers that
-// leaves: they ran with 52-500 bytes of scratch per lane)
+// (two workgroups per CU: within that budget of 256 registers the compiler
+// writes the MFMA results to ordinary registers instead of accumulation
+// registers it then reads back one by one -- a quarter of the double
+// pipeline's main-loop VALU; except for the wide pipeline of the 32-weight
+// block types, whose decode state does not fit: they ran with 52-500 bytes
+// of scratch per lane)
 __global__ void __launch_bounds__((64 * GemmShape<TYPE, EPI, PIPE>::kWaves),
-                                  (PIPE == kPipeWide && TYPE != kQ5_0 && TYPE != kQ8_0 ? 2 : 1))
+                                  (PIPE != kPipeWide || (TYPE != kQ5_0 && TYPE != kQ8_0) ? 2 : 1))
 moe_gemm_kernel(MoeGemmArgs args) {
   using B = GemmB<TYPE>;
   using Sh = GemmShape<TYPE, EPI, PIPE>;
