@@ -295,7 +295,15 @@ static int moe_mfma_tiles(const MoePlan& p, int tokens) {
   const int64_t act_w = std::max(p.ffn, p.shared_ffn);
   const int64_t split_bytes = std::max((int64_t)tokens * (p.top_k + 1) * 4 * act_w,
                                        (int64_t)tokens * 4 * std::max(p.hidden, p.latent_in));
-  if (!types || split_bytes >= ((int64_t)1 << 31)) return 2;
+  // the wide pipeline's relu^2 and down kernels for Q5_0 rows of an odd
+  // number of blocks (not dword multiples) do not fit the registers: layers
+  // with such rows keep 16-pair chunks
+  auto odd_q5 = [](int type, int64_t k) { return type == kQ5_0 && ((k / 32) & 1); };
+  const bool odd = odd_q5(p.up_type, p.latent_in ? p.latent_in : p.hidden) ||
+                   odd_q5(p.down_type, p.ffn) ||
+                   (p.shared_ffn && (odd_q5(p.sh_up_type, p.hidden) ||
+                                     odd_q5(p.sh_down_type, p.shared_ffn)));
+  if (!types || split_bytes >= ((int64_t)1 << 31)) return odd ? 1 : 2;
   return LLHIP_GROUP_PAIRS / 16;
 }
 static int moe_chunk_tokens(int mt) { return mt == 0 ? 1 : 16 * mt; }

@@ -1983,7 +1983,11 @@ static hipError_t launch_gemm_mt(const MoeGemmArgs& a, int mt, int max_chunks, h
         if (a.fused_gate) return launch_gemm_t<TYPE, EPI, 1, kPipeDecode, ALIGNED, true>(a, max_chunks, s);
       return launch_gemm_t<TYPE, EPI, 1, kPipeDecode, ALIGNED>(a, max_chunks, s);
     case 1: return launch_gemm_t<TYPE, EPI, 1, kPipeDouble, ALIGNED>(a, max_chunks, s);
-    case 2: return launch_gemm_t<TYPE, EPI, 2, kPipeWide, ALIGNED>(a, max_chunks, s);
+    case 2:
+      // (Q5_0 rows that are not dword multiples take 16-pair chunks: the
+      // launcher never asks for these)
+      if constexpr (TYPE == kQ5_0 && !ALIGNED && EPI != kEpiSwiglu) return hipErrorInvalidValue;
+      else return launch_gemm_t<TYPE, EPI, 2, kPipeWide, ALIGNED>(a, max_chunks, s);
     default: return hipErrorInvalidValue;
   }
 }

@@ -390,7 +390,9 @@ def test_group_pipeline_separate_shared_launches(hip):
 # The same long chunks for 32-weight block experts beside a K-quant shared
 # expert: the group pipeline needs every tensor in a 32-weight type, so these
 # run on the wide pipeline; ffn 224 makes the down rows 154 (Q5_0) or 238
-# (Q8_0) bytes, not dword multiples.
+# (Q8_0) bytes, not dword multiples.  (Layers with Q5_0 rows of an odd
+# number of blocks keep 16-pair chunks, whose kernels fit the registers: the
+# Q5_0 cases check that path at this batch.)
 @pytest.mark.parametrize("variant,types", [
     ("nemotron", (ggml.Q5_0, ggml.Q5_0)), ("nemotron", (ggml.Q8_0, ggml.Q8_0)),
     ("qwen", (ggml.Q8_0, ggml.Q5_0))])
