@@ -776,7 +776,8 @@ moe_gemm_kernel(MoeGemmArgs args) {
 #pragma unroll
     for (int m = 0; m < NS; ++m)
       sh[m] = TILED ? 0u : ALIGNED ? (koff & 3u) : ((brow[m] + koff) & 3u);
-    // scale table: lane (n, g) decodes groups g*KS/4 .. +KS/4-1 of row n
+    // scale table: lane (n, g) decodes groups g, g + 4, ... of row n (the
+    // four lane groups' entries then sit in different banks)
 #pragma unroll
     for (int m = 0; m < NS; ++m)
 #pragma unroll
@@ -784,7 +785,7 @@ moe_gemm_kernel(MoeGemmArgs args) {
         const uint8_t* row = stage + nb * Sh::MATBUF + (16 * m + n) * B::kPitch;
 #pragma unroll
         for (int e = 0; e < KS / 4; ++e) {
-          const int j = g * (KS / 4) + e;
+          const int j = g + 4 * e;
           float delta, c;
           B::scale(row, sh[m], j, delta, c);
           const bool ok = j < valid;
@@ -981,11 +982,11 @@ moe_gemm_kernel(MoeGemmArgs args) {
     }
   } else if constexpr (PIPE == kPipeDouble && SHARE_A) {
     // As below, with the chunk's activations in LDS: wave w loads tokens
-    // 4w .. 4w+3 (lane l: token 4w + (l >> 4), 16-byte pieces 4 (l & 15) ..
-    // +3 of its 1 KB) into registers while the step computes, and stores
-    // them once every wave is done with the step's; piece P of token t sits
-    // in slot P ^ t of the token's 1 KB, so a fragment's 16 tokens read 16
-    // different bank quads.  The steps and barriers are the workgroup's: a
+    // 4w .. 4w+3 (lane l: token 4w + (l >> 4), 16-byte pieces (l & 15) +
+    // 16 k, k < 4, of its 1 KB) into registers while the step computes, and
+    // stores them once every wave is done with the step's; piece P of token t
+    // sits in slot P ^ t of the token's 1 KB, so a fragment's 16 tokens read
+    // 16 different bank quads, and the 16 lanes of a store write 16.  The steps and barriers are the workgroup's: a
     // wave without rows in a tile loads its quarter and waits with the rest.
     const int n0w = n0 - wave * Sh::ROWS;
     const int ntile = min(a.tiles_per_wg, (a.N - n0w + Sh::WG_ROWS - 1) / Sh::WG_ROWS);
@@ -1001,7 +1002,7 @@ moe_gemm_kernel(MoeGemmArgs args) {
       const int valid = min(KS, groups - kc * KS);
 #pragma unroll
       for (int k = 0; k < 4; ++k) {
-        const int piece = 4 * (lane & 15) + k;  // group piece >> 3
+        const int piece = (lane & 15) + 16 * k;  // group piece >> 3
         qa[k] = (piece >> 3) < valid
                     ? *reinterpret_cast<const u32x4*>(qrow + 512 * kc + 8 * piece)
                     : u32x4{0u, 0u, 0u, 0u};
@@ -1010,7 +1011,7 @@ moe_gemm_kernel(MoeGemmArgs args) {
     auto store_quarter = [&]() {
 #pragma unroll
       for (int k = 0; k < 4; ++k) {
-        const int piece = 4 * (lane & 15) + k;
+        const int piece = (lane & 15) + 16 * k;
         *reinterpret_cast<u32x4*>(alds + qt * 1024 + 16 * (piece ^ qt)) = qa[k];
       }
     };
@@ -1230,10 +1231,11 @@ __device__ __forceinline__ void combine_step(int kc, const uint8_t* stage, uint3
   const int valid = FULL ? KS : min(KS, groups - kc * KS);
   const uint32_t sh = B::kTilePitch ? 0u : ALIGNED ? (koff & 3u) : ((brow + koff) & 3u);
   const uint8_t* row = stage + n * B::kPitch;
-  // scale table: lane (n, g) decodes groups g*KS/4 .. +KS/4-1 of row n
+  // scale table: lane (n, g) decodes groups g, g + 4, ... of row n (the four
+  // lane groups' entries then sit in different banks)
 #pragma unroll
   for (int e = 0; e < KS / 4; ++e) {
-    const int j = g * (KS / 4) + e;
+    const int j = g + 4 * e;
     float delta, c;
     B::scale(row, sh, j, delta, c);
     const bool ok = j < valid;
