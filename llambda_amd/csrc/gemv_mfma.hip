@@ -41,10 +41,12 @@ __device__ __forceinline__ float sum_lane_groups(float v) {
 
 // ------------------------------------------------------------ row staging
 // A wavefront streams its 16-row tile through LDS in chunks of C blocks per
-// row.  Piece j (16 bytes) of row r of the chunk is load lane (r * kPieces +
+// row.  Piece j (16 bytes) of row r of the chunk is load lane (r * kPitch +
 // j): global_load_lds_dwordx4 writes lane i's 16 bytes to M0 + 16 i, so the
-// LDS image of a chunk is the rows' byte ranges back to back, kRow bytes
-// apart, with no VGPR staging.  Each row's range starts at the dword at or
+// LDS image of a chunk is the rows' byte ranges kRow bytes apart, with no
+// VGPR staging.  kPitch is kPieces rounded up to an odd count (the pad piece
+// repeats the row's last piece), so the 16 rows' reads of one offset fall in
+// 16 different bank quads.  Each row's range starts at the dword at or
 // below the chunk's first byte (row starts need only be 2-byte aligned) and
 // may run up to 18 bytes past the chunk (the allocation's pad covers the last
 // row).  Two buffers per wave: the next chunk loads while this one computes.
@@ -52,8 +54,9 @@ template <int BB, int C, bool ALIGNED>
 struct Chunk {
   static constexpr int kSpan = C * BB;
   static constexpr int kPieces = (kSpan + (ALIGNED ? 0 : 3) + 15) / 16;
-  static constexpr int kRow = 16 * kPieces;
-  static constexpr int kLoads = (16 * kPieces + 63) / 64;
+  static constexpr int kPitch = kPieces | 1;
+  static constexpr int kRow = 16 * kPitch;
+  static constexpr int kLoads = (16 * kPitch + 63) / 64;
   static constexpr int kBuffer = 1024 * kLoads;  // per buffer; lanes past 16 rows write slack
 };
 
@@ -62,6 +65,16 @@ struct Chunk {
 // reads its row's entry; others read the zero line), then 8 group sums.
 constexpr int kQ4Table = 8 * 16 * 16;  // bytes per block
 constexpr int kQ6Table = 2 * 4 * 8 * 16;
+
+// Zero lines (LDS [0, 2 KB) is zero) for A lanes without data, in a bank
+// quad (16-byte slot modulo 256 bytes) that no data lane of the same 16-lane
+// group reads in that instruction, so the group's reads take one pass.  Q4_K:
+// the data lanes of lane group g read slots 4g .. 4g+3 of each 256-byte MFMA
+// row (the table and its blocks are 256-byte aligned), the zero lanes slot
+// 4g + 4; Q6_K: the data lanes of MFMA m of half h read slots 8m .. 8m+7
+// (modulo 16) at h * 512 + m * 128, the zero lanes 128 bytes further.
+__device__ __forceinline__ uint32_t zero_line_q4(int g) { return 16u * (uint32_t)((4 * g + 4) & 15); }
+constexpr uint32_t kZeroLineQ6 = 128;
 
 // Table items: Q4_K item i = (block, sub-block s, 4-element step m); Q6_K
 // item i = (block, half, k, l-octet): 8 activations.  first(i) is the item's
@@ -109,8 +122,7 @@ __device__ __forceinline__ Q4Raw q4k_fetch(const uint8_t* p, int g) {
 }
 
 // One Q4_K block of lane (n, g)'s row from its fetched bytes; a = the lane's
-// A address for this block (0 when its A row carries no data: LDS [0, 2 KB)
-// is zero).
+// A address for this block (a zero line when its A row carries no data).
 __device__ __forceinline__ float q4k_block(const Q4Raw& r, const uint8_t* lds, uint32_t a,
                                            const float* gs, int g) {
   const uint4 h = r.h, c0 = r.c0, c1 = r.c1;
@@ -228,7 +240,7 @@ __device__ __forceinline__ Q6Raw q6k_fetch(const uint8_t* p, int g) {
 }
 
 // One Q6_K block of lane (n, g)'s row from its fetched bytes.  am[m] = the
-// lane's A address for MFMA m of the block (0: zero line).
+// lane's A address for MFMA m of the block (kZeroLineQ6: zero line).
 __device__ __forceinline__ float q6k_block(const Q6Raw& r, const uint8_t* lds, const uint32_t am[4],
                                            const float* gs, int g) {
   const float dd = half_bits_to_float(r.d);
@@ -579,19 +591,19 @@ __device__ __forceinline__ void gemv_mfma_body(uint8_t* lds, int wg, int nwg, co
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int n = lane & 15, g = lane >> 4, a = lane & 15;
-  // A addressing: lane_a = the lane's table entry in block 0, or 0 (zero
-  // region) in MFMAs where its A row carries no data.
+  // A addressing: lane_a = the lane's table entry in block 0, or a zero line
+  // in MFMAs where its A row carries no data (zero_line_q4 / kZeroLineQ6).
   uint32_t a_base;
   bool a_m[4];
   if constexpr (TYPE == kQ4_K) {
-    a_base = (g == (a >> 2)) ? table_off + (uint32_t)(a * 16) : 0u;
+    a_base = (g == (a >> 2)) ? table_off + (uint32_t)(a * 16) : zero_line_q4(g);
   } else {
     const bool act = ((a >> 1) & 1) == (g >> 1);
     a_base = table_off + (uint32_t)(((a & 3) * 2 + (g & 1)) * 16);
 #pragma unroll
     for (int m = 0; m < 4; ++m) a_m[m] = act && (a >> 2) == m;
   }
-  const uint32_t a_stride = (TYPE == kQ4_K && a_base == 0u) ? 0u : (uint32_t)T::kTable;
+  const uint32_t a_stride = (TYPE == kQ4_K && g != (a >> 2)) ? 0u : (uint32_t)T::kTable;
 
   const uint8_t* stage = stages + wave * nbuf * Ch::kBuffer;
   const uint32_t stage_lds = lds_address(stage);
@@ -630,9 +642,9 @@ __device__ __forceinline__ void gemv_mfma_body(uint8_t* lds, int wg, int nwg, co
   uint32_t voff[Ch::kLoads];
 #pragma unroll
   for (int i = 0; i < Ch::kLoads; ++i) {
-    const int idx = min(64 * i + lane, 16 * Ch::kPieces - 1);
-    const int r = idx / Ch::kPieces;
-    voff[i] = (uint32_t)r * rb + 16u * (uint32_t)(idx - r * Ch::kPieces);
+    const int idx = min(64 * i + lane, 16 * Ch::kPitch - 1);
+    const int r = idx / Ch::kPitch;
+    voff[i] = (uint32_t)r * rb + 16u * (uint32_t)min(idx - r * Ch::kPitch, Ch::kPieces - 1);
   }
 
   // Row r of the tile starts at base + r * rb; its range is read from the
@@ -653,10 +665,10 @@ __device__ __forceinline__ void gemv_mfma_body(uint8_t* lds, int wg, int nwg, co
       // the last row)
 #pragma unroll
       for (int i = 0; i < Ch::kLoads; ++i) {
-        const int idx = min(64 * i + lane, 16 * Ch::kPieces - 1);
-        const int r = idx / Ch::kPieces;
+        const int idx = min(64 * i + lane, 16 * Ch::kPitch - 1);
+        const int r = idx / Ch::kPitch;
         const uint32_t rr = (uint32_t)min(r, rmax);
-        o[i] = ((bsh + rr * rb) & ~3u) + 16u * (uint32_t)(idx - r * Ch::kPieces);
+        o[i] = ((bsh + rr * rb) & ~3u) + 16u * (uint32_t)min(idx - r * Ch::kPitch, Ch::kPieces - 1);
       }
     }
     return base - bsh;
@@ -750,8 +762,8 @@ __device__ __forceinline__ void gemv_mfma_body(uint8_t* lds, int wg, int nwg, co
         acc += q4k_block(raw[bl], lds, a_base + (uint32_t)b * a_stride, gs, g);
       } else {
         const uint32_t ab = a_base + (uint32_t)b * (uint32_t)T::kTable;
-        const uint32_t am[4] = {a_m[0] ? ab : 0u, a_m[1] ? ab : 0u, a_m[2] ? ab : 0u,
-                                a_m[3] ? ab : 0u};
+        const uint32_t am[4] = {a_m[0] ? ab : kZeroLineQ6, a_m[1] ? ab : kZeroLineQ6,
+                                a_m[2] ? ab : kZeroLineQ6, a_m[3] ? ab : kZeroLineQ6};
         acc += q6k_block(raw[bl], lds, am, gs, g);
       }
     }
@@ -843,14 +855,14 @@ __global__ void __launch_bounds__(64 * kMfmaWaves) gemv_tile_kernel(const MfmaAr
   uint32_t a_base;
   bool a_m[4];
   if constexpr (TYPE == kQ4_K) {
-    a_base = (g == (a >> 2)) ? table_off + (uint32_t)(a * 16) : 0u;
+    a_base = (g == (a >> 2)) ? table_off + (uint32_t)(a * 16) : zero_line_q4(g);
   } else {
     const bool act = ((a >> 1) & 1) == (g >> 1);
     a_base = table_off + (uint32_t)(((a & 3) * 2 + (g & 1)) * 16);
 #pragma unroll
     for (int m = 0; m < 4; ++m) a_m[m] = act && (a >> 2) == m;
   }
-  const uint32_t a_stride = (TYPE == kQ4_K && a_base == 0u) ? 0u : (uint32_t)T::kTable;
+  const uint32_t a_stride = (TYPE == kQ4_K && g != (a >> 2)) ? 0u : (uint32_t)T::kTable;
 
   // the workgroup's contiguous tile range (workgroups b and b + nwg / 2 --
   // one CU when the grid is two per CU -- take adjacent ranges)
@@ -931,8 +943,8 @@ __global__ void __launch_bounds__(64 * kMfmaWaves) gemv_tile_kernel(const MfmaAr
         acc += q4k_block(raw[bl], lds, a_base + (uint32_t)b * a_stride, gs, g);
       } else {
         const uint32_t ab = a_base + (uint32_t)b * (uint32_t)T::kTable;
-        const uint32_t am[4] = {a_m[0] ? ab : 0u, a_m[1] ? ab : 0u, a_m[2] ? ab : 0u,
-                                a_m[3] ? ab : 0u};
+        const uint32_t am[4] = {a_m[0] ? ab : kZeroLineQ6, a_m[1] ? ab : kZeroLineQ6,
+                                a_m[2] ? ab : kZeroLineQ6, a_m[3] ? ab : kZeroLineQ6};
         acc += q6k_block(raw[bl], lds, am, gs, g);
       }
     }
