@@ -176,7 +176,8 @@ hipError_t moe_repack_launch(int type, const uint8_t* src, int64_t slabs, int64_
 // 16-row tile, per 256-weight chunk, the 16 rows' chunks back to back, each
 // padded to a dword (Q4_K 144 bytes, Q6_K 212); rows past the slab's are
 // zeros.  A wave's stage of a chunk is then one contiguous run whose rows
-// start on dwords.  moe_slab_bytes: one slab's bytes in the device layout of
+// start on dwords.  In a Q6_K chunk each 32-byte run of ql and qh (its first
+// 192 bytes) holds dword 4s + g of the GGUF run at dword 2g + s.  moe_slab_bytes: one slab's bytes in the device layout of
 // `type` (tile-major for K-quants, packed rows otherwise).
 bool moe_tiled_type(int type);
 int64_t moe_slab_bytes(int type, int64_t rows, int64_t columns);

@@ -328,6 +328,12 @@ struct GemmB<kQ4_K> {
 // Q6_K: chunk = one super-block (210 B), 16 scale groups of 16 elements.
 // Element e = 128h + 32k + l has scale sc[e / 16] (llambda.lisp:4203-4310,
 // 6919-6978); lane g takes l = 16s + 4g .. +3 of group u = 8h + 2k + s.
+// The tile-major rows (moe_tile_launch) hold each 32-byte run of ql and qh
+// with the words of groups 2t and 2t + 1 that lane g reads side by side
+// (dword 2g + s of the run instead of 4s + g), so that one 8-byte read per
+// lane serves both groups and a half wave's reads meet 32 different bank
+// pairs (four-byte reads of rows 240 bytes apart put rows n and n + 8 in one
+// bank).
 template <>
 struct GemmB<kQ6_K> {
   static constexpr int kSpan = 210, kPieces = 14, kPitch = odd_pitch(kPieces), kSteps = 16,
@@ -339,14 +345,13 @@ struct GemmB<kQ6_K> {
   typedef u32x4 Raw;
   static __device__ __forceinline__ Raw fetch(const uint8_t* row, uint32_t, int u, int g) {
     const int h = u >> 3, k = (u >> 1) & 3, s = u & 1;
-    const uint32_t ol = 64 * h + 32 * (k & 1) + 16 * s + 4 * g, oh = 128 + 32 * h + 16 * s + 4 * g;
-    return u32x4{lds_dword(row, ol >> 2), lds_dword(row, (ol >> 2) + 1), lds_dword(row, oh >> 2),
-                 lds_dword(row, (oh >> 2) + 1)};
+    const uint2 l2 = *reinterpret_cast<const uint2*>(row + 64 * h + 32 * (k & 1) + 8 * g);
+    const uint2 q2 = *reinterpret_cast<const uint2*>(row + 128 + 32 * h + 8 * g);
+    return u32x4{s ? l2.y : l2.x, 0u, s ? q2.y : q2.x, 0u};
   }
-  static __device__ __forceinline__ Frag decode(const Raw& w, uint32_t sh, int u, int) {
+  static __device__ __forceinline__ Frag decode(const Raw& w, uint32_t, int u, int) {
     const int k = (u >> 1) & 3;
-    const uint32_t ql = __builtin_amdgcn_alignbyte(w[1], w[0], sh);
-    const uint32_t qh = __builtin_amdgcn_alignbyte(w[3], w[2], sh);
+    const uint32_t ql = w[0], qh = w[2];  // tile-major: rows start on dwords
     const uint32_t nib = (ql >> (4 * (k >> 1))) & 0x0F0F0F0Fu;
     const uint32_t hb = ((qh >> (2 * k)) & 0x03030303u) << 4;
     return codes4_to_b(nib | hb);
@@ -2167,8 +2172,8 @@ hipError_t moe_repack_launch(int type, const uint8_t* src, int64_t slabs, int64_
 // tile t, chunk kc of slab s: zeros in a row's dword pad and past the slab.
 __global__ void __launch_bounds__(256)
 moe_tile_kernel(const uint16_t* __restrict__ src, int64_t rows, int64_t row_halves, int nchunk,
-                int span_halves, int pitch_halves, int64_t tiles, uint16_t* __restrict__ dst,
-                int64_t total) {
+                int span_halves, int pitch_halves, int64_t tiles, int pair_halves,
+                uint16_t* __restrict__ dst, int64_t total) {
   const int64_t chunk_halves = 16 * (int64_t)pitch_halves;
   const int64_t tile_halves = nchunk * chunk_halves;
   for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total;
@@ -2179,9 +2184,16 @@ moe_tile_kernel(const uint16_t* __restrict__ src, int64_t rows, int64_t row_halv
     const int in_chunk = (int)(in_tile - kc * chunk_halves);
     const int r = in_chunk / pitch_halves, h = in_chunk - r * pitch_halves;
     const int64_t slab = t_all / tiles, row = (t_all - slab * tiles) * 16 + r;
+    // the first pair_halves halves: 32-byte runs whose dword d' = 2g + s
+    // comes from dword 4s + g of the source run
+    int hs = h;
+    if (h < pair_halves) {
+      const int d = (h & 15) >> 1;
+      hs = (h & ~15) + 2 * (4 * (d & 1) + (d >> 1)) + (h & 1);
+    }
     uint16_t v = 0;
     if (row < rows && h < span_halves)
-      v = src[(slab * rows + row) * row_halves + (int64_t)kc * span_halves + h];
+      v = src[(slab * rows + row) * row_halves + (int64_t)kc * span_halves + hs];
     dst[i] = v;
   }
 }
@@ -2205,7 +2217,7 @@ hipError_t moe_tile_launch(int type, const uint8_t* src, int64_t slabs, int64_t 
   const int grid = (int)std::min<int64_t>((total + 255) / 256, 65536);
   hipLaunchKernelGGL(moe_tile_kernel, dim3(grid), dim3(256), 0, stream,
                      reinterpret_cast<const uint16_t*>(src), rows, (int64_t)nchunk * span / 2,
-                     nchunk, span / 2, pitch / 2, (rows + 15) / 16,
+                     nchunk, span / 2, pitch / 2, (rows + 15) / 16, type == kQ6_K ? 96 : 0,
                      reinterpret_cast<uint16_t*>(dst), total);
   return hipGetLastError();
 }
