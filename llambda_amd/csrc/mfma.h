@@ -87,6 +87,20 @@ __device__ __forceinline__ uint32_t lds_address(const void* p) {
   return (uint32_t)(uintptr_t)(lds_ptr_t)(p);
 }
 
+// An 8-byte LDS read that the compiler does not pair with another into one
+// ds_read2_b64: a paired read serves 16 lanes a cycle, so the rows n and
+// n + 8 of a stage (rows of 144 or 240 bytes) meet in one bank; single
+// 8-byte reads serve 32 lanes a cycle and see none (measured with the LDS
+// bank-conflict counter).  The address passes through an empty asm, so no
+// two reads share a base register; equal addresses still combine.
+__device__ __forceinline__ uint2 lds_read8(const void* p) {
+  uint32_t a = lds_address(p);
+  asm("" : "+v"(a));
+  typedef unsigned int pair_t __attribute__((ext_vector_type(2)));
+  const pair_t v = *reinterpret_cast<const __attribute__((address_space(3))) pair_t*>(a);
+  return make_uint2(v.x, v.y);
+}
+
 // 64 lanes x 16 bytes from base + voff[lane] to LDS lds + 16 * lane (vector
 // memory load with LDS destination).  base and lds are wavefront-uniform.
 __device__ __forceinline__ void load_lds16(const uint8_t* base, uint32_t voff, uint32_t lds) {

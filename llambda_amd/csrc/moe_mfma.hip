@@ -296,7 +296,7 @@ struct GemmB<kQ4_K> {
   typedef bf16x8 Frag;
   typedef uint2 Raw;
   static __device__ __forceinline__ Raw fetch(const uint8_t* row, uint32_t, int j, int g) {
-    return *reinterpret_cast<const uint2*>(row + 16 + 32 * (j >> 1) + 8 * g);
+    return lds_read8(row + 16 + 32 * (j >> 1) + 8 * g);
   }
   static __device__ __forceinline__ Frag decode(const Raw& q, uint32_t, int j, int) {
     const uint32_t c0 = (j & 1) ? (q.x >> 4) & 0x0F0F0F0Fu : q.x & 0x0F0F0F0Fu;
@@ -345,8 +345,8 @@ struct GemmB<kQ6_K> {
   typedef u32x4 Raw;
   static __device__ __forceinline__ Raw fetch(const uint8_t* row, uint32_t, int u, int g) {
     const int h = u >> 3, k = (u >> 1) & 3, s = u & 1;
-    const uint2 l2 = *reinterpret_cast<const uint2*>(row + 64 * h + 32 * (k & 1) + 8 * g);
-    const uint2 q2 = *reinterpret_cast<const uint2*>(row + 128 + 32 * h + 8 * g);
+    const uint2 l2 = lds_read8(row + 64 * h + 32 * (k & 1) + 8 * g);
+    const uint2 q2 = lds_read8(row + 128 + 32 * h + 8 * g);
     return u32x4{s ? l2.y : l2.x, 0u, s ? q2.y : q2.x, 0u};
   }
   static __device__ __forceinline__ Frag decode(const Raw& w, uint32_t, int u, int) {
