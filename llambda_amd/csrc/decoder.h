@@ -65,7 +65,7 @@ struct DecoderPlan {
 
 // Positions per attention workgroup and the longest context.
 #ifndef LLHIP_ATTN_CHUNK
-#define LLHIP_ATTN_CHUNK 128
+#define LLHIP_ATTN_CHUNK 64
 #endif
 constexpr int kAttnChunk = LLHIP_ATTN_CHUNK;
 constexpr int kAttnMaxChunks = 32768 / kAttnChunk;

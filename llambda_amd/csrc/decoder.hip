@@ -46,7 +46,8 @@ hipError_t decoder_state_launch(const DecoderPlan& p, int token, int position,
 // kAttnChunk, for the G query heads of its kv head: scores (16 lanes per
 // slot, xor-shuffle reduction), the chunk's max m_c, e_p = exp(s_p - m_c) and
 // their sum S_c, and the unnormalised sum_p e_p v_p.  A second launch
-// combines the chunks in order: M = max m_c, a_c = exp(m_c - M),
+// combines the chunks (four quarters of them in order, then the quarters):
+// M = max m_c, a_c = exp(m_c - M),
 // context = (sum_c a_c pv_c) / (sum_c a_c S_c).  The reference normalises
 // every probability before the weighted sum; the two agree to rounding
 // (single-precision exp of each difference, computed in double as SBCL
@@ -190,68 +191,78 @@ attention_kernel(const float* __restrict__ q, const float* __restrict__ kc,
   }
 }
 
-// Chunks of one query head combined in chunk order: M = max m_c,
-// a_c = exp(m_c - M) (single, computed in double), S = sum a_c S_c,
-// out = (sum a_c pv_c) / S.  Workgroup h, thread d = element d.
+// Chunks of one query head combined: M = max m_c, a_c = exp(m_c - M)
+// (single, computed in double), S = sum a_c S_c, out = (sum a_c pv_c) / S.
+// Workgroup h; thread (q, d) = (t / D, t % D) takes element d over quarter q
+// of the chunks, in chunk order, and the four quarters' sums are added in
+// quarter order.  (The partials were just written by workgroups on other
+// XCDs, so every dependent round of loads is slow: a thread requests its
+// quarter's values, up to kCombineLoads, at once -- a wave holds at most 63
+// vector loads in flight -- and the maxima and sums go through LDS.)
+constexpr int kCombineQuarters = 4;
+constexpr int kCombineLoads = 32;
 template <int D, int G>
-__global__ void __launch_bounds__(D)
+__global__ void __launch_bounds__(kCombineQuarters * D)
 attention_combine_kernel(const float* __restrict__ part, const float* __restrict__ pmax,
                          const float* __restrict__ psum, const int* __restrict__ state,
                          int max_chunks, float* __restrict__ out) {
-  // the partials were just written by workgroups on other XCDs, so every
-  // dependent round of loads is slow: the chunk maxima, sums and this
-  // thread's partial values of up to U chunks are all loaded at once
-  constexpr int U = 64;
-  __shared__ float alpha[kAttnMaxChunks];
-  __shared__ float red[D / 64];
-  const int h = blockIdx.x, d = threadIdx.x, lane = d & 63;
+  constexpr int T = kCombineQuarters * D, U = kCombineLoads;
+  __shared__ float alpha[kAttnMaxChunks], ssum[kAttnMaxChunks];
+  __shared__ float red[T / 64];
+  __shared__ float qacc[kCombineQuarters][D], qs[kCombineQuarters];
+  const int h = blockIdx.x, t = threadIdx.x, lane = t & 63;
+  const int q = t / D, d = t - q * D;
   const int kvh = h / G, hh = h % G;
   const int nchunks = (state[1] + kAttnChunk) / kAttnChunk;
+  const int per = (nchunks + kCombineQuarters - 1) / kCombineQuarters;
+  const int c_lo = q * per, c_hi = min(nchunks, c_lo + per);
   const int64_t base = (int64_t)kvh * max_chunks * G + hh;  // chunk c at base + c * G
   const float* pc = part + base * D + d;
-  float ps[U], pv[U];
+  float pv[U];
 #pragma unroll
-  for (int u = 0; u < U; ++u) {
-    const int c = min(u, nchunks - 1);
-    ps[u] = psum[base + (int64_t)c * G];
-    pv[u] = pc[(int64_t)c * G * D];
-  }
+  for (int u = 0; u < U; ++u) pv[u] = pc[(int64_t)max(0, min(c_lo + u, c_hi - 1)) * G * D];
   float m = -INFINITY;
-  for (int c = d; c < nchunks; c += D) {
+  for (int c = t; c < nchunks; c += T) {
     const float v = pmax[base + (int64_t)c * G];
     alpha[c] = v;
+    ssum[c] = psum[base + (int64_t)c * G];
     m = fmaxf(m, v);
   }
   m = wave_max(m);
-  if (lane == 0) red[d >> 6] = m;
+  if (lane == 0) red[t >> 6] = m;
   __syncthreads();
   m = red[0];
 #pragma unroll
-  for (int w = 1; w < D / 64; ++w) m = fmaxf(m, red[w]);
-  for (int c = d; c < nchunks; c += D) alpha[c] = (float)exp((double)(alpha[c] - m));
+  for (int w = 1; w < T / 64; ++w) m = fmaxf(m, red[w]);
+  for (int c = t; c < nchunks; c += T) alpha[c] = (float)exp((double)(alpha[c] - m));
   __syncthreads();
-  // M = max m_c, a_c = exp(m_c - M), S = sum a_c S_c, out = (sum a_c pv_c) / S,
-  // the sums in chunk order
   float S = 0.f, acc = 0.f;
-  for (int c0 = 0; c0 < nchunks; c0 += U) {
-    if (c0 > 0) {
+  for (int c0 = c_lo; c0 < c_hi; c0 += U) {
+    if (c0 > c_lo) {
 #pragma unroll
-      for (int u = 0; u < U; ++u) {
-        const int c = min(c0 + u, nchunks - 1);
-        ps[u] = psum[base + (int64_t)c * G];
-        pv[u] = pc[(int64_t)c * G * D];
-      }
+      for (int u = 0; u < U; ++u) pv[u] = pc[(int64_t)min(c0 + u, c_hi - 1) * G * D];
     }
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-      if (c0 + u < nchunks) {
+      if (c0 + u < c_hi) {
         const float a = alpha[c0 + u];
-        S += a * ps[u];
+        S += a * ssum[c0 + u];
         acc += a * pv[u];
       }
     }
   }
-  out[(int64_t)h * D + d] = acc / S;
+  qacc[q][d] = acc;
+  if (d == 0) qs[q] = S;
+  __syncthreads();
+  if (q == 0) {
+    float sa = qacc[0][d], ss = qs[0];
+#pragma unroll
+    for (int i = 1; i < kCombineQuarters; ++i) {
+      sa += qacc[i][d];
+      ss += qs[i];
+    }
+    out[(int64_t)h * D + d] = sa / ss;
+  }
 }
 
 bool decoder_head_supported(int head_dim, int group) {
@@ -266,7 +277,8 @@ static hipError_t launch_attention_t(const DecoderPlan& p, const float* q, const
   hipLaunchKernelGGL((attention_kernel<D, G>), grid, dim3(64 * kAttnWaves), 0, stream, q, kc, vc,
                      (int64_t)p.context * D, p.state, p.att_part, p.att_max, p.att_sum,
                      p.att_chunks);
-  hipLaunchKernelGGL((attention_combine_kernel<D, G>), dim3(p.heads), dim3(D), 0, stream,
+  hipLaunchKernelGGL((attention_combine_kernel<D, G>), dim3(p.heads), dim3(kCombineQuarters * D), 0,
+                     stream,
                      p.att_part, p.att_max, p.att_sum, p.state, p.att_chunks, out);
   return hipGetLastError();
 }

@@ -100,10 +100,11 @@ def test_llama_steps_from_empty_cache(hip, name):
         sess.close()
 
 
-@pytest.mark.parametrize("prefill", [127, 128, 129, 290])
+@pytest.mark.parametrize("prefill", [62, 63, 64, 127, 128, 129, 290])
 def test_llama_step_over_prefilled_cache(hip, prefill):
     """Cache slots 0..prefill-1 written from the host; the step at `prefill`
-    attends over 1, 2 or 3 chunks of 128 slots (the cross-chunk combine)."""
+    attends over 1 to 5 chunks of 64 slots (the cross-chunk combine, its
+    quarters of the chunks partly empty)."""
     c, _ = CONFIGS["g4d128"]
     rng = np.random.default_rng(prefill)
     w = synthetic_llama(rng, c)
