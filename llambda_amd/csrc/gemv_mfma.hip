@@ -692,17 +692,24 @@ __device__ __forceinline__ void gemv_mfma_body(uint8_t* lds, int wg, int nwg, co
     reinterpret_cast<u32x4*>(lds)[i] = u32x4{0u, 0u, 0u, 0u};
   using IT = std::conditional_t<TYPE == kQ4_K, Q4Items, Q6Items>;
   const int first = min(nbuf, steps);
-  if (table_one_batch<IT, kMfmaWaves>(nblk) && first == 1) {
-    // one stage per wave: its DMA is issued right behind the table's loads
-    // and streams in while the table is built (never for a wave without
-    // steps -- small matrices leave some waves no tile -- whose step 0 would
-    // lie past the rows)
-    uint32_t o[Ch::kLoads];
-    const uint8_t* base_al = stage_src(0, o);
-    build_table_overlapped<IT, kMfmaWaves, Ch::kLoads>(table, gsum, x, nblk, f.norm_w,
-                                                        f.norm_eps, partial, base_al, o,
-                                                        stage_lds);
-  } else {
+  // (the overlapped form holds a stage of at most seven loads: four-block
+  // chunks take the plain one)
+  bool overlapped = false;
+  if constexpr (Ch::kLoads <= 7) {
+    if (table_one_batch<IT, kMfmaWaves>(nblk) && first == 1) {
+      // one stage per wave: its DMA is issued right behind the table's loads
+      // and streams in while the table is built (never for a wave without
+      // steps -- small matrices leave some waves no tile -- whose step 0
+      // would lie past the rows)
+      uint32_t o[Ch::kLoads];
+      const uint8_t* base_al = stage_src(0, o);
+      build_table_overlapped<IT, kMfmaWaves, Ch::kLoads>(table, gsum, x, nblk, f.norm_w,
+                                                          f.norm_eps, partial, base_al, o,
+                                                          stage_lds);
+      overlapped = true;
+    }
+  }
+  if (!overlapped) {
     // activation table first: its loads would otherwise queue behind the
     // weight stages' and hold every wave's first step back (measured: the
     // 4096 x 4096 Q4_K GEMV 7.5 -> 6.2 us, the Llama decode token -5%)
