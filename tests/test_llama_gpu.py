@@ -8,6 +8,8 @@ the fused GEMV, the chunked attention softmax and the norms differ from the
 reference's serial loops, and a wrong head mapping, rotation or cache slot
 moves logits by O(1); the full-size token, in addition, every logit within
 1e-4 * sum_i |w_ri h_i| of its row (h the oracle's input to the output rows)."""
+import dataclasses
+
 import numpy as np
 import pytest
 
@@ -120,6 +122,26 @@ def test_llama_step_over_prefilled_cache(hip, prefill):
         ref = oracle.llama_step(w, kv, 7, prefill, threads=8)
         _check_logits(got, ref, f"prefill {prefill}")
         _check_slot(sess, w, kv, 0, prefill, 7)
+    finally:
+        sess.close()
+
+
+def test_llama_step_over_a_long_prefilled_cache(hip):
+    """8300 cached slots: 130 chunks of 64, whose combine quarters of 33
+    chunks take a second round of loads."""
+    c = dataclasses.replace(CONFIGS["g4d128"][0], context=8400)
+    prefill = 8300
+    rng = np.random.default_rng(8300)
+    w = synthetic_llama(rng, c)
+    sess = HipLlamaSession(w)
+    kv = _kv(c)
+    kv[:, :, :, :prefill] = rng.normal(size=kv[:, :, :, :prefill].shape)
+    try:
+        for layer in range(c.layer_count):
+            sess.write_kv(layer, 0, kv[layer, 0, :, :prefill], kv[layer, 1, :, :prefill])
+        got = sess.step(7, prefill)
+        ref = oracle.llama_step(w, kv, 7, prefill, threads=8)
+        _check_logits(got, ref, f"prefill {prefill}")
     finally:
         sess.close()
 
